@@ -1,0 +1,47 @@
+// Host-side internals shared by the C-ABI translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "hs_gpu.h"
+
+namespace hs {
+
+// Thread-local last error text (hs_last_error).
+void set_error(const std::string& message);
+void clear_error();
+
+// Argument rejection: records the message and returns HS_ERR_ARGUMENT.
+int reject(const char* message);
+// HIP failure: records "<what>: <hip error string>" and returns HS_ERR_HIP.
+int hip_fail(hipError_t status, const char* what);
+
+// Compute units of the current device (cached per device ordinal).
+int device_cu_count();
+
+inline hipStream_t as_stream(void* stream) { return static_cast<hipStream_t>(stream); }
+
+// Round a byte count up to 256 B so workspace slices stay aligned.
+inline size_t align256(size_t bytes) { return (bytes + 255) & ~size_t(255); }
+
+// ---- launch wrappers implemented in the .hip translation units ----------
+int launch_score(const uint16_t* q, const uint16_t* keys, size_t stride_words,
+                 const int32_t* rows, uint32_t pool_rows, uint32_t tokens, uint16_t* scores,
+                 size_t score_stride, uint32_t* head0_partial, hipStream_t stream);
+
+size_t select_workspace_bytes(uint32_t heads, uint32_t n);
+int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_t n,
+                  float alpha, float ratio, uint32_t flags, const uint32_t* head0_partial,
+                  uint32_t* ids, size_t ids_stride, uint32_t* counts, uint32_t* member,
+                  hs_status_t* status, void* workspace, hipStream_t stream);
+
+size_t attention_workspace_bytes(uint32_t n);
+int launch_attention(const float* q, const uint8_t* pool, size_t row_bytes,
+                     const int32_t* rows, uint32_t pool_rows, const uint32_t* member,
+                     uint32_t n, float* out,
+                     void* workspace, hipStream_t stream);
+
+}  // namespace hs

@@ -1,0 +1,229 @@
+// Library runtime: error reporting, device properties, the fused decode-layer
+// entry point, device self checks of the conversion units, and the
+// deterministic synthetic-input generators used by tests and the benchmark.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <array>
+#include <atomic>
+#include <cmath>
+#include <string>
+
+#include "hs_device.hpp"
+#include "hs_internal.hpp"
+
+namespace hs {
+
+namespace {
+thread_local std::string g_last_error;
+std::array<std::atomic<int>, 64> g_cu_count{};
+}  // namespace
+
+void set_error(const std::string& message) { g_last_error = message; }
+void clear_error() { g_last_error.clear(); }
+
+int reject(const char* message) {
+    g_last_error = message;
+    return HS_ERR_ARGUMENT;
+}
+
+int hip_fail(hipError_t status, const char* what) {
+    g_last_error = std::string(what) + ": " + hipGetErrorString(status);
+    return HS_ERR_HIP;
+}
+
+int device_cu_count() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
+    int cached = g_cu_count[device].load(std::memory_order_relaxed);
+    if (cached > 0) return cached;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        cus <= 0)
+        cus = 256;
+    g_cu_count[device].store(cus, std::memory_order_relaxed);
+    return cus;
+}
+
+namespace {
+
+// ---- fused decode layer ------------------------------------------------------
+
+struct LayerPlan {
+    size_t off_partial, off_member, off_select, off_attn, total;
+};
+
+LayerPlan plan_layer(uint32_t n) {
+    LayerPlan p{};
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+        const size_t here = at;
+        at += align256(bytes);
+        return here;
+    };
+    p.off_partial = take(sizeof(uint32_t) * ((n + 63) / 64));
+    p.off_member = take(sizeof(uint32_t) * 32 * ((n + 31) / 32));
+    p.off_select = take(select_workspace_bytes(32, n));
+    p.off_attn = take(attention_workspace_bytes(n));
+    p.total = at;
+    return p;
+}
+
+// ---- self checks -----------------------------------------------------------
+
+// checksum[hi] = sum over lo of (f2h(bits(hi<<16|lo)) + 1) * (lo + 1), NaN
+// inputs contribute 0 (the CPU fold skips them the same way).
+__global__ void __launch_bounds__(256) f16_checksum_kernel(uint64_t* __restrict__ out) {
+    __shared__ uint64_t part[4];
+    const uint32_t hi = blockIdx.x;
+    uint64_t acc = 0;
+    for (uint32_t lo = threadIdx.x; lo < 65536; lo += 256) {
+        const uint32_t bits = (hi << 16) | lo;
+        const bool nan = (bits & 0x7f800000u) == 0x7f800000u && (bits & 0x7fffffu);
+        if (!nan) acc += static_cast<uint64_t>(f2h(__uint_as_float(bits)) + 1u) * (lo + 1u);
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63u) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) out[hi] = part[0] + part[1] + part[2] + part[3];
+}
+
+__global__ void scale_table_kernel(uint16_t* __restrict__ out) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < 65536) out[i] = static_cast<uint16_t>(scale_raw(i));
+}
+
+// ---- synthetic inputs --------------------------------------------------------
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    x += 0x9e3779b97f4a7c15ull;
+    x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+    x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+    return x ^ (x >> 31);
+}
+// Standard normal pair for counter i of stream seed (Box-Muller).
+__device__ __forceinline__ float2 gaussian2(uint64_t seed, uint64_t i) {
+    const uint64_t r = splitmix64(seed * 0x632be59bd9b4e019ull + i);
+    const float u1 = (static_cast<float>(r >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    const float u2 = static_cast<float>((r >> 16) & 0xffffffu) * (1.0f / 16777216.0f);
+    const float rad = sqrtf(-2.0f * logf(u1));
+    float s, c;
+    sincosf(6.283185307179586f * u2, &s, &c);
+    return make_float2(rad * c, rad * s);
+}
+
+__global__ void gaussian_kernel(uint16_t* __restrict__ dst, size_t count, uint64_t seed,
+                                float scale) {
+    const size_t pair = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t i = pair * 2;
+    if (i >= count) return;
+    const float2 g = gaussian2(seed, pair);
+    dst[i] = static_cast<uint16_t>(f2h(g.x * scale));
+    if (i + 1 < count) dst[i + 1] = static_cast<uint16_t>(f2h(g.y * scale));
+}
+
+// K rows of `heads_per_row` x 128 channels at row_stride_words per token,
+// N(0,1) then RoPE (adjacent pairs, base theta) at position = token.
+__global__ void rope_keys_kernel(uint16_t* __restrict__ dst, uint32_t tokens, size_t stride,
+                                 uint32_t heads, uint64_t seed, float theta) {
+    const size_t pair = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t per_token = static_cast<size_t>(heads) * 64;
+    if (pair >= per_token * tokens) return;
+    const uint32_t t = static_cast<uint32_t>(pair / per_token);
+    const uint32_t within = static_cast<uint32_t>(pair % per_token);
+    const uint32_t i = within & 63u;  // rotation pair index within the head
+    const float2 g = gaussian2(seed, pair);
+    const float freq = powf(theta, -2.0f * static_cast<float>(i) / 128.0f);
+    float s, c;
+    sincosf(static_cast<float>(t) * freq, &s, &c);
+    uint16_t* row = dst + static_cast<size_t>(t) * stride + 2 * within;
+    row[0] = static_cast<uint16_t>(f2h(g.x * c - g.y * s));
+    row[1] = static_cast<uint16_t>(f2h(g.x * s + g.y * c));
+}
+
+}  // namespace
+}  // namespace hs
+
+extern "C" {
+
+const char* hs_version(void) { return "hillserve_amd 0.1 gfx950"; }
+const char* hs_last_error(void) { return hs::g_last_error.c_str(); }
+
+size_t hs_decode_layer_workspace_bytes(uint32_t n) { return hs::plan_layer(n ? n : 1).total; }
+
+int hs_decode_layer(const uint16_t* q16_dev, const float* q32_dev, const uint8_t* pool_dev,
+                    const int32_t* row_of_id_dev, uint32_t pool_rows, uint32_t n, float alpha,
+                    float ratio,
+                    uint32_t flags, uint16_t* scores_dev, uint32_t* ids_dev, size_t ids_stride,
+                    uint32_t* counts_dev, float* out_dev, hs_status_t* status_dev,
+                    void* workspace_dev, void* stream) {
+    hs::clear_error();
+    if (!q16_dev || !q32_dev || !pool_dev || !scores_dev || !ids_dev || !out_dev || !status_dev ||
+        !workspace_dev)
+        return hs::reject("decode layer: null pointer");
+    if (n == 0 || n > 65536) return hs::reject("decode layer: n must be 1..65536");
+    if (flags & ~uint32_t(HS_SELECT_FP32_COUNTS)) return hs::reject("decode layer: unknown flags");
+    hipStream_t s = hs::as_stream(stream);
+    const hs::LayerPlan p = hs::plan_layer(n);
+    char* ws = static_cast<char*>(workspace_dev);
+    uint32_t* partial = reinterpret_cast<uint32_t*>(ws + p.off_partial);
+    uint32_t* member = reinterpret_cast<uint32_t*>(ws + p.off_member);
+    int rc = hs::launch_score(q16_dev, reinterpret_cast<const uint16_t*>(pool_dev), 2048,
+                              row_of_id_dev, pool_rows, n, scores_dev, n, partial, s);
+    if (rc != HS_OK) return rc;
+    rc = hs::launch_select(scores_dev, 32, n, n, alpha, ratio,
+                           flags | HS_SELECT_SCALE_RAW | HS_SELECT_REQUIRE_K, partial, ids_dev,
+                           ids_stride, counts_dev, member, status_dev, ws + p.off_select, s);
+    if (rc != HS_OK) return rc;
+    return hs::launch_attention(q32_dev, pool_dev, 4096, row_of_id_dev, pool_rows, member, n,
+                                out_dev, ws + p.off_attn, s);
+}
+
+int hs_selftest_f16_checksums(uint64_t* checksums_dev, void* stream) {
+    hs::clear_error();
+    if (!checksums_dev) return hs::reject("selftest: null pointer");
+    hipLaunchKernelGGL(hs::f16_checksum_kernel, dim3(65536), dim3(256), 0, hs::as_stream(stream),
+                       checksums_dev);
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hs::hip_fail(st, "selftest launch");
+}
+
+int hs_selftest_scale_table(uint16_t* table_dev, void* stream) {
+    hs::clear_error();
+    if (!table_dev) return hs::reject("selftest: null pointer");
+    hipLaunchKernelGGL(hs::scale_table_kernel, dim3(256), dim3(256), 0, hs::as_stream(stream),
+                       table_dev);
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hs::hip_fail(st, "selftest launch");
+}
+
+int hs_fill_gaussian_f16(uint16_t* dst_dev, size_t count, uint64_t seed, float scale,
+                         void* stream) {
+    hs::clear_error();
+    if (!dst_dev || count == 0) return hs::reject("fill: empty destination");
+    const size_t pairs = (count + 1) / 2;
+    const size_t blocks = (pairs + 255) / 256;
+    if (blocks > 0x7fffffffu) return hs::reject("fill: too large");
+    hipLaunchKernelGGL(hs::gaussian_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                       hs::as_stream(stream), dst_dev, count, seed, scale);
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hs::hip_fail(st, "fill launch");
+}
+
+int hs_fill_rope_keys_f16(uint16_t* dst_dev, uint32_t tokens, size_t row_stride_words,
+                          uint32_t heads_per_row, uint64_t seed, float theta, void* stream) {
+    hs::clear_error();
+    if (!dst_dev || tokens == 0 || heads_per_row == 0 ||
+        row_stride_words < size_t(heads_per_row) * 128)
+        return hs::reject("rope fill: bad shape");
+    const size_t pairs = size_t(tokens) * heads_per_row * 64;
+    const size_t blocks = (pairs + 255) / 256;
+    if (blocks > 0x7fffffffu) return hs::reject("rope fill: too large");
+    hipLaunchKernelGGL(hs::rope_keys_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                       hs::as_stream(stream), dst_dev, tokens, row_stride_words, heads_per_row,
+                       seed, theta);
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hs::hip_fail(st, "rope fill launch");
+}
+
+}  // extern "C"

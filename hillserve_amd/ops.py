@@ -1,0 +1,232 @@
+"""Torch-tensor wrappers over the C ABI (device memory and streams only).
+
+F16 data travel as ``torch.float16`` tensors (bit patterns are what the
+kernels consume); uint32 ids/counts/bitmaps as ``torch.int32``.  Every
+function enqueues on ``stream`` (default: torch's current stream) and
+returns without synchronising, except ``read_status``.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import (HS_SELECT_FP32_COUNTS, HS_SELECT_REQUIRE_K, HS_SELECT_SCALE_RAW, HsError, check,
+               lib)
+
+H, KH, D = 32, 8, 128
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _s(stream):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _need_cuda(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("hillserve_amd operates on device tensors only")
+
+
+def workspace(nbytes: int, device="cuda") -> torch.Tensor:
+    return torch.empty(max(256, int(nbytes)), dtype=torch.uint8, device=device)
+
+
+def new_status(device="cuda") -> torch.Tensor:
+    return torch.zeros(4, dtype=torch.int32, device=device)
+
+
+def read_status(status: torch.Tensor) -> dict:
+    """Synchronise on the status tensor and decode hs_status_t."""
+    v = status.cpu().tolist()
+    return {"code": int(v[0]), "k": int(v[1]) & 0xFFFFFFFF,
+            "boundary_tied_heads": int(v[2]) & 0xFFFFFFFF,
+            "head0_max_key": int(v[3]) & 0xFFFFFFFF}
+
+
+# ---- scoring -----------------------------------------------------------------
+
+def full_gqa_pipeline(q16, keys, tokens, out=None, stream=None):
+    """V3 kernel ABI (hillserve_full_gqa_pipeline): scores F16[32, tokens]."""
+    _need_cuda(q16, keys)
+    if out is None:
+        out = torch.empty((H, tokens), dtype=torch.float16, device=keys.device)
+    check(lib().hs_full_gqa_pipeline(_p(q16), _p(keys), _p(out), tokens, _s(stream)))
+    return out
+
+
+def score(q16, keys, tokens, key_stride_words=1024, rows=None, out=None, score_stride=None,
+          head0_partial=None, pool_rows=None, stream=None):
+    """Ordered-FP32 raw GQA scores F16[32, score_stride] (columns < tokens)."""
+    _need_cuda(q16, keys, rows, out, head0_partial)
+    if score_stride is None:
+        score_stride = tokens if out is None else out.shape[-1]
+    if out is None:
+        out = torch.empty((H, score_stride), dtype=torch.float16, device=keys.device)
+    if pool_rows is None:
+        pool_rows = keys.numel() // key_stride_words
+    check(lib().hs_gqa_score(_p(q16), _p(keys), key_stride_words, _p(rows), pool_rows, tokens,
+                             _p(out), score_stride, _p(head0_partial), _s(stream)))
+    return out
+
+
+# ---- selection ---------------------------------------------------------------
+
+def select_workspace_bytes(heads, n):
+    return lib().hs_gqa_select_workspace_bytes(heads, n)
+
+
+def select(scores, heads, stride, n, alpha, ratio, *, scale_raw=False, fp32_counts=False,
+           require_k=False, head0_partial=None, ids=None, ids_stride=None, counts=None,
+           member=None, status=None, ws=None, stream=None):
+    """select_gqa_scores on device.  Returns (ids, counts, member, status)."""
+    _need_cuda(scores)
+    dev = scores.device
+    kmax = min(n, math.floor(float(n) * float(ctypes.c_float(ratio).value)))
+    if ids_stride is None:
+        ids_stride = max(1, kmax)
+    if ids is None:
+        ids = torch.empty((heads, ids_stride), dtype=torch.int32, device=dev)
+    if counts is None:
+        counts = torch.empty(heads, dtype=torch.int32, device=dev)
+    if status is None:
+        status = new_status(dev)
+    if ws is None:
+        ws = workspace(select_workspace_bytes(heads, n), dev)
+    flags = ((HS_SELECT_SCALE_RAW if scale_raw else 0) | (HS_SELECT_FP32_COUNTS if fp32_counts else 0)
+             | (HS_SELECT_REQUIRE_K if require_k else 0))
+    check(lib().hs_gqa_select(_p(scores), heads, stride, n, alpha, ratio, flags,
+                              _p(head0_partial), _p(ids), ids_stride, _p(counts), _p(member),
+                              _p(status), _p(ws), _s(stream)))
+    return ids, counts, member, status
+
+
+# ---- union / pack / gather -------------------------------------------------------
+
+def physical_union(ids, lens, ids_stride, visible, stream=None):
+    dev = ids.device
+    out = torch.empty(visible, dtype=torch.int32, device=dev)
+    out_n = torch.zeros(1, dtype=torch.int32, device=dev)
+    status = new_status(dev)
+    ws = workspace(lib().hs_gqa_union_workspace_bytes(visible), dev)
+    check(lib().hs_gqa_physical_union(_p(ids), _p(lens), ids_stride, visible, _p(out), _p(out_n),
+                                      _p(status), _p(ws), _s(stream)))
+    return out, out_n, status
+
+
+def pack(pool, ids, lens, ids_stride, positions, count, row_of_id=None, max_id=None,
+         stream=None):
+    """pack_gqa_workspace from the device hot pool -> (K, V, mask, status)."""
+    dev = pool.device
+    nq = positions.numel()
+    qpad = (nq + 63) // 64 * 64
+    k = torch.empty(count * H * D, dtype=torch.float16, device=dev)
+    v = torch.empty(count * H * D, dtype=torch.float16, device=dev)
+    mask = torch.empty(H * qpad * count, dtype=torch.float32, device=dev)
+    status = new_status(dev)
+    pool_rows = pool.numel() * pool.element_size() // 4096
+    if max_id is None:
+        max_id = row_of_id.numel() if row_of_id is not None else pool_rows
+    check(lib().hs_gqa_pack(_p(pool), pool_rows, _p(row_of_id), max_id, _p(ids), _p(lens),
+                            ids_stride,
+                            _p(positions), nq, count, _p(k), _p(v), _p(mask), _p(status),
+                            _s(stream)))
+    return k, v, mask, status
+
+
+def gather_rows(prefetched, misses, row_map, count, stream=None):
+    dev = row_map.device
+    k = torch.empty(count * H * D, dtype=torch.float16, device=dev)
+    v = torch.empty(count * H * D, dtype=torch.float16, device=dev)
+    status = new_status(dev)
+    rows_of = lambda t: 0 if t is None else t.numel() * t.element_size() // 4096
+    check(lib().hs_gqa_gather_rows(_p(prefetched), rows_of(prefetched), _p(misses), rows_of(misses),
+                                   _p(row_map), count, _p(k), _p(v), _p(status), _s(stream)))
+    return k, v, status
+
+
+# ---- attention / fused layer -------------------------------------------------------
+
+def attention_workspace_bytes(n):
+    return lib().hs_gqa_attention_workspace_bytes(n)
+
+
+def sparse_attention(q32, pool, n, member, rows=None, row_bytes=4096, out=None, ws=None,
+                     pool_rows=None, stream=None):
+    _need_cuda(q32, pool, member)
+    dev = pool.device
+    if out is None:
+        out = torch.empty((H, D), dtype=torch.float32, device=dev)
+    if ws is None:
+        ws = workspace(attention_workspace_bytes(n), dev)
+    if pool_rows is None:
+        pool_rows = pool.numel() * pool.element_size() // row_bytes
+    check(lib().hs_gqa_sparse_attention(_p(q32), _p(pool), row_bytes, _p(rows), pool_rows,
+                                        _p(member), n, _p(out), _p(ws), _s(stream)))
+    return out
+
+
+def decode_layer_workspace_bytes(n):
+    return lib().hs_decode_layer_workspace_bytes(n)
+
+
+def decode_layer(q16, q32, pool, n, alpha, ratio, *, rows=None, fp32_counts=False, scores=None,
+                 ids=None, ids_stride=None, counts=None, out=None, status=None, ws=None,
+                 pool_rows=None, stream=None):
+    """score -> select -> sparse attention for one layer (all on device)."""
+    dev = pool.device
+    kmax = min(n, math.floor(float(n) * float(ctypes.c_float(ratio).value)))
+    if ids_stride is None:
+        ids_stride = max(1, kmax)
+    if scores is None:
+        scores = torch.empty((H, n), dtype=torch.float16, device=dev)
+    if ids is None:
+        ids = torch.empty((H, ids_stride), dtype=torch.int32, device=dev)
+    if counts is None:
+        counts = torch.empty(H, dtype=torch.int32, device=dev)
+    if out is None:
+        out = torch.empty((H, D), dtype=torch.float32, device=dev)
+    if status is None:
+        status = new_status(dev)
+    if ws is None:
+        ws = workspace(decode_layer_workspace_bytes(n), dev)
+    if pool_rows is None:
+        pool_rows = pool.numel() * pool.element_size() // 4096
+    check(lib().hs_decode_layer(_p(q16), _p(q32), _p(pool), _p(rows), pool_rows, n, alpha, ratio,
+                                HS_SELECT_FP32_COUNTS if fp32_counts else 0, _p(scores), _p(ids),
+                                ids_stride, _p(counts), _p(out), _p(status), _p(ws), _s(stream)))
+    return scores, ids, counts, out, status
+
+
+# ---- device checks and synthetic data -------------------------------------------------
+
+def selftest_f16_checksums(stream=None):
+    out = torch.empty(65536, dtype=torch.int64, device="cuda")
+    check(lib().hs_selftest_f16_checksums(_p(out), _s(stream)))
+    return out
+
+
+def selftest_scale_table(stream=None):
+    out = torch.empty(65536, dtype=torch.int16, device="cuda")
+    check(lib().hs_selftest_scale_table(_p(out), _s(stream)))
+    return out
+
+
+def fill_gaussian(t, seed, scale=1.0, stream=None):
+    check(lib().hs_fill_gaussian_f16(_p(t), t.numel(), seed, scale, _s(stream)))
+    return t
+
+
+def fill_rope_keys(t, tokens, row_stride_words, heads_per_row, seed, theta=500000.0,
+                   stream=None):
+    check(lib().hs_fill_rope_keys_f16(_p(t), tokens, row_stride_words, heads_per_row, seed, theta,
+                                      _s(stream)))
+    return t
+
+
+__all__ = [name for name in dir() if not name.startswith("_")] + ["HsError"]

@@ -1,0 +1,191 @@
+/*
+ * hs_gpu.h — C ABI of the MI355X (gfx950) sparse-KV decode hot path.
+ *
+ * Plain pointers and sizes only.  Every pointer named *_dev is device memory
+ * owned by the caller; `stream` is a hipStream_t passed as void* (NULL = the
+ * null stream).  Calls are stream-ordered and asynchronous unless noted;
+ * device-side failures (nonfinite scores, count overflow, zero selection) are
+ * reported through a caller-owned device status word (hs_status_t) that the
+ * caller reads after synchronising.  Host-detectable argument errors return a
+ * nonzero HS_ERR_* code immediately and enqueue nothing.
+ *
+ * Geometry is the reference's fixed full128 contract: 32 query heads, 8
+ * physical KV heads, 128 channels, query head h reads KV head h/4
+ * (runtime/full_gqa_contract.hpp:16-20, kernels/full_gqa_pipeline/ABI.json).
+ */
+#ifndef HS_GPU_H
+#define HS_GPU_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+enum {
+    HS_OK = 0,
+    HS_ERR_ARGUMENT = 1,     /* shape/stride/extent/parameter rejected       */
+    HS_ERR_NONFINITE = 2,    /* nonfinite score (gqa_policy.cpp:51,53)       */
+    HS_ERR_THRESHOLD = 3,    /* F16 threshold overflow (gqa_policy.cpp:52)   */
+    HS_ERR_COUNT = 4,        /* F16 count overflow (gqa_policy.cpp:56)       */
+    HS_ERR_MEAN = 5,         /* F16 mean overflow (gqa_policy.cpp:58)        */
+    HS_ERR_ZERO_SELECTION = 6, /* k == 0 (full_gqa_runtime.cpp:573)          */
+    HS_ERR_DUPLICATE = 7,    /* duplicate/future id (gqa_pack.hpp:17,33)     */
+    HS_ERR_MISSING = 8,      /* selected id without KV row (gqa_pack.hpp:44) */
+    HS_ERR_HIP = 9,          /* HIP runtime call failed                      */
+    HS_ERR_UNSUPPORTED = 10  /* valid for the reference, beyond this build   */
+};
+
+/* Device-side result of one selection; written by hs_gqa_select*. */
+typedef struct hs_status {
+    int32_t code;            /* HS_OK or HS_ERR_*                            */
+    uint32_t k;              /* selected per query head                      */
+    uint32_t boundary_tied_heads;
+    uint32_t head0_max_key;  /* order key of head-0 maximum (diagnostic)     */
+} hs_status_t;
+
+/* Library identity and the list of exported entry points (for loaders). */
+const char *hs_version(void);
+/* Last host-side error message of the calling thread ("" if none). */
+const char *hs_last_error(void);
+
+/* ---- (1) scoring ---------------------------------------------------------
+ * V3 kernel ABI: replaces hillserve_full_gqa_pipeline
+ * (kernels/full_gqa_pipeline/kernel.hpp:22-25, kernel.cpp:237-253).
+ * q F16[32,128], keys F16[N,8,128] (2048 B/token), scores F16[32,N].
+ * 64 <= tokens <= 32768, tokens % 64 == 0; any other count returns
+ * HS_ERR_ARGUMENT without touching memory (kernel.cpp:251).
+ * Ordered FP32: s = +0; for c in 0..127: s = fl(s + fl(q*k)); F16 RNE. */
+int hs_full_gqa_pipeline(const void *query_dev, const void *keys_dev,
+                         void *scores_dev, uint32_t tokens, void *stream);
+
+/* General scorer: FullGqaCpuScorer::score on device memory
+ * (policy/full_gqa_cpu.hpp:27-50).  Keys at keys_dev + t*key_stride_words
+ * (1024 = packed K, 2048 = interleaved K|V rows of the hot pool).
+ * rows_dev (nullable) maps logical token t -> pool row, like the
+ * concatenated FullGqaKeyView list; rows outside [0, pool_rows) are read as
+ * zero keys (no access).  pool_rows is ignored when rows_dev is NULL.  Scores written to
+ * scores_dev[h*score_stride + t] for t < tokens; 1 <= tokens <= 65536.
+ * head0_partial_dev (nullable, ceil(tokens/64) uint32) receives the order
+ * key maximum of head-0 raw scores per 64-token tile, for hs_gqa_select. */
+int hs_gqa_score(const uint16_t *q_dev, const uint16_t *keys_dev,
+                 size_t key_stride_words, const int32_t *rows_dev,
+                 uint32_t pool_rows, uint32_t tokens, uint16_t *scores_dev,
+                 size_t score_stride, uint32_t *head0_partial_dev,
+                 void *stream);
+
+/* ---- (2) selection -------------------------------------------------------
+ * select_gqa_scores (policy/gqa_policy.cpp:47-70) on device.
+ * scores_dev F16 [heads][stride]; first n columns are candidates.
+ * flags: HS_SELECT_SCALE_RAW applies scaled = F16(raw / sqrtf(128))
+ * (policy/full_gqa_runtime.cpp:571) before selecting; HS_SELECT_FP32_COUNTS
+ * is the reference's fp32_counts; HS_SELECT_REQUIRE_K rejects k == 0.
+ * Outputs: ids_dev [heads][ids_stride] uint32 in rank order (key desc, id
+ * asc), counts_dev [heads] uint32, status_dev (k, tied heads, code), and
+ * optionally member_dev [heads][ceil(n/32)] uint32 bitmaps of the selected
+ * ids (input of hs_gqa_sparse_attention).  ids_stride must be >= the
+ * largest possible k = min(n, floor(n*ratio)).  workspace_dev holds
+ * hs_gqa_select_workspace_bytes(heads, n) bytes of scratch.
+ * head0_partial_dev: NULL, or the per-tile maxima from hs_gqa_score over
+ * the same raw scores (skips one pass over head 0). */
+enum {
+    HS_SELECT_SCALE_RAW = 1u,
+    HS_SELECT_FP32_COUNTS = 2u,
+    HS_SELECT_REQUIRE_K = 4u
+};
+size_t hs_gqa_select_workspace_bytes(uint32_t heads, uint32_t n);
+int hs_gqa_select(const uint16_t *scores_dev, uint32_t heads, size_t stride,
+                  uint32_t n, float alpha, float ratio, uint32_t flags,
+                  const uint32_t *head0_partial_dev, uint32_t *ids_dev,
+                  size_t ids_stride, uint32_t *counts_dev, uint32_t *member_dev,
+                  hs_status_t *status_dev, void *workspace_dev, void *stream);
+
+/* ---- (3) union / gather / pack ------------------------------------------
+ * gqa_physical_union (runtime/gqa_pack.hpp:12-22): 32 id lists
+ * ids_dev[h*ids_stride + j], j < lens_dev[h] -> sorted unique ids in out_dev,
+ * count in *out_n_dev.  Duplicate-within-head or id >= visible sets
+ * status code HS_ERR_DUPLICATE.  workspace: hs_gqa_union_workspace_bytes. */
+size_t hs_gqa_union_workspace_bytes(uint32_t visible);
+int hs_gqa_physical_union(const uint32_t *ids_dev, const uint32_t *lens_dev,
+                          size_t ids_stride, uint32_t visible,
+                          uint32_t *out_dev, uint32_t *out_n_dev,
+                          hs_status_t *status_dev, void *workspace_dev,
+                          void *stream);
+
+/* pack_gqa_workspace (runtime/gqa_pack.hpp:26-58) from the device hot pool.
+ * pool_dev rows of 4096 B (F16 K[8][128] then V[8][128]); row_of_id_dev
+ * (nullable = identity, max_id entries) maps token id -> pool row; a row
+ * outside [0, pool_rows) is absent (HS_ERR_MISSING in the status).
+ * ids_dev/lens_dev as above (lens <= count, nonzero), positions_dev [nq]
+ * ascending query positions (1 <= nq <= 256).  Writes K F16[count][32][128],
+ * V F16[32][128][count], mask F32[32][qpad][count], qpad = ceil(nq/64)*64;
+ * byte-identical to the reference, zero/-inf padding included. */
+int hs_gqa_pack(const uint8_t *pool_dev, uint32_t pool_rows,
+                const int32_t *row_of_id_dev, uint32_t max_id,
+                const uint32_t *ids_dev,
+                const uint32_t *lens_dev, size_t ids_stride,
+                const uint64_t *positions_dev, uint32_t nq, uint32_t count,
+                uint16_t *k_dev, uint16_t *v_dev, float *mask_dev,
+                hs_status_t *status_dev, void *stream);
+
+/* gather_gqa (runtime/gqa_prefetch_cuda.cu:12-22): map_dev[h*count+s] >= 0
+ * reads prefetched row, <= -2 reads miss row -2-map, -1 writes zeros.
+ * Rows are 2048 F16 words (K[8][128] then V[8][128]).  Map entries beyond
+ * prefetched_rows / miss_rows are refused on the device (zeros written,
+ * HS_ERR_MISSING in the status), as GQAPrefetchCuda::deliver refuses them on
+ * the host (runtime/gqa_prefetch_cuda.cu:69). */
+int hs_gqa_gather_rows(const uint16_t *prefetched_dev,
+                       uint32_t prefetched_rows, const uint16_t *misses_dev,
+                       uint32_t miss_rows, const int32_t *map_dev,
+                       uint32_t count, uint16_t *k_dev, uint16_t *v_dev,
+                       hs_status_t *status_dev, void *stream);
+
+/* ---- (4) sparse decode attention ----------------------------------------
+ * Decode attention of patches/llama-b6000-external-attention-device.patch:
+ * 49-66 over the selection, read straight from the hot pool (no pack):
+ * s = (q_h . K_id) / sqrt(128), p = softmax(s), o_h = sum p V_id.  Each
+ * (id, KV head) row is read once for the union of its 4 query heads.
+ * q_dev F32 [32][128]; member_dev from hs_gqa_select ([32][ceil(n/32)]);
+ * out_dev F32 [32][128].  With row_of_id_dev, rows outside [0, pool_rows)
+ * contribute nothing.  workspace: hs_gqa_attention_workspace_bytes. */
+size_t hs_gqa_attention_workspace_bytes(uint32_t n);
+int hs_gqa_sparse_attention(const float *q_dev, const uint8_t *pool_dev,
+                            size_t row_bytes, const int32_t *row_of_id_dev,
+                            uint32_t pool_rows, const uint32_t *member_dev,
+                            uint32_t n,
+                            float *out_dev, void *workspace_dev, void *stream);
+
+/* ---- fused layer step ----------------------------------------------------
+ * One sparse decode layer: score (rehearsal q16 over the hot pool's K
+ * halves) -> select (scaled, alpha, ratio) -> sparse attention (q32).
+ * pool rows 4096 B.  workspace: hs_decode_layer_workspace_bytes. */
+size_t hs_decode_layer_workspace_bytes(uint32_t n);
+int hs_decode_layer(const uint16_t *q16_dev, const float *q32_dev,
+                    const uint8_t *pool_dev, const int32_t *row_of_id_dev,
+                    uint32_t pool_rows, uint32_t n, float alpha, float ratio, uint32_t flags,
+                    uint16_t *scores_dev, uint32_t *ids_dev, size_t ids_stride,
+                    uint32_t *counts_dev, float *out_dev,
+                    hs_status_t *status_dev, void *workspace_dev,
+                    void *stream);
+
+/* ---- device self checks (conversion units) ------------------------------
+ * Hardware F32->F16 (RNE) over all 2^32 patterns, folded into 65536
+ * per-chunk checksums (chunk = high 16 bits); see tests for the fold. */
+int hs_selftest_f16_checksums(uint64_t *checksums_dev, void *stream);
+/* scaled value table for all 65536 raw F16 patterns */
+int hs_selftest_scale_table(uint16_t *table_dev, void *stream);
+
+/* ---- synthetic inputs (bench and tests; generated on device) -------------
+ * Deterministic counter-based generator: value i of stream `seed` is a
+ * Gaussian N(0,1) (Box-Muller over splitmix64), optionally RoPE-rotated at
+ * position t with base theta (adjacent pairs), stored as F16. */
+int hs_fill_gaussian_f16(uint16_t *dst_dev, size_t count, uint64_t seed,
+                         float scale, void *stream);
+int hs_fill_rope_keys_f16(uint16_t *dst_dev, uint32_t tokens,
+                          size_t row_stride_words, uint32_t heads_per_row,
+                          uint64_t seed, float theta, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,87 @@
+"""The C ABI library loads and exports every function include/hs_gpu.h
+declares; host-side argument checks reject bad shapes before any GPU work
+(no compute call is made here)."""
+import ctypes
+
+import pytest
+
+
+@pytest.fixture(scope="module")
+def hs():
+    import hillserve_amd
+    hillserve_amd.lib()
+    return hillserve_amd
+
+
+def test_exports_every_declared_function(hs):
+    declared = hs.header_functions()
+    assert len(declared) >= 18
+    missing = [name for name in declared if not hasattr(hs.lib(), name)]
+    assert missing == []
+    assert set(hs.SIGNATURES) == set(declared)
+
+
+def test_version(hs):
+    assert b"gfx950" in hs.lib().hs_version()
+
+
+def test_v3_rejects_invalid_counts_without_access(hs):
+    # kernels/full_gqa_pipeline/kernel_check.cpp:116-121: null Q/K/S with an
+    # invalid N must be refused without touching memory.
+    for n in [0, 1, 32, 63, 65, 32769, 0xFFFFFFFF]:
+        assert hs.lib().hs_full_gqa_pipeline(None, None, None, n, None) == hs.HS_ERR_ARGUMENT
+        assert "64<=N<=32768" in hs.last_error()
+
+
+def test_select_rejects_bad_parameters(hs):
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: shape checks come first
+    L = hs.lib()
+    args = dict(scores=fake, heads=32, stride=64, n=64, alpha=1.0, ratio=0.2, flags=0,
+                partial=None, ids=fake, ids_stride=64, counts=None, member=None, status=fake,
+                ws=fake, stream=None)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return L.hs_gqa_select(a["scores"], a["heads"], a["stride"], a["n"], a["alpha"],
+                               a["ratio"], a["flags"], a["partial"], a["ids"], a["ids_stride"],
+                               a["counts"], a["member"], a["status"], a["ws"], a["stream"])
+
+    assert call(heads=0) == hs.HS_ERR_ARGUMENT
+    assert call(heads=129) == hs.HS_ERR_ARGUMENT
+    assert call(n=0) == hs.HS_ERR_ARGUMENT
+    assert call(n=65537, stride=70000) == hs.HS_ERR_ARGUMENT
+    assert call(stride=63) == hs.HS_ERR_ARGUMENT
+    assert call(alpha=-1.0) == hs.HS_ERR_ARGUMENT
+    assert call(alpha=float("inf")) == hs.HS_ERR_ARGUMENT
+    assert call(ratio=0.0) == hs.HS_ERR_ARGUMENT
+    assert call(ratio=1.5) == hs.HS_ERR_ARGUMENT
+    assert call(ids_stride=11) == hs.HS_ERR_ARGUMENT  # floor(64*0.2f) = 12
+    assert call(flags=8) == hs.HS_ERR_ARGUMENT
+    assert call(scores=None) == hs.HS_ERR_ARGUMENT
+
+
+def test_score_rejects_bad_shapes(hs):
+    fake = ctypes.c_void_p(0x1000)
+    L = hs.lib()
+    assert L.hs_gqa_score(fake, fake, 1000, None, 0, 64, fake, 64, None, None) == hs.HS_ERR_ARGUMENT
+    assert L.hs_gqa_score(fake, fake, 1024, None, 0, 0, fake, 64, None, None) == hs.HS_ERR_ARGUMENT
+    assert L.hs_gqa_score(fake, fake, 1024, None, 0, 65537, fake, 70000, None, None) == hs.HS_ERR_ARGUMENT
+    assert L.hs_gqa_score(fake, fake, 1024, None, 0, 64, fake, 63, None, None) == hs.HS_ERR_ARGUMENT
+    assert L.hs_gqa_score(fake, ctypes.c_void_p(0x1008), 1024, None, 0, 64, fake, 64, None,
+                          None) == hs.HS_ERR_ARGUMENT  # keys not 16-byte aligned
+
+
+def test_pack_union_gather_reject_bad_shapes(hs):
+    fake = ctypes.c_void_p(0x1000)
+    L = hs.lib()
+    assert L.hs_gqa_physical_union(fake, fake, 8, 0, fake, fake, fake, fake, None) == hs.HS_ERR_ARGUMENT
+    assert L.hs_gqa_physical_union(fake, fake, 8, 66049, fake, fake, fake, fake, None) == hs.HS_ERR_ARGUMENT
+    assert L.hs_gqa_pack(fake, 1, None, 1, fake, fake, 8, fake, 0, 32, fake, fake, fake, fake,
+                         None) == hs.HS_ERR_ARGUMENT  # nq == 0
+    assert L.hs_gqa_pack(fake, 1, None, 1, fake, fake, 8, fake, 257, 32, fake, fake, fake, fake,
+                         None) == hs.HS_ERR_ARGUMENT  # nq > 256
+    assert L.hs_gqa_pack(fake, 1, None, 1, fake, fake, 8, fake, 1, 0, fake, fake, fake, fake,
+                         None) == hs.HS_ERR_ARGUMENT  # count == 0
+    assert L.hs_gqa_gather_rows(fake, 1, fake, 1, fake, 0, fake, fake, fake, None) == hs.HS_ERR_ARGUMENT
+    assert L.hs_gqa_sparse_attention(fake, fake, 1000, None, 0, fake, 64, fake, fake,
+                                     None) == hs.HS_ERR_ARGUMENT

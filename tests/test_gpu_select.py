@@ -1,0 +1,177 @@
+"""GPU parity of kernel #2 (selection) against the oracle: exact k, counts,
+ordered ids and boundary ties; error codes with the reference's precedence."""
+import numpy as np
+import pytest
+import torch
+
+from hs_data import f16_bits, from_dev, rng, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def hb(x):
+    return int(np.float16(x).view(np.uint16))
+
+
+def gpu_select(hs, scores, heads, stride, n, alpha, ratio, **kw):
+    s = to_dev(np.ascontiguousarray(scores, dtype=np.uint16).reshape(-1))
+    ids, counts, member, status = hs.ops.select(s, heads, stride, n, alpha, ratio, **kw)
+    st = hs.ops.read_status(status)
+    k = st["k"]
+    return st, from_dev(ids)[:, :k], from_dev(counts), member
+
+
+def check_against_port(hs, port, scores, heads, stride, n, alpha, ratio, fp32=False):
+    rc, k, ids, counts, tied = port.select(scores, heads, stride, n, alpha, ratio, fp32)
+    st, gids, gcounts, _ = gpu_select(hs, scores, heads, stride, n, alpha, ratio,
+                                      fp32_counts=fp32)
+    assert st["code"] == rc
+    if rc == 0:
+        assert st["k"] == k
+        assert np.array_equal(gcounts, counts)
+        assert np.array_equal(gids, ids)
+        assert st["boundary_tied_heads"] == tied
+    return st
+
+
+def test_known_answers(hs, port):
+    s = np.array([hb(x) for x in [10, 9, 8, 7, 1, 1, 1, 1]], dtype=np.uint16)
+    st, ids, counts, _ = gpu_select(hs, s, 2, 4, 4, 2.0, 1.0)
+    assert st["code"] == 0 and st["k"] == 1 and list(counts) == [3, 0]
+    assert ids[0][0] == 0 and ids[1][0] == 0
+    pad = np.full(16, hb(1000), dtype=np.uint16)
+    for h in range(2):
+        for t in range(5):
+            pad[h * 8 + t] = hb(t)
+    st, ids, _, _ = gpu_select(hs, pad, 2, 8, 5, 10, 0.4)
+    assert st["k"] == 2 and list(ids[0]) == [4, 3]
+    many = np.full(2049, hb(0), dtype=np.uint16)
+    st, _, counts, _ = gpu_select(hs, many, 1, 2049, 2049, 0, 1)
+    assert counts[0] == 2049 and st["k"] == 2048
+    st, _, _, _ = gpu_select(hs, many, 1, 2049, 2049, 0, 1, fp32_counts=True)
+    assert st["k"] == 2049
+
+
+def test_quality_alpha_ladder(hs):
+    P = 128
+    s = np.array([[hb(100 - 2 * t) for t in range(P)] for _ in range(32)], dtype=np.uint16)
+    for alpha, kk, cc in [(5, 3, 3), (10, 6, 6), (20, 11, 11), (50, 25, 26)]:
+        st, ids, counts, _ = gpu_select(hs, s, 32, P, P, alpha, 0.2)
+        assert st["k"] == kk and np.all(counts == cc) and np.all(ids == np.arange(kk))
+
+
+def test_count_rounding_16k(hs):
+    N = 16384
+    s = np.full((32, N), hb(-1000), dtype=np.uint16)
+    s[:, :2049] = hb(0)
+    st, ids, counts, _ = gpu_select(hs, s, 32, N, N, 10.0, 0.2)
+    assert st["k"] == 2048 and counts[0] == 2049 and ids[0][-1] == 2047
+
+
+def test_random_orders(hs, port):
+    g = rng(1741)
+    heads, n, stride = 32, 257, 288
+    for _ in range(6):
+        s = np.full((heads, stride), hb(1000), dtype=np.uint16)
+        s[:, :n] = f16_bits((g.integers(0, 97, size=(heads, n)) - 48) / 2.0)
+        t = np.arange(n)
+        zero = t % 17 == 0
+        s[:, :n][:, zero] = np.where(t[zero] % 2, 0, 0x8000).astype(np.uint16)
+        check_against_port(hs, port, s, heads, stride, n, 10, 0.2)
+
+
+@pytest.mark.parametrize("n,alpha,ratio", [(4096, 0.1, 0.2), (4096, 1.0, 0.2), (4096, 5.0, 0.2),
+                                           (32768, 5.0, 0.2), (32768, 2.5, 0.2),
+                                           (3001, 3.0, 0.5), (65536, 5.0, 0.2)])
+def test_gaussian_against_oracle(hs, port, n, alpha, ratio):
+    g = rng(n + int(alpha * 100))
+    raw = f16_bits(g.standard_normal((32, n)) * 20.0)
+    scaled = port.scale(raw)
+    st = check_against_port(hs, port, scaled, 32, n, n, alpha, ratio)
+    assert st["code"] == 0
+
+
+def test_heavy_ties_and_signed_zero(hs, port):
+    g = rng(5)
+    n = 2000
+    s = f16_bits(g.integers(-3, 4, size=(32, n)).astype(np.float64))
+    s[g.random((32, n)) < 0.3] = 0x8000
+    st = check_against_port(hs, port, s, 32, n, n, 3.0, 0.5)
+    assert st["boundary_tied_heads"] > 0
+
+
+def test_zero_key_boundary_bits(hs, port):
+    # boundary tie decided on raw bits: +0 then -0 at the cut is not "tied"
+    n = 64
+    s = np.full((1, n), hb(-5), dtype=np.uint16)
+    s[0, :3] = hb(1)
+    s[0, 3] = 0x0000
+    s[0, 4] = 0x8000
+    for ratio in (4 / 64, 5 / 64):
+        check_against_port(hs, port, s, 1, n, n, 10.0, ratio)
+
+
+def test_large_k_global_sort(hs, port):
+    n = 40000
+    g = rng(9)
+    s = f16_bits(g.standard_normal((4, n)))
+    st = check_against_port(hs, port, s, 4, n, n, 30.0, 1.0)
+    assert st["k"] > 16384
+
+
+def test_scale_raw_with_scorer_partials(hs, port):
+    from hs_data import v3_sample, config1_inputs
+    q, k, _ = config1_inputs(3, n=2048)
+    n = 2048
+    partial = torch.zeros(n // 64, dtype=torch.int32, device="cuda")
+    raw_dev = hs.ops.score(to_dev(q), to_dev(k.reshape(-1)), n, head0_partial=partial)
+    raw = from_dev(raw_dev)
+    assert np.array_equal(raw, port.score(q, k.reshape(-1), n))
+    scaled = port.scale(raw)
+    rc, kk, ids, counts, tied = port.select(scaled, 32, n, n, 1.0, 0.2)
+    ids_d, counts_d, member, status = hs.ops.select(raw_dev, 32, n, n, 1.0, 0.2, scale_raw=True,
+                                                    head0_partial=partial)
+    st = hs.ops.read_status(status)
+    assert st["code"] == 0 and st["k"] == kk
+    assert np.array_equal(from_dev(ids_d)[:, :kk], ids)
+    assert np.array_equal(from_dev(counts_d), counts)
+
+
+def test_member_bitmaps(hs, port):
+    n = 1000
+    g = rng(21)
+    s = f16_bits(g.standard_normal((32, n)))
+    words = (n + 31) // 32
+    member = torch.zeros(32 * words, dtype=torch.int32, device="cuda")
+    ids, _, _, status = hs.ops.select(to_dev(s.reshape(-1)), 32, n, n, 2.0, 0.2, member=member)
+    st = hs.ops.read_status(status)
+    bits = from_dev(member).reshape(32, words)
+    got = from_dev(ids)[:, : st["k"]]
+    for h in range(32):
+        expected = np.zeros(words, dtype=np.uint32)
+        for i in got[h]:
+            expected[i >> 5] |= np.uint32(1) << np.uint32(i & 31)
+        assert np.array_equal(bits[h], expected)
+
+
+def test_error_codes(hs):
+    s = np.full((2, 8), hb(1), dtype=np.uint16)
+    s[1, 3] = 0x7C00
+    assert gpu_select(hs, s, 2, 8, 8, 1, 0.5)[0]["code"] == hs.HS_ERR_NONFINITE
+    s[1, 3] = hb(1)
+    s[0, 5] = 0xFE00
+    assert gpu_select(hs, s, 2, 8, 8, 1, 0.5)[0]["code"] == hs.HS_ERR_NONFINITE
+    low = np.full((1, 4), hb(-65504), dtype=np.uint16)
+    assert gpu_select(hs, low, 1, 4, 4, 100.0, 1)[0]["code"] == hs.HS_ERR_THRESHOLD
+    over = np.full(65520, hb(0), dtype=np.uint16)
+    assert gpu_select(hs, over, 1, 65520, 65520, 0, 1)[0]["code"] == hs.HS_ERR_COUNT
+    st, ids, counts, _ = gpu_select(hs, over, 1, 65520, 65520, 0, 0.2, fp32_counts=True)
+    assert st["code"] == 0 and st["k"] == 13104 and ids[0][0] == 0 and ids[0][-1] == 13103
+    tiny = np.full((32, 64), hb(-100), dtype=np.uint16)
+    tiny[0, 0] = hb(100)
+    st = gpu_select(hs, tiny, 32, 64, 64, 1.0, 0.2, require_k=True)[0]
+    assert st["code"] == hs.HS_ERR_ZERO_SELECTION
+    st = gpu_select(hs, tiny, 32, 64, 64, 1.0, 0.2)[0]
+    assert st["code"] == 0 and st["k"] == 0
+    with pytest.raises(hs.HsError):
+        gpu_select(hs, tiny, 32, 64, 64, -1.0, 0.2)
