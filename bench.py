@@ -1,0 +1,270 @@
+"""Benchmark of the MI355X sparse-KV decode hot path (one GPU).
+
+Headline (BASELINE.json metric, configs[1]): GQA keys scored per second for a
+decode step of 30 sparse layers at N=32768 (32 query / 8 KV heads, D=128):
+per layer the ordered-FP32 scorer over that layer's own F16 K[32768,8,128]
+(RoPE-structured synthetic keys, theta 500000) and the head-0 alpha-margin
+selection at the 20 % cap.  30 distinct 64 MiB key buffers rotate, so the
+256 MB MALL cannot serve repeats.
+
+Also reported on the same line:
+  roofline      the scoring kernel (dominant): algorithmic bytes per launch
+                (N*2112 + 8192) / its average duration, from HIP events around
+                every scoring launch inside the timed region.
+  layer_step    configs[2]: one full sparse layer (score over the hot pool ->
+                select at the cap -> sparse attention), microseconds per layer
+                over 30 distinct hot pools, and its algorithmic HBM rate.
+  cpu_baseline  the reference's own CPU path (FullGqaCpuScorer + scaling +
+                select_gqa_scores, compiled from the reference sources into
+                oracle/_ref) on a bounded sample, timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+N = 32768
+LAYERS = 30
+ALPHA = 5.0
+RATIO = 0.2
+HBM_PEAK_GBS = 8000.0
+METRIC = "GQA keys scored/s + HBM GB/s at N=32768; per-layer sparse decode step µs"
+SCORE_BYTES = N * 2048 + N * 64 + 8192  # K scan + F16 scores out + Q
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=40)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="bounded CPU-baseline sample duration")
+    p.add_argument("--layer-steps", type=int, default=20)
+    return p.parse_args()
+
+
+def union_bytes(hs, member, n):
+    """sum over KV heads g of |U_g| * 512 B, U_g = union of heads 4g..4g+3."""
+    import torch
+    words = (n + 31) // 32
+    m = member.view(32, words).to(torch.int64) & 0xFFFFFFFF
+    total = 0
+    for g in range(8):
+        u = m[4 * g] | m[4 * g + 1] | m[4 * g + 2] | m[4 * g + 3]
+        total += int(sum(bin(int(x)).count("1") for x in u.cpu().tolist()))
+    return total * 512, total
+
+
+def cpu_baseline(q16_host, k_host, seconds):
+    """Time the reference CPU scoring+selection on one layer's inputs."""
+    import numpy as np
+    import oracle
+    threads = os.cpu_count() or 1
+    ref = oracle.ref()
+    kind = "reference" if ref is not None else "port"
+    table = None
+    if ref is not None:
+        root = np.float32(math.sqrt(128.0))
+        table = np.array([ref.L.hsref_half_bits(float(np.float32(ref.L.hsref_half_value(b)) / root))
+                          for b in range(65536)], dtype=np.uint16)
+    port = oracle.port()
+    keys = 0
+    runs = 0
+    t0 = time.perf_counter()
+    while True:
+        if ref is not None:
+            raw = ref.score(q16_host, k_host, N, 1024, threads=threads, impl=0)
+            scaled = table[raw]
+            rc, *_ = ref.select(scaled, 32, N, N, ALPHA, RATIO, width=int(N * 0.2) + 1)
+        else:
+            raw = port.score(q16_host, k_host, N, 1024)
+            rc, *_ = port.select(port.scale(raw), 32, N, N, ALPHA, RATIO)
+        assert rc == 0
+        keys += N
+        runs += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {
+        "value": keys / dt, "unit": "keys/s", "cores": threads if kind == "reference" else 1,
+        "kind": kind,
+        "sample": (f"{runs} x one layer (N={N}, score with FullGqaCpuScorer automatic impl on "
+                   f"{threads} threads + scaling + select_gqa_scores alpha {ALPHA} cap 0.2) "
+                   f"= {keys} keys in {dt:.1f} s"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(every GPU box in this setup has one GPU; see DESIGN.md for how the path shards)",
+              file=sys.stderr)
+        return 2
+    import numpy as np
+    import torch
+    import hillserve_amd as hs
+    from hillserve_amd import ops
+
+    assert torch.cuda.is_available(), "no GPU visible"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+    kmax = math.floor(N * float(np.float32(RATIO)))
+
+    # ---- 30 layers of packed K -----------------------------------
+    log("allocating 30 layers of K[32768,8,128] F16 (1.9 GB) + queries")
+    keys = [torch.empty(N * 1024, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
+    qs = [torch.empty(4096, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
+    for layer in range(LAYERS):
+        ops.fill_rope_keys(keys[layer], N, 1024, 8, seed=1000 + layer, theta=500000.0)
+        ops.fill_gaussian(qs[layer], seed=5000 + layer)
+    raw = torch.empty((32, N), dtype=torch.float16, device=dev)
+    partial = torch.empty((N + 63) // 64, dtype=torch.int32, device=dev)
+    ids = torch.empty((32, kmax), dtype=torch.int32, device=dev)
+    counts = torch.empty(32, dtype=torch.int32, device=dev)
+    status = ops.new_status(dev)
+    ws = ops.workspace(ops.select_workspace_bytes(32, N), dev)
+    torch.cuda.synchronize()
+
+    def new_event():
+        return torch.cuda.Event(enable_timing=True)
+
+    # one (start, end) event pair around every scoring launch of the timed steps
+    ev = [[(new_event(), new_event()) for _ in range(LAYERS)] for _ in range(args.steps)]
+
+    def step(marks=None):
+        for layer in range(LAYERS):
+            if marks is not None:
+                marks[layer][0].record(stream)
+            ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
+            if marks is not None:
+                marks[layer][1].record(stream)
+            ops.select(raw, 32, N, N, ALPHA, RATIO, scale_raw=True, head0_partial=partial,
+                       ids=ids, ids_stride=kmax, counts=counts, status=status, ws=ws)
+
+    for _ in range(args.warmup):
+        step()
+    st = ops.read_status(status)
+    assert st["code"] == 0 and st["k"] == kmax, st
+    begin, end = new_event(), new_event()
+    torch.cuda.synchronize()
+    begin.record(stream)
+    for i in range(args.steps):
+        step(ev[i])
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = begin.elapsed_time(end) / args.steps
+    score_ms = [a.elapsed_time(b) for marks in ev for a, b in marks]
+    keys_per_s = LAYERS * N / (ms_per_step / 1e3)
+    step_bytes = LAYERS * (SCORE_BYTES + 2 * 32 * N * 2 + 4 * 32 * kmax)
+    avg_score_us = 1e3 * sum(score_ms) / len(score_ms)
+    score_gbs = SCORE_BYTES / (avg_score_us * 1e-6) / 1e9
+    log(f"configs[1]: {ms_per_step:.3f} ms/step ({LAYERS} layers), {keys_per_s/1e9:.2f} G keys/s; "
+        f"score kernel {avg_score_us:.2f} us avg = {score_gbs:.0f} GB/s")
+
+    # ---- full sparse layer over 30 hot pools ---------------------
+    log("allocating 30 hot pools of 32768 x 4096 B (3.8 GB)")
+    del keys
+    pools = [torch.empty(N * 2048, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
+    q32s = [torch.empty((32, 128), dtype=torch.float32, device=dev) for _ in range(LAYERS)]
+    for layer in range(LAYERS):
+        # K halves RoPE-structured, V halves Gaussian
+        ops.fill_rope_keys(pools[layer], N, 2048, 8, seed=2000 + layer, theta=500000.0)
+        v_view = pools[layer].view(N, 2048)[:, 1024:]
+        tmp = torch.empty((N, 1024), dtype=torch.float16, device=dev)
+        ops.fill_gaussian(tmp, seed=3000 + layer)
+        v_view.copy_(tmp)
+        q32s[layer].normal_(generator=torch.Generator(device=dev).manual_seed(layer))
+    del tmp
+    out = torch.empty((32, 128), dtype=torch.float32, device=dev)
+    lws = ops.workspace(ops.decode_layer_workspace_bytes(N), dev)
+    torch.cuda.synchronize()
+
+    def layer_pass():
+        for layer in range(LAYERS):
+            ops.decode_layer(qs[layer], q32s[layer], pools[layer], N, ALPHA, RATIO, scores=raw,
+                             ids=ids, ids_stride=kmax, counts=counts, out=out, status=status,
+                             ws=lws)
+
+    layer_pass()
+    st = ops.read_status(status)
+    assert st["code"] == 0 and st["k"] == kmax, st
+    # member bitmaps of the last layer sit at the workspace's member slice
+    member_off = ((N + 63) // 64 * 4 + 255) // 256 * 256
+    member = lws[member_off: member_off + 32 * ((N + 31) // 32) * 4].view(torch.int32)
+    ubytes, utokens = union_bytes(hs, member, N)
+    b3, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    b3.record(stream)
+    for _ in range(args.layer_steps):
+        layer_pass()
+    e3.record(stream)
+    torch.cuda.synchronize()
+    layer_us = 1e3 * b3.elapsed_time(e3) / (args.layer_steps * LAYERS)
+    layer_bytes = SCORE_BYTES + 2 * 32 * N * 2 + 4 * 32 * kmax + ubytes + 8192 + 16384
+    layer_gbs = layer_bytes / (layer_us * 1e-6) / 1e9
+    log(f"configs[2]: {layer_us:.1f} us/layer, {layer_gbs:.0f} GB/s algorithmic "
+        f"(union {utokens} (id,KV-head) rows of the last layer)")
+
+    # ---- CPU baseline on a bounded sample ----------------------------------------
+    k_sample = torch.empty(N * 1024, dtype=torch.float16, device=dev)
+    ops.fill_rope_keys(k_sample, N, 1024, 8, seed=1000, theta=500000.0)
+    k_host = k_sample.cpu().view(torch.int16).numpy().view(np.uint16)
+    q_host = qs[0].cpu().view(torch.int16).numpy().view(np.uint16)
+    log(f"cpu baseline: ~{args.cpu_seconds:.0f} s of the reference CPU path")
+    cpu = cpu_baseline(q_host, k_host, args.cpu_seconds)
+
+    result = {
+        "metric": METRIC,
+        "value": keys_per_s,
+        "unit": "keys/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (device-generated RoPE-structured Gaussian F16 keys, Gaussian F16 queries)",
+        "config": {
+            "workload": "configs[1]: score + select, 30 sparse layers per decode step, N=32768",
+            "tokens": N, "layers": LAYERS, "query_heads": 32, "kv_heads": 8, "head_dim": 128,
+            "alpha": ALPHA, "cap_ratio": RATIO, "k": kmax, "io_dtype": "f16",
+        },
+        "hbm_gbps": step_bytes / (ms_per_step * 1e-3) / 1e9,
+        "roofline": {
+            "bound": "hbm", "achieved": score_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": score_gbs / HBM_PEAK_GBS, "traffic": None,
+            "kernel": "score_kernel", "avg_launch_us": avg_score_us,
+            "algorithmic_bytes_per_launch": SCORE_BYTES,
+        },
+        "layer_step": {
+            "workload": "configs[2]: score over hot pool + select at cap + sparse attention",
+            "us_per_layer": layer_us, "algorithmic_bytes": layer_bytes,
+            "achieved_gbps": layer_gbs, "frac_of_hbm_peak": layer_gbs / HBM_PEAK_GBS,
+            "union_rows": utokens,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

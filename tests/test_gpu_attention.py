@@ -1,0 +1,57 @@
+"""GPU sparse decode attention (kernel #4) against the FP64 oracle on the same
+selection: relative error <= 2e-3."""
+import numpy as np
+import pytest
+import torch
+
+from hs_data import f16_bits, from_dev, pool_rows, rng, rope_keys, to_dev
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def member_words(ids_rows, n):
+    words = (n + 31) // 32
+    m = np.zeros((32, words), dtype=np.uint32)
+    for h, r in enumerate(ids_rows):
+        r = np.asarray(r, dtype=np.int64)
+        np.bitwise_or.at(m[h], r >> 5, (np.uint32(1) << (r & 31).astype(np.uint32)))
+    return m
+
+
+def rel_err(got, ref):
+    num = np.linalg.norm(got - ref, axis=1)
+    den = np.linalg.norm(ref, axis=1)
+    return float(np.max(num / den))
+
+
+@pytest.mark.parametrize("n,frac", [(257, 0.5), (4096, 0.2), (32768, 0.2), (40000, 0.05)])
+def test_random_selection(hs, port, n, frac):
+    g = rng(n)
+    k = f16_bits(g.standard_normal((n, 8, 128)))
+    v = f16_bits(g.standard_normal((n, 8, 128)))
+    pool = pool_rows(k, v)
+    q = g.standard_normal((32, 128)).astype(np.float32)
+    ids = [np.sort(g.choice(n, size=max(1, int(n * frac)), replace=False)) for _ in range(32)]
+    member = member_words(ids, n)
+    out = hs.ops.sparse_attention(torch.from_numpy(q).cuda(), to_dev(pool.reshape(-1)), n,
+                                  to_dev(member.reshape(-1)))
+    ref = port.attention(q, pool.view(np.uint8), ids)
+    assert rel_err(out.cpu().numpy().astype(np.float64), ref) <= TOL
+
+
+def test_row_map_and_peaked_softmax(hs, port):
+    n = 5000
+    g = rng(8)
+    k = rope_keys(n, 8)
+    v = f16_bits(g.standard_normal((n, 8, 128)))
+    perm = g.permutation(n).astype(np.int32)
+    inv = np.argsort(perm)
+    pool = pool_rows(k, v)[inv]  # row r holds id inv[r]; perm[id] = row
+    q = (g.standard_normal((32, 128)) * 3.0).astype(np.float32)  # sharp softmax
+    ids = [np.sort(g.choice(n, size=700, replace=False)) for _ in range(32)]
+    member = member_words(ids, n)
+    out = hs.ops.sparse_attention(torch.from_numpy(q).cuda(), to_dev(pool.reshape(-1)), n,
+                                  to_dev(member.reshape(-1)), rows=to_dev(perm))
+    ref = port.attention(q, pool.view(np.uint8).reshape(-1), ids, rows=perm)
+    assert rel_err(out.cpu().numpy().astype(np.float64), ref) <= TOL

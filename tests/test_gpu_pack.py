@@ -1,0 +1,112 @@
+"""GPU parity of kernel #3 (union, pack, row-map gather): byte-exact."""
+import numpy as np
+import pytest
+import torch
+
+from hs_data import from_dev, rng, to_dev
+from test_oracle_pack import kat_payload, random_trial
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_ids(selected):
+    stride = max(1, max(len(r) for r in selected))
+    ids = np.zeros((32, stride), dtype=np.uint32)
+    lens = np.zeros(32, dtype=np.uint32)
+    for h, r in enumerate(selected):
+        ids[h, : len(r)] = r
+        lens[h] = len(r)
+    return to_dev(ids), to_dev(lens), stride
+
+
+def gpu_pack(hs, selected, queries, physical, payload, count, extra_rows=0):
+    ids, lens, stride = dev_ids(selected)
+    row_of_id = np.full(max(int(np.max(physical)) + 1, 1) + extra_rows, -1, dtype=np.int32)
+    row_of_id[np.asarray(physical, dtype=np.int64)] = np.arange(len(physical), dtype=np.int32)
+    pool = torch.from_numpy(np.ascontiguousarray(payload)).cuda()
+    pos = torch.tensor(np.asarray(queries, dtype=np.uint64).view(np.int64), device="cuda")
+    k, v, mask, status = hs.ops.pack(pool, ids, lens, stride, pos, count,
+                                     row_of_id=to_dev(row_of_id))
+    st = hs.ops.read_status(status)
+    return st, from_dev(k), from_dev(v), mask.cpu().numpy()
+
+
+def test_pack_known_values(hs, port):
+    ids = [[8, 12] for _ in range(32)]
+    ids[4] = [12, 8]
+    st, k, v, mask = gpu_pack(hs, ids, [10, 12], [8, 12], kat_payload(), 32)
+    rc, pk, pv, pmask = port.pack(ids, [10, 12], [8, 12], kat_payload(), 32)
+    assert st["code"] == 0 and rc == 0
+    assert np.array_equal(k, pk) and np.array_equal(v, pv)
+    assert np.array_equal(mask.view(np.uint32), pmask.view(np.uint32))
+    bad = [list(r) for r in ids]
+    bad[0] = [13]
+    assert gpu_pack(hs, bad, [12], [8, 12], kat_payload(), 32)[0]["code"] == hs.HS_ERR_MISSING
+
+
+@pytest.mark.parametrize("trial", range(0, 48, 3))
+def test_pack_random(hs, port, trial):
+    g = rng(781 + trial)
+    n, slots, rows, payload, selected, queries = random_trial(g, trial)
+    st, k, v, mask = gpu_pack(hs, selected, queries, rows, payload, slots)
+    rc, pk, pv, pmask = port.pack(selected, queries, rows, payload, slots)
+    assert st["code"] == 0 and rc == 0
+    assert np.array_equal(k, pk) and np.array_equal(v, pv)
+    assert np.array_equal(mask.view(np.uint32), pmask.view(np.uint32))
+
+
+def test_pack_many_queries_and_slack_slots(hs, port):
+    g = rng(55)
+    n = 500
+    rows = g.permutation(n).astype(np.uint32)
+    payload = g.integers(0, 256, size=n * 4096, dtype=np.uint8)
+    selected = [np.sort(g.choice(n, size=int(g.integers(1, 200)), replace=False)) for _ in range(32)]
+    queries = sorted(g.choice(n, size=70, replace=False).tolist())
+    queries[-1] = n - 1
+    st, k, v, mask = gpu_pack(hs, selected, queries, rows, payload, 224)
+    rc, pk, pv, pmask = port.pack(selected, queries, rows, payload, 224)
+    assert st["code"] == 0 and rc == 0
+    assert np.array_equal(k, pk) and np.array_equal(v, pv)
+    assert np.array_equal(mask.view(np.uint32), pmask.view(np.uint32))
+
+
+@pytest.mark.parametrize("trial", range(0, 48, 7))
+def test_union_random(hs, port, trial):
+    g = rng(900 + trial)
+    n, slots, rows, payload, selected, queries = random_trial(g, trial)
+    ids, lens, stride = dev_ids(selected)
+    out, out_n, status = hs.ops.physical_union(ids, lens, stride, n)
+    st = hs.ops.read_status(status)
+    m = int(out_n.item())
+    assert st["code"] == 0
+    assert np.array_equal(from_dev(out)[:m], port.physical_union(selected, n)[1])
+    dup = [list(r) for r in selected]
+    dup[31].append(dup[31][0])
+    ids, lens, stride = dev_ids(dup)
+    _, _, status = hs.ops.physical_union(ids, lens, stride, n)
+    assert hs.ops.read_status(status)["code"] == hs.HS_ERR_DUPLICATE
+
+
+def test_gather_rows(hs, port):
+    g = rng(4242)
+    n, slots, rows, payload, selected, queries = random_trial(g, 7)
+    pre_rows = [int(x) for x in rows[: n // 2]]
+    miss_rows = [int(x) for x in rows[n // 2:]]
+    where = {int(id_): i for i, id_ in enumerate(rows)}
+    pre = np.concatenate([payload[where[i] * 4096:(where[i] + 1) * 4096] for i in pre_rows])
+    mis = np.concatenate([payload[where[i] * 4096:(where[i] + 1) * 4096] for i in miss_rows])
+    row_map = np.full(32 * slots, -1, dtype=np.int32)
+    for h in range(32):
+        for s, id_ in enumerate(selected[h]):
+            id_ = int(id_)
+            row_map[h * slots + s] = (pre_rows.index(id_) if id_ in set(pre_rows)
+                                      else -2 - miss_rows.index(id_))
+    k, v, status = hs.ops.gather_rows(torch.from_numpy(pre).cuda(), torch.from_numpy(mis).cuda(),
+                                      to_dev(row_map), slots)
+    pk, pv = port.gather_rows(pre.view(np.uint16), mis.view(np.uint16), row_map, slots)
+    assert hs.ops.read_status(status)["code"] == 0
+    assert np.array_equal(from_dev(k), pk) and np.array_equal(from_dev(v), pv)
+    row_map[5] = len(pre_rows)  # beyond the prefetched payload
+    _, _, status = hs.ops.gather_rows(torch.from_numpy(pre).cuda(), torch.from_numpy(mis).cuda(),
+                                      to_dev(row_map), slots)
+    assert hs.ops.read_status(status)["code"] == hs.HS_ERR_MISSING
