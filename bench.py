@@ -9,8 +9,9 @@ selection at the 20 % cap.  30 distinct 64 MiB key buffers rotate, so the
 
 Also reported on the same line:
   roofline      the scoring kernel (dominant): algorithmic bytes per launch
-                (N*2112 + 8192) / its average duration, from HIP events around
-                every scoring launch inside the timed region.
+                (N*2112 + 8192) / its average duration, from HIP events
+                bracketing 30*K back-to-back scoring launches (one per layer
+                buffer) right after the timed steps, on the same stream.
   layer_step    configs[2]: one full sparse layer (score over the hot pool ->
                 select at the cap -> sparse attention), microseconds per layer
                 over 30 distinct hot pools, and its algorithmic HBM rate.
@@ -54,6 +55,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bounded CPU-baseline sample duration")
     p.add_argument("--layer-steps", type=int, default=20)
+    p.add_argument("--only", choices=["score", "select", "layer"], default=None,
+                   help="profiling aid: run just one kernel family over the 30 layers "
+                        "(prints its own timing line, not the benchmark JSON)")
     return p.parse_args()
 
 
@@ -108,6 +112,36 @@ def cpu_baseline(q16_host, k_host, seconds):
     }
 
 
+def profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status, ws, kmax):
+    """Back-to-back launches of one kernel family over the 30 layers."""
+    def run():
+        for layer in range(LAYERS):
+            if args.only == "score":
+                ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
+            else:
+                ops.select(raw, 32, N, N, ALPHA, RATIO, scale_raw=True, head0_partial=partial,
+                           ids=ids, ids_stride=kmax, counts=counts, status=status, ws=ws)
+    for layer in range(LAYERS):  # valid raw scores and partials for the select loop
+        ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
+    # calibration for HBM counters: one plain 64 MiB device copy (64 MiB read + written)
+    src = torch.empty(N * 1024, dtype=torch.float16, device=raw.device)
+    torch.empty_like(src).copy_(src)
+    for _ in range(args.warmup):
+        run()
+    b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    b.record(stream)
+    for _ in range(args.steps):
+        run()
+    e.record(stream)
+    torch.cuda.synchronize()
+    us = 1e3 * b.elapsed_time(e) / (args.steps * LAYERS)
+    extra = f", {SCORE_BYTES / (us * 1e-6) / 1e9:.0f} GB/s" if args.only == "score" else ""
+    print(f"only {args.only}: {us:.2f} us per launch (back to back, {LAYERS} layers x "
+          f"{args.steps} steps){extra}", flush=True)
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -144,18 +178,15 @@ def main():
     def new_event():
         return torch.cuda.Event(enable_timing=True)
 
-    # one (start, end) event pair around every scoring launch of the timed steps
-    ev = [[(new_event(), new_event()) for _ in range(LAYERS)] for _ in range(args.steps)]
-
-    def step(marks=None):
+    def step():
         for layer in range(LAYERS):
-            if marks is not None:
-                marks[layer][0].record(stream)
             ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
-            if marks is not None:
-                marks[layer][1].record(stream)
             ops.select(raw, 32, N, N, ALPHA, RATIO, scale_raw=True, head0_partial=partial,
                        ids=ids, ids_stride=kmax, counts=counts, status=status, ws=ws)
+
+    if args.only in ("score", "select"):
+        return profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status,
+                            ws, kmax)
 
     for _ in range(args.warmup):
         step()
@@ -165,11 +196,21 @@ def main():
     torch.cuda.synchronize()
     begin.record(stream)
     for i in range(args.steps):
-        step(ev[i])
+        step()
     end.record(stream)
     torch.cuda.synchronize()
     ms_per_step = begin.elapsed_time(end) / args.steps
-    score_ms = [a.elapsed_time(b) for marks in ev for a, b in marks]
+    st = ops.read_status(status)
+    assert st["code"] == 0 and st["k"] == kmax, st
+    # scoring kernel alone: 30*K back-to-back launches over the rotating layers
+    sb, se = new_event(), new_event()
+    sb.record(stream)
+    for _ in range(args.steps):
+        for layer in range(LAYERS):
+            ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
+    se.record(stream)
+    torch.cuda.synchronize()
+    score_ms = [sb.elapsed_time(se) / (args.steps * LAYERS)]
     keys_per_s = LAYERS * N / (ms_per_step / 1e3)
     step_bytes = LAYERS * (SCORE_BYTES + 2 * 32 * N * 2 + 4 * 32 * kmax)
     avg_score_us = 1e3 * sum(score_ms) / len(score_ms)

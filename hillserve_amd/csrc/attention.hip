@@ -98,30 +98,43 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
 #pragma unroll
         for (uint32_t e = 0; e < 8; ++e) qr[j][e] = q[(4 * g + j) * 128 + part16 * 8 + e];
     const uint32_t koff = g * 256 + part16 * 16;
-    for (uint32_t e = wave * 4 + grp; e < total; e += 16) {
-        const uint32_t id = sel_id[e];
-        const size_t r = kRows ? static_cast<size_t>(rows[id]) : id;
-        const uint4 kw = *reinterpret_cast<const uint4*>(pool + r * row_bytes + koff);
-        float kf[8];
-        unpack8(kw, kf);
-        float d[4];
+    constexpr uint32_t kBatch = 8;  // K rows in flight per lane group
+    for (uint32_t e0 = wave * 4 + grp; e0 < total; e0 += 16 * kBatch) {
+        uint4 kw[kBatch];
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-            float acc = 0.0f;
-#pragma unroll
-            for (uint32_t c = 0; c < 8; ++c) acc = __builtin_fmaf(qr[j][c], kf[c], acc);
-            d[j] = acc;
+        for (uint32_t u = 0; u < kBatch; ++u) {
+            const uint32_t e = e0 + 16 * u;
+            if (e < total) {
+                const uint32_t id = sel_id[e];
+                const size_t r = kRows ? static_cast<size_t>(rows[id]) : id;
+                kw[u] = *reinterpret_cast<const uint4*>(pool + r * row_bytes + koff);
+            }
         }
 #pragma unroll
-        for (uint32_t off = 8; off > 0; off >>= 1)
+        for (uint32_t u = 0; u < kBatch; ++u) {
+            const uint32_t e = e0 + 16 * u;
+            if (e >= total) break;  // uniform across the 16 lanes of the group
+            float kf[8];
+            unpack8(kw[u], kf);
+            float d[4];
 #pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) d[j] += __shfl_xor(d[j], off, 64);
-        if (part16 == 0) {
-            const uint32_t mk = sel_mask[e];
-            sc[e] = make_float4((mk & 1u) ? d[0] * kScale : -INFINITY,
-                                (mk & 2u) ? d[1] * kScale : -INFINITY,
-                                (mk & 4u) ? d[2] * kScale : -INFINITY,
-                                (mk & 8u) ? d[3] * kScale : -INFINITY);
+            for (uint32_t j = 0; j < 4; ++j) {
+                float acc = 0.0f;
+#pragma unroll
+                for (uint32_t c = 0; c < 8; ++c) acc = __builtin_fmaf(qr[j][c], kf[c], acc);
+                d[j] = acc;
+            }
+#pragma unroll
+            for (uint32_t off = 8; off > 0; off >>= 1)
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j) d[j] += __shfl_xor(d[j], off, 64);
+            if (part16 == 0) {
+                const uint32_t mk = sel_mask[e];
+                sc[e] = make_float4((mk & 1u) ? d[0] * kScale : -INFINITY,
+                                    (mk & 2u) ? d[1] * kScale : -INFINITY,
+                                    (mk & 4u) ? d[2] * kScale : -INFINITY,
+                                    (mk & 8u) ? d[3] * kScale : -INFINITY);
+            }
         }
     }
     __syncthreads();
@@ -167,18 +180,30 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
 #pragma unroll
         for (uint32_t c = 0; c < 8; ++c) o[j][c] = 0.0f;
     const uint32_t voff = 2048 + g * 256 + part16 * 16;
-    for (uint32_t e = wave * 4 + grp; e < total; e += 16) {
-        const uint32_t id = sel_id[e];
-        const size_t r = kRows ? static_cast<size_t>(rows[id]) : id;
-        const uint4 vw = *reinterpret_cast<const uint4*>(pool + r * row_bytes + voff);
-        float vf[8];
-        unpack8(vw, vf);
-        const float4 p = sc[e];
-        const float pj[4] = {p.x, p.y, p.z, p.w};
+    for (uint32_t e0 = wave * 4 + grp; e0 < total; e0 += 16 * kBatch) {
+        uint4 vw[kBatch];
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j)
+        for (uint32_t u = 0; u < kBatch; ++u) {
+            const uint32_t e = e0 + 16 * u;
+            if (e < total) {
+                const uint32_t id = sel_id[e];
+                const size_t r = kRows ? static_cast<size_t>(rows[id]) : id;
+                vw[u] = *reinterpret_cast<const uint4*>(pool + r * row_bytes + voff);
+            }
+        }
 #pragma unroll
-            for (uint32_t c = 0; c < 8; ++c) o[j][c] = __builtin_fmaf(pj[j], vf[c], o[j][c]);
+        for (uint32_t u = 0; u < kBatch; ++u) {
+            const uint32_t e = e0 + 16 * u;
+            if (e >= total) break;
+            float vf[8];
+            unpack8(vw[u], vf);
+            const float4 p = sc[e];
+            const float pj[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j)
+#pragma unroll
+                for (uint32_t c = 0; c < 8; ++c) o[j][c] = __builtin_fmaf(pj[j], vf[c], o[j][c]);
+        }
     }
     // reduce the 4 id-groups of the wave (lanes l, l+16, l+32, l+48)
 #pragma unroll
@@ -206,24 +231,46 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
     }
 }
 
-// Merge the per-chunk (m, l, o) records of each query head.
-__global__ void __launch_bounds__(128)
+// Merge the per-chunk (m, l, o) records of each query head: one workgroup per
+// head, every record read by a different thread (no serial load chain).
+constexpr uint32_t kMaxChunks = 128;  // n <= 65536
+__global__ void __launch_bounds__(512)
 attn_combine_kernel(const float* __restrict__ part, uint32_t chunks, float* __restrict__ out) {
-    const uint32_t h = blockIdx.x, g = h >> 2, j = h & 3u, c = threadIdx.x;
+    __shared__ float weight[kMaxChunks];
+    __shared__ float red[8];
+    __shared__ float acc4[4][128];
+    const uint32_t h = blockIdx.x, g = h >> 2, j = h & 3u, tid = threadIdx.x;
+    const uint32_t lane = tid & 63u, wave = tid >> 6;
     const float* recs = part + static_cast<size_t>(g) * chunks * 4 * kRecord + j * kRecord;
-    float top = -INFINITY;
-    for (uint32_t i = 0; i < chunks; ++i) top = fmaxf(top, recs[i * 4 * kRecord]);
-    float l = 0.0f, acc = 0.0f;
-    if (top != -INFINITY) {
-        for (uint32_t i = 0; i < chunks; ++i) {
-            const float* r = recs + i * 4 * kRecord;
-            if (r[0] == -INFINITY) continue;
-            const float w = __expf(r[0] - top);
-            l = __builtin_fmaf(r[1], w, l);
-            acc = __builtin_fmaf(r[2 + c], w, acc);
-        }
+    const float m = tid < chunks ? recs[tid * 4 * kRecord] : -INFINITY;
+    const float l = tid < chunks ? recs[tid * 4 * kRecord + 1] : 0.0f;
+    float top = wave_max_f32(m);
+    if (lane == 0) red[wave] = top;
+    __syncthreads();
+    top = red[0];
+#pragma unroll
+    for (uint32_t w = 1; w < 8; ++w) top = fmaxf(top, red[w]);
+    const float w_self = (m == -INFINITY || top == -INFINITY) ? 0.0f : __expf(m - top);
+    if (tid < chunks) weight[tid] = w_self;
+    __syncthreads();
+    float lsum = wave_sum_f32(l * w_self);
+    if (lane == 0) red[wave] = lsum;
+    __syncthreads();
+    float L = 0.0f;
+#pragma unroll
+    for (uint32_t w = 0; w < 8; ++w) L += red[w];
+    const uint32_t c = tid & 127u, quarter = tid >> 7;
+    float a = 0.0f;
+    for (uint32_t i = quarter; i < chunks; i += 4) {
+        const float wi = weight[i];
+        if (wi != 0.0f) a = __builtin_fmaf(recs[i * 4 * kRecord + 2 + c], wi, a);
     }
-    out[h * 128 + c] = l > 0.0f ? acc / l : 0.0f;
+    acc4[quarter][c] = a;
+    __syncthreads();
+    if (tid < 128) {
+        const float sum = acc4[0][tid] + acc4[1][tid] + acc4[2][tid] + acc4[3][tid];
+        out[h * 128 + tid] = L > 0.0f ? sum / L : 0.0f;
+    }
 }
 
 }  // namespace
@@ -251,7 +298,7 @@ int launch_attention(const float* q, const uint8_t* pool, size_t row_bytes, cons
         hipLaunchKernelGGL(attn_partial_kernel<false>, dim3(chunks, 8), dim3(kThreads), 0, stream,
                            q, pool, static_cast<uint32_t>(row_bytes), rows, 0u, member, n,
                            chunks, part);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(32), dim3(128), 0, stream, part, chunks, out);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(32), dim3(512), 0, stream, part, chunks, out);
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "attention launch");
 }

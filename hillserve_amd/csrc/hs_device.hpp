@@ -13,7 +13,11 @@ namespace hs {
 __device__ __forceinline__ float h2f(uint32_t bits) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
 }
+// The empty asm pins the FP32 value in a VGPR: without it the backend may fold
+// the producing FMA and this conversion into one v_fma_mixlo_f16, which rounds
+// the exact product-sum straight to F16 instead of FP32 first, then F16.
 __device__ __forceinline__ uint32_t f2h(float f) {
+    asm volatile("" : "+v"(f));
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
@@ -30,9 +34,21 @@ __device__ __forceinline__ uint32_t key_bits(uint32_t key) {
 }
 
 // scaled = F16(f32(raw) / sqrtf(128)), policy/full_gqa_runtime.cpp:571.
-// __fdiv_rn is the IEEE correctly rounded FP32 quotient.
+// The FP32 quotient of the magnitude comes from the reciprocal estimate plus
+// one FMA residual correction (q0 = x*r, e = x - q0*c exactly, q1 = q0 + e*r),
+// which is the correctly rounded quotient for every F16 input; the sign is
+// reattached afterwards (so -0 stays -0) and inf/NaN map like the
+// reference's half_bits (inf, canonical NaN).  Checked on the device against
+// the CPU restatement for all 65536 inputs.
 __device__ __forceinline__ uint32_t scale_raw(uint32_t raw) {
-    return f2h(__fdiv_rn(h2f(raw), 11.313708498984760390f));
+    constexpr float kRoot = 0x1.6a09e6p+3f;   // RN(sqrt(128)) = sqrtf(128.f)
+    constexpr float kRecip = 0x1.6a09e6p-4f;  // RN(1 / kRoot)
+    const uint32_t sign = raw & 0x8000u;
+    if ((raw & 0x7c00u) == 0x7c00u) return sign | ((raw & 0x3ffu) ? 0x7e00u : 0x7c00u);
+    const float x = h2f(raw & 0x7fffu);
+    const float q0 = x * kRecip;
+    const float e = __builtin_fmaf(-q0, kRoot, x);
+    return f2h(__builtin_fmaf(e, kRecip, q0)) | sign;
 }
 
 __device__ __forceinline__ bool finite_half(uint32_t bits) {

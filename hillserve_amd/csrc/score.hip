@@ -9,17 +9,19 @@
 // multiples of 2^-48 and never FP32-subnormal.  Each lane therefore carries
 // four dependent 128-step FMA chains (the 4 query heads of its KV head).
 //
-// Layout and data movement:
-//  * A tile is 64 tokens x 4 KV heads (one "half" of every token's 2048 B K
-//    row).  The workgroup (4 waves) streams it from HBM with 128-bit loads in
-//    which each wave instruction covers one token's contiguous 1 KiB half
-//    row, and stages it in LDS (64 x 1040 B; the 16 B pad per token spreads a
-//    wave's 64 row reads over distinct banks).
-//  * Wave w owns KV head 4*half+w for all 64 tokens (lane = token), so its
-//    Q operands (4 heads x 128 channels) are wave-uniform and come through
-//    the scalar unit; the FMA reads K from LDS and Q from SGPRs.
-//  * Persistent grid (2 workgroups per CU): while a tile is computed from
-//    LDS the next tile's 64 KiB is already in flight into VGPRs.
+// Work split (no workgroup barriers):
+//  * A wave owns one KV head of 64 consecutive tokens (a "tile") and carries
+//    the 4 query heads of that KV head.  Its Q operands (4 x 128 channels) are
+//    wave-uniform and come through the scalar unit, so every ordered FMA is
+//    one v_fma_mix_f32 with Q from an SGPR and K from a VGPR.
+//  * Keys are fetched coalesced: load instruction j covers tokens 4j..4j+3 of
+//    the tile, 16 lanes per 256 B head row, i.e. 8 whole 128 B lines per
+//    instruction.  The wave transposes the tile through its own 16 KiB LDS
+//    region (XOR-swizzled 16 B chunks: conflict-free writes and reads) so that
+//    afterwards lane t holds token t's 128 channels in order.
+//  * Waves are independent pipelines: the next tile's loads are issued right
+//    after the current tile is parked in LDS, so they overlap its compute.
+//    8 waves per CU keep ~32 MB of keys in flight across the chip.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -31,65 +33,62 @@ namespace hs {
 namespace {
 
 constexpr uint32_t kTileTokens = 64;
-constexpr uint32_t kRowU4 = 65;  // 64 x 16 B (one 1 KiB half row) + 16 B pad
+constexpr uint32_t kWavesPerBlock = 2;
+constexpr uint32_t kChunks = 16;  // 16-byte chunks per 128-channel F16 head row
 
 __device__ __forceinline__ float lo_half(uint32_t w) { return h2f(w & 0xffffu); }
 __device__ __forceinline__ float hi_half(uint32_t w) { return h2f(w >> 16); }
 
+// LDS slot (in 16 B units) of chunk c of tile token t.
+__device__ __forceinline__ uint32_t slot(uint32_t t, uint32_t c) { return t * kChunks + (c ^ (t & 15u)); }
+
 template <bool kRows>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(kWavesPerBlock * 64)
 score_kernel(const uint32_t* __restrict__ q32, const uint16_t* __restrict__ keys,
              uint32_t stride_words, const int32_t* __restrict__ rows, uint32_t pool_rows,
-             uint32_t n,
-             uint16_t* __restrict__ out, uint32_t out_stride,
+             uint32_t n, uint16_t* __restrict__ out, uint32_t out_stride,
              uint32_t* __restrict__ head0_partial) {
-    __shared__ uint4 tile[kTileTokens * kRowU4];
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    __shared__ uint4 lds[kWavesPerBlock][kTileTokens * kChunks];
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t token_tiles = (n + kTileTokens - 1) / kTileTokens;
-    const uint32_t tiles = token_tiles * 2;
-    uint4 staged[16];
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint4* region = lds[w];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + w);
+    const uint32_t waves = gridDim.x * kWavesPerBlock;
+    const uint32_t tiles = ((n + kTileTokens - 1) / kTileTokens) * 8;  // (token tile, KV head)
 
-    auto load = [&](uint32_t tile_id) {
-        const uint32_t base = (tile_id >> 1) * kTileTokens;
-        const uint32_t half = tile_id & 1u;
+    // Row index of token (tile >> 3) * 64 + lane, or ~0 when it reads as zero keys
+    // (past n, or a mapped row outside the pool).
+    auto row_of = [&](uint32_t id) -> uint32_t {
+        const uint32_t token = (id >> 3) * kTileTokens + lane;
+        if (token >= n) return 0xffffffffu;
+        if (!kRows) return token;
+        const uint32_t r = static_cast<uint32_t>(rows[token]);
+        return r < pool_rows ? r : 0xffffffffu;
+    };
+    // Instruction j: lane reads chunk (lane & 15) of tile token 4j + (lane >> 4).
+    auto load = [&](uint32_t id, uint32_t my_row, uint4 (&v)[16]) {
+        const uint16_t* base = keys + (id & 7u) * 128u + (lane & 15u) * 8u;
 #pragma unroll
         for (uint32_t j = 0; j < 16; ++j) {
-            const uint32_t token = base + j * 4 + wave;  // wave-uniform
-            const uint32_t row = token < n ? (kRows ? static_cast<uint32_t>(rows[token]) : token)
-                                           : 0xffffffffu;
-            // mapped rows outside the pool read as zero keys (no access)
-            if (token < n && (!kRows || row < pool_rows)) {
-                const uint4* src = reinterpret_cast<const uint4*>(
-                    keys + static_cast<size_t>(row) * stride_words + half * 512u);
-                staged[j] = src[lane];
-            } else {
-                staged[j] = make_uint4(0u, 0u, 0u, 0u);
-            }
+            const uint32_t r = __shfl(my_row, 4 * j + (lane >> 4), 64);
+            v[j] = r != 0xffffffffu
+                       ? *reinterpret_cast<const uint4*>(base + static_cast<size_t>(r) * stride_words)
+                       : make_uint4(0u, 0u, 0u, 0u);
         }
     };
-
-    uint32_t tile_id = blockIdx.x;
-    if (tile_id < tiles) load(tile_id);
-    for (; tile_id < tiles; tile_id += gridDim.x) {
-        __syncthreads();  // previous tile fully consumed from LDS
+    auto stash = [&](const uint4 (&v)[16]) {
 #pragma unroll
-        for (uint32_t j = 0; j < 16; ++j) tile[(j * 4 + wave) * kRowU4 + lane] = staged[j];
-        __syncthreads();
-        const uint32_t next = tile_id + gridDim.x;
-        if (next < tiles) load(next);
-
-        const uint32_t base = (tile_id >> 1) * kTileTokens;
-        const uint32_t half = tile_id & 1u;
-        const uint32_t kv = half * 4 + wave;  // wave-uniform KV head
+        for (uint32_t j = 0; j < 16; ++j) region[slot(4 * j + (lane >> 4), lane & 15u)] = v[j];
+    };
+    auto compute = [&](uint32_t id) {
+        const uint32_t head_kv = id & 7u;  // wave-uniform
         // q32 holds F16 pairs; head h channel c lives in q32[(h*128 + c)/2].
-        const uint32_t* qh = q32 + kv * 4 * 64;
-        const uint4* row = tile + lane * kRowU4 + wave * 16;
+        const uint32_t* qh = q32 + head_kv * 4 * 64;
         float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll 4
+#pragma unroll
         for (uint32_t j = 0; j < 16; ++j) {
-            const uint4 k8 = row[j];
-            const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
+            const uint4 k4 = region[slot(lane, j)];
+            const uint32_t kw[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
             for (uint32_t p = 0; p < 4; ++p) {
                 const uint32_t c2 = j * 4 + p;  // channel pair index
@@ -106,19 +105,38 @@ score_kernel(const uint32_t* __restrict__ q32, const uint16_t* __restrict__ keys
                 a3 = __builtin_fmaf(hi_half(q3), khi, a3);
             }
         }
-        const uint32_t token = base + lane;
+        const uint32_t token = (id >> 3) * kTileTokens + lane;
         const uint32_t s0 = f2h(a0), s1 = f2h(a1), s2 = f2h(a2), s3 = f2h(a3);
         if (token < n) {
-            uint16_t* o = out + static_cast<size_t>(kv * 4) * out_stride + token;
+            uint16_t* o = out + static_cast<size_t>(head_kv * 4) * out_stride + token;
             o[0] = static_cast<uint16_t>(s0);
             o[out_stride] = static_cast<uint16_t>(s1);
             o[2 * static_cast<size_t>(out_stride)] = static_cast<uint16_t>(s2);
             o[3 * static_cast<size_t>(out_stride)] = static_cast<uint16_t>(s3);
         }
-        if (head0_partial != nullptr && kv == 0) {
+        if (head0_partial != nullptr && head_kv == 0) {
             const uint32_t best = wave_max_u32(token < n ? order_key(s0) : 0u);
-            if (lane == 0) head0_partial[base / kTileTokens] = best;
+            if (lane == 0) head0_partial[id >> 3] = best;
         }
+    };
+
+    uint4 v[16];
+    uint32_t id = wave;
+    if (id >= tiles) return;
+    uint32_t next_row = row_of(id);
+    load(id, next_row, v);
+    if (id + waves < tiles) next_row = row_of(id + waves);
+    while (id < tiles) {
+        const uint32_t next = id + waves;
+        stash(v);
+        __builtin_amdgcn_wave_barrier();
+        if (next < tiles) {
+            load(next, next_row, v);
+            if (next + waves < tiles) next_row = row_of(next + waves);
+        }
+        compute(id);
+        __builtin_amdgcn_wave_barrier();
+        id = next;
     }
 }
 
@@ -137,15 +155,18 @@ int launch_score(const uint16_t* q, const uint16_t* keys, size_t stride_words,
         return reject("score: keys must be 16-byte aligned");
     if ((reinterpret_cast<uintptr_t>(q) & 3u) != 0)
         return reject("score: query must be 4-byte aligned");
-    const uint32_t tiles = ((tokens + kTileTokens - 1) / kTileTokens) * 2;
-    const uint32_t grid = std::min<uint32_t>(tiles, 2u * static_cast<uint32_t>(device_cu_count()));
+    // 8 waves per CU (two per SIMD, 128 KiB of LDS), each streaming its share
+    // of (token tile, KV head) pairs
+    const uint32_t tiles = ((tokens + kTileTokens - 1) / kTileTokens) * 8;
+    const uint32_t max_blocks = (8u / kWavesPerBlock) * static_cast<uint32_t>(device_cu_count());
+    const uint32_t grid = std::min<uint32_t>((tiles + kWavesPerBlock - 1) / kWavesPerBlock, max_blocks);
     const uint32_t* q32 = reinterpret_cast<const uint32_t*>(q);
     if (rows)
-        hipLaunchKernelGGL(score_kernel<true>, dim3(grid), dim3(256), 0, stream, q32, keys,
+        hipLaunchKernelGGL(score_kernel<true>, dim3(grid), dim3(kWavesPerBlock * 64), 0, stream, q32, keys,
                            static_cast<uint32_t>(stride_words), rows, pool_rows, tokens, scores,
                            static_cast<uint32_t>(score_stride), head0_partial);
     else
-        hipLaunchKernelGGL(score_kernel<false>, dim3(grid), dim3(256), 0, stream, q32, keys,
+        hipLaunchKernelGGL(score_kernel<false>, dim3(grid), dim3(kWavesPerBlock * 64), 0, stream, q32, keys,
                            static_cast<uint32_t>(stride_words), rows, 0u, tokens, scores,
                            static_cast<uint32_t>(score_stride), head0_partial);
     const hipError_t status = hipGetLastError();

@@ -33,7 +33,9 @@ enum {
     HS_ERR_DUPLICATE = 7,    /* duplicate/future id (gqa_pack.hpp:17,33)     */
     HS_ERR_MISSING = 8,      /* selected id without KV row (gqa_pack.hpp:44) */
     HS_ERR_HIP = 9,          /* HIP runtime call failed                      */
-    HS_ERR_UNSUPPORTED = 10  /* valid for the reference, beyond this build   */
+    HS_ERR_UNSUPPORTED = 10, /* valid for the reference, beyond this build   */
+    HS_ERR_BARRIER = 11      /* device-wide barrier timed out (never expected
+                                under the cooperative launch it relies on)   */
 };
 
 /* Device-side result of one selection; written by hs_gqa_select*. */

@@ -175,3 +175,23 @@ def test_error_codes(hs):
     assert st["code"] == 0 and st["k"] == 0
     with pytest.raises(hs.HsError):
         gpu_select(hs, tiny, 32, 64, 64, -1.0, 0.2)
+
+
+def test_scaling_edge_inputs_order(hs, port):
+    # Raw scores whose scaled F16 value depends on rounding the FP32 quotient
+    # first (the 52 mantissa-0x0a5 inputs and neighbours): with scale_raw the
+    # full order (ratio 1) must match the oracle exactly, ties included.
+    specials = [e << 10 | 0x0A5 for e in range(1, 30)]
+    vals = sorted({v + d for v in specials for d in (-1, 0, 1)} |
+                  {0x8000 | v for v in specials})
+    g = rng(52)
+    n = len(vals) * 2
+    rows = np.stack([g.permutation(np.array(vals * 2, dtype=np.uint16)) for _ in range(32)])
+    scaled = port.scale(rows)
+    rc, kk, pids, pcounts, tied = port.select(scaled, 32, n, n, 60000.0, 1.0)
+    ids, counts, _, status = hs.ops.select(to_dev(rows.reshape(-1)), 32, n, n, 60000.0, 1.0,
+                                           scale_raw=True)
+    st = hs.ops.read_status(status)
+    assert rc == 0 and st["code"] == 0 and st["k"] == kk == n
+    assert np.array_equal(from_dev(ids)[:, :kk], pids)
+    assert st["boundary_tied_heads"] == tied
