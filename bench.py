@@ -55,7 +55,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bounded CPU-baseline sample duration")
     p.add_argument("--layer-steps", type=int, default=20)
-    p.add_argument("--only", choices=["score", "select", "layer"], default=None,
+    p.add_argument("--only", choices=["score", "select", "select_id", "layer"], default=None,
                    help="profiling aid: run just one kernel family over the 30 layers "
                         "(prints its own timing line, not the benchmark JSON)")
     return p.parse_args()
@@ -120,7 +120,8 @@ def profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, 
                 ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
             else:
                 ops.select(raw, 32, N, N, ALPHA, RATIO, scale_raw=True, head0_partial=partial,
-                           ids=ids, ids_stride=kmax, counts=counts, status=status, ws=ws)
+                           ids=ids, ids_stride=kmax, counts=counts, status=status, ws=ws,
+                           id_order=args.only == "select_id")
     for layer in range(LAYERS):  # valid raw scores and partials for the select loop
         ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
     # calibration for HBM counters: one plain 64 MiB device copy (64 MiB read + written)
@@ -184,7 +185,7 @@ def main():
             ops.select(raw, 32, N, N, ALPHA, RATIO, scale_raw=True, head0_partial=partial,
                        ids=ids, ids_stride=kmax, counts=counts, status=status, ws=ws)
 
-    if args.only in ("score", "select"):
+    if args.only in ("score", "select", "select_id"):
         return profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status,
                             ws, kmax)
 

@@ -30,11 +30,11 @@ HS_ERR_DUPLICATE = 7
 HS_ERR_MISSING = 8
 HS_ERR_HIP = 9
 HS_ERR_UNSUPPORTED = 10
-HS_ERR_BARRIER = 11
 
 HS_SELECT_SCALE_RAW = 1
 HS_SELECT_FP32_COUNTS = 2
 HS_SELECT_REQUIRE_K = 4
+HS_SELECT_ID_ORDER = 8
 
 ERROR_NAMES = {
     HS_ERR_ARGUMENT: "argument",
@@ -47,7 +47,6 @@ ERROR_NAMES = {
     HS_ERR_MISSING: "missing KV row",
     HS_ERR_HIP: "HIP runtime",
     HS_ERR_UNSUPPORTED: "unsupported",
-    HS_ERR_BARRIER: "device barrier timeout",
 }
 
 

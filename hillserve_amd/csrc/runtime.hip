@@ -172,7 +172,8 @@ int hs_decode_layer(const uint16_t* q16_dev, const float* q32_dev, const uint8_t
                               row_of_id_dev, pool_rows, n, scores_dev, n, partial, s);
     if (rc != HS_OK) return rc;
     rc = hs::launch_select(scores_dev, 32, n, n, alpha, ratio,
-                           flags | HS_SELECT_SCALE_RAW | HS_SELECT_REQUIRE_K, partial, ids_dev,
+                           flags | HS_SELECT_SCALE_RAW | HS_SELECT_REQUIRE_K | HS_SELECT_ID_ORDER,
+                           partial, ids_dev,
                            ids_stride, counts_dev, member, status_dev, ws + p.off_select, s);
     if (rc != HS_OK) return rc;
     return hs::launch_attention(q32_dev, pool_dev, 4096, row_of_id_dev, pool_rows, member, n,

@@ -11,25 +11,34 @@
 //   ids_h = first k of the order (order key desc, id asc) (policy/half_order.hpp)
 // Errors follow the reference's precedence: nonfinite head 0, threshold,
 // then per head in order nonfinite / count overflow, then mean overflow.
+// The F16-rounded counts are integers <= 65504 and heads <= 128, so every
+// partial sum is an integer below 2^24: the FP32 total is exact in any
+// summation order.
 //
-// One launch, one 1024-thread workgroup per head (heads <= compute units, so
-// every group is resident together; the host checks it):
-//  1. every thread loads a contiguous run of its head's scores (32 or 64) into
-//     registers once, with 128-bit loads; the head-0 maximum comes from the
-//     scorer's per-tile maxima (or from head0_max_kernel);
-//  2. the group counts its head against the threshold and builds a 256-bin
-//     histogram of the order key's high byte (one private copy per wave);
-//  3. the groups meet at one device-wide barrier (epoch-tagged flags in the
-//     workspace; the spin is bounded and a timeout reports HS_ERR_BARRIER
-//     instead of waiting forever) and each computes k from all heads' counts
-//     with the reference's F16 rounding;
-//  4. radix select of the k-th key (high byte from the histogram, low byte
-//     from one pass over the registers), stable compaction in id order, and a
-//     two-pass LSD radix sort (8-bit digits, wave-ballot ranking) of the k
-//     composites ((0xffff-key)<<16 | id) in LDS: ascending composite order is
-//     exactly (key desc, id asc);
-//  5. ids, counts and membership bitmaps are written; group 0 waits for the
-//     others, publishes hs_status_t and advances the epoch.
+// Work split: each head is cut into S <= 16 slices of 4096 consecutive ids;
+// every (head, slice) pair is one 512-thread workgroup whose threads own 8
+// consecutive ids each.  The phases that need a head-wide or device-wide view
+// are separate launches on the caller's stream: a kernel boundary is the
+// cheapest device-wide barrier on this part (one cache flush per launch,
+// where in-kernel barriers across the XCDs' separate L2 caches pay an L2
+// write-back or invalidate in every workgroup), and it needs no co-resident
+// groups.
+//  1. count:  scale, count the slice against the threshold (head-0 maximum
+//             from the scorer's per-tile maxima), flag nonfinite scores,
+//             256-bin histogram of the order key's high byte;
+//  2. plan:   every group derives k from all counts (group 0 publishes k, the
+//             counts and the status), sums its head's slice histograms, finds
+//             the high byte of the k-th key and histograms the low byte of
+//             that bucket in its slice;
+//  3. select: K* (the k-th key), the ties taken (lowest ids first) and each
+//             slice's share follow from the slice histograms; the group
+//             writes its membership bits and either its ids in ascending id
+//             order (HS_SELECT_ID_ORDER) or, for rank order, its selection
+//             stable-sorted by key; boundary ties are counted into the status
+//             with device-scope atomics;
+//  4. rank:   (rank order only) each id lands at its rank in its slice plus
+//             the number of keys of every other slice of the head ahead of
+//             it (binary search; ties order by slice, i.e. by id).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -41,48 +50,74 @@
 namespace hs {
 namespace {
 
-constexpr uint32_t kThreads = 1024;
+constexpr uint32_t kThreads = 512;
 constexpr uint32_t kWaves = kThreads / 64;
-constexpr uint32_t kLdsSortCap = 16384;  // composites sorted in LDS (2 x 64 KiB)
-constexpr uint32_t kMaxN = 65536;        // ids fit the composite's low 16 bits
+constexpr uint32_t kRun = 8;                     // ids per thread
+constexpr uint32_t kSlice = kThreads * kRun;     // ids per group
+constexpr uint32_t kMaxN = 65536;
 constexpr uint32_t kMaxHeads = 128;
-constexpr uint32_t kSpinLimit = 1u << 22;
+constexpr uint32_t kMaxSlices = kMaxN / kSlice;  // 16
+constexpr uint32_t kRankCap = 16384;             // a head's sorted keys staged in LDS
 
-// Cross-group state, at offset 0 of the workspace.  No reset is needed: each
-// call tags its flags with epoch+1, where every group reads `epoch` before it
-// arrives and group 0 advances it after every group is done.
-struct SelectSync {
-    uint32_t epoch;
-    uint32_t pad[63];
-    uint32_t arrive[kMaxHeads];
-    uint32_t done[kMaxHeads];
-    uint32_t count[kMaxHeads];
-    uint32_t bad[kMaxHeads];
-    uint32_t tied[kMaxHeads];
+// Published by group 0 of the plan launch.
+struct SelectPlanDev {
+    int32_t code;
+    uint32_t k;
 };
 
 struct SelectPlan {
-    uint32_t partials = 0, kmax = 0, sort_cap = 0;
-    size_t off_sync = 0, off_partial = 0, off_sort = 0, total = 0;
+    uint32_t S = 0, groups = 0, partials = 0, cap = 0;
+    size_t off_plan = 0, off_partial = 0, off_count = 0, off_bad = 0, off_hi = 0, off_lo = 0,
+           off_sort = 0, off_m = 0, off_tie = 0, total = 0;
 };
 
 SelectPlan plan_select(uint32_t heads, uint32_t n, uint32_t kmax) {
     SelectPlan p;
+    p.S = (n + kSlice - 1) / kSlice;
+    p.groups = heads * p.S;
     p.partials = (n + 63) / 64;
-    p.kmax = kmax;
-    p.sort_cap = kmax > kLdsSortCap ? kmax : 0;
+    p.cap = std::max<uint32_t>(1u, std::min(kSlice, kmax));
     size_t at = 0;
     auto take = [&](size_t bytes) {
         const size_t here = at;
         at += align256(bytes);
         return here;
     };
-    p.off_sync = take(sizeof(SelectSync));
+    p.off_plan = take(sizeof(SelectPlanDev));
     p.off_partial = take(sizeof(uint32_t) * p.partials);
-    p.off_sort = take(sizeof(uint32_t) * size_t(heads) * 2 * p.sort_cap);
+    p.off_count = take(sizeof(uint32_t) * p.groups);
+    p.off_bad = take(sizeof(uint32_t) * p.groups);
+    p.off_hi = take(sizeof(uint32_t) * 256 * p.groups);
+    p.off_lo = take(sizeof(uint32_t) * 256 * p.groups);
+    p.off_sort = take(sizeof(uint32_t) * size_t(p.groups) * p.cap);
+    p.off_m = take(sizeof(uint32_t) * p.groups);
+    p.off_tie = take(sizeof(unsigned long long) * heads);
     p.total = at;
     return p;
 }
+
+struct SelectArgs {
+    const uint16_t* scores;
+    uint32_t heads, stride, n, S;
+    float alpha, ratio;
+    uint32_t flags;
+    const uint32_t* partial;
+    uint32_t partials;
+    SelectPlanDev* plan;
+    uint32_t* g_count;  // [groups] slice counts >= thr
+    uint32_t* g_bad;    // [groups] slice has a nonfinite score
+    uint32_t* g_hi;     // [groups][256] high-byte histograms
+    uint32_t* g_lo;     // [groups][256] low-byte histograms of the k-th key's bucket
+    uint32_t* g_sort;   // [groups][cap] rank-sorted composites of each slice
+    uint32_t* g_m;      // [groups] selected per slice
+    unsigned long long* g_tie;  // [heads] bits around a signed-zero cut
+    uint32_t cap;
+    uint32_t* ids;
+    uint32_t ids_stride;
+    uint32_t* counts_out;
+    uint32_t* member;
+    hs_status_t* status;
+};
 
 // Per 64-element tile of head 0: maximum order key of the input scores
 // (0 = nothing).  Scaling is monotone, so raw keys serve the scaled maximum.
@@ -103,7 +138,7 @@ __device__ __forceinline__ float threshold_from_key(uint32_t key, bool scale, fl
     return h2f(f2h(m - alpha));
 }
 
-// Block-wide reductions / scan over the 1024 threads through LDS.
+// Block-wide reductions / scan through LDS.
 __device__ uint32_t block_max(uint32_t v, uint32_t* tmp) {
     v = wave_max_u32(v);
     if ((threadIdx.x & 63u) == 0) tmp[threadIdx.x >> 6] = v;
@@ -187,371 +222,584 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t digit, bool valid) {
     return m;
 }
 
-__device__ __forceinline__ bool wait_flag(const uint32_t* flag, uint32_t target) {
-    for (uint32_t i = 0; i < kSpinLimit; ++i) {
-        if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == target)
-            return true;
-        __builtin_amdgcn_s_sleep(2);
-    }
-    return false;
-}
-
-__device__ __forceinline__ uint32_t half_at(const uint32_t* packed, uint32_t j) {
+__device__ __forceinline__ uint32_t half_at(const uint32_t (&packed)[kRun / 2], uint32_t j) {
     return (packed[j >> 1] >> ((j & 1u) * 16u)) & 0xffffu;
 }
 
-template <uint32_t kRun, bool kGlobalSort>
-__global__ void __launch_bounds__(kThreads)
-select_kernel(const uint16_t* __restrict__ scores, uint32_t heads, uint32_t stride, uint32_t n,
-              float alpha, float ratio, uint32_t flags, const uint32_t* __restrict__ partial,
-              uint32_t partials, SelectSync* __restrict__ sync, uint32_t* __restrict__ sort_buf,
-              uint32_t sort_cap, uint32_t* __restrict__ ids, uint32_t ids_stride,
-              uint32_t* __restrict__ counts_out, uint32_t* __restrict__ member,
-              hs_status_t* __restrict__ status) {
-    constexpr uint32_t kLds = kGlobalSort ? 1 : kLdsSortCap;
-    __shared__ uint32_t sort_a[kLds];
-    __shared__ uint32_t sort_b[kLds];
-    __shared__ uint32_t whist[kWaves][256];
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t tmp[kWaves];
-    __shared__ uint32_t sh[16];
-    __shared__ uint32_t head_count[kMaxHeads];
-    __shared__ uint32_t head_bad[kMaxHeads];
-    enum { kEpoch, kCode, kK, kBucket, kAbove, kBucket2, kAbove2, kTieLo, kTieHi, kFail };
-
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, head = blockIdx.x;
-    const bool scale = (flags & HS_SELECT_SCALE_RAW) != 0;
-    const bool fp32_counts = (flags & HS_SELECT_FP32_COUNTS) != 0;
-    const uint16_t* row = scores + static_cast<size_t>(head) * stride;
-    uint32_t* A = kGlobalSort ? sort_buf + static_cast<size_t>(head) * 2 * sort_cap : sort_a;
-    uint32_t* B = kGlobalSort ? A + sort_cap : sort_b;
-    const uint32_t words = (n + 31) / 32;
-    const uint32_t cap = kGlobalSort ? sort_cap : kLdsSortCap;
-
-    // ---- 0. epoch, cleared histograms, head-0 maximum ----------------------
-    if (tid < 16) sh[tid] = 0;
-    for (uint32_t i = tid; i < kWaves * 256; i += kThreads) (&whist[0][0])[i] = 0;
-    __syncthreads();
-    if (tid == 0)
-        sh[kEpoch] = __hip_atomic_load(&sync->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t best = 0;
-    for (uint32_t i = tid; i < partials; i += kThreads) best = partial[i] > best ? partial[i] : best;
-
-    // ---- 1. this thread's run of scores into registers ----------------------
-    const uint32_t begin = tid * kRun;
-    uint32_t packed[kRun / 2];
-    const bool vec = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
-#pragma unroll
-    for (uint32_t j = 0; j < kRun / 8; ++j) {
-        const uint32_t i0 = begin + 8 * j;
-        uint32_t w[4];
-        if (vec && i0 + 8 <= n) {
-            const uint4 v = *reinterpret_cast<const uint4*>(row + i0);
-            w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-        } else {
-#pragma unroll
-            for (uint32_t c = 0; c < 4; ++c) {
-                const uint32_t lo = i0 + 2 * c < n ? row[i0 + 2 * c] : 0u;
-                const uint32_t hi = i0 + 2 * c + 1 < n ? row[i0 + 2 * c + 1] : 0u;
-                w[c] = lo | (hi << 16);
-            }
-        }
+// This thread's 8 ids of head h into registers (scaled when asked); ids past
+// n read as 0 and are masked by the callers.
+__device__ __forceinline__ void load_run(const SelectArgs& a, uint32_t h, uint32_t begin,
+                                         uint32_t (&packed)[kRun / 2]) {
+    const uint16_t* row = a.scores + static_cast<size_t>(h) * a.stride;
+    uint32_t w[4];
+    if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0 && begin + 8 <= a.n) {
+        const uint4 v = *reinterpret_cast<const uint4*>(row + begin);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else {
 #pragma unroll
         for (uint32_t c = 0; c < 4; ++c) {
-            uint32_t v = w[c];
-            if (scale) v = scale_raw(v & 0xffffu) | (scale_raw(v >> 16) << 16);
-            packed[4 * j + c] = v;
+            const uint32_t lo = begin + 2 * c < a.n ? row[begin + 2 * c] : 0u;
+            const uint32_t hi = begin + 2 * c + 1 < a.n ? row[begin + 2 * c + 1] : 0u;
+            w[c] = lo | (hi << 16);
         }
     }
-    best = block_max(best, tmp);
-    const float thr = threshold_from_key(best, scale, alpha);
-    const uint32_t epoch = sh[kEpoch];
+    const bool scale = (a.flags & HS_SELECT_SCALE_RAW) != 0;
+#pragma unroll
+    for (uint32_t c = 0; c < 4; ++c)
+        packed[c] = scale ? (scale_raw(w[c] & 0xffffu) | (scale_raw(w[c] >> 16) << 16)) : w[c];
+}
 
-    // ---- 2. count, nonfinite flag, high-byte histogram of this head ----------
+// Order-key histograms: 4 copies per wave, 257 words apart, so lanes that hit
+// the same bucket spread over 4 banks and 4 addresses.
+constexpr uint32_t kCopies = 4, kCopyStride = 257;
+constexpr uint32_t kHistWords = kWaves * kCopies * kCopyStride;
+__device__ __forceinline__ void hist_clear(uint32_t* whist) {
+    for (uint32_t i = threadIdx.x; i < kHistWords; i += kThreads) whist[i] = 0;
+}
+__device__ __forceinline__ void hist_add(uint32_t* whist, uint32_t bucket) {
+    const uint32_t copy = (threadIdx.x >> 6) * kCopies + (threadIdx.x & (kCopies - 1));
+    atomicAdd(&whist[copy * kCopyStride + bucket], 1u);
+}
+__device__ __forceinline__ uint32_t hist_total(const uint32_t* whist, uint32_t bucket) {
+    uint32_t c = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kWaves * kCopies; ++i) c += whist[i * kCopyStride + bucket];
+    return c;
+}
+
+// Maximum of the head-0 per-tile maxima (n <= 65536: at most 1024 of them).
+__device__ __forceinline__ uint32_t partial_max(const SelectArgs& a) {
+    uint32_t v[2];
+#pragma unroll
+    for (uint32_t u = 0; u < 2; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
+        v[u] = i < a.partials ? a.partial[i] : 0u;
+    }
+    return v[0] > v[1] ? v[0] : v[1];
+}
+
+// ---- 1. count ---------------------------------------------------------------
+__global__ void __launch_bounds__(kThreads) count_kernel(SelectArgs a) {
+    __shared__ uint32_t whist[kHistWords];
+    __shared__ uint32_t tmp[kWaves];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t g = blockIdx.x, h = g / a.S, s = g - h * a.S;
+    const uint32_t begin = s * kSlice + tid * kRun;
+    uint32_t best = partial_max(a);
+    uint32_t packed[kRun / 2];
+    load_run(a, h, begin, packed);
+    hist_clear(whist);
+    best = block_max(best, tmp);  // its barrier also orders the histogram clear
+    const float thr = threshold_from_key(best, (a.flags & HS_SELECT_SCALE_RAW) != 0, a.alpha);
     uint32_t count = 0, bad = 0;
 #pragma unroll
     for (uint32_t j = 0; j < kRun; ++j) {
-        if (begin + j < n) {
+        if (begin + j < a.n) {
             const uint32_t b = half_at(packed, j);
-            if (!finite_half(b)) bad = 1;
-            else count += h2f(b) >= thr ? 1u : 0u;
+            if (!finite_half(b)) {
+                bad = 1;
+            } else {
+                count += h2f(b) >= thr ? 1u : 0u;
+                hist_add(whist, order_key(b) >> 8);
+            }
         }
-        // one LDS add per distinct bucket among the wave's lanes
-        const bool valid = begin + j < n && finite_half(half_at(packed, j));
-        const uint32_t bucket = order_key(half_at(packed, j)) >> 8;
-        const uint64_t peers = match_digit(bucket, valid);
-        if (valid && lanes_below(peers) == 0)
-            atomicAdd(&whist[wave][bucket], static_cast<uint32_t>(__popcll(peers)));
     }
     count = block_sum(count, tmp);
     bad = block_max(bad, tmp);
-    if (tid < 256) {
-        uint32_t c = 0;
-#pragma unroll
-        for (uint32_t w = 0; w < kWaves; ++w) c += whist[w][tid];
-        hist[tid] = c;
+    if (tid < 256) a.g_hi[static_cast<size_t>(g) * 256 + tid] = hist_total(whist, tid);
+    if (tid == 0) {
+        a.g_count[g] = count;
+        a.g_bad[g] = bad;
     }
+}
 
-    // ---- 3. device-wide barrier: every head's count is known ----------------
-    if (tid == 0) {
-        sync->count[head] = count;
-        sync->bad[head] = bad;
-        __threadfence();
-        __hip_atomic_store(&sync->arrive[head], epoch + 1, __ATOMIC_RELEASE,
-                           __HIP_MEMORY_SCOPE_AGENT);
+// ---- 2. plan ----------------------------------------------------------------
+__global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
+    __shared__ uint32_t whist[kHistWords];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t tmp[kWaves];
+    __shared__ uint32_t head_count[kMaxHeads];
+    __shared__ uint32_t head_bad[kMaxHeads];
+    __shared__ uint32_t sh[4];
+    enum { kCode, kK, kBucket, kAbove };
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t g = blockIdx.x, S = a.S, h = g / S, s = g - h * S, n = a.n;
+    const uint32_t groups = a.heads * S;
+    const bool scale = (a.flags & HS_SELECT_SCALE_RAW) != 0;
+    const bool fp32_counts = (a.flags & HS_SELECT_FP32_COUNTS) != 0;
+
+    // every global read of this kernel is issued up front
+    uint32_t best = partial_max(a);
+    uint32_t cnt[4], bad[4], hi_part[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {  // heads * S <= 2048 slice counts
+        const uint32_t i = tid + u * kThreads;
+        cnt[u] = i < groups ? a.g_count[i] : 0u;
+        bad[u] = i < groups ? a.g_bad[i] : 0u;
     }
-    if (tid < heads) {
-        // every head's (count, nonfinite) in parallel, one round trip
-        if (!wait_flag(&sync->arrive[tid], epoch + 1)) sh[kFail] = 1;
-        head_count[tid] =
-            __hip_atomic_load(&sync->count[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        head_bad[tid] = __hip_atomic_load(&sync->bad[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) {  // this head's S * 256 <= 4096 bins
+        const uint32_t i = tid + u * kThreads;
+        hi_part[u] = i < S * 256 ? a.g_hi[static_cast<size_t>(h * S) * 256 + i] : 0u;
     }
+    uint32_t packed[kRun / 2];
+    const uint32_t begin = s * kSlice + tid * kRun;
+    load_run(a, h, begin, packed);
+
+    hist_clear(whist);
+    if (tid < 256) hist[tid] = 0;
+    if (tid < a.heads) head_count[tid] = head_bad[tid] = 0;
     __syncthreads();
-    if (tid == 0) {
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {
+        const uint32_t i = tid + u * kThreads;
+        if (i < groups) {
+            atomicAdd(&head_count[i / S], cnt[u]);
+            atomicOr(&head_bad[i / S], bad[u]);
+        }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u)
+        if (hi_part[u]) atomicAdd(&hist[(tid + u * kThreads) & 255u], hi_part[u]);
+    best = block_max(best, tmp);  // its barrier also publishes the sums above
+    const float thr = threshold_from_key(best, scale, a.alpha);
+
+    // k from every head's count (wave 0)
+    if (wave == 0) {
         int code = HS_OK;
         uint32_t k = 0;
-        if (sh[kFail]) {
-            code = HS_ERR_BARRIER;
-        } else if (head_bad[0]) {
+        if (head_bad[0]) {
             code = HS_ERR_NONFINITE;
         } else if (!isfinite(thr)) {
             code = HS_ERR_THRESHOLD;
         } else {
             float total = 0.0f;
-            for (uint32_t h = 0; h < heads; ++h) {
-                const uint32_t c = head_count[h];
-                if (head_bad[h]) {
-                    code = HS_ERR_NONFINITE;
-                    break;
+            for (uint32_t first = 0; first < a.heads && code == HS_OK; first += 64) {
+                const uint32_t hh = first + lane;
+                const bool valid = hh < a.heads;
+                const uint32_t c = valid ? head_count[hh] : 0u;
+                const bool hb = valid && head_bad[hh] != 0;
+                const float rounded =
+                    fp32_counts ? static_cast<float>(c) : h2f(f2h(static_cast<float>(c)));
+                const bool err = valid && (hb || !isfinite(rounded));
+                const uint64_t errs = __ballot(err);
+                if (errs) {
+                    const uint32_t at =
+                        static_cast<uint32_t>(__ffsll(static_cast<long long>(errs))) - 1;
+                    code = __shfl(hb ? 1 : 0, at, 64) ? HS_ERR_NONFINITE : HS_ERR_COUNT;
                 }
-                const float rounded = fp32_counts ? static_cast<float>(c)
-                                                  : h2f(f2h(static_cast<float>(c)));
-                if (!isfinite(rounded)) {
-                    code = HS_ERR_COUNT;
-                    break;
-                }
-                total += rounded;
+                total += wave_sum_f32(valid && !err ? rounded : 0.0f);
             }
             if (code == HS_OK) {
-                const float q = __fdiv_rn(total, static_cast<float>(heads));
+                const float q = __fdiv_rn(total, static_cast<float>(a.heads));
                 const float mean = fp32_counts ? q : h2f(f2h(q));
                 if (!isfinite(mean)) {
                     code = HS_ERR_MEAN;
                 } else {
                     uint64_t kk = static_cast<uint64_t>(mean);
                     const uint64_t cap_k = static_cast<uint64_t>(
-                        floor(static_cast<double>(n) * static_cast<double>(ratio)));
+                        floor(static_cast<double>(n) * static_cast<double>(a.ratio)));
                     kk = kk < cap_k ? kk : cap_k;
                     kk = kk < n ? kk : n;
                     k = static_cast<uint32_t>(kk);
-                    if (k == 0 && (flags & HS_SELECT_REQUIRE_K)) code = HS_ERR_ZERO_SELECTION;
-                    if (k > cap) code = HS_ERR_ARGUMENT;  // host sizing guarantees k <= cap
+                    if (k == 0 && (a.flags & HS_SELECT_REQUIRE_K)) code = HS_ERR_ZERO_SELECTION;
                 }
             }
         }
-        if (counts_out) counts_out[head] = count;
-        sh[kCode] = static_cast<uint32_t>(code);
-        sh[kK] = k;
+        if (lane == 0) {
+            sh[kCode] = static_cast<uint32_t>(code);
+            sh[kK] = k;
+            if (g == 0) {
+                a.plan->code = code;
+                a.plan->k = code == HS_OK ? k : 0u;
+                a.status->code = code;
+                a.status->k = code == HS_OK ? k : 0u;
+                a.status->boundary_tied_heads = 0;
+                a.status->head0_max_key = best;
+            }
+        }
+        // high byte of this head's k-th key
+        if (code == HS_OK && k > 0) find_bucket(hist, k, &sh[kBucket], &sh[kAbove]);
+    }
+    if (g == 0 && tid < a.heads) {
+        if (a.counts_out) a.counts_out[tid] = head_count[tid];
+        a.g_tie[tid] = 0ull;
     }
     __syncthreads();
     const int code = static_cast<int>(sh[kCode]);
     const uint32_t k = sh[kK];
-    if (code != HS_OK) {
-        if (code == HS_ERR_BARRIER) {
-            if (tid == 0) atomicExch(reinterpret_cast<int*>(&status->code), HS_ERR_BARRIER);
-        } else if (head == 0 && tid == 0) {
-            status->code = code;
-            status->k = 0;
-            status->boundary_tied_heads = 0;
-            status->head0_max_key = best;
-            __threadfence();
-            __hip_atomic_store(&sync->epoch, epoch + 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
-        return;
-    }
+    if (code != HS_OK || k == 0) return;
 
-    uint32_t tied = 0;
-    uint32_t bitword[kRun / 32];
+    // low-byte histogram of that bucket in this slice
+    const uint32_t hi = sh[kBucket] & 255u;
 #pragma unroll
-    for (uint32_t w = 0; w < kRun / 32; ++w) bitword[w] = 0;
-    if (k > 0) {
-        // ---- 4a. radix select of the k-th key ---------------------------------
-        find_bucket(hist, k, &sh[kBucket], &sh[kAbove]);
-        __syncthreads();
-        const uint32_t hi = sh[kBucket] & 255u, above_hi = sh[kAbove];
-        if (tid < 256) hist[tid] = 0;
-        __syncthreads();
-#pragma unroll
-        for (uint32_t j = 0; j < kRun; ++j) {
-            if (begin + j < n) {
-                const uint32_t key = order_key(half_at(packed, j));
-                if ((key >> 8) == hi) atomicAdd(&hist[key & 255u], 1u);
-            }
+    for (uint32_t j = 0; j < kRun; ++j) {
+        if (begin + j < n) {
+            const uint32_t key = order_key(half_at(packed, j));
+            if ((key >> 8) == hi) hist_add(whist, key & 255u);
         }
-        __syncthreads();
-        find_bucket(hist, k - above_hi, &sh[kBucket2], &sh[kAbove2]);
-        __syncthreads();
-        const uint32_t lo = sh[kBucket2] & 255u;
-        const uint32_t kstar = (hi << 8) | lo;
-        const uint32_t c_above = above_hi + sh[kAbove2];
-        const uint32_t c_equal = hist[lo];
-        const uint32_t t_need = k - c_above;  // ties taken, by ascending id
-
-        // ---- 4b. stable compaction in id order --------------------------------
-        uint32_t my_above = 0, my_ties = 0;
-#pragma unroll
-        for (uint32_t j = 0; j < kRun; ++j) {
-            if (begin + j < n) {
-                const uint32_t key = order_key(half_at(packed, j));
-                my_above += key > kstar;
-                my_ties += key == kstar;
-            }
-        }
-        const uint32_t tie_before = block_exclusive_scan(my_ties, tmp);
-        const uint32_t tie_sel =
-            tie_before >= t_need ? 0u : std::min(my_ties, t_need - tie_before);
-        uint32_t pos = block_exclusive_scan(my_above + tie_sel, tmp);
-        uint32_t tie_rank = tie_before;
-#pragma unroll
-        for (uint32_t j = 0; j < kRun; ++j) {
-            const uint32_t i = begin + j;
-            if (i < n) {
-                const uint32_t bits = half_at(packed, j);
-                const uint32_t key = order_key(bits);
-                bool take = key > kstar;
-                if (key == kstar) {
-                    take = tie_rank < t_need;
-                    if (tie_rank == t_need - 1) sh[kTieLo] = bits;
-                    if (tie_rank == t_need) sh[kTieHi] = bits;
-                    ++tie_rank;
-                }
-                if (take && pos < k) {  // pos < k by construction
-                    A[pos++] = ((0xffffu - key) << 16) | i;
-                    bitword[j >> 5] |= 1u << (j & 31u);
-                }
-            }
-        }
-        __syncthreads();
-
-        // ---- 4c. two-pass LSD radix sort of the k composites ---------------------
-        const uint32_t per_wave = ((k + kWaves - 1) / kWaves + 63) / 64 * 64;
-        const uint32_t first = wave * per_wave;
-#pragma unroll 1
-        for (uint32_t pass = 0; pass < 2; ++pass) {
-            const uint32_t* src = pass ? B : A;
-            uint32_t* dst = pass ? A : B;
-            const uint32_t shift = 16 + 8 * pass;
-            for (uint32_t i = tid; i < kWaves * 256; i += kThreads) (&whist[0][0])[i] = 0;
-            __syncthreads();
-            for (uint32_t c = 0; c < per_wave; c += 64) {
-                const uint32_t e = first + c + lane;
-                const bool valid = e < k;
-                const uint32_t x = valid ? src[e] : 0u;
-                const uint32_t digit = (x >> shift) & 255u;
-                const uint64_t peers = match_digit(digit, valid);
-                if (valid && lanes_below(peers) == 0)
-                    whist[wave][digit] += static_cast<uint32_t>(__popcll(peers));
-                __builtin_amdgcn_wave_barrier();
-            }
-            __syncthreads();
-            uint32_t total = 0;
-            if (tid < 256) {
-#pragma unroll
-                for (uint32_t w = 0; w < kWaves; ++w) {
-                    const uint32_t c = whist[w][tid];
-                    whist[w][tid] = total;
-                    total += c;
-                }
-            }
-            // exclusive scan of the 256 digit totals (waves 0..3)
-            uint32_t x = total;
-#pragma unroll
-            for (uint32_t off = 1; off < 64; off <<= 1) {
-                const uint32_t y = __shfl_up(x, off, 64);
-                if (lane >= off) x += y;
-            }
-            if (tid < 256 && lane == 63) tmp[wave] = x;
-            __syncthreads();
-            if (tid < 256) {
-                uint32_t base = x - total;
-                for (uint32_t w = 0; w < wave; ++w) base += tmp[w];
-#pragma unroll
-                for (uint32_t w = 0; w < kWaves; ++w) whist[w][tid] += base;
-            }
-            __syncthreads();
-            for (uint32_t c = 0; c < per_wave; c += 64) {
-                const uint32_t e = first + c + lane;
-                const bool valid = e < k;
-                const uint32_t xv = valid ? src[e] : 0u;
-                const uint32_t digit = (xv >> shift) & 255u;
-                const uint64_t peers = match_digit(digit, valid);
-                const uint32_t rank = lanes_below(peers);
-                if (valid) {
-                    const uint32_t at = whist[wave][digit] + rank;
-                    if (at < k) dst[at] = xv;
-                }
-                __builtin_amdgcn_wave_barrier();
-                if (valid && rank == 0)
-                    whist[wave][digit] += static_cast<uint32_t>(__popcll(peers));
-                __builtin_amdgcn_wave_barrier();
-            }
-            __syncthreads();
-        }
-        uint32_t* out = ids + static_cast<size_t>(head) * ids_stride;
-        for (uint32_t j = tid; j < k; j += kThreads) out[j] = A[j] & 0xffffu;
-        // boundary tie (gqa_policy.cpp:65): the (k+1)-th element exists with
-        // equal bits.  Equal keys imply equal bits except for -0 / +0.
-        if (k < n && c_above + c_equal > k)
-            tied = kstar != 0x8000u ? 1u : (sh[kTieLo] == sh[kTieHi] ? 1u : 0u);
-    }
-    if (member) {
-        uint32_t* dst = member + static_cast<size_t>(head) * words;
-#pragma unroll
-        for (uint32_t w = 0; w < kRun / 32; ++w) {
-            const uint32_t at = tid * (kRun / 32) + w;
-            if (at < words) dst[at] = bitword[w];
-        }
-    }
-
-    // ---- 5. group 0 publishes the status after every head is done ---------------
-    if (tid == 0) {
-        sync->tied[head] = tied;
-        __threadfence();
-        __hip_atomic_store(&sync->done[head], epoch + 1, __ATOMIC_RELEASE,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (head != 0) return;
-    if (tid < heads) {
-        if (!wait_flag(&sync->done[tid], epoch + 1)) sh[kFail] = 1;
-        head_count[tid] = __hip_atomic_load(&sync->tied[tid], __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (tid == 0) {
-        uint32_t total_ties = 0;
-        for (uint32_t h = 0; h < heads; ++h) total_ties += head_count[h];
-        status->code = sh[kFail] ? HS_ERR_BARRIER : HS_OK;
-        status->k = k;
-        status->boundary_tied_heads = total_ties;
-        status->head0_max_key = best;
-        __threadfence();
-        __hip_atomic_store(&sync->epoch, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < 256) a.g_lo[static_cast<size_t>(g) * 256 + tid] = hist_total(whist, tid);
+}
+
+// Stable LSD radix sort (two 8-bit passes over bits 16..31) of m composites
+// ((0xffff - key) << 16 | id in slice) from A through B back into A:
+// ascending composite order is (key desc, id asc).  whist: kWaves x 256.
+__device__ void sort_composites(uint32_t* A, uint32_t* B, uint32_t m, uint32_t (*whist)[256],
+                                uint32_t* tmp) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t per_wave = ((m + kWaves - 1) / kWaves + 63) / 64 * 64;
+    const uint32_t first = wave * per_wave;
+#pragma unroll 1
+    for (uint32_t pass = 0; pass < 2; ++pass) {
+        const uint32_t* src = pass ? B : A;
+        uint32_t* dst = pass ? A : B;
+        const uint32_t shift = 16 + 8 * pass;
+        for (uint32_t i = tid; i < kWaves * 256; i += kThreads) (&whist[0][0])[i] = 0;
+        __syncthreads();
+        for (uint32_t c = 0; c < per_wave; c += 64) {
+            const uint32_t e = first + c + lane;
+            const bool valid = e < m;
+            const uint32_t x = valid ? src[e] : 0u;
+            const uint32_t digit = (x >> shift) & 255u;
+            const uint64_t peers = match_digit(digit, valid);
+            if (valid && lanes_below(peers) == 0)
+                whist[wave][digit] += static_cast<uint32_t>(__popcll(peers));
+            __builtin_amdgcn_wave_barrier();
+        }
+        __syncthreads();
+        // exclusive offsets in (digit, wave) order
+        uint32_t total = 0;
+        if (tid < 256) {
+#pragma unroll
+            for (uint32_t w = 0; w < kWaves; ++w) {
+                const uint32_t c = whist[w][tid];
+                whist[w][tid] = total;
+                total += c;
+            }
+        }
+        uint32_t x = total;
+#pragma unroll
+        for (uint32_t off = 1; off < 64; off <<= 1) {
+            const uint32_t y = __shfl_up(x, off, 64);
+            if (lane >= off) x += y;
+        }
+        if (tid < 256 && lane == 63) tmp[wave] = x;
+        __syncthreads();
+        if (tid < 256) {
+            uint32_t base = x - total;
+            for (uint32_t w = 0; w < wave; ++w) base += tmp[w];
+#pragma unroll
+            for (uint32_t w = 0; w < kWaves; ++w) whist[w][tid] += base;
+        }
+        __syncthreads();
+        for (uint32_t c = 0; c < per_wave; c += 64) {
+            const uint32_t e = first + c + lane;
+            const bool valid = e < m;
+            const uint32_t xv = valid ? src[e] : 0u;
+            const uint32_t digit = (xv >> shift) & 255u;
+            const uint64_t peers = match_digit(digit, valid);
+            const uint32_t rank = lanes_below(peers);
+            if (valid) {
+                const uint32_t at = whist[wave][digit] + rank;
+                if (at < m) dst[at] = xv;
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (valid && rank == 0) whist[wave][digit] += static_cast<uint32_t>(__popcll(peers));
+            __builtin_amdgcn_wave_barrier();
+        }
+        __syncthreads();
     }
 }
 
-template <uint32_t kRun, bool kGlobal>
-hipError_t launch_variant(dim3 grid, void** args, hipStream_t stream) {
-    return hipLaunchKernel(reinterpret_cast<const void*>(&select_kernel<kRun, kGlobal>), grid,
-                           dim3(kThreads), args, 0, stream);
+// Raw bits of the ties ranked t_need-1 (bit 62 + bits 0..15) and t_need
+// (bit 63 + bits 16..31) at a signed-zero cut; whichever record arrives second
+// compares them and counts the head as tied when the bits match.
+__device__ void note_zero_tie(const SelectArgs& a, uint32_t h, uint32_t bits, bool upper) {
+    const unsigned long long mine =
+        upper ? ((1ull << 63) | (static_cast<unsigned long long>(bits) << 16))
+              : ((1ull << 62) | bits);
+    const unsigned long long old = atomicOr(&a.g_tie[h], mine);
+    const unsigned long long other = upper ? (1ull << 62) : (1ull << 63);
+    if (old & other) {
+        const unsigned long long both = old | mine;
+        if (((both >> 16) & 0xffffull) == (both & 0xffffull))
+            atomicAdd(&a.status->boundary_tied_heads, 1u);
+    }
+}
+
+// ---- 3. select --------------------------------------------------------------
+template <bool kRankOrder>
+__global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
+    __shared__ uint32_t whist[kRankOrder ? kWaves : 1][256];
+    __shared__ uint32_t hist[2][256];
+    __shared__ uint32_t slice_hist[2][kMaxSlices][256];
+    __shared__ uint32_t sort_lds[kRankOrder ? 2 * kSlice : 1];
+    __shared__ uint32_t tmp[kWaves];
+    __shared__ uint32_t sh[8];
+    __shared__ uint32_t s_above[kMaxSlices], s_ties[kMaxSlices];
+    enum { kBucket, kAbove, kBucket2, kAbove2, kTieBase, kTaken, kSelBase, kSel };
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t g = blockIdx.x, S = a.S, h = g / S, s = g - h * S, n = a.n;
+    const uint32_t base = s * kSlice, begin = base + tid * kRun;
+    const int code = a.plan->code;
+    const uint32_t k = a.plan->k;
+    const uint32_t words = (n + 31) / 32;
+    if (code != HS_OK) return;
+    if (k == 0) {
+        // empty selection: clear this run's membership bits
+        if (a.member && (tid & 3u) == 0 && begin / 32 < words)
+            a.member[static_cast<size_t>(h) * words + begin / 32] = 0u;
+        return;
+    }
+
+    // this head's slice histograms (high bytes; low bytes of the k-th key's
+    // bucket) and this thread's run, all requested before any is used
+    uint32_t hv[8], lv[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) {
+        const uint32_t i = tid + u * kThreads;
+        const bool ok = i < S * 256;
+        hv[u] = ok ? a.g_hi[static_cast<size_t>(h * S) * 256 + i] : 0u;
+        lv[u] = ok ? a.g_lo[static_cast<size_t>(h * S) * 256 + i] : 0u;
+    }
+    uint32_t packed[kRun / 2];
+    load_run(a, h, begin, packed);
+    if (tid < 256) hist[0][tid] = hist[1][tid] = 0;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) {
+        const uint32_t i = tid + u * kThreads;
+        if (i < S * 256) {
+            (&slice_hist[0][0][0])[i] = hv[u];
+            (&slice_hist[1][0][0])[i] = lv[u];
+            if (hv[u]) atomicAdd(&hist[0][i & 255u], hv[u]);
+            if (lv[u]) atomicAdd(&hist[1][i & 255u], lv[u]);
+        }
+    }
+    __syncthreads();
+    find_bucket(hist[0], k, &sh[kBucket], &sh[kAbove]);
+    __syncthreads();
+    const uint32_t hi = sh[kBucket] & 255u, above_hi = sh[kAbove];
+    find_bucket(hist[1], k - above_hi, &sh[kBucket2], &sh[kAbove2]);
+    __syncthreads();
+    const uint32_t lo = sh[kBucket2] & 255u;
+    const uint32_t kstar = (hi << 8) | lo;
+    const uint32_t c_above = above_hi + sh[kAbove2];
+    const uint32_t c_equal = hist[1][lo];
+    const uint32_t t_need = k - c_above;  // ties taken, lowest ids first (>= 1)
+    // each slice's count above K* and its ties
+    for (uint32_t j = wave; j < S; j += kWaves) {
+        uint32_t above = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t bin = 4 * lane + q;
+            above += bin > hi ? slice_hist[0][j][bin] : 0u;
+            above += bin > lo ? slice_hist[1][j][bin] : 0u;
+        }
+        above = wave_sum_u32(above);
+        if (lane == 0) {
+            s_above[j] = above;
+            s_ties[j] = slice_hist[1][j][lo];
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t ties_before = 0, sel_before = 0;
+        for (uint32_t j = 0; j <= s; ++j) {
+            const uint32_t left = t_need > ties_before ? t_need - ties_before : 0u;
+            const uint32_t taken = std::min(s_ties[j], left);
+            if (j == s) {
+                sh[kTieBase] = ties_before;
+                sh[kTaken] = taken;
+                sh[kSelBase] = sel_before;
+                sh[kSel] = s_above[j] + taken;
+            }
+            ties_before += s_ties[j];
+            sel_before += s_above[j] + taken;
+        }
+        // boundary tie (gqa_policy.cpp:65): the (k+1)-th element exists with
+        // equal bits; equal keys mean equal bits except -0 / +0 (key 0x8000).
+        if (s == 0 && k < n && c_above + c_equal > k && kstar != 0x8000u)
+            atomicAdd(&a.status->boundary_tied_heads, 1u);
+    }
+    __syncthreads();
+    const uint32_t tie_base = sh[kTieBase], taken = sh[kTaken], sel_base = sh[kSelBase];
+    const bool zero_cut = kstar == 0x8000u && k < n && c_above + c_equal > k;
+
+    // membership, and the selection in id order
+    uint32_t my_above = 0, my_ties = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kRun; ++j) {
+        if (begin + j < n) {
+            const uint32_t key = order_key(half_at(packed, j));
+            my_above += key > kstar;
+            my_ties += key == kstar;
+        }
+    }
+    const uint32_t tie_start = block_exclusive_scan(my_ties, tmp);
+    const uint32_t my_taken = tie_start >= taken ? 0u : std::min(my_ties, taken - tie_start);
+    uint32_t pos = block_exclusive_scan(my_above + my_taken, tmp);
+    uint32_t tie_rank = tie_start;
+    uint32_t bits8 = 0;
+    uint32_t* out = a.ids + static_cast<size_t>(h) * a.ids_stride;
+#pragma unroll
+    for (uint32_t j = 0; j < kRun; ++j) {
+        const uint32_t i = begin + j;
+        if (i < n) {
+            const uint32_t bits = half_at(packed, j);
+            const uint32_t key = order_key(bits);
+            bool take = key > kstar;
+            if (key == kstar) {
+                take = tie_rank < taken;
+                if (zero_cut) {
+                    const uint32_t rank = tie_base + tie_rank;
+                    if (rank + 1 == t_need) note_zero_tie(a, h, bits, false);
+                    if (rank == t_need) note_zero_tie(a, h, bits, true);
+                }
+                ++tie_rank;
+            }
+            if (take) {
+                bits8 |= 1u << j;
+                if (!kRankOrder) {
+                    if (sel_base + pos < k) out[sel_base + pos] = i;
+                } else if (pos < kSlice) {
+                    sort_lds[pos] = ((0xffffu - key) << 16) | (i - base);
+                }
+                ++pos;
+            }
+        }
+    }
+    if (a.member) {
+        uint32_t word = bits8 << (8u * (tid & 3u));
+        word |= __shfl_xor(word, 1, 64);
+        word |= __shfl_xor(word, 2, 64);
+        if ((tid & 3u) == 0 && begin / 32 < words)
+            a.member[static_cast<size_t>(h) * words + begin / 32] = word;
+    }
+    if constexpr (kRankOrder) {
+        const uint32_t m = std::min(sh[kSel], a.cap);
+        __syncthreads();
+        sort_composites(sort_lds, sort_lds + kSlice, m, whist, tmp);
+        uint32_t* dst = a.g_sort + static_cast<size_t>(g) * a.cap;
+        for (uint32_t r = tid; r < m; r += kThreads) dst[r] = sort_lds[r];
+        if (tid == 0) a.g_m[g] = m;
+    }
+}
+
+// ---- 4. rank ----------------------------------------------------------------
+// Keys of four slices searched in lockstep: for each of the lists
+// key_at(q, .) of lengths len[q] (sorted by descending key), the number of
+// keys >= v (strict[q]: > v).  Fixed-step and branchless.
+template <typename KeyAt>
+__device__ __forceinline__ uint32_t count_before4(KeyAt key_at, const uint32_t (&len)[4],
+                                                  const bool (&strict)[4], uint32_t v) {
+    uint32_t pos[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (uint32_t step = kSlice; step >= 1; step >>= 1) {
+        uint32_t x[4];
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t cand = pos[q] + step;
+            x[q] = cand <= len[q] ? key_at(q, cand - 1) : 0u;
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t cand = pos[q] + step;
+            const bool ahead = strict[q] ? x[q] > v : x[q] >= v;
+            pos[q] = (cand <= len[q] && ahead) ? cand : pos[q];
+        }
+    }
+    return pos[0] + pos[1] + pos[2] + pos[3];
+}
+
+__global__ void __launch_bounds__(kThreads) rank_kernel(SelectArgs a) {
+    __shared__ uint16_t staged[kRankCap];
+    __shared__ uint32_t s_m[kMaxSlices], s_off[kMaxSlices];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t g = blockIdx.x, S = a.S, h = g / S, s = g - h * S;
+    if (a.plan->code != HS_OK) return;
+    const uint32_t k = a.plan->k;
+    if (k == 0) return;
+    const uint32_t* lists = a.g_sort + static_cast<size_t>(h * S) * a.cap;
+    // this slice's sorted composites (at most 8 per thread), requested first
+    uint32_t mine[kRun];
+#pragma unroll
+    for (uint32_t u = 0; u < kRun; ++u) {
+        const uint32_t r = tid + u * kThreads;
+        mine[u] = r < a.cap ? lists[static_cast<size_t>(s) * a.cap + r] : 0u;
+    }
+    if (tid < 64) {
+        const uint32_t m = tid < S ? a.g_m[h * S + tid] : 0u;
+        uint32_t x = m;
+#pragma unroll
+        for (uint32_t off = 1; off < kMaxSlices; off <<= 1) {
+            const uint32_t y = __shfl_up(x, off, 64);
+            if (tid >= off) x += y;
+        }
+        if (tid < kMaxSlices) {
+            s_m[tid] = m;  // 0 past S
+            s_off[tid] = x - m;
+        }
+    }
+    __syncthreads();
+    const bool in_lds = k <= kRankCap;  // the head's k keys fit the staging area
+    if (in_lds) {
+        // staged[off_j + r] = key of slice j's r-th composite, 8 loads in flight
+        for (uint32_t first = 0; first < k; first += 8 * kThreads) {
+            uint32_t v[8], at[8];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; ++u) {
+                const uint32_t idx = first + tid + u * kThreads;
+                uint32_t j = 0;
+#pragma unroll
+                for (uint32_t t = 1; t < kMaxSlices; ++t) j += (t < S && s_off[t] <= idx) ? 1u : 0u;
+                at[u] = idx;
+                v[u] = idx < k ? lists[static_cast<size_t>(j) * a.cap + (idx - s_off[j])] : 0u;
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 8; ++u)
+                if (at[u] < k) staged[at[u]] = static_cast<uint16_t>(0xffffu - (v[u] >> 16));
+        }
+        __syncthreads();
+    }
+    uint32_t* out = a.ids + static_cast<size_t>(h) * a.ids_stride;
+    const uint32_t m_self = s_m[s];
+    for (uint32_t u = 0; u < kRun; ++u) {
+        const uint32_t r = tid + u * kThreads;
+        if (r >= m_self) break;
+        const uint32_t x = mine[u];
+        const uint32_t key = 0xffffu - (x >> 16);
+        uint32_t at = r;
+        for (uint32_t j0 = 0; j0 < S; j0 += 4) {
+            uint32_t len[4], off[4];
+            bool strict[4];
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+                const uint32_t j = j0 + q;
+                const bool other = j < S && j != s;
+                len[q] = other ? s_m[j] : 0u;
+                off[q] = other ? s_off[j] : 0u;
+                strict[q] = j > s;  // equal keys of later slices have larger ids
+            }
+            if (in_lds)
+                at += count_before4([&](uint32_t q, uint32_t i) { return uint32_t(staged[off[q] + i]); },
+                                    len, strict, key);
+            else
+                at += count_before4(
+                    [&](uint32_t q, uint32_t i) {
+                        return 0xffffu - (lists[static_cast<size_t>(j0 + q) * a.cap + i] >> 16);
+                    },
+                    len, strict, key);
+        }
+        if (at < k) out[at] = s * kSlice + (x & 0xffffu);
+    }
 }
 
 }  // namespace
 
-size_t select_workspace_bytes(uint32_t heads, uint32_t n) {
-    return plan_select(heads, n, n).total;
-}
+size_t select_workspace_bytes(uint32_t heads, uint32_t n) { return plan_select(heads, n, n).total; }
 
 int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_t n, float alpha,
                   float ratio, uint32_t flags, const uint32_t* head0_partial, uint32_t* ids,
@@ -563,11 +811,9 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
     if (stride < n || stride > 0xffffffffu) return reject("GQA selector shape: stride < n");
     if (!std::isfinite(alpha) || alpha < 0 || !std::isfinite(ratio) || ratio <= 0 || ratio > 1)
         return reject("GQA selector numeric parameters");
-    if (flags & ~uint32_t(HS_SELECT_SCALE_RAW | HS_SELECT_FP32_COUNTS | HS_SELECT_REQUIRE_K))
+    if (flags & ~uint32_t(HS_SELECT_SCALE_RAW | HS_SELECT_FP32_COUNTS | HS_SELECT_REQUIRE_K |
+                          HS_SELECT_ID_ORDER))
         return reject("select: unknown flags");
-    // one resident workgroup per head (1024 threads, up to 145 KiB LDS each)
-    if (heads > static_cast<uint32_t>(device_cu_count()))
-        return reject("select: more heads than compute units");
     const uint64_t kmax = std::min<uint64_t>(
         n, static_cast<uint64_t>(std::floor(static_cast<double>(n) * static_cast<double>(ratio))));
     if (ids_stride < kmax || ids_stride > 0xffffffffu)
@@ -575,29 +821,47 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
     // A workspace of select_workspace_bytes(heads, n) covers every ratio.
     const SelectPlan p = plan_select(heads, n, static_cast<uint32_t>(kmax));
     char* ws = static_cast<char*>(workspace);
-    SelectSync* sync = reinterpret_cast<SelectSync*>(ws + p.off_sync);
-    const uint32_t* partial = head0_partial;
-    if (!partial) {
+    SelectArgs args;
+    args.scores = scores;
+    args.heads = heads;
+    args.stride = static_cast<uint32_t>(stride);
+    args.n = n;
+    args.S = p.S;
+    args.alpha = alpha;
+    args.ratio = ratio;
+    args.flags = flags;
+    args.partial = head0_partial;
+    args.partials = p.partials;
+    args.plan = reinterpret_cast<SelectPlanDev*>(ws + p.off_plan);
+    args.g_count = reinterpret_cast<uint32_t*>(ws + p.off_count);
+    args.g_bad = reinterpret_cast<uint32_t*>(ws + p.off_bad);
+    args.g_hi = reinterpret_cast<uint32_t*>(ws + p.off_hi);
+    args.g_lo = reinterpret_cast<uint32_t*>(ws + p.off_lo);
+    args.g_sort = reinterpret_cast<uint32_t*>(ws + p.off_sort);
+    args.g_m = reinterpret_cast<uint32_t*>(ws + p.off_m);
+    args.g_tie = reinterpret_cast<unsigned long long*>(ws + p.off_tie);
+    args.cap = p.cap;
+    args.ids = ids;
+    args.ids_stride = static_cast<uint32_t>(ids_stride);
+    args.counts_out = counts;
+    args.member = member;
+    args.status = status;
+    if (!head0_partial) {
         uint32_t* own = reinterpret_cast<uint32_t*>(ws + p.off_partial);
         hipLaunchKernelGGL(head0_max_kernel, dim3((p.partials + 3) / 4), dim3(256), 0, stream,
                            scores, n, own);
-        partial = own;
+        args.partial = own;
     }
-    uint32_t* sort_buf = reinterpret_cast<uint32_t*>(ws + p.off_sort);
-    uint32_t stride32 = static_cast<uint32_t>(stride);
-    uint32_t ids_stride32 = static_cast<uint32_t>(ids_stride);
-    uint32_t partials = p.partials, sort_cap = p.sort_cap;
-    void* args[] = {&scores, &heads, &stride32, &n, &alpha, &ratio, &flags, &partial, &partials,
-                    &sync, &sort_buf, &sort_cap, &ids, &ids_stride32, &counts, &member, &status};
-    const bool global = p.sort_cap != 0;
-    hipError_t st;
-    if (n <= 32 * kThreads)
-        st = global ? launch_variant<32, true>(dim3(heads), args, stream)
-                    : launch_variant<32, false>(dim3(heads), args, stream);
-    else
-        st = global ? launch_variant<64, true>(dim3(heads), args, stream)
-                    : launch_variant<64, false>(dim3(heads), args, stream);
-    if (st == hipSuccess) st = hipGetLastError();
+    const dim3 grid(p.groups), block(kThreads);
+    hipLaunchKernelGGL(count_kernel, grid, block, 0, stream, args);
+    hipLaunchKernelGGL(plan_kernel, grid, block, 0, stream, args);
+    if (flags & HS_SELECT_ID_ORDER) {
+        hipLaunchKernelGGL(slice_select_kernel<false>, grid, block, 0, stream, args);
+    } else {
+        hipLaunchKernelGGL(slice_select_kernel<true>, grid, block, 0, stream, args);
+        hipLaunchKernelGGL(rank_kernel, grid, block, 0, stream, args);
+    }
+    const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "select launch");
 }
 

@@ -33,9 +33,7 @@ enum {
     HS_ERR_DUPLICATE = 7,    /* duplicate/future id (gqa_pack.hpp:17,33)     */
     HS_ERR_MISSING = 8,      /* selected id without KV row (gqa_pack.hpp:44) */
     HS_ERR_HIP = 9,          /* HIP runtime call failed                      */
-    HS_ERR_UNSUPPORTED = 10, /* valid for the reference, beyond this build   */
-    HS_ERR_BARRIER = 11      /* device-wide barrier timed out (never expected
-                                under the cooperative launch it relies on)   */
+    HS_ERR_UNSUPPORTED = 10  /* valid for the reference, beyond this build   */
 };
 
 /* Device-side result of one selection; written by hs_gqa_select*. */
@@ -81,19 +79,27 @@ int hs_gqa_score(const uint16_t *q_dev, const uint16_t *keys_dev,
  * scores_dev F16 [heads][stride]; first n columns are candidates.
  * flags: HS_SELECT_SCALE_RAW applies scaled = F16(raw / sqrtf(128))
  * (policy/full_gqa_runtime.cpp:571) before selecting; HS_SELECT_FP32_COUNTS
- * is the reference's fp32_counts; HS_SELECT_REQUIRE_K rejects k == 0.
+ * is the reference's fp32_counts; HS_SELECT_REQUIRE_K rejects k == 0;
+ * HS_SELECT_ID_ORDER lists each head's selection in ascending id order (the
+ * same set; skips the rank sort).
  * Outputs: ids_dev [heads][ids_stride] uint32 in rank order (key desc, id
- * asc), counts_dev [heads] uint32, status_dev (k, tied heads, code), and
+ * asc) unless HS_SELECT_ID_ORDER, counts_dev [heads] uint32, status_dev
+ * (k, tied heads, code), and
  * optionally member_dev [heads][ceil(n/32)] uint32 bitmaps of the selected
  * ids (input of hs_gqa_sparse_attention).  ids_stride must be >= the
  * largest possible k = min(n, floor(n*ratio)).  workspace_dev holds
- * hs_gqa_select_workspace_bytes(heads, n) bytes of scratch.
+ * hs_gqa_select_workspace_bytes(heads, n) bytes of scratch (no
+ * initialisation needed).
  * head0_partial_dev: NULL, or the per-tile maxima from hs_gqa_score over
- * the same raw scores (skips one pass over head 0). */
+ * the same raw scores (skips one pass over head 0).
+ * One call is 3 launches on `stream` (4 in rank order, +1 without
+ * head0_partial_dev); calls sharing a workspace must be ordered on one
+ * stream. */
 enum {
     HS_SELECT_SCALE_RAW = 1u,
     HS_SELECT_FP32_COUNTS = 2u,
-    HS_SELECT_REQUIRE_K = 4u
+    HS_SELECT_REQUIRE_K = 4u,
+    HS_SELECT_ID_ORDER = 8u
 };
 size_t hs_gqa_select_workspace_bytes(uint32_t heads, uint32_t n);
 int hs_gqa_select(const uint16_t *scores_dev, uint32_t heads, size_t stride,
@@ -159,7 +165,8 @@ int hs_gqa_sparse_attention(const float *q_dev, const uint8_t *pool_dev,
 
 /* ---- fused layer step ----------------------------------------------------
  * One sparse decode layer: score (rehearsal q16 over the hot pool's K
- * halves) -> select (scaled, alpha, ratio) -> sparse attention (q32).
+ * halves) -> select (scaled, alpha, ratio; ids in ascending id order) ->
+ * sparse attention (q32).
  * pool rows 4096 B.  workspace: hs_decode_layer_workspace_bytes. */
 size_t hs_decode_layer_workspace_bytes(uint32_t n);
 int hs_decode_layer(const uint16_t *q16_dev, const float *q32_dev,

@@ -56,7 +56,7 @@ def test_select_rejects_bad_parameters(hs):
     assert call(ratio=0.0) == hs.HS_ERR_ARGUMENT
     assert call(ratio=1.5) == hs.HS_ERR_ARGUMENT
     assert call(ids_stride=11) == hs.HS_ERR_ARGUMENT  # floor(64*0.2f) = 12
-    assert call(flags=8) == hs.HS_ERR_ARGUMENT
+    assert call(flags=16) == hs.HS_ERR_ARGUMENT
     assert call(scores=None) == hs.HS_ERR_ARGUMENT
 
 

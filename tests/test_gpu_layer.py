@@ -48,8 +48,8 @@ def test_config3_layer(hs, port, n, alpha):
     assert np.array_equal(from_dev(scores), raw)
     rc, kk, pids, pcounts, tied = port.select(port.scale(raw), 32, n, n, alpha, 0.2)
     assert st["code"] == 0 and st["k"] == kk and st["boundary_tied_heads"] == tied
-    gids = from_dev(ids)[:, :kk]
-    assert np.array_equal(gids, pids) and np.array_equal(from_dev(counts), pcounts)
+    gids = from_dev(ids)[:, :kk]  # the layer lists each head's selection by ascending id
+    assert np.array_equal(gids, np.sort(pids, axis=1)) and np.array_equal(from_dev(counts), pcounts)
     ref = port.attention(q32, pool.view(np.uint8).reshape(-1), [list(r) for r in pids])
     assert rel_err(out.cpu().numpy().astype(np.float64), ref) <= 2e-3
     if alpha == 5.0:

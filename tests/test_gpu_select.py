@@ -23,14 +23,17 @@ def gpu_select(hs, scores, heads, stride, n, alpha, ratio, **kw):
 
 def check_against_port(hs, port, scores, heads, stride, n, alpha, ratio, fp32=False):
     rc, k, ids, counts, tied = port.select(scores, heads, stride, n, alpha, ratio, fp32)
-    st, gids, gcounts, _ = gpu_select(hs, scores, heads, stride, n, alpha, ratio,
-                                      fp32_counts=fp32)
-    assert st["code"] == rc
-    if rc == 0:
-        assert st["k"] == k
-        assert np.array_equal(gcounts, counts)
-        assert np.array_equal(gids, ids)
-        assert st["boundary_tied_heads"] == tied
+    # rank order (the reference's output) and ascending id order (same set)
+    for id_order in (False, True):
+        st, gids, gcounts, _ = gpu_select(hs, scores, heads, stride, n, alpha, ratio,
+                                          fp32_counts=fp32, id_order=id_order)
+        assert st["code"] == rc, id_order
+        if rc == 0:
+            assert st["k"] == k
+            assert np.array_equal(gcounts, counts)
+            want = np.sort(ids, axis=1) if id_order else ids
+            assert np.array_equal(gids, want), f"ids differ (id_order={id_order})"
+            assert st["boundary_tied_heads"] == tied
     return st
 
 
@@ -195,3 +198,56 @@ def test_scaling_edge_inputs_order(hs, port):
     assert rc == 0 and st["code"] == 0 and st["k"] == kk == n
     assert np.array_equal(from_dev(ids)[:, :kk], pids)
     assert st["boundary_tied_heads"] == tied
+
+
+def member_from_ids(ids, n):
+    words = (n + 31) // 32
+    out = np.zeros((ids.shape[0], words), dtype=np.uint32)
+    for h in range(ids.shape[0]):
+        np.bitwise_or.at(out[h], ids[h] >> 5, np.uint32(1) << (ids[h] & 31).astype(np.uint32))
+    return out
+
+
+@pytest.mark.parametrize("heads,n", [(1, 65536), (32, 65536), (64, 65536), (128, 65536),
+                                     (8, 40000), (32, 4097), (3, 12345)])
+def test_slices_and_run_lengths(hs, port, heads, n):
+    # Every slicing of the head (1..16 slices, 8..64 ids per thread) with
+    # coarse integer scores, so tie runs straddle slice boundaries; signed
+    # zeros sit at the cut for some heads.
+    g = rng(heads * 7919 + n)
+    s = f16_bits(g.integers(-6, 7, size=(heads, n)).astype(np.float64))
+    s[g.random((heads, n)) < 0.05] = 0x8000
+    for alpha, ratio in ((3.0, 0.2), (0.5, 0.05), (12.0, 1.0)):
+        rc, k, ids, counts, tied = port.select(s, heads, n, n, alpha, ratio)
+        for id_order in (False, True):
+            words = (n + 31) // 32
+            member = torch.zeros(heads * words, dtype=torch.int32, device="cuda")
+            st, gids, gcounts, _ = gpu_select(hs, s, heads, n, n, alpha, ratio, member=member,
+                                              id_order=id_order)
+            assert st["code"] == rc
+            if rc != 0:  # e.g. a count of 65536 overflows F16 (HS_ERR_COUNT)
+                continue
+            assert st["k"] == k and st["boundary_tied_heads"] == tied
+            assert np.array_equal(gcounts, counts)
+            assert np.array_equal(gids, np.sort(ids, axis=1) if id_order else ids)
+            bits = from_dev(member).view(np.uint32).reshape(heads, words)
+            assert np.array_equal(bits, member_from_ids(ids, n))
+
+
+def test_repeated_calls_share_workspace(hs, port):
+    # One workspace across calls of different shapes, never cleared: every
+    # launch writes what a later launch of the same call reads.
+    ws = hs.ops.workspace(hs.ops.select_workspace_bytes(32, 32768))
+    g = rng(77)
+    for heads, n, alpha in ((32, 32768, 2.0), (32, 1000, 1.0), (4, 32768, 3.0), (32, 32768, 0.7),
+                            (1, 64, 0.1)):
+        raw = f16_bits(g.standard_normal((heads, n)) * 4.0)
+        rc, k, ids, counts, tied = port.select(raw, heads, n, n, alpha, 0.2)
+        for id_order in (True, False):
+            dev_ids, dev_counts, _, status = hs.ops.select(
+                to_dev(raw.reshape(-1)), heads, n, n, alpha, 0.2, ws=ws, id_order=id_order)
+            st = hs.ops.read_status(status)
+            assert st["code"] == rc and st["k"] == k
+            got = from_dev(dev_ids)[:, :k]
+            assert np.array_equal(got, np.sort(ids, axis=1) if id_order else ids)
+            assert np.array_equal(from_dev(dev_counts), counts)
