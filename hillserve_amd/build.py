@@ -3,8 +3,9 @@
 Every HIP source under hillserve_amd/csrc is compiled with hipcc for gfx950
 (no other architecture), then linked into one shared library whose exported
 symbols are the C ABI declared in include/hs_gpu.h.  The C++17 host adapters
-(gqa_gpu.cpp) and their contract test executable are built from the same
-sources.  Usage:  python -m hillserve_amd.build  (or __graft_entry__.build()).
+(csrc/gqa_gpu.cpp) are linked into the same library, and their contract
+test executable (tests/cpp/gqa_gpu_contracts) is linked against it.
+Usage:  python -m hillserve_amd.build  (or __graft_entry__.build()).
 """
 from __future__ import annotations
 
@@ -20,9 +21,14 @@ PKG = ROOT / "hillserve_amd"
 CSRC = PKG / "csrc"
 OBJ = ROOT / "_build" / "obj"
 LIB = PKG / "libhillserve_amd.so"
+# C++ contract tests of the host adapters (built next to their source)
+CONTRACTS = ROOT / "tests" / "cpp" / "gqa_gpu_contracts"
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+# host-only C++ that calls the HIP runtime API
+HOST = [f"-I{ROCM / 'include'}", "-D__HIP_PLATFORM_AMD__", "-x", "c++"]
 
 # Flags for device code.  -packed-fp32-ops keeps the compiler from forming
 # v_pk_{add,mul,fma}_f32; -ffp-contract=off means every FMA in the kernels is
@@ -67,7 +73,7 @@ def _compile(src: Path) -> Path:
     if src.suffix == ".hip":
         cmd = [HIPCC, *COMMON, *DEVICE, "-c", str(src), "-o", str(obj)]
     else:  # host-only C++17 translation unit that calls the C ABI / HIP runtime
-        cmd = [HIPCC, *COMMON, "-x", "c++", "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *COMMON, *HOST, "-c", str(src), "-o", str(obj)]
     _run(cmd)
     return obj
 
@@ -84,11 +90,11 @@ def build(verbose: bool = True) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
-    test_src = CSRC / "gqa_gpu_contracts.cpp"
+    test_src = CONTRACTS.with_suffix(".cpp")
     if test_src.exists():
-        exe = PKG / "gqa_gpu_contracts"
-        _run([HIPCC, *COMMON, "-x", "c++", str(test_src), "-o", str(exe), f"-L{PKG}",
-              "-lhillserve_amd", f"-Wl,-rpath,$ORIGIN"])
+        _run([HIPCC, *COMMON, *HOST, str(test_src), "-x", "none", "-o", str(CONTRACTS),
+              f"-L{PKG}", "-lhillserve_amd", f"-L{ROCM / 'lib'}", "-lamdhip64",
+              "-Wl,-rpath,$ORIGIN/../../hillserve_amd"])
     if verbose:
         print(f"built {LIB.relative_to(ROOT)} ({LIB.stat().st_size} bytes) for {ARCH}")
     return LIB

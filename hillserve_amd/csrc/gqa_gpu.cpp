@@ -1,0 +1,411 @@
+// C++17 host adapters: the reference's hot-path call seams over the C ABI.
+// Host-only translation unit (HIP runtime API for device memory and copies).
+#include "hs_gqa.hpp"
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <limits>
+#include <mutex>
+
+namespace hillserve::gpu {
+namespace {
+
+using Clock = std::chrono::steady_clock;
+double ms_since(Clock::time_point t) {
+    return std::chrono::duration<double, std::milli>(Clock::now() - t).count();
+}
+
+void hip_check(hipError_t status, const char* what) {
+    if (status != hipSuccess)
+        throw DeviceError(HS_ERR_HIP, std::string(what) + ": " + hipGetErrorString(status));
+}
+
+// Return code of an hs_* entry point: argument rejections become
+// std::invalid_argument with the library's message, the rest DeviceError.
+void api_check(int rc) {
+    if (rc == HS_OK) return;
+    const std::string message = hs_last_error();
+    if (rc == HS_ERR_ARGUMENT) throw std::invalid_argument(message);
+    throw DeviceError(rc, message);
+}
+
+// Grow-only device allocation.
+class DeviceBuffer {
+public:
+    DeviceBuffer() = default;
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    ~DeviceBuffer() {
+        if (ptr_) (void)hipFree(ptr_);
+    }
+    void* ensure(std::size_t bytes) {
+        if (bytes > size_) {
+            if (ptr_) hip_check(hipFree(ptr_), "hipFree");
+            ptr_ = nullptr;
+            size_ = 0;
+            hip_check(hipMalloc(&ptr_, std::max<std::size_t>(bytes, 256)), "hipMalloc");
+            size_ = std::max<std::size_t>(bytes, 256);
+        }
+        return ptr_;
+    }
+    template <typename T>
+    T* as(std::size_t count) {
+        return static_cast<T*>(ensure(count * sizeof(T)));
+    }
+    std::size_t size() const noexcept { return size_; }
+
+private:
+    void* ptr_ = nullptr;
+    std::size_t size_ = 0;
+};
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+void upload(void* dst, const void* src, std::size_t bytes, void* stream) {
+    if (bytes)
+        hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)),
+                  "hipMemcpyAsync H2D");
+}
+void download(void* dst, const void* src, std::size_t bytes, void* stream) {
+    if (bytes)
+        hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)),
+                  "hipMemcpyAsync D2H");
+}
+void sync(void* stream) { hip_check(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize"); }
+
+hs_status_t read_status(const hs_status_t* status_dev, void* stream) {
+    hs_status_t st{};
+    download(&st, status_dev, sizeof st, stream);
+    sync(stream);
+    return st;
+}
+
+bool finite_half(std::uint16_t bits) { return (bits & 0x7c00u) != 0x7c00u; }
+
+constexpr std::size_t kHeads = 32, kKvHeads = 8, kDim = 128;
+constexpr std::size_t kMaxScoreChunk = 65536;  // tokens per hs_gqa_score call
+
+// Buffers of the free functions, one set per calling thread.
+struct Scratch {
+    DeviceBuffer in, out, ids, counts, member, status, ws, aux1, aux2, aux3;
+};
+Scratch& scratch() {
+    thread_local Scratch s;
+    return s;
+}
+
+}  // namespace
+
+// ---- scorer ----------------------------------------------------------------------
+
+struct FullGqaGpuScorer::Impl {
+    void* stream = nullptr;
+    std::mutex invocation;
+    DeviceBuffer query, output;
+};
+
+FullGqaGpuScorer::FullGqaGpuScorer(void* stream) : impl_(std::make_unique<Impl>()) {
+    impl_->stream = stream;
+}
+FullGqaGpuScorer::~FullGqaGpuScorer() = default;
+const char* FullGqaGpuScorer::implementation_name() const noexcept {
+    return "gfx950_ordered_fp32_fma";
+}
+std::size_t FullGqaGpuScorer::workspace_bytes() const noexcept {
+    return impl_->query.size() + impl_->output.size();
+}
+void* FullGqaGpuScorer::stream() const noexcept { return impl_->stream; }
+
+namespace {
+std::size_t checked_tokens(const std::vector<FullGqaKeyView>& views) {
+    std::size_t tokens = 0;
+    for (const auto& view : views) {
+        if (!view.data || view.tokens == 0 ||
+            (view.token_stride_words != 1024 && view.token_stride_words != 2048) ||
+            view.tokens > std::numeric_limits<std::uint32_t>::max() - tokens)
+            throw std::invalid_argument("full GQA GPU key view shape/stride/extent");
+        tokens += view.tokens;
+    }
+    return tokens;
+}
+}  // namespace
+
+void FullGqaGpuScorer::score_device(const std::uint16_t* query_dev,
+                                    const std::vector<FullGqaKeyView>& views,
+                                    std::uint16_t* output_dev, std::size_t output_stride) {
+    if (!query_dev || !output_dev || views.empty())
+        throw std::invalid_argument("full GQA GPU query/views shape");
+    const std::size_t tokens = checked_tokens(views);
+    if (output_stride < tokens) throw std::invalid_argument("full GQA GPU output stride");
+    std::size_t offset = 0;
+    for (const auto& view : views) {
+        for (std::size_t first = 0; first < view.tokens; first += kMaxScoreChunk) {
+            const std::size_t n = std::min(kMaxScoreChunk, view.tokens - first);
+            api_check(hs_gqa_score(query_dev, view.data + first * view.token_stride_words,
+                                   view.token_stride_words, nullptr, 0,
+                                   static_cast<std::uint32_t>(n), output_dev + offset + first,
+                                   output_stride, nullptr, impl_->stream));
+        }
+        offset += view.tokens;
+    }
+}
+
+void FullGqaGpuScorer::score(const std::vector<std::uint16_t>& query,
+                             const std::vector<FullGqaKeyView>& views,
+                             std::vector<std::uint16_t>& output) {
+    std::lock_guard<std::mutex> call(impl_->invocation);
+    if (&query == &output)
+        throw std::invalid_argument("full GQA GPU output must not alias the query");
+    if (query.size() != kHeads * kDim || views.empty())
+        throw std::invalid_argument("full GQA GPU query/views shape");
+    const std::size_t tokens = checked_tokens(views);
+    auto* q_dev = impl_->query.as<std::uint16_t>(kHeads * kDim);
+    auto* out_dev = impl_->output.as<std::uint16_t>(kHeads * tokens);
+    upload(q_dev, query.data(), kHeads * kDim * 2, impl_->stream);
+    score_device(q_dev, views, out_dev, tokens);
+    output.resize(kHeads * tokens);
+    download(output.data(), out_dev, output.size() * 2, impl_->stream);
+    sync(impl_->stream);
+}
+
+// ---- selector --------------------------------------------------------------------
+
+GQASelection select_gqa_scores(const std::vector<std::uint16_t>& score, std::size_t h,
+                               std::size_t stride, std::size_t n, float alpha, float ratio,
+                               bool fp32_counts) {
+    // policy/gqa_policy.cpp:48-49
+    if (!(h > 0 && h <= 128 && n > 0 && n <= stride && score.size() == h * stride))
+        throw std::runtime_error("GQA selector shape");
+    if (!(std::isfinite(alpha) && alpha >= 0 && std::isfinite(ratio) && ratio > 0 && ratio <= 1))
+        throw std::runtime_error("GQA selector numeric parameters");
+    if (n > 131072 || stride > std::numeric_limits<std::uint32_t>::max())
+        throw std::invalid_argument("GQA selector: more than 131072 candidates (beyond this build)");
+    Scratch& s = scratch();
+    void* stream = nullptr;
+    const std::size_t kmax =
+        std::min<std::size_t>(n, static_cast<std::size_t>(std::floor(double(n) * double(ratio))));
+    const std::size_t ids_stride = std::max<std::size_t>(kmax, 1);
+    auto* scores_dev = s.in.as<std::uint16_t>(h * stride);
+    auto* ids_dev = s.ids.as<std::uint32_t>(h * ids_stride);
+    auto* counts_dev = s.counts.as<std::uint32_t>(h);
+    auto* status_dev = s.status.as<hs_status_t>(1);
+    void* ws = s.ws.ensure(hs_gqa_select_workspace_bytes(static_cast<std::uint32_t>(h),
+                                                         static_cast<std::uint32_t>(n)));
+    upload(scores_dev, score.data(), score.size() * 2, stream);
+    api_check(hs_gqa_select(scores_dev, static_cast<std::uint32_t>(h), stride,
+                            static_cast<std::uint32_t>(n), alpha, ratio,
+                            fp32_counts ? HS_SELECT_FP32_COUNTS : 0u, nullptr, ids_dev, ids_stride,
+                            counts_dev, nullptr, status_dev, ws, stream));
+    const hs_status_t st = read_status(status_dev, stream);
+    switch (st.code) {
+        case HS_OK: break;
+        case HS_ERR_NONFINITE: {
+            // gqa_policy.cpp:51 names head 0 when it holds the nonfinite value
+            const bool head0 = std::any_of(score.begin(), score.begin() + n,
+                                           [](std::uint16_t b) { return !finite_half(b); });
+            throw std::runtime_error(head0 ? "nonfinite head0 score" : "nonfinite GQA score");
+        }
+        case HS_ERR_THRESHOLD: throw std::runtime_error("F16 threshold overflow");
+        case HS_ERR_COUNT:
+            throw std::runtime_error("public F16 count overflow; long-count policy extension required");
+        case HS_ERR_MEAN:
+            throw std::runtime_error("public F16 mean overflow; long-count policy extension required");
+        default: throw DeviceError(st.code, "GQA selector device status");
+    }
+    GQASelection r;
+    r.k = st.k;
+    r.boundary_tied_heads = st.boundary_tied_heads;
+    r.counts.resize(h);
+    std::vector<std::uint32_t> ids(h * ids_stride);
+    download(r.counts.data(), counts_dev, h * 4, stream);
+    download(ids.data(), ids_dev, ids.size() * 4, stream);
+    sync(stream);
+    r.ids.resize(h);
+    for (std::size_t head = 0; head < h; ++head)
+        r.ids[head].assign(ids.begin() + head * ids_stride, ids.begin() + head * ids_stride + r.k);
+    return r;
+}
+
+// ---- union and pack --------------------------------------------------------------
+
+namespace {
+// Flattened [32][width] uint32 id lists + lengths; ids beyond 32 bits are
+// returned as `future` (they can never be below visible).
+std::size_t flatten(const std::vector<std::vector<std::uint64_t>>& ids, std::vector<std::uint32_t>& flat,
+                    std::vector<std::uint32_t>& lens, bool& future) {
+    std::size_t width = 1;
+    for (const auto& head : ids) width = std::max(width, head.size());
+    flat.assign(ids.size() * width, 0);
+    lens.resize(ids.size());
+    future = false;
+    for (std::size_t h = 0; h < ids.size(); ++h) {
+        lens[h] = static_cast<std::uint32_t>(ids[h].size());
+        for (std::size_t j = 0; j < ids[h].size(); ++j) {
+            if (ids[h][j] > std::numeric_limits<std::uint32_t>::max()) future = true;
+            flat[h * width + j] = static_cast<std::uint32_t>(ids[h][j]);
+        }
+    }
+    return width;
+}
+}  // namespace
+
+std::vector<std::uint64_t> gqa_physical_union(const std::vector<std::vector<std::uint64_t>>& ids,
+                                              std::size_t visible) {
+    if (ids.size() != 32 || !visible || visible > 66048)
+        throw std::invalid_argument("GQA union bounds");  // gqa_pack.hpp:14
+    std::vector<std::uint32_t> flat, lens;
+    bool future = false;
+    const std::size_t width = flatten(ids, flat, lens, future);
+    if (future) throw std::invalid_argument("GQA duplicate/future selected ID");
+    Scratch& s = scratch();
+    void* stream = nullptr;
+    auto* ids_dev = s.ids.as<std::uint32_t>(flat.size());
+    auto* lens_dev = s.counts.as<std::uint32_t>(32);
+    auto* out_dev = s.out.as<std::uint32_t>(visible);
+    auto* n_dev = s.aux1.as<std::uint32_t>(1);
+    auto* status_dev = s.status.as<hs_status_t>(1);
+    void* ws = s.ws.ensure(hs_gqa_union_workspace_bytes(static_cast<std::uint32_t>(visible)));
+    upload(ids_dev, flat.data(), flat.size() * 4, stream);
+    upload(lens_dev, lens.data(), 32 * 4, stream);
+    api_check(hs_gqa_physical_union(ids_dev, lens_dev, width, static_cast<std::uint32_t>(visible),
+                                    out_dev, n_dev, status_dev, ws, stream));
+    const hs_status_t st = read_status(status_dev, stream);
+    if (st.code == HS_ERR_DUPLICATE) throw std::invalid_argument("GQA duplicate/future selected ID");
+    if (st.code != HS_OK) throw DeviceError(st.code, "GQA union device status");
+    std::uint32_t count = 0;
+    download(&count, n_dev, 4, stream);
+    sync(stream);
+    std::vector<std::uint32_t> out(count);
+    download(out.data(), out_dev, count * 4, stream);
+    sync(stream);
+    return std::vector<std::uint64_t>(out.begin(), out.end());
+}
+
+void pack_gqa_workspace(const std::vector<std::vector<std::uint64_t>>& ids,
+                        const std::vector<std::uint64_t>& positions,
+                        const std::vector<std::uint64_t>& physical,
+                        const std::vector<std::uint8_t>& payload, std::size_t count,
+                        std::uint16_t* k, std::uint16_t* v, float* mask) {
+    // runtime/gqa_pack.hpp:29-36 (shape, then physical positions)
+    if (ids.size() != 32 || positions.empty() || positions.size() > 256 ||
+        positions.back() >= 66048 || !count || count > 66048 ||
+        payload.size() != physical.size() * 4096)
+        throw std::invalid_argument("GQA packing shape");
+    const std::size_t max_id = positions.back() + 1;
+    std::vector<std::int32_t> row_of_id(max_id, -1);
+    for (std::size_t i = 0; i < physical.size(); ++i) {
+        const auto id = physical[i];
+        if (id >= row_of_id.size() || row_of_id[id] != -1)
+            throw std::invalid_argument("duplicate/future physical position");
+        row_of_id[id] = static_cast<std::int32_t>(i);
+    }
+    for (const auto& head : ids)
+        if (head.empty() || head.size() > count)
+            throw std::invalid_argument("per-head selection exceeds slots");
+    std::vector<std::uint32_t> flat, lens;
+    bool future = false;
+    const std::size_t width = flatten(ids, flat, lens, future);
+    if (future) throw std::invalid_argument("future or missing selected KV");
+    const std::size_t qpad = (positions.size() + 63) / 64 * 64;
+    Scratch& s = scratch();
+    void* stream = nullptr;
+    auto* pool_dev = s.in.as<std::uint8_t>(std::max<std::size_t>(payload.size(), 4096));
+    auto* map_dev = s.aux1.as<std::int32_t>(max_id);
+    auto* ids_dev = s.ids.as<std::uint32_t>(flat.size());
+    auto* lens_dev = s.counts.as<std::uint32_t>(32);
+    auto* pos_dev = s.aux2.as<std::uint64_t>(positions.size());
+    auto* status_dev = s.status.as<hs_status_t>(1);
+    const std::size_t kv_words = count * 4096;
+    auto* k_dev = s.out.as<std::uint16_t>(2 * kv_words);
+    auto* v_dev = k_dev + kv_words;
+    auto* mask_dev = s.aux3.as<float>(count * qpad * 32);
+    upload(pool_dev, payload.data(), payload.size(), stream);
+    upload(map_dev, row_of_id.data(), max_id * 4, stream);
+    upload(ids_dev, flat.data(), flat.size() * 4, stream);
+    upload(lens_dev, lens.data(), 32 * 4, stream);
+    upload(pos_dev, positions.data(), positions.size() * 8, stream);
+    api_check(hs_gqa_pack(pool_dev, static_cast<std::uint32_t>(physical.size()), map_dev,
+                          static_cast<std::uint32_t>(max_id), ids_dev, lens_dev, width, pos_dev,
+                          static_cast<std::uint32_t>(positions.size()),
+                          static_cast<std::uint32_t>(count), k_dev, v_dev, mask_dev, status_dev,
+                          stream));
+    const hs_status_t st = read_status(status_dev, stream);
+    if (st.code == HS_ERR_MISSING || st.code == HS_ERR_DUPLICATE)
+        throw std::invalid_argument("future or missing selected KV");  // gqa_pack.hpp:44
+    if (st.code != HS_OK) throw DeviceError(st.code, "GQA pack device status");
+    download(k, k_dev, kv_words * 2, stream);
+    download(v, v_dev, kv_words * 2, stream);
+    download(mask, mask_dev, count * qpad * 32 * 4, stream);
+    sync(stream);
+}
+
+// ---- score backend ---------------------------------------------------------------
+
+struct GpuScoreBackend::Impl {
+    std::string abi;
+    void* stream = nullptr;
+    std::mutex invocation;
+    DeviceBuffer query, keys, scores;
+};
+
+GpuScoreBackend::GpuScoreBackend(std::string abi, void* stream) : impl_(std::make_unique<Impl>()) {
+    if (abi != "HS_FULL_GQA_F16_V2" && abi != "HS_FULL_GQA_PIPELINE_F16_V3")
+        throw std::invalid_argument("unsupported score ABI; legacy cross-head raw-sum image cannot be substituted");
+    impl_->abi = std::move(abi);
+    impl_->stream = stream;
+}
+GpuScoreBackend::~GpuScoreBackend() = default;
+
+DeviceScores GpuScoreBackend::score_raw_gqa(const std::vector<std::uint16_t>& q,
+                                            const std::vector<std::uint16_t>& k, std::size_t qh,
+                                            std::size_t kh, std::size_t n, std::size_t d) {
+    std::lock_guard<std::mutex> call(impl_->invocation);
+    // smartssd/adapter.hpp:97-104
+    const bool pipeline = impl_->abi == "HS_FULL_GQA_PIPELINE_F16_V3";
+    if (qh != 32 || kh != 8 || d != 128 || !n || n > 32768)
+        throw std::invalid_argument("raw GQA requires explicit V2/V3 ABI and Q32/KV8/D128,1<=N<=32768");
+    if (pipeline && (n < 64 || n % 64))
+        throw std::invalid_argument("HS_FULL_GQA_PIPELINE_F16_V3 requires64<=N<=32768,N%64==0;no padding or fallback");
+    if (q.size() != kHeads * kDim || k.size() != n * kKvHeads * kDim)
+        throw std::invalid_argument("raw GQA query/key vector sizes");
+    DeviceScores result;
+    const auto start = Clock::now();
+    auto* q_dev = impl_->query.as<std::uint16_t>(q.size());
+    auto* k_dev = impl_->keys.as<std::uint16_t>(k.size());
+    auto* s_dev = impl_->scores.as<std::uint16_t>(kHeads * n);
+    upload(q_dev, q.data(), q.size() * 2, impl_->stream);
+    upload(k_dev, k.data(), k.size() * 2, impl_->stream);
+    sync(impl_->stream);
+    result.timings.h2d_ms = ms_since(start);
+    result.timings.h2d_bytes = (q.size() + k.size()) * 2;
+    const auto launch = Clock::now();
+    if (pipeline)
+        api_check(hs_full_gqa_pipeline(q_dev, k_dev, s_dev, static_cast<std::uint32_t>(n),
+                                       impl_->stream));
+    else
+        api_check(hs_gqa_score(q_dev, k_dev, 1024, nullptr, 0, static_cast<std::uint32_t>(n),
+                               s_dev, n, nullptr, impl_->stream));
+    sync(impl_->stream);
+    result.timings.launch_wait_ms = ms_since(launch);
+    const auto copy = Clock::now();
+    result.values.resize(kHeads * n);
+    download(result.values.data(), s_dev, result.values.size() * 2, impl_->stream);
+    sync(impl_->stream);
+    result.timings.d2h_ms = ms_since(copy);
+    result.timings.d2h_bytes = result.values.size() * 2;
+    result.timings.total_ms = ms_since(start);
+    if (!std::all_of(result.values.begin(), result.values.end(), finite_half))
+        throw std::runtime_error("nonfinite raw GQA score");  // smartssd/xrt_backend.cpp:381
+    return result;
+}
+
+DeviceScores GpuScoreBackend::score(const std::vector<std::uint16_t>&,
+                                    const std::vector<std::uint16_t>&, std::size_t, std::size_t,
+                                    std::size_t) {
+    throw std::invalid_argument("per-query-head partial score layout unavailable in the GPU backend; use score_raw_gqa");
+}
+
+}  // namespace hillserve::gpu

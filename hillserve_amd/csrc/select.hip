@@ -15,7 +15,7 @@
 // partial sum is an integer below 2^24: the FP32 total is exact in any
 // summation order.
 //
-// Work split: each head is cut into S <= 16 slices of 4096 consecutive ids;
+// Work split: each head is cut into S <= 32 slices of 4096 consecutive ids;
 // every (head, slice) pair is one 512-thread workgroup whose threads own 8
 // consecutive ids each.  The phases that need a head-wide or device-wide view
 // are separate launches on the caller's stream: a kernel boundary is the
@@ -54,9 +54,9 @@ constexpr uint32_t kThreads = 512;
 constexpr uint32_t kWaves = kThreads / 64;
 constexpr uint32_t kRun = 8;                     // ids per thread
 constexpr uint32_t kSlice = kThreads * kRun;     // ids per group
-constexpr uint32_t kMaxN = 65536;
+constexpr uint32_t kMaxN = 131072;              // policy/gqa_policy_tests.cpp long ids
 constexpr uint32_t kMaxHeads = 128;
-constexpr uint32_t kMaxSlices = kMaxN / kSlice;  // 16
+constexpr uint32_t kMaxSlices = kMaxN / kSlice;  // 32
 constexpr uint32_t kRankCap = 16384;             // a head's sorted keys staged in LDS
 
 // Published by group 0 of the plan launch.
@@ -267,15 +267,19 @@ __device__ __forceinline__ uint32_t hist_total(const uint32_t* whist, uint32_t b
     return c;
 }
 
-// Maximum of the head-0 per-tile maxima (n <= 65536: at most 1024 of them).
+// Maximum of the head-0 per-tile maxima (at most kMaxN / 64 of them).
 __device__ __forceinline__ uint32_t partial_max(const SelectArgs& a) {
-    uint32_t v[2];
+    constexpr uint32_t kLoads = kMaxN / 64 / kThreads;
+    uint32_t v[kLoads];
 #pragma unroll
-    for (uint32_t u = 0; u < 2; ++u) {
+    for (uint32_t u = 0; u < kLoads; ++u) {
         const uint32_t i = threadIdx.x + u * kThreads;
         v[u] = i < a.partials ? a.partial[i] : 0u;
     }
-    return v[0] > v[1] ? v[0] : v[1];
+    uint32_t best = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < kLoads; ++u) best = v[u] > best ? v[u] : best;
+    return best;
 }
 
 // ---- 1. count ---------------------------------------------------------------
@@ -330,15 +334,17 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
 
     // every global read of this kernel is issued up front
     uint32_t best = partial_max(a);
-    uint32_t cnt[4], bad[4], hi_part[8];
+    constexpr uint32_t kCountLoads = kMaxHeads * kMaxSlices / kThreads;  // 8
+    constexpr uint32_t kBinLoads = kMaxSlices * 256 / kThreads;           // 16
+    uint32_t cnt[kCountLoads], bad[kCountLoads], hi_part[kBinLoads];
 #pragma unroll
-    for (uint32_t u = 0; u < 4; ++u) {  // heads * S <= 2048 slice counts
+    for (uint32_t u = 0; u < kCountLoads; ++u) {  // heads * S slice counts
         const uint32_t i = tid + u * kThreads;
         cnt[u] = i < groups ? a.g_count[i] : 0u;
         bad[u] = i < groups ? a.g_bad[i] : 0u;
     }
 #pragma unroll
-    for (uint32_t u = 0; u < 8; ++u) {  // this head's S * 256 <= 4096 bins
+    for (uint32_t u = 0; u < kBinLoads; ++u) {  // this head's S * 256 bins
         const uint32_t i = tid + u * kThreads;
         hi_part[u] = i < S * 256 ? a.g_hi[static_cast<size_t>(h * S) * 256 + i] : 0u;
     }
@@ -351,7 +357,7 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
     if (tid < a.heads) head_count[tid] = head_bad[tid] = 0;
     __syncthreads();
 #pragma unroll
-    for (uint32_t u = 0; u < 4; ++u) {
+    for (uint32_t u = 0; u < kCountLoads; ++u) {
         const uint32_t i = tid + u * kThreads;
         if (i < groups) {
             atomicAdd(&head_count[i / S], cnt[u]);
@@ -359,7 +365,7 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
         }
     }
 #pragma unroll
-    for (uint32_t u = 0; u < 8; ++u)
+    for (uint32_t u = 0; u < kBinLoads; ++u)
         if (hi_part[u]) atomicAdd(&hist[(tid + u * kThreads) & 255u], hi_part[u]);
     best = block_max(best, tmp);  // its barrier also publishes the sums above
     const float thr = threshold_from_key(best, scale, a.alpha);
@@ -556,9 +562,10 @@ __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
 
     // this head's slice histograms (high bytes; low bytes of the k-th key's
     // bucket) and this thread's run, all requested before any is used
-    uint32_t hv[8], lv[8];
+    constexpr uint32_t kBinLoads = kMaxSlices * 256 / kThreads;  // 16
+    uint32_t hv[kBinLoads], lv[kBinLoads];
 #pragma unroll
-    for (uint32_t u = 0; u < 8; ++u) {
+    for (uint32_t u = 0; u < kBinLoads; ++u) {
         const uint32_t i = tid + u * kThreads;
         const bool ok = i < S * 256;
         hv[u] = ok ? a.g_hi[static_cast<size_t>(h * S) * 256 + i] : 0u;
@@ -569,7 +576,7 @@ __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
     if (tid < 256) hist[0][tid] = hist[1][tid] = 0;
     __syncthreads();
 #pragma unroll
-    for (uint32_t u = 0; u < 8; ++u) {
+    for (uint32_t u = 0; u < kBinLoads; ++u) {
         const uint32_t i = tid + u * kThreads;
         if (i < S * 256) {
             (&slice_hist[0][0][0])[i] = hv[u];
@@ -752,9 +759,12 @@ __global__ void __launch_bounds__(kThreads) rank_kernel(SelectArgs a) {
 #pragma unroll
             for (uint32_t u = 0; u < 8; ++u) {
                 const uint32_t idx = first + tid + u * kThreads;
+                // last slice starting at or before idx (empty slices share
+                // their successor's offset and are skipped)
                 uint32_t j = 0;
 #pragma unroll
-                for (uint32_t t = 1; t < kMaxSlices; ++t) j += (t < S && s_off[t] <= idx) ? 1u : 0u;
+                for (uint32_t step = kMaxSlices / 2; step >= 1; step >>= 1)
+                    j = (j + step < S && s_off[j + step] <= idx) ? j + step : j;
                 at[u] = idx;
                 v[u] = idx < k ? lists[static_cast<size_t>(j) * a.cap + (idx - s_off[j])] : 0u;
             }
@@ -807,7 +817,7 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
                   void* workspace, hipStream_t stream) {
     if (!scores || !ids || !status || !workspace) return reject("select: null pointer");
     if (heads == 0 || heads > kMaxHeads) return reject("GQA selector shape: heads must be 1..128");
-    if (n == 0 || n > kMaxN) return reject("GQA selector shape: n must be 1..65536");
+    if (n == 0 || n > kMaxN) return reject("GQA selector shape: n must be 1..131072");
     if (stride < n || stride > 0xffffffffu) return reject("GQA selector shape: stride < n");
     if (!std::isfinite(alpha) || alpha < 0 || !std::isfinite(ratio) || ratio <= 0 || ratio > 1)
         return reject("GQA selector numeric parameters");

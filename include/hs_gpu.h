@@ -76,7 +76,8 @@ int hs_gqa_score(const uint16_t *q_dev, const uint16_t *keys_dev,
 
 /* ---- (2) selection -------------------------------------------------------
  * select_gqa_scores (policy/gqa_policy.cpp:47-70) on device.
- * scores_dev F16 [heads][stride]; first n columns are candidates.
+ * scores_dev F16 [heads][stride]; first n columns are candidates (heads
+ * 1..128, n 1..131072).
  * flags: HS_SELECT_SCALE_RAW applies scaled = F16(raw / sqrtf(128))
  * (policy/full_gqa_runtime.cpp:571) before selecting; HS_SELECT_FP32_COUNTS
  * is the reference's fp32_counts; HS_SELECT_REQUIRE_K rejects k == 0;

@@ -1,0 +1,131 @@
+// hs_gqa.hpp — C++17 host interface of the MI355X sparse-KV hot path.
+//
+// The reference runtime calls its hot path through four C++ seams; this
+// header offers the same names, argument meanings and exception types on top
+// of the C ABI in hs_gpu.h, so a caller switches by namespace:
+//   hillserve::FullGqaCpuScorer::score   (policy/full_gqa_cpu.hpp:27-50)
+//        -> hillserve::gpu::FullGqaGpuScorer::score
+//   hillserve::policy::select_gqa_scores (policy/gqa_policy.hpp:14-21)
+//        -> hillserve::gpu::select_gqa_scores
+//   hillserve::gqa_physical_union / pack_gqa_workspace (runtime/gqa_pack.hpp:12-58)
+//        -> hillserve::gpu::gqa_physical_union / pack_gqa_workspace
+//   hillserve::FpgaScoreBackend::score_raw_gqa (smartssd/adapter.hpp:73-76)
+//        -> hillserve::gpu::GpuScoreBackend::score_raw_gqa
+// The host-vector overloads copy in, run on the device and copy out
+// (synchronous, like the reference calls); the *_device members take device
+// pointers and only enqueue on the object's stream.
+// Errors: shape/argument problems throw std::invalid_argument, numeric
+// failures detected on the device (nonfinite scores, F16 count overflow)
+// throw std::runtime_error, each with the reference's message text; HIP
+// runtime failures throw hillserve::gpu::DeviceError.
+#pragma once
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "hs_gpu.h"
+
+namespace hillserve::gpu {
+
+class DeviceError : public std::runtime_error {
+public:
+    DeviceError(int code, const std::string& what) : std::runtime_error(what), code_(code) {}
+    int code() const noexcept { return code_; }
+
+private:
+    int code_;
+};
+
+// A run of device-resident keys: tokens rows of F16 [8][128] at
+// token_stride_words (1024 packed K, 2048 interleaved K|V pool rows).
+struct FullGqaKeyView {
+    const std::uint16_t* data = nullptr;  // device memory
+    std::size_t tokens = 0;
+    std::size_t token_stride_words = 1024;
+};
+
+class FullGqaGpuScorer {
+public:
+    // stream: hipStream_t as void* (nullptr = null stream).  Calls on one
+    // instance are serialized; device buffers are kept across calls.
+    explicit FullGqaGpuScorer(void* stream = nullptr);
+    ~FullGqaGpuScorer();
+    FullGqaGpuScorer(const FullGqaGpuScorer&) = delete;
+    FullGqaGpuScorer& operator=(const FullGqaGpuScorer&) = delete;
+    // query F16 [32*128] (host), views concatenated in caller order, output
+    // F16 head-major [32][total tokens] (host, resized).  Synchronous.
+    void score(const std::vector<std::uint16_t>& query, const std::vector<FullGqaKeyView>& views,
+               std::vector<std::uint16_t>& output);
+    // query_dev F16 [32*128], output_dev [32][output_stride]; enqueue only.
+    void score_device(const std::uint16_t* query_dev, const std::vector<FullGqaKeyView>& views,
+                      std::uint16_t* output_dev, std::size_t output_stride);
+    const char* implementation_name() const noexcept;
+    std::size_t workspace_bytes() const noexcept;
+    void* stream() const noexcept;
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
+struct GQASelection {
+    std::vector<std::vector<std::uint64_t>> ids;  // rank order: key desc, id asc
+    std::vector<std::uint32_t> counts;
+    std::size_t k = 0, boundary_tied_heads = 0;
+};
+// scaled_scores F16 [heads][stride] (host); the first valid_tokens columns
+// are candidates.  heads 1..128, valid_tokens 1..131072.
+GQASelection select_gqa_scores(const std::vector<std::uint16_t>& scaled_scores, std::size_t heads,
+                               std::size_t stride, std::size_t valid_tokens, float alpha,
+                               float cap_ratio, bool fp32_counts = false);
+
+// Sorted unique ids over the 32 heads; duplicates within a head or ids >=
+// visible throw std::invalid_argument.
+std::vector<std::uint64_t> gqa_physical_union(const std::vector<std::vector<std::uint64_t>>& ids,
+                                              std::size_t visible);
+
+// payload holds physical.size() rows of 4096 B (F16 K[8][128] then V[8][128])
+// in physical order; k, v (count*4096 F16) and mask (count*qpad*32 F32) are
+// host buffers written like the reference packer, padding included.
+void pack_gqa_workspace(const std::vector<std::vector<std::uint64_t>>& ids,
+                        const std::vector<std::uint64_t>& positions,
+                        const std::vector<std::uint64_t>& physical,
+                        const std::vector<std::uint8_t>& payload, std::size_t count,
+                        std::uint16_t* k, std::uint16_t* v, float* mask);
+
+struct ScoreDeviceTimings {
+    double h2d_ms = 0, launch_wait_ms = 0, d2h_ms = 0, total_ms = 0;
+    std::uint64_t h2d_bytes = 0, d2h_bytes = 0;
+};
+struct DeviceScores {
+    std::vector<std::uint16_t> values;
+    ScoreDeviceTimings timings;
+};
+
+// The explicit full-dimension GQA ABI of the score backend: Q[32,128],
+// K[token,8,128], S[32,token].  abi "HS_FULL_GQA_PIPELINE_F16_V3" enforces
+// 64 <= n <= 32768, n % 64 == 0; "HS_FULL_GQA_F16_V2" accepts 1..32768
+// (smartssd/adapter.hpp:97-104).  Nonfinite scores throw.
+class GpuScoreBackend {
+public:
+    explicit GpuScoreBackend(std::string abi = "HS_FULL_GQA_PIPELINE_F16_V3", void* stream = nullptr);
+    ~GpuScoreBackend();
+    GpuScoreBackend(const GpuScoreBackend&) = delete;
+    GpuScoreBackend& operator=(const GpuScoreBackend&) = delete;
+    DeviceScores score_raw_gqa(const std::vector<std::uint16_t>& q,
+                               const std::vector<std::uint16_t>& k, std::size_t query_heads,
+                               std::size_t kv_heads, std::size_t tokens, std::size_t channels);
+    // The per-query-head partial layout is not served (as the reference's
+    // GQA-only images): throws std::invalid_argument.
+    DeviceScores score(const std::vector<std::uint16_t>& q, const std::vector<std::uint16_t>& k,
+                       std::size_t heads, std::size_t tokens, std::size_t channels);
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
+}  // namespace hillserve::gpu

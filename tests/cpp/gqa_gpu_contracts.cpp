@@ -1,0 +1,515 @@
+// Contract tests of the C++ host adapters (include/hs_gqa.hpp) on the GPU.
+// They follow the reference's own C++ tests case by case, each against an
+// independent scalar oracle written here:
+//   selector  tests/gqa_policy_tests.cpp:25-59, tests/quality_alpha_tests.cpp:35-77
+//   scorer    tests/full_gqa_cpu_tests.cpp:19-121
+//   kernel    tests/full_gqa_kernel_check.cpp:31-37,70-139 (V2/V3 ABI)
+//   pack      tests/gqa_pack_tests.cpp:6-38
+// Exit status: 0 passed, 1 failed, 77 no GPU visible (nothing run).
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <cstring>
+#include <iostream>
+#include <limits>
+#include <numeric>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "hs_gqa.hpp"
+
+namespace {
+using namespace hillserve::gpu;
+constexpr std::size_t H = 32, KH = 8, D = 128;
+std::size_t comparisons = 0, cases = 0;
+
+void check(bool ok, const std::string& why) {
+    if (!ok) throw std::runtime_error(why);
+}
+template <class F>
+void rejects(F fn, const std::string& why) {
+    bool threw = false;
+    try {
+        fn();
+    } catch (const std::exception&) {
+        threw = true;
+    }
+    check(threw, why);
+}
+
+// binary16 <-> binary32 (IEEE 754, round to nearest even), written for this test.
+float half_value(std::uint16_t b) {
+    const int sign = b >> 15, exp = (b >> 10) & 31, man = b & 1023;
+    float v;
+    if (exp == 0) v = std::ldexp(float(man), -24);
+    else if (exp == 31) v = man ? std::numeric_limits<float>::quiet_NaN() : std::numeric_limits<float>::infinity();
+    else v = std::ldexp(float(man | 1024), exp - 25);
+    return sign ? -v : v;
+}
+std::uint16_t half_bits(float f) {
+    std::uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const std::uint32_t sign = (x >> 16) & 0x8000u;
+    const std::uint32_t a = x & 0x7fffffffu;
+    if (a > 0x7f800000u) return std::uint16_t(sign | 0x7e00u);
+    if (a >= 0x477ff000u) return std::uint16_t(sign | 0x7c00u);  // rounds past 65504
+    if (a < 0x38800000u) {                                         // subnormal or zero
+        const float scaled = std::fabs(f) * 16777216.0f;          // exact: |f| < 2^-14
+        return std::uint16_t(sign | std::uint32_t(std::nearbyint(scaled)));
+    }
+    const std::uint32_t exp = (a >> 23) - 112, man = a & 0x7fffffu;
+    std::uint32_t h = (exp << 10) | (man >> 13);
+    const std::uint32_t rest = man & 0x1fffu;
+    if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) ++h;
+    return std::uint16_t(sign | h);
+}
+
+// ---- device helpers --------------------------------------------------------------
+struct Dev {
+    void* p = nullptr;
+    explicit Dev(std::size_t bytes) {
+        if (hipMalloc(&p, std::max<std::size_t>(bytes, 16)) != hipSuccess) throw std::runtime_error("hipMalloc");
+    }
+    ~Dev() { (void)hipFree(p); }
+    template <class T>
+    T* as() const { return static_cast<T*>(p); }
+};
+template <class T>
+void to_dev(const Dev& d, const std::vector<T>& h) {
+    if (hipMemcpy(d.p, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+        throw std::runtime_error("hipMemcpy H2D");
+}
+
+// ---- selector --------------------------------------------------------------------
+std::vector<std::vector<std::uint64_t>> sorted_expectation(const std::vector<std::uint16_t>& s,
+                                                           std::size_t heads, std::size_t stride,
+                                                           std::size_t n, std::size_t k) {
+    std::vector<std::vector<std::uint64_t>> out(heads);
+    for (std::size_t h = 0; h < heads; ++h) {
+        std::vector<std::uint64_t> e(n);
+        std::iota(e.begin(), e.end(), 0);
+        std::sort(e.begin(), e.end(), [&](auto a, auto b) {
+            const float av = half_value(s[h * stride + a]), bv = half_value(s[h * stride + b]);
+            return av != bv ? av > bv : a < b;
+        });
+        e.resize(k);
+        out[h] = e;
+    }
+    return out;
+}
+
+void selector_contracts() {
+    // head-0 broadcast vs per-head maximum; inclusive threshold (gqa_policy_tests.cpp:26-27)
+    std::vector<std::uint16_t> score;
+    for (float x : {10.f, 9.f, 8.f, 7.f, 1.f, 1.f, 1.f, 1.f}) score.push_back(half_bits(x));
+    auto x = select_gqa_scores(score, 2, 4, 4, 2.f, 1.f);
+    check(x.counts == std::vector<std::uint32_t>({3, 0}) && x.k == 1, "head0/inclusive/count floor semantics");
+    check(x.ids[0][0] == 0 && x.ids[1][0] == 0, "deterministic original-ID ties");
+    // capacity padding beyond valid tokens is not a candidate (:29-30)
+    std::vector<std::uint16_t> padded(2 * 8, half_bits(1000));
+    for (std::size_t h = 0; h < 2; ++h)
+        for (std::size_t t = 0; t < 5; ++t) padded[h * 8 + t] = half_bits(float(t));
+    auto p = select_gqa_scores(padded, 2, 8, 5, 10, 0.4f);
+    check(p.k == 2 && p.ids[0] == std::vector<std::uint64_t>({4, 3}), "padding/current candidate selection");
+    // F16 count rounding at 2049 (:32)
+    std::vector<std::uint16_t> many(2049, half_bits(0));
+    auto rounded = select_gqa_scores(many, 1, 2049, 2049, 0, 1);
+    check(rounded.counts[0] == 2049 && rounded.k == 2048, "F16 count2049 rounds2048");
+    // long addressing (:34)
+    std::vector<std::uint16_t> long_scores(131072, half_bits(-10));
+    long_scores.back() = half_bits(1);
+    auto last = select_gqa_scores(long_scores, 1, long_scores.size(), long_scores.size(), 0, 1);
+    check(last.k == 1 && last.ids[0][0] == 131071, "global long-token ID not truncated");
+    // F16 count overflow and the FP32-count extension (:35-41)
+    std::vector<std::uint16_t> overflow(65520, half_bits(0));
+    rejects([&] { select_gqa_scores(overflow, 1, overflow.size(), overflow.size(), 0, 1); },
+            "F16 count overflow must fail");
+    auto wide = select_gqa_scores(overflow, 1, overflow.size(), overflow.size(), 0, .2f, true);
+    check(wide.counts[0] == 65520 && wide.k == 13104 && wide.ids[0].front() == 0 && wide.ids[0].back() == 13103,
+          "explicit FP32 count extension keeps ordered cap");
+    auto exact = select_gqa_scores(many, 1, 2049, 2049, 0, 1, true);
+    check(exact.k == 2049, "explicit FP32 count has no hidden F16 rounding");
+    // random orders with signed zeros (:49-57)
+    std::mt19937 rng(1741);
+    for (int trial = 0; trial < 24; ++trial) {
+        const std::size_t heads = 32, n = 257, stride = 288;
+        std::vector<std::uint16_t> input(heads * stride, half_bits(1000));
+        for (std::size_t h = 0; h < heads; ++h)
+            for (std::size_t t = 0; t < n; ++t)
+                input[h * stride + t] = (t % 17 == 0) ? std::uint16_t(t % 2 ? 0 : 0x8000)
+                                                      : half_bits(float(int(rng() % 97) - 48) / 2);
+        const auto selected = select_gqa_scores(input, heads, stride, n, 10, .2f);
+        check(selected.ids == sorted_expectation(input, heads, stride, n, selected.k),
+              "ordered selected IDs differ from the sorted expectation");
+        ++cases;
+    }
+    // quality alpha ladder (quality_alpha_tests.cpp:35-77)
+    constexpr std::size_t P = 128;
+    const std::array<float, 4> alphas{5.f, 10.f, 20.f, 50.f};
+    std::vector<std::uint16_t> scores(H * P);
+    for (std::size_t h = 0; h < H; ++h)
+        for (std::size_t t = 0; t < P; ++t) scores[h * P + t] = half_bits(100.f - 2.f * float(t));
+    const std::array<std::size_t, 4> expected{3, 6, 11, 25};
+    const std::array<std::uint32_t, 4> counts{3, 6, 11, 26};
+    for (std::size_t a = 0; a < alphas.size(); ++a) {
+        auto s = select_gqa_scores(scores, H, P, P, alphas[a], .2f);
+        check(s.k == expected[a], "alpha/count/20percent-cap changed on same input");
+        for (std::size_t h = 0; h < H; ++h) {
+            check(s.counts[h] == counts[a], "inclusive threshold count changed");
+            for (std::size_t t = 0; t < s.k; ++t) check(s.ids[h][t] == t, "alpha changed score ranking");
+        }
+    }
+    for (float alpha : alphas) {
+        std::fill(scores.begin(), scores.end(), half_bits(-1000.f));
+        const auto threshold_bits = half_bits(100.f - alpha);
+        for (std::size_t h = 0; h < H; ++h) {
+            scores[h * P] = half_bits(100.f);
+            scores[h * P + 1] = threshold_bits;
+            scores[h * P + 2] = threshold_bits;
+            scores[h * P + 3] = std::uint16_t(threshold_bits - 1);
+        }
+        auto tied = select_gqa_scores(scores, H, P, P, alpha, .2f);
+        check(tied.k == 3 && tied.counts[0] == 3 && tied.ids[0] == std::vector<std::uint64_t>({0, 1, 2}),
+              "threshold equality or original-ID tie order changed");
+        scores[0] = half_bits(120.f);
+        auto broadcast = select_gqa_scores(scores, H, P, P, alpha, .2f);
+        const float new_threshold = half_value(half_bits(120.f - alpha));
+        check(broadcast.counts[1] == std::uint32_t(100.f >= new_threshold),
+              "head0 maximum was silently replaced by per-head maxima");
+    }
+    constexpr std::size_t N = 16384;
+    std::vector<std::uint16_t> rounded_scores(H * N, half_bits(-1000.f));
+    for (std::size_t h = 0; h < H; ++h) std::fill_n(rounded_scores.begin() + h * N, 2049, half_bits(0.f));
+    for (float alpha : alphas) {
+        auto s = select_gqa_scores(rounded_scores, H, N, N, alpha, .2f);
+        check(s.k == 2048 && s.counts[0] == 2049 && s.ids[0].back() == 2047,
+              "alpha variant must retain F16 count rounding and original-ID ties");
+    }
+    // shape and parameter rejections (gqa_policy.cpp:48-49)
+    rejects([&] { select_gqa_scores(score, 0, 4, 4, 1, 1); }, "zero heads");
+    rejects([&] { select_gqa_scores(score, 2, 4, 5, 1, 1); }, "valid beyond stride");
+    rejects([&] { select_gqa_scores(score, 2, 3, 3, 1, 1); }, "size mismatch");
+    rejects([&] { select_gqa_scores(score, 2, 4, 4, -1, 1); }, "negative alpha");
+    rejects([&] { select_gqa_scores(score, 2, 4, 4, 1, 0); }, "zero ratio");
+    std::vector<std::uint16_t> bad = score;
+    bad[5] = 0x7c00;
+    rejects([&] { select_gqa_scores(bad, 2, 4, 4, 1, 1); }, "nonfinite score must fail");
+    cases += 12;
+}
+
+// ---- scorer ----------------------------------------------------------------------
+std::uint32_t random_state = 0x7f123451;  // full_gqa_cpu_tests.cpp:19-27
+std::uint32_t random_word() {
+    random_state ^= random_state << 13;
+    random_state ^= random_state >> 17;
+    random_state ^= random_state << 5;
+    return random_state;
+}
+std::uint16_t finite_half() {
+    static constexpr std::uint16_t edge[] = {0, 0x8000, 1, 0x8001, 0x03ff, 0x83ff, 0x0400, 0x8400,
+                                             0x3c00, 0xbc00, 0x7bff, 0xfbff, 0x3555, 0xb555};
+    const auto word = random_word();
+    return word % 5 == 0 ? edge[(word >> 8) % (sizeof(edge) / sizeof(edge[0]))]
+                         : std::uint16_t((word & 0x83ff) | (((word >> 10) % 31) << 10));
+}
+
+struct HostView {
+    std::size_t first_token, tokens, stride;
+};
+// Ordered FP32 dot products: s = fl(s + fl(q*k)), channels ascending.
+std::vector<std::uint16_t> independent_scores(const std::vector<std::uint16_t>& q,
+                                              const std::vector<std::uint16_t>& data,
+                                              const std::vector<HostView>& views) {
+    std::vector<const std::uint16_t*> keys;
+    for (const auto& v : views)
+        for (std::size_t t = 0; t < v.tokens; ++t) keys.push_back(data.data() + (v.first_token + t) * v.stride);
+    const std::size_t n = keys.size();
+    std::vector<std::uint16_t> out(H * n);
+    for (std::size_t h = 0; h < H; ++h)
+        for (std::size_t t = 0; t < n; ++t) {
+            volatile float sum = 0;
+            for (std::size_t c = 0; c < D; ++c) {
+                volatile float mul = half_value(q[h * D + c]) * half_value(keys[t][(h / 4) * D + c]);
+                sum = sum + mul;
+            }
+            out[h * n + t] = half_bits(sum);
+        }
+    return out;
+}
+
+void score_check(FullGqaGpuScorer& scorer, const std::vector<std::uint16_t>& q,
+                 const std::vector<std::uint16_t>& data, const Dev& dev, const std::vector<HostView>& views) {
+    std::vector<FullGqaKeyView> dviews;
+    for (const auto& v : views)
+        dviews.push_back({dev.as<std::uint16_t>() + v.first_token * v.stride, v.tokens, v.stride});
+    std::vector<std::uint16_t> out;
+    scorer.score(q, dviews, out);
+    const auto oracle = independent_scores(q, data, views);
+    for (std::size_t i = 0; i < out.size(); ++i)
+        if (out[i] != oracle[i])
+            throw std::runtime_error("score bit mismatch at " + std::to_string(i) + ": " +
+                                     std::to_string(out[i]) + " != " + std::to_string(oracle[i]));
+    comparisons += out.size();
+    auto next = q;  // a second call reusing the scorer's buffers
+    for (auto& value : next) value ^= 0x8000;
+    scorer.score(next, dviews, out);
+    check(out == independent_scores(next, data, views), "second call mismatch");
+    comparisons += out.size();
+    ++cases;
+}
+
+void scorer_contracts() {
+    FullGqaGpuScorer scorer;
+    for (std::size_t n : {1u, 2u, 7u, 8u, 9u, 17u, 65u, 129u})
+        for (std::size_t stride : {1024u, 2048u}) {
+            std::vector<std::uint16_t> q(H * D), data(n * stride, 0x7e00);
+            for (auto& x : q) x = finite_half();
+            for (std::size_t t = 0; t < n; ++t)
+                for (std::size_t c = 0; c < KH * D; ++c) data[t * stride + c] = finite_half();
+            Dev dev(data.size() * 2);
+            to_dev(dev, data);
+            score_check(scorer, q, data, dev, {{0, n, stride}});
+            // noncontiguous views, an odd tail and a duplicate token (:76-78)
+            if (n >= 9) score_check(scorer, q, data, dev, {{7, 2, stride}, {0, 3, stride}, {1, 1, stride}});
+        }
+    // minimum subnormals, exact cancellation, negative zero and overflow (:81-90)
+    std::vector<std::uint16_t> q(H * D, 1), data(9 * 1024, 1);
+    Dev dev(data.size() * 2);
+    to_dev(dev, data);
+    score_check(scorer, q, data, dev, {{0, 9, 1024}});
+    for (std::size_t i = 0; i < q.size(); ++i) q[i] = i % 2 ? 0xfbff : 0x7bff;
+    std::fill(data.begin(), data.end(), 0x7bff);
+    to_dev(dev, data);
+    score_check(scorer, q, data, dev, {{0, 9, 1024}});
+    std::fill(q.begin(), q.end(), 0x7bff);
+    score_check(scorer, q, data, dev, {{0, 9, 1024}});
+    std::fill(q.begin(), q.end(), 0x8000);
+    score_check(scorer, q, data, dev, {{0, 9, 1024}});
+    // argument rejections (:96-103)
+    std::vector<std::uint16_t> out;
+    const auto* key = dev.as<std::uint16_t>();
+    rejects([&] { scorer.score({}, {{key, 1, 1024}}, out); }, "empty query accepted");
+    rejects([&] { scorer.score(q, {}, out); }, "empty views accepted");
+    rejects([&] { scorer.score(q, {{nullptr, 1, 1024}}, out); }, "null view accepted");
+    rejects([&] { scorer.score(q, {{key, 0, 1024}}, out); }, "empty view accepted");
+    rejects([&] { scorer.score(q, {{key, 1, 1}}, out); }, "bad stride accepted");
+    rejects([&] { scorer.score(q, {{key, std::numeric_limits<std::size_t>::max(), 1024}}, out); },
+            "overflowing view accepted");
+    rejects([&] { scorer.score(q, {{key, 1, 1024}}, q); }, "aliased output accepted");
+}
+
+// ---- kernel ABI (V2 / V3) ----------------------------------------------------------
+std::uint32_t kernel_rng = 0x62c83e17;  // full_gqa_kernel_check.cpp:31-37
+std::uint16_t sample() {
+    auto word = [] {
+        kernel_rng ^= kernel_rng << 13;
+        kernel_rng ^= kernel_rng >> 17;
+        kernel_rng ^= kernel_rng << 5;
+        return kernel_rng;
+    };
+    const std::uint32_t s = word() & 0x8000u;
+    const std::uint32_t e = (word() % 17u) << 10;
+    return std::uint16_t(s | e | (word() & 1023u));
+}
+
+void backend_compare(GpuScoreBackend& backend, const std::vector<std::uint16_t>& q,
+                     const std::vector<std::uint16_t>& k, std::size_t n) {
+    const auto got = backend.score_raw_gqa(q, k, 32, 8, n, 128);
+    const auto want = independent_scores(q, k, {{0, n, 1024}});
+    for (std::size_t i = 0; i < want.size(); ++i)
+        if (got.values[i] != want[i])
+            throw std::runtime_error("raw GQA bit mismatch at " + std::to_string(i));
+    comparisons += want.size();
+    ++cases;
+}
+
+void kernel_contracts() {
+    // invalid counts touch no memory, even with null Q/K (:84-89, kernel.cpp:251)
+    {
+        Dev sentinel(2);
+        const std::vector<std::uint16_t> mark{0x1234};
+        to_dev(sentinel, mark);
+        for (std::uint32_t n : {0u, 32769u, 0xffffffffu, 63u, 65u})
+            check(hs_full_gqa_pipeline(nullptr, nullptr, sentinel.p, n, nullptr) == HS_ERR_ARGUMENT,
+                  "invalid V3 count accepted");
+        std::uint16_t back = 0;
+        check(hipMemcpy(&back, sentinel.p, 2, hipMemcpyDeviceToHost) == hipSuccess && back == 0x1234,
+              "invalid-shape call wrote output");
+    }
+    GpuScoreBackend v2("HS_FULL_GQA_F16_V2");
+    for (unsigned n : {1u, 15u, 16u, 17u, 31u, 32u, 33u, 129u, 1024u}) {
+        std::vector<std::uint16_t> q(4096), k(std::size_t(n) * 1024);
+        for (auto& x : q) x = sample();
+        for (auto& x : k) x = sample();
+        backend_compare(v2, q, k, n);
+    }
+    // subnormal markers and ordered cancellation (:42-61)
+    for (unsigned n : {16u, 17u}) {
+        std::vector<std::uint16_t> q(4096), k(std::size_t(n) * 1024);
+        for (auto& x : q) x = sample();
+        for (auto& x : k) x = sample();
+        std::fill(q.begin(), q.begin() + 128, 0);
+        q[0] = 0x3c00;
+        std::fill(q.begin() + 28 * 128, q.begin() + 29 * 128, 0);
+        q[28 * 128 + 3] = 0x3c00;
+        std::fill(q.begin() + 31 * 128, q.end(), 0);
+        q[31 * 128] = 0x6c00;
+        q[31 * 128 + 1] = 0x3c00;
+        q[31 * 128 + 2] = 0xec00;
+        for (unsigned t = 0; t < n; ++t) {
+            k[t * 1024] = std::uint16_t(t + 1);
+            const auto last = (t * 8 + 7) * 128;
+            k[last] = 0x6c00;
+            k[last + 1] = 0x3c00;
+            k[last + 2] = 0x6c00;
+            k[last + 3] = std::uint16_t(0x8000u | (t + 1));
+        }
+        const auto got = v2.score_raw_gqa(q, k, 32, 8, n, 128).values;
+        for (unsigned t = 0; t < n; ++t) {
+            check(got[t] == t + 1, "positive subnormal marker");
+            check(got[28 * n + t] == std::uint16_t(0x8000u | (t + 1)), "negative subnormal marker");
+            check(got[31 * n + t] == 0, "ordered cancellation");
+        }
+        backend_compare(v2, q, k, n);
+    }
+    // physical head / channel markers and the cancellation witness (:103-118)
+    {
+        const unsigned n = 17;
+        std::vector<std::uint16_t> q(4096), k(n * 1024);
+        for (unsigned h = 0; h < 32; ++h) q[h * 128 + (h * 7) % 128] = half_bits(float(h + 1) / 32);
+        for (unsigned t = 0; t < n; ++t)
+            for (unsigned h = 0; h < 8; ++h)
+                for (unsigned c = 0; c < 128; ++c) k[(t * 8 + h) * 128 + c] = half_bits(float(t * 1024 + h * 128 + c) / 16384);
+        backend_compare(v2, q, k, n);
+        const std::uint16_t edge[] = {0, 0x8000, 1, 0x8001, 0x3ff, 0x400, 0x3c00, 0xbc00, 0x7bff, 0xfbff};
+        std::fill(q.begin(), q.end(), 0);
+        for (unsigned h = 0; h < 32; ++h) {
+            q[h * 128] = 0x6c00;
+            q[h * 128 + 1] = 0x3c00;
+            q[h * 128 + 2] = 0xec00;
+            for (unsigned c = 3; c < 128; ++c) q[h * 128 + c] = edge[(h + c) % 10];
+        }
+        for (unsigned t = 0; t < n; ++t)
+            for (unsigned h = 0; h < 8; ++h) {
+                k[(t * 8 + h) * 128] = 0x6c00;
+                k[(t * 8 + h) * 128 + 1] = 0x3c00;
+                k[(t * 8 + h) * 128 + 2] = 0x6c00;
+                for (unsigned c = 3; c < 128; ++c) k[(t * 8 + h) * 128 + c] = std::uint16_t((t + h + c) % 1024);
+            }
+        backend_compare(v2, q, k, n);
+    }
+    GpuScoreBackend v3;  // HS_FULL_GQA_PIPELINE_F16_V3
+    for (unsigned n : {64u, 128u, 1024u, 32768u}) {
+        std::vector<std::uint16_t> q(4096), k(std::size_t(n) * 1024);
+        for (auto& x : q) x = sample();
+        for (auto& x : k) x = sample();
+        backend_compare(v3, q, k, n);
+    }
+    std::vector<std::uint16_t> q(4096, 0x3c00), k(65 * 1024, 0x3c00);
+    rejects([&] { v3.score_raw_gqa(q, k, 32, 8, 65, 128); }, "V3 accepted N%64 != 0");
+    rejects([&] { v2.score_raw_gqa(q, k, 32, 8, 65, 64); }, "channels other than 128 accepted");
+    rejects([&] { v2.score_raw_gqa(q, k, 32, 4, 65, 128); }, "KV heads other than 8 accepted");
+    rejects([&] { v2.score(q, k, 32, 65, 128); }, "partial layout must not be served");
+    rejects([] { GpuScoreBackend legacy("HS_PARTIAL_F16_V1"); }, "partial ABI accepted for raw GQA");
+}
+
+// ---- union / pack ----------------------------------------------------------------
+void pack_contracts() {
+    // fixed values and causal mask (gqa_pack_tests.cpp:7-15)
+    std::vector<std::vector<std::uint64_t>> ids(32, {8, 12});
+    ids[4] = {12, 8};
+    std::vector<std::uint64_t> physical = {8, 12};
+    std::vector<std::uint16_t> raw(4096);
+    for (std::size_t t = 0; t < 2; ++t)
+        for (std::size_t h = 0; h < 8; ++h)
+            for (std::size_t d = 0; d < 128; ++d) {
+                raw[t * 2048 + h * 128 + d] = std::uint16_t(1000 * t + 100 * h + d);
+                raw[t * 2048 + 1024 + h * 128 + d] = std::uint16_t(5000 + 1000 * t + 100 * h + d);
+            }
+    std::vector<std::uint8_t> payload(raw.size() * 2);
+    std::memcpy(payload.data(), raw.data(), payload.size());
+    std::vector<std::uint16_t> k(32 * 4096), v(k.size());
+    std::vector<float> mask(32 * 64 * 32);
+    pack_gqa_workspace(ids, {10, 12}, physical, payload, 32, k.data(), v.data(), mask.data());
+    check(k[0] == 0 && k[4096] == 1000 && k[4 * 128] == 1100 && k[4096 + 4 * 128] == 100, "K layout");
+    check(v[(4 * 128) * 32] == 6100 && v[(4 * 128) * 32 + 1] == 5100, "V layout");
+    check(k[2 * 4096 + 127] == 0 && v[127 * 32 + 2] == 0, "zero padding");
+    check(mask[0] == 0 && std::isinf(mask[1]) && mask[32 + 1] == 0, "causal mask");
+    check(std::isinf(mask[(4 * 64) * 32]) && mask[(4 * 64) * 32 + 1] == 0 && std::isinf(mask[2 * 32]), "mask rows");
+    ids[0] = {13};
+    rejects([&] { pack_gqa_workspace(ids, {12}, physical, payload, 32, k.data(), v.data(), mask.data()); },
+            "missing selected KV accepted");
+    // random trials against a scalar layout oracle (:16-36)
+    std::mt19937 rng(781);
+    for (int trial = 0; trial < 48; ++trial) {
+        const std::size_t n = 65 + trial * 4, slots = (n + 31) / 32 * 32;
+        std::vector<std::uint64_t> rows(n);
+        std::iota(rows.begin(), rows.end(), 0);
+        std::shuffle(rows.begin(), rows.end(), rng);
+        std::vector<std::uint8_t> bytes(n * 4096);
+        for (auto& b : bytes) b = std::uint8_t(rng());
+        std::vector<std::vector<std::uint64_t>> selected(32);
+        for (auto& head : selected) {
+            head = rows;
+            if (trial % 2) head.resize(1 + rng() % n);
+            std::shuffle(head.begin(), head.end(), rng);
+        }
+        std::vector<std::uint64_t> queries{n / 2, n - 1};
+        std::vector<std::uint16_t> got_k(slots * 4096), got_v(got_k.size()), ref_k(got_k.size(), 0),
+            ref_v(got_k.size(), 0);
+        std::vector<float> got_mask(slots * 64 * 32),
+            ref_mask(got_mask.size(), -std::numeric_limits<float>::infinity());
+        for (std::size_t h = 0; h < 32; ++h)
+            for (std::size_t slot = 0; slot < selected[h].size(); ++slot) {
+                const auto id = selected[h][slot];
+                const auto row = std::size_t(std::find(rows.begin(), rows.end(), id) - rows.begin());
+                const auto* src = bytes.data() + row * 4096;
+                for (std::size_t d = 0; d < 128; ++d) {
+                    std::memcpy(&ref_k[slot * 4096 + h * 128 + d], src + (h / 4 * 128 + d) * 2, 2);
+                    std::memcpy(&ref_v[(h * 128 + d) * slots + slot], src + 2048 + (h / 4 * 128 + d) * 2, 2);
+                }
+                for (std::size_t q = 0; q < queries.size(); ++q)
+                    if (id <= queries[q]) ref_mask[(h * 64 + q) * slots + slot] = 0;
+            }
+        pack_gqa_workspace(selected, queries, rows, bytes, slots, got_k.data(), got_v.data(), got_mask.data());
+        check(got_k == ref_k && got_v == ref_v, "packed K/V differ from the layout oracle");
+        check(std::memcmp(got_mask.data(), ref_mask.data(), got_mask.size() * 4) == 0, "mask differs");
+        const auto physical_union = gqa_physical_union(selected, n);
+        std::vector<std::uint64_t> expected;
+        for (const auto& head : selected) expected.insert(expected.end(), head.begin(), head.end());
+        std::sort(expected.begin(), expected.end());
+        expected.erase(std::unique(expected.begin(), expected.end()), expected.end());
+        check(physical_union == expected, "physical union differs");
+        selected[31].push_back(selected[31].front());
+        rejects([&] { gqa_physical_union(selected, n); }, "duplicate ID accepted");
+        ++cases;
+    }
+    rejects([&] { gqa_physical_union(std::vector<std::vector<std::uint64_t>>(31), 8); }, "union bounds");
+    rejects([&] { gqa_physical_union(std::vector<std::vector<std::uint64_t>>(32, {9}), 8); }, "future ID");
+}
+
+}  // namespace
+
+int main() {
+    int devices = 0;
+    if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0) {
+        std::cout << "{\"status\":\"skipped\",\"reason\":\"no GPU visible\"}" << std::endl;
+        return 77;
+    }
+    try {
+        selector_contracts();
+        scorer_contracts();
+        kernel_contracts();
+        pack_contracts();
+        std::cout << "{\"status\":\"passed\",\"cases\":" << cases
+                  << ",\"bitwise_scores_compared\":" << comparisons << "}" << std::endl;
+        return 0;
+    } catch (const std::exception& e) {
+        std::cerr << e.what() << std::endl;
+        return 1;
+    }
+}

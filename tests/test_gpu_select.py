@@ -53,6 +53,12 @@ def test_known_answers(hs, port):
     assert counts[0] == 2049 and st["k"] == 2048
     st, _, _, _ = gpu_select(hs, many, 1, 2049, 2049, 0, 1, fp32_counts=True)
     assert st["k"] == 2049
+    # global long-token id not truncated (131072 candidates, 32 slices)
+    long_scores = np.full(131072, hb(-10), dtype=np.uint16)
+    long_scores[-1] = hb(1)
+    for id_order in (False, True):
+        st, ids, _, _ = gpu_select(hs, long_scores, 1, 131072, 131072, 0, 1, id_order=id_order)
+        assert st["code"] == 0 and st["k"] == 1 and ids[0][0] == 131071
 
 
 def test_quality_alpha_ladder(hs):
@@ -209,7 +215,8 @@ def member_from_ids(ids, n):
 
 
 @pytest.mark.parametrize("heads,n", [(1, 65536), (32, 65536), (64, 65536), (128, 65536),
-                                     (8, 40000), (32, 4097), (3, 12345)])
+                                     (8, 40000), (32, 4097), (3, 12345), (2, 131072),
+                                     (128, 100000)])
 def test_slices_and_run_lengths(hs, port, heads, n):
     # Every slicing of the head (1..16 slices, 8..64 ids per thread) with
     # coarse integer scores, so tie runs straddle slice boundaries; signed
