@@ -112,6 +112,20 @@ def cpu_baseline(q16_host, k_host, seconds):
     }
 
 
+TRAFFIC_PROFILE = "profiles/score_kernel_hbm_counters.md"
+
+
+def pmc_traffic():
+    """HBM bytes per score_kernel launch from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (copy-calibrated); None if absent."""
+    import re
+    path = Path(__file__).resolve().parent / TRAFFIC_PROFILE
+    if not path.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", path.read_text())
+    return int(m.group(1)) if m else None
+
+
 def profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status, ws, kmax):
     """Back-to-back launches of one kernel family over the 30 layers."""
     def run():
@@ -292,7 +306,8 @@ def main():
         "hbm_gbps": step_bytes / (ms_per_step * 1e-3) / 1e9,
         "roofline": {
             "bound": "hbm", "achieved": score_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": score_gbs / HBM_PEAK_GBS, "traffic": None,
+            "frac": score_gbs / HBM_PEAK_GBS, "traffic": pmc_traffic(),
+            "traffic_source": TRAFFIC_PROFILE,
             "kernel": "score_kernel", "avg_launch_us": avg_score_us,
             "algorithmic_bytes_per_launch": SCORE_BYTES,
         },
