@@ -115,6 +115,8 @@ def cpu_baseline(q16_host, k_host, seconds):
 TRAFFIC_PROFILE = "profiles/score_kernel_hbm_counters.md"
 
 
+
+
 def pmc_traffic():
     """HBM bytes per score_kernel launch from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (copy-calibrated); None if absent."""

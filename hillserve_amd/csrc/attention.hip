@@ -12,11 +12,13 @@
 //    512 token ids.  It ORs the 4 query heads' selection bitmaps, compacts the
 //    union in id order, and reads each selected (id, g) K row and V row
 //    exactly once for all of its query heads -> HBM bytes = sum_g |U_g|*512.
-//  * 16 lanes per id, 16 B (8 channels) per lane, 4 ids per wave instruction:
-//    every K/V access is a contiguous 256 B run.
-//  * pass 1 scores (4 heads per id, cross-lane reduction over 16 lanes),
-//    chunk-local max and exp, pass 2 accumulates p*V in registers; the
-//    (m, l, o[128]) partials of all chunks are merged by attn_combine.
+//  * one pass: 16 lanes per id, 16 B (8 channels) per lane, so every K and
+//    V access is a contiguous 256 B run; the K and V halves of a row (same
+//    4 KiB pool row) are requested together, which streams ~1.4x faster
+//    than a K pass followed by a V pass.  Scores are reduced over the 16
+//    lanes with 8 cross-lane moves, softmax is online (rescaled once per
+//    batch of rows), and p*V accumulates in registers.
+//  * the (m, l, o[128]) partials of all chunks are merged by attn_combine.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -40,18 +42,49 @@ __device__ __forceinline__ void unpack8(const uint4 w, float* f) {
     f[6] = h2f(w.w & 0xffffu); f[7] = h2f(w.w >> 16);
 }
 
+// Sum of the 4 per-lane partial dot products d[0..3] over the 16 lanes of a
+// group, returned to every lane: a reduce-scatter (xor 8, 4, 2, 1: each lane
+// ends holding the total of head 2*b3 + b2) and an all-gather (xor 4, 8, 12)
+// -- 8 cross-lane moves instead of 16.
+__device__ __forceinline__ void group_sum4(float (&d)[4], uint32_t part16) {
+    const bool b3 = (part16 & 8u) != 0, b2 = (part16 & 4u) != 0;
+    float keep0 = b3 ? d[2] : d[0], keep1 = b3 ? d[3] : d[1];
+    const float send0 = b3 ? d[0] : d[2], send1 = b3 ? d[1] : d[3];
+    keep0 += __shfl_xor(send0, 8, 64);
+    keep1 += __shfl_xor(send1, 8, 64);
+    float t = b2 ? keep1 : keep0;
+    t += __shfl_xor(b2 ? keep0 : keep1, 4, 64);
+    t += __shfl_xor(t, 2, 64);
+    t += __shfl_xor(t, 1, 64);
+    // lane holds head 2*b3 + b2; gather the other three
+    const float x4 = __shfl_xor(t, 4, 64);   // head 2*b3 + !b2
+    const float x8 = __shfl_xor(t, 8, 64);   // head 2*!b3 + b2
+    const float x12 = __shfl_xor(t, 12, 64); // head 2*!b3 + !b2
+    const float same_b3_lo = b2 ? x4 : t, same_b3_hi = b2 ? t : x4;
+    const float other_b3_lo = b2 ? x12 : x8, other_b3_hi = b2 ? x8 : x12;
+    d[0] = b3 ? other_b3_lo : same_b3_lo;
+    d[1] = b3 ? other_b3_hi : same_b3_hi;
+    d[2] = b3 ? same_b3_lo : other_b3_lo;
+    d[3] = b3 ? same_b3_hi : other_b3_hi;
+}
+
+// One pass over the selected rows: every (id, g) row's K and V halves are
+// requested together (same 4 KiB pool row), 16 lanes per row with 8 channels
+// each.  Each 16-lane group keeps an online softmax state (m, l, o) per query
+// head over its rows, rescaled once per batch of kBatch rows; the groups'
+// states are merged at the end (wave shuffles, then LDS across waves).
 template <bool kRows>
 __global__ void __launch_bounds__(kThreads)
 attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ pool,
                     uint32_t row_bytes, const int32_t* __restrict__ rows, uint32_t pool_rows,
                     const uint32_t* __restrict__ member, uint32_t n, uint32_t chunks,
                     float* __restrict__ part) {
+    constexpr uint32_t kBatch = 4;  // rows in flight per 16-lane group (K + V)
     __shared__ uint32_t sel_id[kChunk];
     __shared__ uint32_t sel_mask[kChunk];
-    __shared__ float4 sc[kChunk];          // scores, then probabilities
     __shared__ uint32_t wave_tot[4];
-    __shared__ float red[4][4];
-    __shared__ float osum[4][4][128];      // [wave][head][channel]
+    __shared__ float wm[4][4], wl[4][4];    // [wave][head] merged m, l
+    __shared__ float osum[4][4][128];       // [wave][head][channel]
 
     const uint32_t chunk = blockIdx.x, g = blockIdx.y;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -90,30 +123,41 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
     if (m1) { sel_id[pos] = id0 + 1; sel_mask[pos] = m1; }
     __syncthreads();
 
-    // ---- pass 1: scores ------------------------------------------------------
-    const uint32_t grp = lane >> 4, part16 = lane & 15u;
+    // ---- one pass: scores, online softmax, p * V -----------------------------
+    const uint32_t grp = tid >> 4, part16 = lane & 15u;  // 16 groups per workgroup
     float qr[4][8];
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j)
 #pragma unroll
         for (uint32_t e = 0; e < 8; ++e) qr[j][e] = q[(4 * g + j) * 128 + part16 * 8 + e];
-    const uint32_t koff = g * 256 + part16 * 16;
-    constexpr uint32_t kBatch = 8;  // K rows in flight per lane group
-    for (uint32_t e0 = wave * 4 + grp; e0 < total; e0 += 16 * kBatch) {
-        uint4 kw[kBatch];
+    const uint32_t koff = g * 256 + part16 * 16, voff = 2048 + koff;
+    float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float o[4][8];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j)
+#pragma unroll
+        for (uint32_t c = 0; c < 8; ++c) o[j][c] = 0.0f;
+
+    for (uint32_t e0 = grp; e0 < total; e0 += 16 * kBatch) {
+        uint4 kw[kBatch], vw[kBatch];
 #pragma unroll
         for (uint32_t u = 0; u < kBatch; ++u) {
             const uint32_t e = e0 + 16 * u;
+            kw[u] = vw[u] = make_uint4(0u, 0u, 0u, 0u);
             if (e < total) {
                 const uint32_t id = sel_id[e];
                 const size_t r = kRows ? static_cast<size_t>(rows[id]) : id;
-                kw[u] = *reinterpret_cast<const uint4*>(pool + r * row_bytes + koff);
+                const uint8_t* row = pool + r * row_bytes;
+                kw[u] = *reinterpret_cast<const uint4*>(row + koff);
+                vw[u] = *reinterpret_cast<const uint4*>(row + voff);
             }
         }
+        float s[kBatch][4];
+        float bm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
         for (uint32_t u = 0; u < kBatch; ++u) {
             const uint32_t e = e0 + 16 * u;
-            if (e >= total) break;  // uniform across the 16 lanes of the group
             float kf[8];
             unpack8(kw[u], kf);
             float d[4];
@@ -124,110 +168,86 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
                 for (uint32_t c = 0; c < 8; ++c) acc = __builtin_fmaf(qr[j][c], kf[c], acc);
                 d[j] = acc;
             }
+            group_sum4(d, part16);
+            const uint32_t mk = e < total ? sel_mask[e] : 0u;
 #pragma unroll
-            for (uint32_t off = 8; off > 0; off >>= 1)
-#pragma unroll
-                for (uint32_t j = 0; j < 4; ++j) d[j] += __shfl_xor(d[j], off, 64);
-            if (part16 == 0) {
-                const uint32_t mk = sel_mask[e];
-                sc[e] = make_float4((mk & 1u) ? d[0] * kScale : -INFINITY,
-                                    (mk & 2u) ? d[1] * kScale : -INFINITY,
-                                    (mk & 4u) ? d[2] * kScale : -INFINITY,
-                                    (mk & 8u) ? d[3] * kScale : -INFINITY);
-            }
-        }
-    }
-    __syncthreads();
-
-    // ---- chunk max, probabilities, sum -------------------------------------
-    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    for (uint32_t e = tid; e < total; e += kThreads) {
-        const float4 s = sc[e];
-        mx[0] = fmaxf(mx[0], s.x); mx[1] = fmaxf(mx[1], s.y);
-        mx[2] = fmaxf(mx[2], s.z); mx[3] = fmaxf(mx[3], s.w);
-    }
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-        mx[j] = wave_max_f32(mx[j]);
-        if (lane == 0) red[wave][j] = mx[j];
-    }
-    __syncthreads();
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j)
-        mx[j] = fmaxf(fmaxf(red[0][j], red[1][j]), fmaxf(red[2][j], red[3][j]));
-    __syncthreads();
-    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t e = tid; e < total; e += kThreads) {
-        const float4 s = sc[e];
-        const float p0 = s.x == -INFINITY ? 0.0f : __expf(s.x - mx[0]);
-        const float p1 = s.y == -INFINITY ? 0.0f : __expf(s.y - mx[1]);
-        const float p2 = s.z == -INFINITY ? 0.0f : __expf(s.z - mx[2]);
-        const float p3 = s.w == -INFINITY ? 0.0f : __expf(s.w - mx[3]);
-        sc[e] = make_float4(p0, p1, p2, p3);
-        sum[0] += p0; sum[1] += p1; sum[2] += p2; sum[3] += p3;
-    }
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-        sum[j] = wave_sum_f32(sum[j]);
-        if (lane == 0) red[wave][j] = sum[j];
-    }
-    __syncthreads();
-
-    // ---- pass 2: o = sum p * V ---------------------------------------------
-    float o[4][8];
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j)
-#pragma unroll
-        for (uint32_t c = 0; c < 8; ++c) o[j][c] = 0.0f;
-    const uint32_t voff = 2048 + g * 256 + part16 * 16;
-    for (uint32_t e0 = wave * 4 + grp; e0 < total; e0 += 16 * kBatch) {
-        uint4 vw[kBatch];
-#pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u) {
-            const uint32_t e = e0 + 16 * u;
-            if (e < total) {
-                const uint32_t id = sel_id[e];
-                const size_t r = kRows ? static_cast<size_t>(rows[id]) : id;
-                vw[u] = *reinterpret_cast<const uint4*>(pool + r * row_bytes + voff);
+            for (uint32_t j = 0; j < 4; ++j) {
+                s[u][j] = ((mk >> j) & 1u) ? d[j] * kScale : -INFINITY;
+                bm[j] = fmaxf(bm[j], s[u][j]);
             }
         }
 #pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            const float mn = fmaxf(m[j], bm[j]);
+            if (mn == -INFINITY) continue;  // nothing selected for head j so far
+            const float scale = m[j] == -INFINITY ? 0.0f : __expf(m[j] - mn);
+            l[j] *= scale;
+#pragma unroll
+            for (uint32_t c = 0; c < 8; ++c) o[j][c] *= scale;
+            m[j] = mn;
+        }
+#pragma unroll
         for (uint32_t u = 0; u < kBatch; ++u) {
-            const uint32_t e = e0 + 16 * u;
-            if (e >= total) break;
             float vf[8];
             unpack8(vw[u], vf);
-            const float4 p = sc[e];
-            const float pj[4] = {p.x, p.y, p.z, p.w};
 #pragma unroll
-            for (uint32_t j = 0; j < 4; ++j)
+            for (uint32_t j = 0; j < 4; ++j) {
+                const float p = s[u][j] == -INFINITY ? 0.0f : __expf(s[u][j] - m[j]);
+                l[j] += p;
 #pragma unroll
-                for (uint32_t c = 0; c < 8; ++c) o[j][c] = __builtin_fmaf(pj[j], vf[c], o[j][c]);
+                for (uint32_t c = 0; c < 8; ++c) o[j][c] = __builtin_fmaf(p, vf[c], o[j][c]);
+            }
         }
     }
-    // reduce the 4 id-groups of the wave (lanes l, l+16, l+32, l+48)
+
+    // ---- merge the 4 groups of each wave (lanes l, l^16, l^32, l^48) ---------
 #pragma unroll
-    for (uint32_t j = 0; j < 4; ++j)
+    for (uint32_t off = 16; off < 64; off <<= 1) {
 #pragma unroll
-        for (uint32_t c = 0; c < 8; ++c) {
-            o[j][c] += __shfl_xor(o[j][c], 16, 64);
-            o[j][c] += __shfl_xor(o[j][c], 32, 64);
+        for (uint32_t j = 0; j < 4; ++j) {
+            const float mo = __shfl_xor(m[j], off, 64), lo = __shfl_xor(l[j], off, 64);
+            const float mn = fmaxf(m[j], mo);
+            const float a = (m[j] == -INFINITY) ? 0.0f : __expf(m[j] - mn);
+            const float b = (mo == -INFINITY) ? 0.0f : __expf(mo - mn);
+            l[j] = l[j] * a + lo * b;
+#pragma unroll
+            for (uint32_t c = 0; c < 8; ++c) {
+                const float oo = __shfl_xor(o[j][c], off, 64);
+                o[j][c] = o[j][c] * a + oo * b;
+            }
+            m[j] = mn;
         }
-    if (grp == 0) {
+    }
+    if (lane < 16) {
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j)
+        for (uint32_t j = 0; j < 4; ++j) {
 #pragma unroll
             for (uint32_t c = 0; c < 8; ++c) osum[wave][j][part16 * 8 + c] = o[j][c];
+            if (lane == 0) {
+                wm[wave][j] = m[j];
+                wl[wave][j] = l[j];
+            }
+        }
     }
     __syncthreads();
+
+    // ---- merge the 4 waves into this chunk's (m, l, o) record per head -------
     float* rec = part + (static_cast<size_t>(g) * chunks + chunk) * 4 * kRecord;
     for (uint32_t i = tid; i < 4 * 128; i += kThreads) {
         const uint32_t j = i >> 7, c = i & 127u;
-        rec[j * kRecord + 2 + c] = osum[0][j][c] + osum[1][j][c] + osum[2][j][c] + osum[3][j][c];
-    }
-    if (tid < 4) {
-        rec[tid * kRecord + 0] = mx[tid];
-        rec[tid * kRecord + 1] = red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid];
+        const float mt = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
+        float acc = 0.0f, lsum = 0.0f;
+#pragma unroll
+        for (uint32_t w = 0; w < 4; ++w) {
+            const float a = (wm[w][j] == -INFINITY) ? 0.0f : __expf(wm[w][j] - mt);
+            acc = __builtin_fmaf(osum[w][j][c], a, acc);
+            lsum = __builtin_fmaf(wl[w][j], a, lsum);
+        }
+        rec[j * kRecord + 2 + c] = acc;
+        if (c == 0) {
+            rec[j * kRecord + 0] = mt;
+            rec[j * kRecord + 1] = lsum;
+        }
     }
 }
 
@@ -261,9 +281,18 @@ attn_combine_kernel(const float* __restrict__ part, uint32_t chunks, float* __re
     for (uint32_t w = 0; w < 8; ++w) L += red[w];
     const uint32_t c = tid & 127u, quarter = tid >> 7;
     float a = 0.0f;
-    for (uint32_t i = quarter; i < chunks; i += 4) {
-        const float wi = weight[i];
-        if (wi != 0.0f) a = __builtin_fmaf(recs[i * 4 * kRecord + 2 + c], wi, a);
+    // each thread's records are requested together (<= 32 of them)
+    constexpr uint32_t kLoads = kMaxChunks / 4;
+    float v[kLoads];
+#pragma unroll
+    for (uint32_t u = 0; u < kLoads; ++u) {
+        const uint32_t i = quarter + 4 * u;
+        v[u] = i < chunks ? recs[i * 4 * kRecord + 2 + c] : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kLoads; ++u) {
+        const uint32_t i = quarter + 4 * u;
+        if (i < chunks && weight[i] != 0.0f) a = __builtin_fmaf(v[u], weight[i], a);
     }
     acc4[quarter][c] = a;
     __syncthreads();

@@ -696,11 +696,13 @@ __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
 }
 
 // ---- 4. rank ----------------------------------------------------------------
-// Keys of four slices searched in lockstep: for each of the lists
-// key_at(q, .) of lengths len[q] (sorted by descending key), the number of
-// keys >= v (strict[q]: > v).  Fixed-step and branchless.
-template <typename KeyAt>
-__device__ __forceinline__ uint32_t count_before4(KeyAt key_at, const uint32_t (&len)[4],
+// Number of keys >= v (strict: > v) in each of four lists sorted by
+// descending key, searched in lockstep: fixed steps, and every probe reads
+// an in-bounds element (clamped) so no step branches; empty lists read
+// element 0 of the staging area and never advance.
+__device__ __forceinline__ uint32_t count_before4(const uint16_t* staged,
+                                                  const uint32_t (&off)[4],
+                                                  const uint32_t (&len)[4],
                                                   const bool (&strict)[4], uint32_t v) {
     uint32_t pos[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -709,7 +711,8 @@ __device__ __forceinline__ uint32_t count_before4(KeyAt key_at, const uint32_t (
 #pragma unroll
         for (uint32_t q = 0; q < 4; ++q) {
             const uint32_t cand = pos[q] + step;
-            x[q] = cand <= len[q] ? key_at(q, cand - 1) : 0u;
+            const uint32_t at = len[q] ? off[q] + (cand <= len[q] ? cand : len[q]) - 1 : 0u;
+            x[q] = staged[at];
         }
 #pragma unroll
         for (uint32_t q = 0; q < 4; ++q) {
@@ -720,9 +723,33 @@ __device__ __forceinline__ uint32_t count_before4(KeyAt key_at, const uint32_t (
     }
     return pos[0] + pos[1] + pos[2] + pos[3];
 }
+// The same over one slice's sorted composites in global memory (heads whose
+// selection exceeds the LDS staging area).
+__device__ uint32_t count_before_global(const uint32_t* list, uint32_t m, uint32_t v, bool strict) {
+    uint32_t lo = 0, hi = m;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        const uint32_t x = 0xffffu - (list[mid] >> 16);
+        if (strict ? x > v : x >= v) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
 
+// Counting rank over a key range of at most kRankRange values: for a selected
+// key v of slice s at rank r of the slice's sorted list,
+//   position = #{head keys > v} + #{keys == v in slices before s}
+//            + (r - first rank of v in slice s)
+// (equal keys order by id, i.e. by slice, then by rank within the slice).
+constexpr uint32_t kRankRange = 8192;
+
+template <bool kStaged>
 __global__ void __launch_bounds__(kThreads) rank_kernel(SelectArgs a) {
-    __shared__ uint16_t staged[kRankCap];
+    __shared__ uint16_t staged[kStaged ? kRankCap : 1];
+    __shared__ uint8_t owner[kStaged ? kRankCap : 1];  // slice of each staged key
+    __shared__ uint32_t above[kStaged ? kRankRange : 1];   // head keys > v (after the scan)
+    __shared__ uint32_t earlier[kStaged ? kRankRange : 1]; // keys == v in slices before s
+    __shared__ uint32_t tmp[kWaves];
     __shared__ uint32_t s_m[kMaxSlices], s_off[kMaxSlices];
     const uint32_t tid = threadIdx.x;
     const uint32_t g = blockIdx.x, S = a.S, h = g / S, s = g - h * S;
@@ -751,57 +778,122 @@ __global__ void __launch_bounds__(kThreads) rank_kernel(SelectArgs a) {
         }
     }
     __syncthreads();
-    const bool in_lds = k <= kRankCap;  // the head's k keys fit the staging area
-    if (in_lds) {
-        // staged[off_j + r] = key of slice j's r-th composite, 8 loads in flight
+    if constexpr (kStaged) {
+        // owner table, then every slice's keys in one round of loads
+        for (uint32_t j = 0; j < S; ++j)
+            for (uint32_t r = tid; r < s_m[j]; r += kThreads) owner[s_off[j] + r] = static_cast<uint8_t>(j);
+        __syncthreads();
         for (uint32_t first = 0; first < k; first += 8 * kThreads) {
-            uint32_t v[8], at[8];
+            uint32_t v[8];
 #pragma unroll
             for (uint32_t u = 0; u < 8; ++u) {
                 const uint32_t idx = first + tid + u * kThreads;
-                // last slice starting at or before idx (empty slices share
-                // their successor's offset and are skipped)
-                uint32_t j = 0;
-#pragma unroll
-                for (uint32_t step = kMaxSlices / 2; step >= 1; step >>= 1)
-                    j = (j + step < S && s_off[j + step] <= idx) ? j + step : j;
-                at[u] = idx;
-                v[u] = idx < k ? lists[static_cast<size_t>(j) * a.cap + (idx - s_off[j])] : 0u;
+                v[u] = 0;
+                if (idx < k) {
+                    const uint32_t j = owner[idx];
+                    v[u] = lists[static_cast<size_t>(j) * a.cap + (idx - s_off[j])];
+                }
             }
 #pragma unroll
-            for (uint32_t u = 0; u < 8; ++u)
-                if (at[u] < k) staged[at[u]] = static_cast<uint16_t>(0xffffu - (v[u] >> 16));
+            for (uint32_t u = 0; u < 8; ++u) {
+                const uint32_t idx = first + tid + u * kThreads;
+                if (idx < k) staged[idx] = static_cast<uint16_t>(0xffffu - (v[u] >> 16));
+            }
         }
         __syncthreads();
     }
     uint32_t* out = a.ids + static_cast<size_t>(h) * a.ids_stride;
     const uint32_t m_self = s_m[s];
+    if constexpr (kStaged) {
+        // key range of the head's selection: [lo_key, lo_key + range)
+        uint32_t kmin = 0xffffu, kmax = 0u;
+        for (uint32_t i = tid; i < k; i += kThreads) {
+            kmin = min(kmin, uint32_t(staged[i]));
+            kmax = max(kmax, uint32_t(staged[i]));
+        }
+        kmax = block_max(kmax, tmp);
+        kmin = 0xffffu - block_max(0xffffu - kmin, tmp);
+        const uint32_t range = kmax - kmin + 1;
+        if (range <= kRankRange) {
+            for (uint32_t i = tid; i < range; i += kThreads) above[i] = earlier[i] = 0;
+            __syncthreads();
+            const uint32_t own_begin = s_off[s];
+            for (uint32_t i = tid; i < k; i += kThreads) {
+                const uint32_t v = staged[i] - kmin;
+                atomicAdd(&above[v], 1u);
+                if (i < own_begin) atomicAdd(&earlier[v], 1u);
+            }
+            __syncthreads();
+            // exclusive suffix sums: above[v] = #{keys > v}; each thread owns a
+            // contiguous run of bins, scanned from the top
+            const uint32_t per = (range + kThreads - 1) / kThreads;
+            const uint32_t first = (kThreads - 1 - tid) * per;  // thread 0 owns the top bins
+            uint32_t sum = 0;
+            for (uint32_t i = 0; i < per; ++i) {
+                const uint32_t b = first + i;
+                if (b < range) sum += above[b];
+            }
+            const uint32_t higher = block_exclusive_scan(sum, tmp);  // bins above this run
+            uint32_t run = higher + sum;
+            for (uint32_t i = 0; i < per; ++i) {
+                const uint32_t b = first + i;  // ascending within the run
+                if (b < range) {
+                    const uint32_t c = above[b];
+                    run -= c;
+                    above[b] = run;
+                }
+            }
+            __syncthreads();
+            const uint16_t* own = staged + own_begin;  // this slice's keys, sorted desc
+            for (uint32_t u = 0; u < kRun; ++u) {
+                const uint32_t r = tid + u * kThreads;
+                if (r >= m_self) break;
+                const uint32_t x = mine[u];
+                const uint32_t key = 0xffffu - (x >> 16);
+                // first rank of this key in the own list (equal keys are adjacent)
+                uint32_t lo = r, hi = r;
+                while (lo > 0 && own[lo - 1] == key && hi - lo < 32) --lo;
+                if (lo > 0 && own[lo - 1] == key) {  // long run: binary search its start
+                    uint32_t a0 = 0, a1 = lo;
+                    while (a0 < a1) {
+                        const uint32_t mid = (a0 + a1) >> 1;
+                        if (own[mid] > key) a0 = mid + 1;
+                        else a1 = mid;
+                    }
+                    lo = a0;
+                }
+                const uint32_t v = key - kmin;
+                const uint32_t at = above[v] + earlier[v] + (r - lo);
+                if (at < k) out[at] = s * kSlice + (x & 0xffffu);
+            }
+            return;
+        }
+    }
     for (uint32_t u = 0; u < kRun; ++u) {
         const uint32_t r = tid + u * kThreads;
         if (r >= m_self) break;
         const uint32_t x = mine[u];
         const uint32_t key = 0xffffu - (x >> 16);
         uint32_t at = r;
-        for (uint32_t j0 = 0; j0 < S; j0 += 4) {
-            uint32_t len[4], off[4];
-            bool strict[4];
+        if constexpr (kStaged) {
+            for (uint32_t j0 = 0; j0 < S; j0 += 4) {
+                uint32_t len[4], off[4];
+                bool strict[4];
 #pragma unroll
-            for (uint32_t q = 0; q < 4; ++q) {
-                const uint32_t j = j0 + q;
-                const bool other = j < S && j != s;
-                len[q] = other ? s_m[j] : 0u;
-                off[q] = other ? s_off[j] : 0u;
-                strict[q] = j > s;  // equal keys of later slices have larger ids
+                for (uint32_t q = 0; q < 4; ++q) {
+                    const uint32_t j = j0 + q;
+                    const bool other = j < S && j != s;
+                    len[q] = other ? s_m[j] : 0u;
+                    off[q] = other ? s_off[j] : 0u;
+                    strict[q] = j > s;  // equal keys of later slices have larger ids
+                }
+                at += count_before4(staged, off, len, strict, key);
             }
-            if (in_lds)
-                at += count_before4([&](uint32_t q, uint32_t i) { return uint32_t(staged[off[q] + i]); },
-                                    len, strict, key);
-            else
-                at += count_before4(
-                    [&](uint32_t q, uint32_t i) {
-                        return 0xffffu - (lists[static_cast<size_t>(j0 + q) * a.cap + i] >> 16);
-                    },
-                    len, strict, key);
+        } else {
+            for (uint32_t j = 0; j < S; ++j)
+                if (j != s)
+                    at += count_before_global(lists + static_cast<size_t>(j) * a.cap, s_m[j], key,
+                                              j > s);
         }
         if (at < k) out[at] = s * kSlice + (x & 0xffffu);
     }
@@ -869,7 +961,11 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
         hipLaunchKernelGGL(slice_select_kernel<false>, grid, block, 0, stream, args);
     } else {
         hipLaunchKernelGGL(slice_select_kernel<true>, grid, block, 0, stream, args);
-        hipLaunchKernelGGL(rank_kernel, grid, block, 0, stream, args);
+        // k <= kmax: the staged variant serves every head whose selection fits LDS
+        if (kmax <= kRankCap)
+            hipLaunchKernelGGL(rank_kernel<true>, grid, block, 0, stream, args);
+        else
+            hipLaunchKernelGGL(rank_kernel<false>, grid, block, 0, stream, args);
     }
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "select launch");
