@@ -36,9 +36,9 @@
 //             order (HS_SELECT_ID_ORDER) or, for rank order, its selection
 //             stable-sorted by key; boundary ties are counted into the status
 //             with device-scope atomics;
-//  4. rank:   (rank order only) each id lands at its rank in its slice plus
-//             the number of keys of every other slice of the head ahead of
-//             it (binary search; ties order by slice, i.e. by id).
+//  4. rank:   (rank order only) each id lands at (#head keys above its key)
+//             + (#equal keys in earlier slices) + (its rank among equal keys
+//             of its slice), from histograms over the selected key range.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -68,7 +68,8 @@ struct SelectPlanDev {
 struct SelectPlan {
     uint32_t S = 0, groups = 0, partials = 0, cap = 0;
     size_t off_plan = 0, off_partial = 0, off_count = 0, off_bad = 0, off_hi = 0, off_lo = 0,
-           off_sort = 0, off_m = 0, off_tie = 0, total = 0;
+           off_sort = 0, off_keys = 0, off_m = 0, off_tie = 0, total = 0;
+    uint32_t kcap = 0;  // per-head capacity of the rank-sorted lists (>= k)
 };
 
 SelectPlan plan_select(uint32_t heads, uint32_t n, uint32_t kmax) {
@@ -89,8 +90,10 @@ SelectPlan plan_select(uint32_t heads, uint32_t n, uint32_t kmax) {
     p.off_bad = take(sizeof(uint32_t) * p.groups);
     p.off_hi = take(sizeof(uint32_t) * 256 * p.groups);
     p.off_lo = take(sizeof(uint32_t) * 256 * p.groups);
-    p.off_sort = take(sizeof(uint32_t) * size_t(p.groups) * p.cap);
-    p.off_m = take(sizeof(uint32_t) * p.groups);
+    p.kcap = std::max<uint32_t>(1u, kmax);
+    p.off_sort = take(sizeof(uint32_t) * size_t(heads) * p.kcap);
+    p.off_keys = take(sizeof(uint16_t) * size_t(heads) * p.kcap);
+    p.off_m = take(sizeof(uint32_t) * 4 * p.groups);
     p.off_tie = take(sizeof(unsigned long long) * heads);
     p.total = at;
     return p;
@@ -108,8 +111,10 @@ struct SelectArgs {
     uint32_t* g_bad;    // [groups] slice has a nonfinite score
     uint32_t* g_hi;     // [groups][256] high-byte histograms
     uint32_t* g_lo;     // [groups][256] low-byte histograms of the k-th key's bucket
-    uint32_t* g_sort;   // [groups][cap] rank-sorted composites of each slice
-    uint32_t* g_m;      // [groups] selected per slice
+    uint32_t* g_sort;   // [heads][kcap] each slice's sorted composites at its id-order offset
+    uint16_t* g_keys;   // [heads][kcap] the same lists' keys
+    uint32_t* g_m;      // [groups][4] selected count, id-order offset, max key, K*
+    uint32_t kcap;
     unsigned long long* g_tie;  // [heads] bits around a signed-zero cut
     uint32_t cap;
     uint32_t* ids;
@@ -315,6 +320,11 @@ __global__ void __launch_bounds__(kThreads) count_kernel(SelectArgs a) {
         a.g_count[g] = count;
         a.g_bad[g] = bad;
     }
+    // the tie records the next launch accumulates into start from zero here
+    if (g == 0) {
+        if (tid == 0) a.status->boundary_tied_heads = 0;
+        if (tid < a.heads) a.g_tie[tid] = 0ull;
+    }
 }
 
 // ---- 2. plan ----------------------------------------------------------------
@@ -420,17 +430,13 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
                 a.plan->k = code == HS_OK ? k : 0u;
                 a.status->code = code;
                 a.status->k = code == HS_OK ? k : 0u;
-                a.status->boundary_tied_heads = 0;
                 a.status->head0_max_key = best;
             }
         }
         // high byte of this head's k-th key
         if (code == HS_OK && k > 0) find_bucket(hist, k, &sh[kBucket], &sh[kAbove]);
     }
-    if (g == 0 && tid < a.heads) {
-        if (a.counts_out) a.counts_out[tid] = head_count[tid];
-        a.g_tie[tid] = 0ull;
-    }
+    if (g == 0 && tid < a.heads && a.counts_out) a.counts_out[tid] = head_count[tid];
     __syncthreads();
     const int code = static_cast<int>(sh[kCode]);
     const uint32_t k = sh[kK];
@@ -519,6 +525,66 @@ __device__ void sort_composites(uint32_t* A, uint32_t* B, uint32_t m, uint32_t (
     }
 }
 
+// Counting sort of m composites ((0xffff - key) << 16 | id in slice) in A,
+// using B, when the keys span at most kSortRange values from kmin and no key
+// occurs more than kGroupCap times: key histogram, exclusive suffix scan
+// (larger keys first), scatter into the key groups, then each group placed
+// in id order by counting its smaller ids.  Returns false, with A untouched,
+// when the limits do not hold.  start/cursor: kSortRange words of LDS each.
+constexpr uint32_t kSortRange = 8192, kGroupCap = 64;
+__device__ bool sort_counting(uint32_t* A, uint32_t* B, uint32_t m, uint32_t kmin, uint32_t* start,
+                              uint32_t* cursor, uint32_t* tmp) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t kmax = 0;
+    for (uint32_t q = tid; q < m; q += kThreads) kmax = max(kmax, 0xffffu - (A[q] >> 16));
+    kmax = block_max(kmax, tmp);
+    if (m == 0) return true;
+    if (kmax < kmin || kmax - kmin >= kSortRange) return false;
+    const uint32_t range = kmax - kmin + 1;
+    for (uint32_t i = tid; i < range; i += kThreads) start[i] = 0;
+    __syncthreads();
+    for (uint32_t q = tid; q < m; q += kThreads) atomicAdd(&start[0xffffu - (A[q] >> 16) - kmin], 1u);
+    __syncthreads();
+    // each thread owns a run of bins, thread 0 the top ones
+    const uint32_t per = (range + kThreads - 1) / kThreads;
+    const uint32_t first = (kThreads - 1 - tid) * per;
+    uint32_t sum = 0, big = 0;
+    for (uint32_t i = 0; i < per; ++i) {
+        const uint32_t b = first + i;
+        if (b < range) {
+            sum += start[b];
+            big = max(big, start[b]);
+        }
+    }
+    big = block_max(big, tmp);
+    if (big > kGroupCap) return false;
+    uint32_t run = block_exclusive_scan(sum, tmp) + sum;
+    for (uint32_t i = 0; i < per; ++i) {
+        const uint32_t b = first + i;
+        if (b < range) {
+            run -= start[b];
+            start[b] = run;
+            cursor[b] = run;
+        }
+    }
+    __syncthreads();
+    for (uint32_t q = tid; q < m; q += kThreads) {
+        const uint32_t e = A[q];
+        B[atomicAdd(&cursor[0xffffu - (e >> 16) - kmin], 1u)] = e;
+    }
+    __syncthreads();
+    for (uint32_t q = tid; q < m; q += kThreads) {
+        const uint32_t e = B[q];
+        const uint32_t b = 0xffffu - (e >> 16) - kmin;
+        const uint32_t gs = start[b], gc = cursor[b] - gs;
+        uint32_t r = 0;
+        for (uint32_t i = 0; i < gc; ++i) r += (B[gs + i] & 0xffffu) < (e & 0xffffu) ? 1u : 0u;
+        A[gs + r] = e;
+    }
+    __syncthreads();
+    return true;
+}
+
 // Raw bits of the ties ranked t_need-1 (bit 62 + bits 0..15) and t_need
 // (bit 63 + bits 16..31) at a signed-zero cut; whichever record arrives second
 // compares them and counts the head as tied when the bits match.
@@ -540,7 +606,8 @@ template <bool kRankOrder>
 __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
     __shared__ uint32_t whist[kRankOrder ? kWaves : 1][256];
     __shared__ uint32_t hist[2][256];
-    __shared__ uint32_t slice_hist[2][kMaxSlices][256];
+    __shared__ uint32_t slice_hist[2][kMaxSlices][256];  // later: the counting sort's tables
+    static_assert(2 * kMaxSlices * 256 >= 2 * kSortRange, "sort tables fit the slice histograms");
     __shared__ uint32_t sort_lds[kRankOrder ? 2 * kSlice : 1];
     __shared__ uint32_t tmp[kWaves];
     __shared__ uint32_t sh[8];
@@ -612,23 +679,35 @@ __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        uint32_t ties_before = 0, sel_before = 0;
-        for (uint32_t j = 0; j <= s; ++j) {
-            const uint32_t left = t_need > ties_before ? t_need - ties_before : 0u;
-            const uint32_t taken = std::min(s_ties[j], left);
-            if (j == s) {
-                sh[kTieBase] = ties_before;
-                sh[kTaken] = taken;
-                sh[kSelBase] = sel_before;
-                sh[kSel] = s_above[j] + taken;
-            }
-            ties_before += s_ties[j];
-            sel_before += s_above[j] + taken;
+    if (wave == 0) {
+        // lane j = slice j: ties before it, ties it takes, selected before it
+        const uint32_t ties = lane < S ? s_ties[lane] : 0u;
+        uint32_t ties_before = ties;
+#pragma unroll
+        for (uint32_t off = 1; off < kMaxSlices; off <<= 1) {
+            const uint32_t y = __shfl_up(ties_before, off, 64);
+            if (lane >= off) ties_before += y;
+        }
+        ties_before -= ties;
+        const uint32_t left = t_need > ties_before ? t_need - ties_before : 0u;
+        const uint32_t taken = std::min(ties, left);
+        const uint32_t sel = (lane < S ? s_above[lane] : 0u) + taken;
+        uint32_t sel_before = sel;
+#pragma unroll
+        for (uint32_t off = 1; off < kMaxSlices; off <<= 1) {
+            const uint32_t y = __shfl_up(sel_before, off, 64);
+            if (lane >= off) sel_before += y;
+        }
+        sel_before -= sel;
+        if (lane == s) {
+            sh[kTieBase] = ties_before;
+            sh[kTaken] = taken;
+            sh[kSelBase] = sel_before;
+            sh[kSel] = sel;
         }
         // boundary tie (gqa_policy.cpp:65): the (k+1)-th element exists with
         // equal bits; equal keys mean equal bits except -0 / +0 (key 0x8000).
-        if (s == 0 && k < n && c_above + c_equal > k && kstar != 0x8000u)
+        if (lane == 0 && s == 0 && k < n && c_above + c_equal > k && kstar != 0x8000u)
             atomicAdd(&a.status->boundary_tied_heads, 1u);
     }
     __syncthreads();
@@ -688,10 +767,25 @@ __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
     if constexpr (kRankOrder) {
         const uint32_t m = std::min(sh[kSel], a.cap);
         __syncthreads();
-        sort_composites(sort_lds, sort_lds + kSlice, m, whist, tmp);
-        uint32_t* dst = a.g_sort + static_cast<size_t>(g) * a.cap;
-        for (uint32_t r = tid; r < m; r += kThreads) dst[r] = sort_lds[r];
-        if (tid == 0) a.g_m[g] = m;
+        // the slice histograms are spent: their 2 x kSortRange words serve the sort
+        uint32_t* start = &slice_hist[0][0][0];
+        if (!sort_counting(sort_lds, sort_lds + kSlice, m, kstar, start, start + kSortRange, tmp))
+            sort_composites(sort_lds, sort_lds + kSlice, m, whist, tmp);
+        // this slice's run of the head's lists: [sel_base, sel_base + m)
+        uint32_t* dst = a.g_sort + static_cast<size_t>(h) * a.kcap;
+        uint16_t* kdst = a.g_keys + static_cast<size_t>(h) * a.kcap;
+        for (uint32_t r = tid; r < m && sel_base + r < a.kcap; r += kThreads) {
+            const uint32_t x = sort_lds[r];
+            dst[sel_base + r] = x;
+            kdst[sel_base + r] = static_cast<uint16_t>(0xffffu - (x >> 16));
+        }
+        if (tid == 0) {
+            uint32_t* info = a.g_m + 4 * static_cast<size_t>(g);
+            info[0] = m;
+            info[1] = sel_base;
+            info[2] = m ? 0xffffu - (sort_lds[0] >> 16) : 0u;  // largest key of the slice
+            info[3] = kstar;
+        }
     }
 }
 
@@ -746,73 +840,56 @@ constexpr uint32_t kRankRange = 8192;
 template <bool kStaged>
 __global__ void __launch_bounds__(kThreads) rank_kernel(SelectArgs a) {
     __shared__ uint16_t staged[kStaged ? kRankCap : 1];
-    __shared__ uint8_t owner[kStaged ? kRankCap : 1];  // slice of each staged key
     __shared__ uint32_t above[kStaged ? kRankRange : 1];   // head keys > v (after the scan)
     __shared__ uint32_t earlier[kStaged ? kRankRange : 1]; // keys == v in slices before s
     __shared__ uint32_t tmp[kWaves];
-    __shared__ uint32_t s_m[kMaxSlices], s_off[kMaxSlices];
+    __shared__ uint32_t s_m[kMaxSlices], s_off[kMaxSlices], s_top[kMaxSlices];
+    __shared__ uint32_t s_kstar;
     const uint32_t tid = threadIdx.x;
     const uint32_t g = blockIdx.x, S = a.S, h = g / S, s = g - h * S;
     if (a.plan->code != HS_OK) return;
     const uint32_t k = a.plan->k;
     if (k == 0) return;
-    const uint32_t* lists = a.g_sort + static_cast<size_t>(h * S) * a.cap;
-    // this slice's sorted composites (at most 8 per thread), requested first
-    uint32_t mine[kRun];
-#pragma unroll
-    for (uint32_t u = 0; u < kRun; ++u) {
-        const uint32_t r = tid + u * kThreads;
-        mine[u] = r < a.cap ? lists[static_cast<size_t>(s) * a.cap + r] : 0u;
+    const uint32_t* lists = a.g_sort + static_cast<size_t>(h) * a.kcap;
+    const uint16_t* keys = a.g_keys + static_cast<size_t>(h) * a.kcap;
+    // slice runs (count, offset, largest key, K*), and the head's keys
+    if (tid < S) {
+        const uint32_t* info = a.g_m + 4 * static_cast<size_t>(h * S + tid);
+        s_m[tid] = info[0];
+        s_off[tid] = info[1];
+        s_top[tid] = info[2];
+        if (tid == 0) s_kstar = info[3];
     }
-    if (tid < 64) {
-        const uint32_t m = tid < S ? a.g_m[h * S + tid] : 0u;
-        uint32_t x = m;
-#pragma unroll
-        for (uint32_t off = 1; off < kMaxSlices; off <<= 1) {
-            const uint32_t y = __shfl_up(x, off, 64);
-            if (tid >= off) x += y;
-        }
-        if (tid < kMaxSlices) {
-            s_m[tid] = m;  // 0 past S
-            s_off[tid] = x - m;
-        }
-    }
-    __syncthreads();
     if constexpr (kStaged) {
-        // owner table, then every slice's keys in one round of loads
-        for (uint32_t j = 0; j < S; ++j)
-            for (uint32_t r = tid; r < s_m[j]; r += kThreads) owner[s_off[j] + r] = static_cast<uint8_t>(j);
-        __syncthreads();
         for (uint32_t first = 0; first < k; first += 8 * kThreads) {
             uint32_t v[8];
 #pragma unroll
             for (uint32_t u = 0; u < 8; ++u) {
                 const uint32_t idx = first + tid + u * kThreads;
-                v[u] = 0;
-                if (idx < k) {
-                    const uint32_t j = owner[idx];
-                    v[u] = lists[static_cast<size_t>(j) * a.cap + (idx - s_off[j])];
-                }
+                v[u] = idx < k ? keys[idx] : 0u;
             }
 #pragma unroll
             for (uint32_t u = 0; u < 8; ++u) {
                 const uint32_t idx = first + tid + u * kThreads;
-                if (idx < k) staged[idx] = static_cast<uint16_t>(0xffffu - (v[u] >> 16));
+                if (idx < k) staged[idx] = static_cast<uint16_t>(v[u]);
             }
         }
-        __syncthreads();
+    }
+    __syncthreads();
+    // this slice's sorted composites (at most 8 per thread)
+    uint32_t mine[kRun];
+#pragma unroll
+    for (uint32_t u = 0; u < kRun; ++u) {
+        const uint32_t r = tid + u * kThreads;
+        mine[u] = r < s_m[s] ? lists[s_off[s] + r] : 0u;
     }
     uint32_t* out = a.ids + static_cast<size_t>(h) * a.ids_stride;
     const uint32_t m_self = s_m[s];
     if constexpr (kStaged) {
-        // key range of the head's selection: [lo_key, lo_key + range)
-        uint32_t kmin = 0xffffu, kmax = 0u;
-        for (uint32_t i = tid; i < k; i += kThreads) {
-            kmin = min(kmin, uint32_t(staged[i]));
-            kmax = max(kmax, uint32_t(staged[i]));
-        }
-        kmax = block_max(kmax, tmp);
-        kmin = 0xffffu - block_max(0xffffu - kmin, tmp);
+        // key range of the head's selection: [K*, largest key]
+        const uint32_t kmin = s_kstar;
+        uint32_t kmax = kmin;
+        for (uint32_t j = 0; j < S; ++j) kmax = max(kmax, s_top[j]);
         const uint32_t range = kmax - kmin + 1;
         if (range <= kRankRange) {
             for (uint32_t i = tid; i < range; i += kThreads) above[i] = earlier[i] = 0;
@@ -892,8 +969,7 @@ __global__ void __launch_bounds__(kThreads) rank_kernel(SelectArgs a) {
         } else {
             for (uint32_t j = 0; j < S; ++j)
                 if (j != s)
-                    at += count_before_global(lists + static_cast<size_t>(j) * a.cap, s_m[j], key,
-                                              j > s);
+                    at += count_before_global(lists + s_off[j], s_m[j], key, j > s);
         }
         if (at < k) out[at] = s * kSlice + (x & 0xffffu);
     }
@@ -940,7 +1016,9 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
     args.g_hi = reinterpret_cast<uint32_t*>(ws + p.off_hi);
     args.g_lo = reinterpret_cast<uint32_t*>(ws + p.off_lo);
     args.g_sort = reinterpret_cast<uint32_t*>(ws + p.off_sort);
+    args.g_keys = reinterpret_cast<uint16_t*>(ws + p.off_keys);
     args.g_m = reinterpret_cast<uint32_t*>(ws + p.off_m);
+    args.kcap = p.kcap;
     args.g_tie = reinterpret_cast<unsigned long long*>(ws + p.off_tie);
     args.cap = p.cap;
     args.ids = ids;
