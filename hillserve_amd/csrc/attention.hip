@@ -8,16 +8,19 @@
 // whose mask entry is 0.  FP32 accumulation, FP32 softmax.
 //
 // Work split (flash-decoding over the token axis):
-//  * grid (chunks, 8 KV heads); a workgroup owns one KV head g and a range of
-//    512 token ids.  It ORs the 4 query heads' selection bitmaps, compacts the
-//    union in id order, and reads each selected (id, g) K row and V row
-//    exactly once for all of its query heads -> HBM bytes = sum_g |U_g|*512.
+//  * grid (chunks); a workgroup owns 128 token ids and all 8 KV heads, one
+//    wave per KV head g.  A wave ORs its 4 query heads' selection bitmaps,
+//    compacts the union in id order, and reads each selected (id, g) K row
+//    and V row exactly once for all of its query heads -> HBM bytes =
+//    sum_g |U_g|*512.  The 8 waves read the 8 heads' segments of the same
+//    4 KiB pool rows at about the same time.
 //  * one pass: 16 lanes per id, 16 B (8 channels) per lane, so every K and
 //    V access is a contiguous 256 B run; the K and V halves of a row (same
 //    4 KiB pool row) are requested together, which streams ~1.4x faster
 //    than a K pass followed by a V pass.  Scores are reduced over the 16
-//    lanes with 8 cross-lane moves, softmax is online (rescaled once per
-//    batch of rows), and p*V accumulates in registers.
+//    lanes with 4 DPP adds per head, softmax is online (rescaled once per
+//    batch of rows), and p*V accumulates in registers.  Loads run one batch
+//    ahead of their use.
 //  * the (m, l, o[128]) partials of all chunks are merged by attn_combine.
 #include <hip/hip_runtime.h>
 
@@ -30,8 +33,8 @@
 namespace hs {
 namespace {
 
-constexpr uint32_t kChunk = 512;   // token ids per workgroup
-constexpr uint32_t kThreads = 256; // 4 waves
+constexpr uint32_t kChunk = 128;   // token ids per workgroup
+constexpr uint32_t kThreads = 512; // 8 waves: one per KV head
 constexpr uint32_t kRecord = 2 + 128;
 constexpr float kScale = 0.088388347648318440550f;  // 1/sqrt(128)
 
@@ -42,89 +45,75 @@ __device__ __forceinline__ void unpack8(const uint4 w, float* f) {
     f[6] = h2f(w.w & 0xffffu); f[7] = h2f(w.w >> 16);
 }
 
-// Sum of the 4 per-lane partial dot products d[0..3] over the 16 lanes of a
-// group, returned to every lane: a reduce-scatter (xor 8, 4, 2, 1: each lane
-// ends holding the total of head 2*b3 + b2) and an all-gather (xor 4, 8, 12)
-// -- 8 cross-lane moves instead of 16.
-__device__ __forceinline__ void group_sum4(float (&d)[4], uint32_t part16) {
-    const bool b3 = (part16 & 8u) != 0, b2 = (part16 & 4u) != 0;
-    float keep0 = b3 ? d[2] : d[0], keep1 = b3 ? d[3] : d[1];
-    const float send0 = b3 ? d[0] : d[2], send1 = b3 ? d[1] : d[3];
-    keep0 += __shfl_xor(send0, 8, 64);
-    keep1 += __shfl_xor(send1, 8, 64);
-    float t = b2 ? keep1 : keep0;
-    t += __shfl_xor(b2 ? keep0 : keep1, 4, 64);
-    t += __shfl_xor(t, 2, 64);
-    t += __shfl_xor(t, 1, 64);
-    // lane holds head 2*b3 + b2; gather the other three
-    const float x4 = __shfl_xor(t, 4, 64);   // head 2*b3 + !b2
-    const float x8 = __shfl_xor(t, 8, 64);   // head 2*!b3 + b2
-    const float x12 = __shfl_xor(t, 12, 64); // head 2*!b3 + !b2
-    const float same_b3_lo = b2 ? x4 : t, same_b3_hi = b2 ? t : x4;
-    const float other_b3_lo = b2 ? x12 : x8, other_b3_hi = b2 ? x8 : x12;
-    d[0] = b3 ? other_b3_lo : same_b3_lo;
-    d[1] = b3 ? other_b3_hi : same_b3_hi;
-    d[2] = b3 ? same_b3_lo : other_b3_lo;
-    d[3] = b3 ? same_b3_hi : other_b3_hi;
+// Sum over the 16 lanes of a DPP row (one 16-lane group), returned to every
+// lane with the same bits: quad xor 1, quad xor 2, then the row mirror
+// (quad a <-> 3-a) and the half-row mirror (quad a <-> a^1).  Each step adds
+// two equal-order partial sums, so the result does not depend on the lane.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x140>(v);  // row_mirror
+    v += dpp_f32<0x141>(v);  // row_half_mirror
+    return v;
 }
 
-// One pass over the selected rows: every (id, g) row's K and V halves are
-// requested together (same 4 KiB pool row), 16 lanes per row with 8 channels
-// each.  Each 16-lane group keeps an online softmax state (m, l, o) per query
-// head over its rows, rescaled once per batch of kBatch rows; the groups'
-// states are merged at the end (wave shuffles, then LDS across waves).
+// One pass over the selected rows.  A workgroup owns kChunk consecutive ids
+// and all 8 KV heads, one wave per KV head, so the K and V segments of the
+// 8 heads in one 4 KiB pool row are requested close together in time.  In a
+// wave, 16 lanes take one (id, g) row at a time with 8 channels per lane; K
+// and V are requested together, the next batch of rows before the current
+// one is used.  Each 16-lane group keeps an online softmax state (m, l, o)
+// per query head, rescaled once per batch; the 4 groups of the wave are
+// merged with cross-lane moves and the wave writes the chunk's record.
 template <bool kRows>
 __global__ void __launch_bounds__(kThreads)
 attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ pool,
                     uint32_t row_bytes, const int32_t* __restrict__ rows, uint32_t pool_rows,
                     const uint32_t* __restrict__ member, uint32_t n, uint32_t chunks,
                     float* __restrict__ part) {
-    constexpr uint32_t kBatch = 4;  // rows in flight per 16-lane group (K + V)
-    __shared__ uint32_t sel_id[kChunk];
-    __shared__ uint32_t sel_mask[kChunk];
-    __shared__ uint32_t wave_tot[4];
-    __shared__ float wm[4][4], wl[4][4];    // [wave][head] merged m, l
-    __shared__ float osum[4][4][128];       // [wave][head][channel]
+    constexpr uint32_t kBatch = 2;  // rows per batch of a 16-lane group (K + V); 2 batches in flight
+    __shared__ uint32_t sel_row[8][kChunk];
+    __shared__ uint8_t sel_mask[8][kChunk];
 
-    const uint32_t chunk = blockIdx.x, g = blockIdx.y;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t chunk = blockIdx.x;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t g = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave = KV head
     const uint32_t words = (n + 31) / 32;
     const uint32_t base = chunk * kChunk;
 
     // ---- union of the 4 query heads' selections, compacted in id order ----
-    uint32_t id0 = base + 2 * tid, m0 = 0, m1 = 0;
+    uint32_t total = 0;
 #pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-        const uint32_t* bits = member + static_cast<size_t>(4 * g + j) * words;
-        if (id0 < n) m0 |= ((bits[id0 >> 5] >> (id0 & 31u)) & 1u) << j;
-        if (id0 + 1 < n) m1 |= ((bits[(id0 + 1) >> 5] >> ((id0 + 1) & 31u)) & 1u) << j;
-    }
-    if (kRows) {  // ids whose row lies outside the pool contribute nothing
-        if (m0 && static_cast<uint32_t>(rows[id0]) >= pool_rows) m0 = 0;
-        if (m1 && static_cast<uint32_t>(rows[id0 + 1]) >= pool_rows) m1 = 0;
-    }
-    const uint32_t mine = (m0 != 0) + (m1 != 0);
-    uint32_t x = mine;
+    for (uint32_t c = 0; c < kChunk; c += 64) {
+        const uint32_t id = base + c + lane;
+        uint32_t mk = 0, r = id;
+        if (id < n) {
 #pragma unroll
-    for (uint32_t off = 1; off < 64; off <<= 1) {
-        const uint32_t y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
+            for (uint32_t j = 0; j < 4; ++j) {
+                const uint32_t w = member[static_cast<size_t>(4 * g + j) * words + (id >> 5)];
+                mk |= ((w >> (id & 31u)) & 1u) << j;
+            }
+            if (kRows && mk) {
+                r = static_cast<uint32_t>(rows[id]);
+                if (r >= pool_rows) mk = 0;  // rows outside the pool contribute nothing
+            }
+        }
+        const uint64_t any = __ballot(mk != 0);
+        if (mk) {
+            const uint32_t at = total + lanes_below(any);
+            sel_row[g][at] = r;
+            sel_mask[g][at] = static_cast<uint8_t>(mk);
+        }
+        total += static_cast<uint32_t>(__popcll(any));
     }
-    if (lane == 63) wave_tot[wave] = x;
-    __syncthreads();
-    uint32_t before = 0, total = 0;
-#pragma unroll
-    for (uint32_t w = 0; w < 4; ++w) {
-        before += w < wave ? wave_tot[w] : 0u;
-        total += wave_tot[w];
-    }
-    uint32_t pos = before + x - mine;
-    if (m0) { sel_id[pos] = id0; sel_mask[pos] = m0; ++pos; }
-    if (m1) { sel_id[pos] = id0 + 1; sel_mask[pos] = m1; }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
 
     // ---- one pass: scores, online softmax, p * V -----------------------------
-    const uint32_t grp = tid >> 4, part16 = lane & 15u;  // 16 groups per workgroup
+    const uint32_t grp = lane >> 4, part16 = lane & 15u;  // 4 groups per wave
     float qr[4][8];
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j)
@@ -139,25 +128,24 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
 #pragma unroll
         for (uint32_t c = 0; c < 8; ++c) o[j][c] = 0.0f;
 
-    for (uint32_t e0 = grp; e0 < total; e0 += 16 * kBatch) {
-        uint4 kw[kBatch], vw[kBatch];
+    // rows e = e0 + 4u (u < kBatch) form a batch of this group
+    auto load_batch = [&](uint32_t e0, uint4 (&kw)[kBatch], uint4 (&vw)[kBatch]) {
 #pragma unroll
         for (uint32_t u = 0; u < kBatch; ++u) {
-            const uint32_t e = e0 + 16 * u;
-            kw[u] = vw[u] = make_uint4(0u, 0u, 0u, 0u);
-            if (e < total) {
-                const uint32_t id = sel_id[e];
-                const size_t r = kRows ? static_cast<size_t>(rows[id]) : id;
-                const uint8_t* row = pool + r * row_bytes;
-                kw[u] = *reinterpret_cast<const uint4*>(row + koff);
-                vw[u] = *reinterpret_cast<const uint4*>(row + voff);
-            }
+            // past the end, the last row is read again and masked out below;
+            // straight-line loads let the next batch stay in flight
+            const size_t r = sel_row[g][min(e0 + 4 * u, total - 1)];
+            const uint8_t* row = pool + r * row_bytes;
+            kw[u] = *reinterpret_cast<const uint4*>(row + koff);
+            vw[u] = *reinterpret_cast<const uint4*>(row + voff);
         }
+    };
+    auto use_batch = [&](uint32_t e0, const uint4 (&kw)[kBatch], const uint4 (&vw)[kBatch]) {
         float s[kBatch][4];
         float bm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
         for (uint32_t u = 0; u < kBatch; ++u) {
-            const uint32_t e = e0 + 16 * u;
+            const uint32_t e = e0 + 4 * u;
             float kf[8];
             unpack8(kw[u], kf);
             float d[4];
@@ -168,8 +156,10 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
                 for (uint32_t c = 0; c < 8; ++c) acc = __builtin_fmaf(qr[j][c], kf[c], acc);
                 d[j] = acc;
             }
-            group_sum4(d, part16);
-            const uint32_t mk = e < total ? sel_mask[e] : 0u;
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) d[j] = row_sum16(d[j]);
+            const uint32_t mk_at = sel_mask[g][min(e, total - 1)];
+            const uint32_t mk = e < total ? mk_at : 0u;
 #pragma unroll
             for (uint32_t j = 0; j < 4; ++j) {
                 s[u][j] = ((mk >> j) & 1u) ? d[j] * kScale : -INFINITY;
@@ -179,7 +169,7 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
             const float mn = fmaxf(m[j], bm[j]);
-            if (mn == -INFINITY) continue;  // nothing selected for head j so far
+            // scale 0 while head j has no selected row (m = -inf)
             const float scale = m[j] == -INFINITY ? 0.0f : __expf(m[j] - mn);
             l[j] *= scale;
 #pragma unroll
@@ -198,9 +188,28 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
                 for (uint32_t c = 0; c < 8; ++c) o[j][c] = __builtin_fmaf(p, vf[c], o[j][c]);
             }
         }
+    };
+    constexpr uint32_t kStep = 4 * kBatch;
+    // All 4 groups of a wave step together, over pairs of batches (the loop
+    // bound is wave-uniform; an odd batch count ends with one fully masked
+    // batch).  Each batch is requested, unconditionally, before the previous
+    // one is used, and no exit test sits between a batch's loads and its use,
+    // so the compiler keeps the loads where they are and the wait before each
+    // use leaves the next batch in flight.
+    uint4 ka[kBatch], va[kBatch], kb[kBatch], vb[kBatch];
+    const uint32_t pairs = (total + 2 * kStep - 1) / (2 * kStep);
+    load_batch(grp, ka, va);
+    for (uint32_t p = 0; p < pairs; ++p) {
+        const uint32_t b0 = p * 2 * kStep + grp;
+        load_batch(b0 + kStep, kb, vb);
+        __builtin_amdgcn_sched_barrier(0);
+        use_batch(b0, ka, va);
+        load_batch(b0 + 2 * kStep, ka, va);
+        __builtin_amdgcn_sched_barrier(0);
+        use_batch(b0 + kStep, kb, vb);
     }
 
-    // ---- merge the 4 groups of each wave (lanes l, l^16, l^32, l^48) ---------
+    // ---- merge the 4 groups of the wave (lanes l, l^16, l^32, l^48) ----------
 #pragma unroll
     for (uint32_t off = 16; off < 64; off <<= 1) {
 #pragma unroll
@@ -218,47 +227,34 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
             m[j] = mn;
         }
     }
+    // ---- this chunk's (m, l, o[128]) record per query head of KV head g -------
     if (lane < 16) {
+        float* rec = part + (static_cast<size_t>(g) * chunks + chunk) * 4 * kRecord;
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
 #pragma unroll
-            for (uint32_t c = 0; c < 8; ++c) osum[wave][j][part16 * 8 + c] = o[j][c];
+            for (uint32_t c = 0; c < 8; ++c) rec[j * kRecord + 2 + part16 * 8 + c] = o[j][c];
             if (lane == 0) {
-                wm[wave][j] = m[j];
-                wl[wave][j] = l[j];
+                rec[j * kRecord + 0] = m[j];
+                rec[j * kRecord + 1] = l[j];
             }
-        }
-    }
-    __syncthreads();
-
-    // ---- merge the 4 waves into this chunk's (m, l, o) record per head -------
-    float* rec = part + (static_cast<size_t>(g) * chunks + chunk) * 4 * kRecord;
-    for (uint32_t i = tid; i < 4 * 128; i += kThreads) {
-        const uint32_t j = i >> 7, c = i & 127u;
-        const float mt = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
-        float acc = 0.0f, lsum = 0.0f;
-#pragma unroll
-        for (uint32_t w = 0; w < 4; ++w) {
-            const float a = (wm[w][j] == -INFINITY) ? 0.0f : __expf(wm[w][j] - mt);
-            acc = __builtin_fmaf(osum[w][j][c], a, acc);
-            lsum = __builtin_fmaf(wl[w][j], a, lsum);
-        }
-        rec[j * kRecord + 2 + c] = acc;
-        if (c == 0) {
-            rec[j * kRecord + 0] = mt;
-            rec[j * kRecord + 1] = lsum;
         }
     }
 }
 
-// Merge the per-chunk (m, l, o) records of each query head: one workgroup per
-// head, every record read by a different thread (no serial load chain).
-constexpr uint32_t kMaxChunks = 128;  // n <= 65536
-__global__ void __launch_bounds__(512)
+// Merge the per-chunk (m, l, o) records of each query head.  Grid (32 query
+// heads, 4 groups of 32 channels): a workgroup computes the chunk weights
+// exp(m_i - max m) and their l sum, then 16 rows of 32 threads each sum the
+// weighted o of every 16th chunk (8 records requested together per thread)
+// and the 16 partial sums are added in LDS.
+constexpr uint32_t kMaxChunks = 65536 / kChunk;
+constexpr uint32_t kCombineThreads = 512;
+static_assert(kMaxChunks <= kCombineThreads, "one chunk weight per thread");
+__global__ void __launch_bounds__(kCombineThreads)
 attn_combine_kernel(const float* __restrict__ part, uint32_t chunks, float* __restrict__ out) {
     __shared__ float weight[kMaxChunks];
     __shared__ float red[8];
-    __shared__ float acc4[4][128];
+    __shared__ float acc16[16][33];
     const uint32_t h = blockIdx.x, g = h >> 2, j = h & 3u, tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = tid >> 6;
     const float* recs = part + static_cast<size_t>(g) * chunks * 4 * kRecord + j * kRecord;
@@ -273,32 +269,36 @@ attn_combine_kernel(const float* __restrict__ part, uint32_t chunks, float* __re
     const float w_self = (m == -INFINITY || top == -INFINITY) ? 0.0f : __expf(m - top);
     if (tid < chunks) weight[tid] = w_self;
     __syncthreads();
-    float lsum = wave_sum_f32(l * w_self);
+    const float lsum = wave_sum_f32(l * w_self);
+    __syncthreads();  // every wave has read red[] before it is reused
     if (lane == 0) red[wave] = lsum;
     __syncthreads();
     float L = 0.0f;
 #pragma unroll
     for (uint32_t w = 0; w < 8; ++w) L += red[w];
-    const uint32_t c = tid & 127u, quarter = tid >> 7;
+    const uint32_t c = tid & 31u, r = tid >> 5, ch = blockIdx.y * 32 + c;
     float a = 0.0f;
-    // each thread's records are requested together (<= 32 of them)
-    constexpr uint32_t kLoads = kMaxChunks / 4;
-    float v[kLoads];
+    constexpr uint32_t kLoads = 8;
+    for (uint32_t i0 = r; i0 < chunks; i0 += 16 * kLoads) {
+        float v[kLoads];
 #pragma unroll
-    for (uint32_t u = 0; u < kLoads; ++u) {
-        const uint32_t i = quarter + 4 * u;
-        v[u] = i < chunks ? recs[i * 4 * kRecord + 2 + c] : 0.0f;
-    }
+        for (uint32_t u = 0; u < kLoads; ++u) {
+            const uint32_t i = i0 + 16 * u;
+            v[u] = i < chunks ? recs[i * 4 * kRecord + 2 + ch] : 0.0f;
+        }
 #pragma unroll
-    for (uint32_t u = 0; u < kLoads; ++u) {
-        const uint32_t i = quarter + 4 * u;
-        if (i < chunks && weight[i] != 0.0f) a = __builtin_fmaf(v[u], weight[i], a);
+        for (uint32_t u = 0; u < kLoads; ++u) {
+            const uint32_t i = i0 + 16 * u;
+            if (i < chunks && weight[i] != 0.0f) a = __builtin_fmaf(v[u], weight[i], a);
+        }
     }
-    acc4[quarter][c] = a;
+    acc16[r][c] = a;
     __syncthreads();
-    if (tid < 128) {
-        const float sum = acc4[0][tid] + acc4[1][tid] + acc4[2][tid] + acc4[3][tid];
-        out[h * 128 + tid] = L > 0.0f ? sum / L : 0.0f;
+    if (tid < 32) {
+        float sum = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < 16; ++k) sum += acc16[k][tid];
+        out[h * 128 + ch] = L > 0.0f ? sum / L : 0.0f;
     }
 }
 
@@ -320,14 +320,15 @@ int launch_attention(const float* q, const uint8_t* pool, size_t row_bytes, cons
     const uint32_t chunks = (n + kChunk - 1) / kChunk;
     float* part = static_cast<float*>(workspace);
     if (rows)
-        hipLaunchKernelGGL(attn_partial_kernel<true>, dim3(chunks, 8), dim3(kThreads), 0, stream, q,
+        hipLaunchKernelGGL(attn_partial_kernel<true>, dim3(chunks), dim3(kThreads), 0, stream, q,
                            pool, static_cast<uint32_t>(row_bytes), rows, pool_rows, member, n,
                            chunks, part);
     else
-        hipLaunchKernelGGL(attn_partial_kernel<false>, dim3(chunks, 8), dim3(kThreads), 0, stream,
+        hipLaunchKernelGGL(attn_partial_kernel<false>, dim3(chunks), dim3(kThreads), 0, stream,
                            q, pool, static_cast<uint32_t>(row_bytes), rows, 0u, member, n,
                            chunks, part);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(32), dim3(512), 0, stream, part, chunks, out);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(32, 4), dim3(kCombineThreads), 0, stream, part, chunks,
+                       out);
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "attention launch");
 }
