@@ -58,6 +58,12 @@ constexpr uint32_t kMaxN = 131072;              // policy/gqa_policy_tests.cpp l
 constexpr uint32_t kMaxHeads = 128;
 constexpr uint32_t kMaxSlices = kMaxN / kSlice;  // 32
 constexpr uint32_t kRankCap = 16384;             // a head's sorted keys staged in LDS
+// per-head path (n <= kHeadMaxN): one 1024-thread workgroup per head
+constexpr uint32_t kHThreads = 1024;
+constexpr uint32_t kHWaves = kHThreads / 64;
+constexpr uint32_t kHRun = 32;                     // ids per thread: one membership word
+constexpr uint32_t kHeadMaxN = kHThreads * kHRun;  // 32768
+constexpr uint32_t kHeadMaxK = 8192;               // rank order: selection sorted in LDS
 
 // Published by group 0 of the plan launch.
 struct SelectPlanDev {
@@ -68,7 +74,8 @@ struct SelectPlanDev {
 struct SelectPlan {
     uint32_t S = 0, groups = 0, partials = 0, cap = 0;
     size_t off_plan = 0, off_partial = 0, off_count = 0, off_bad = 0, off_hi = 0, off_lo = 0,
-           off_sort = 0, off_keys = 0, off_m = 0, off_tie = 0, total = 0;
+           off_sort = 0, off_keys = 0, off_m = 0, off_tie = 0, off_key16 = 0, total = 0;
+    uint32_t key_stride = 0;  // per-head row of the order-key copy (per-head path only)
     uint32_t kcap = 0;  // per-head capacity of the rank-sorted lists (>= k)
 };
 
@@ -95,6 +102,8 @@ SelectPlan plan_select(uint32_t heads, uint32_t n, uint32_t kmax) {
     p.off_keys = take(sizeof(uint16_t) * size_t(heads) * p.kcap);
     p.off_m = take(sizeof(uint32_t) * 4 * p.groups);
     p.off_tie = take(sizeof(unsigned long long) * heads);
+    p.key_stride = n <= kHeadMaxN ? (n + 7) / 8 * 8 : 0u;
+    p.off_key16 = take(sizeof(uint16_t) * size_t(heads) * p.key_stride);
     p.total = at;
     return p;
 }
@@ -116,6 +125,8 @@ struct SelectArgs {
     uint32_t* g_m;      // [groups][4] selected count, id-order offset, max key, K*
     uint32_t kcap;
     unsigned long long* g_tie;  // [heads] bits around a signed-zero cut
+    uint16_t* g_key16;  // [heads][key_stride] order keys of the (scaled) scores, or null
+    uint32_t key_stride;
     uint32_t cap;
     uint32_t* ids;
     uint32_t ids_stride;
@@ -143,27 +154,30 @@ __device__ __forceinline__ float threshold_from_key(uint32_t key, bool scale, fl
     return h2f(f2h(m - alpha));
 }
 
-// Block-wide reductions / scan through LDS.
+// Block-wide reductions / scan through LDS (tmp: one word per wave).
+template <uint32_t kT = kThreads>
 __device__ uint32_t block_max(uint32_t v, uint32_t* tmp) {
     v = wave_max_u32(v);
     if ((threadIdx.x & 63u) == 0) tmp[threadIdx.x >> 6] = v;
     __syncthreads();
     uint32_t best = 0;
 #pragma unroll
-    for (uint32_t w = 0; w < kWaves; ++w) best = tmp[w] > best ? tmp[w] : best;
+    for (uint32_t w = 0; w < kT / 64; ++w) best = tmp[w] > best ? tmp[w] : best;
     __syncthreads();
     return best;
 }
+template <uint32_t kT = kThreads>
 __device__ uint32_t block_sum(uint32_t v, uint32_t* tmp) {
     v = wave_sum_u32(v);
     if ((threadIdx.x & 63u) == 0) tmp[threadIdx.x >> 6] = v;
     __syncthreads();
     uint32_t total = 0;
 #pragma unroll
-    for (uint32_t w = 0; w < kWaves; ++w) total += tmp[w];
+    for (uint32_t w = 0; w < kT / 64; ++w) total += tmp[w];
     __syncthreads();
     return total;
 }
+template <uint32_t kT = kThreads>
 __device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* tmp) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     uint32_t x = v;
@@ -176,7 +190,7 @@ __device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* tmp) {
     __syncthreads();
     uint32_t before = 0;
 #pragma unroll
-    for (uint32_t w = 0; w < kWaves; ++w) before += w < wave ? tmp[w] : 0u;
+    for (uint32_t w = 0; w < kT / 64; ++w) before += w < wave ? tmp[w] : 0u;
     __syncthreads();
     return before + x - v;
 }
@@ -227,31 +241,40 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t digit, bool valid) {
     return m;
 }
 
-__device__ __forceinline__ uint32_t half_at(const uint32_t (&packed)[kRun / 2], uint32_t j) {
+template <uint32_t kWords>
+__device__ __forceinline__ uint32_t half_at(const uint32_t (&packed)[kWords], uint32_t j) {
     return (packed[j >> 1] >> ((j & 1u) * 16u)) & 0xffffu;
 }
 
-// This thread's 8 ids of head h into registers (scaled when asked); ids past
-// n read as 0 and are masked by the callers.
+// This thread's kR consecutive ids of head h from `begin` into registers
+// (scaled when asked); ids past n read as 0 and are masked by the callers.
+template <uint32_t kR>
 __device__ __forceinline__ void load_run(const SelectArgs& a, uint32_t h, uint32_t begin,
-                                         uint32_t (&packed)[kRun / 2]) {
+                                         uint32_t (&packed)[kR / 2]) {
+    static_assert(kR % 8 == 0, "runs are whole 16-byte words");
     const uint16_t* row = a.scores + static_cast<size_t>(h) * a.stride;
-    uint32_t w[4];
-    if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0 && begin + 8 <= a.n) {
-        const uint4 v = *reinterpret_cast<const uint4*>(row + begin);
-        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-    } else {
+    const bool vec = (reinterpret_cast<uintptr_t>(row) & 15u) == 0 && begin + kR <= a.n;
 #pragma unroll
-        for (uint32_t c = 0; c < 4; ++c) {
-            const uint32_t lo = begin + 2 * c < a.n ? row[begin + 2 * c] : 0u;
-            const uint32_t hi = begin + 2 * c + 1 < a.n ? row[begin + 2 * c + 1] : 0u;
-            w[c] = lo | (hi << 16);
+    for (uint32_t v = 0; v < kR / 8; ++v) {
+        uint32_t* w = packed + 4 * v;
+        const uint32_t at = begin + 8 * v;
+        if (vec) {
+            const uint4 x = *reinterpret_cast<const uint4*>(row + at);
+            w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+        } else {
+#pragma unroll
+            for (uint32_t c = 0; c < 4; ++c) {
+                const uint32_t lo = at + 2 * c < a.n ? row[at + 2 * c] : 0u;
+                const uint32_t hi = at + 2 * c + 1 < a.n ? row[at + 2 * c + 1] : 0u;
+                w[c] = lo | (hi << 16);
+            }
         }
     }
-    const bool scale = (a.flags & HS_SELECT_SCALE_RAW) != 0;
+    if (a.flags & HS_SELECT_SCALE_RAW) {
 #pragma unroll
-    for (uint32_t c = 0; c < 4; ++c)
-        packed[c] = scale ? (scale_raw(w[c] & 0xffffu) | (scale_raw(w[c] >> 16) << 16)) : w[c];
+        for (uint32_t c = 0; c < kR / 2; ++c)
+            packed[c] = scale_raw(packed[c] & 0xffffu) | (scale_raw(packed[c] >> 16) << 16);
+    }
 }
 
 // Order-key histograms: 4 copies per wave, 257 words apart, so lanes that hit
@@ -296,15 +319,17 @@ __global__ void __launch_bounds__(kThreads) count_kernel(SelectArgs a) {
     const uint32_t begin = s * kSlice + tid * kRun;
     uint32_t best = partial_max(a);
     uint32_t packed[kRun / 2];
-    load_run(a, h, begin, packed);
+    load_run<kRun>(a, h, begin, packed);
     hist_clear(whist);
     best = block_max(best, tmp);  // its barrier also orders the histogram clear
     const float thr = threshold_from_key(best, (a.flags & HS_SELECT_SCALE_RAW) != 0, a.alpha);
     uint32_t count = 0, bad = 0;
+    uint32_t keyw[kRun / 2] = {};
 #pragma unroll
     for (uint32_t j = 0; j < kRun; ++j) {
+        const uint32_t b = half_at(packed, j);
+        keyw[j >> 1] |= order_key(b) << ((j & 1u) * 16u);
         if (begin + j < a.n) {
-            const uint32_t b = half_at(packed, j);
             if (!finite_half(b)) {
                 bad = 1;
             } else {
@@ -313,6 +338,10 @@ __global__ void __launch_bounds__(kThreads) count_kernel(SelectArgs a) {
             }
         }
     }
+    // the per-head path reads these order keys instead of rescaling
+    if (a.g_key16 && begin < a.key_stride)
+        *reinterpret_cast<uint4*>(a.g_key16 + static_cast<size_t>(h) * a.key_stride + begin) =
+            make_uint4(keyw[0], keyw[1], keyw[2], keyw[3]);
     count = block_sum(count, tmp);
     bad = block_max(bad, tmp);
     if (tid < 256) a.g_hi[static_cast<size_t>(g) * 256 + tid] = hist_total(whist, tid);
@@ -325,6 +354,46 @@ __global__ void __launch_bounds__(kThreads) count_kernel(SelectArgs a) {
         if (tid == 0) a.status->boundary_tied_heads = 0;
         if (tid < a.heads) a.g_tie[tid] = 0ull;
     }
+}
+
+// k from every head's count and nonfinite flag (policy/gqa_policy.cpp:51-63),
+// with the reference's error precedence.  Called by one whole wave; every lane
+// returns the same code and k.
+__device__ int derive_k(const SelectArgs& a, const uint32_t* head_count, const uint32_t* head_bad,
+                        float thr, uint32_t& k) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const bool fp32_counts = (a.flags & HS_SELECT_FP32_COUNTS) != 0;
+    int code = HS_OK;
+    k = 0;
+    if (head_bad[0]) return HS_ERR_NONFINITE;
+    if (!isfinite(thr)) return HS_ERR_THRESHOLD;
+    float total = 0.0f;
+    for (uint32_t first = 0; first < a.heads && code == HS_OK; first += 64) {
+        const uint32_t hh = first + lane;
+        const bool valid = hh < a.heads;
+        const uint32_t c = valid ? head_count[hh] : 0u;
+        const bool hb = valid && head_bad[hh] != 0;
+        const float rounded = fp32_counts ? static_cast<float>(c) : h2f(f2h(static_cast<float>(c)));
+        const bool err = valid && (hb || !isfinite(rounded));
+        const uint64_t errs = __ballot(err);
+        if (errs) {
+            const uint32_t at = static_cast<uint32_t>(__ffsll(static_cast<long long>(errs))) - 1;
+            code = __shfl(hb ? 1 : 0, at, 64) ? HS_ERR_NONFINITE : HS_ERR_COUNT;
+        }
+        total += wave_sum_f32(valid && !err ? rounded : 0.0f);
+    }
+    if (code != HS_OK) return code;
+    const float q = __fdiv_rn(total, static_cast<float>(a.heads));
+    const float mean = fp32_counts ? q : h2f(f2h(q));
+    if (!isfinite(mean)) return HS_ERR_MEAN;
+    uint64_t kk = static_cast<uint64_t>(mean);
+    const uint64_t cap_k =
+        static_cast<uint64_t>(floor(static_cast<double>(a.n) * static_cast<double>(a.ratio)));
+    kk = kk < cap_k ? kk : cap_k;
+    kk = kk < a.n ? kk : a.n;
+    k = static_cast<uint32_t>(kk);
+    if (k == 0 && (a.flags & HS_SELECT_REQUIRE_K)) return HS_ERR_ZERO_SELECTION;
+    return HS_OK;
 }
 
 // ---- 2. plan ----------------------------------------------------------------
@@ -340,7 +409,6 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
     const uint32_t g = blockIdx.x, S = a.S, h = g / S, s = g - h * S, n = a.n;
     const uint32_t groups = a.heads * S;
     const bool scale = (a.flags & HS_SELECT_SCALE_RAW) != 0;
-    const bool fp32_counts = (a.flags & HS_SELECT_FP32_COUNTS) != 0;
 
     // every global read of this kernel is issued up front
     uint32_t best = partial_max(a);
@@ -360,7 +428,7 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
     }
     uint32_t packed[kRun / 2];
     const uint32_t begin = s * kSlice + tid * kRun;
-    load_run(a, h, begin, packed);
+    load_run<kRun>(a, h, begin, packed);
 
     hist_clear(whist);
     if (tid < 256) hist[tid] = 0;
@@ -382,46 +450,8 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
 
     // k from every head's count (wave 0)
     if (wave == 0) {
-        int code = HS_OK;
         uint32_t k = 0;
-        if (head_bad[0]) {
-            code = HS_ERR_NONFINITE;
-        } else if (!isfinite(thr)) {
-            code = HS_ERR_THRESHOLD;
-        } else {
-            float total = 0.0f;
-            for (uint32_t first = 0; first < a.heads && code == HS_OK; first += 64) {
-                const uint32_t hh = first + lane;
-                const bool valid = hh < a.heads;
-                const uint32_t c = valid ? head_count[hh] : 0u;
-                const bool hb = valid && head_bad[hh] != 0;
-                const float rounded =
-                    fp32_counts ? static_cast<float>(c) : h2f(f2h(static_cast<float>(c)));
-                const bool err = valid && (hb || !isfinite(rounded));
-                const uint64_t errs = __ballot(err);
-                if (errs) {
-                    const uint32_t at =
-                        static_cast<uint32_t>(__ffsll(static_cast<long long>(errs))) - 1;
-                    code = __shfl(hb ? 1 : 0, at, 64) ? HS_ERR_NONFINITE : HS_ERR_COUNT;
-                }
-                total += wave_sum_f32(valid && !err ? rounded : 0.0f);
-            }
-            if (code == HS_OK) {
-                const float q = __fdiv_rn(total, static_cast<float>(a.heads));
-                const float mean = fp32_counts ? q : h2f(f2h(q));
-                if (!isfinite(mean)) {
-                    code = HS_ERR_MEAN;
-                } else {
-                    uint64_t kk = static_cast<uint64_t>(mean);
-                    const uint64_t cap_k = static_cast<uint64_t>(
-                        floor(static_cast<double>(n) * static_cast<double>(a.ratio)));
-                    kk = kk < cap_k ? kk : cap_k;
-                    kk = kk < n ? kk : n;
-                    k = static_cast<uint32_t>(kk);
-                    if (k == 0 && (a.flags & HS_SELECT_REQUIRE_K)) code = HS_ERR_ZERO_SELECTION;
-                }
-            }
-        }
+        const int code = derive_k(a, head_count, head_bad, thr, k);
         if (lane == 0) {
             sh[kCode] = static_cast<uint32_t>(code);
             sh[kK] = k;
@@ -457,18 +487,20 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
 
 // Stable LSD radix sort (two 8-bit passes over bits 16..31) of m composites
 // ((0xffff - key) << 16 | id in slice) from A through B back into A:
-// ascending composite order is (key desc, id asc).  whist: kWaves x 256.
+// ascending composite order is (key desc, id asc).  whist: kT / 64 x 256.
+template <uint32_t kT = kThreads>
 __device__ void sort_composites(uint32_t* A, uint32_t* B, uint32_t m, uint32_t (*whist)[256],
                                 uint32_t* tmp) {
+    constexpr uint32_t kW = kT / 64;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t per_wave = ((m + kWaves - 1) / kWaves + 63) / 64 * 64;
+    const uint32_t per_wave = ((m + kW - 1) / kW + 63) / 64 * 64;
     const uint32_t first = wave * per_wave;
 #pragma unroll 1
     for (uint32_t pass = 0; pass < 2; ++pass) {
         const uint32_t* src = pass ? B : A;
         uint32_t* dst = pass ? A : B;
         const uint32_t shift = 16 + 8 * pass;
-        for (uint32_t i = tid; i < kWaves * 256; i += kThreads) (&whist[0][0])[i] = 0;
+        for (uint32_t i = tid; i < kW * 256; i += kT) (&whist[0][0])[i] = 0;
         __syncthreads();
         for (uint32_t c = 0; c < per_wave; c += 64) {
             const uint32_t e = first + c + lane;
@@ -485,7 +517,7 @@ __device__ void sort_composites(uint32_t* A, uint32_t* B, uint32_t m, uint32_t (
         uint32_t total = 0;
         if (tid < 256) {
 #pragma unroll
-            for (uint32_t w = 0; w < kWaves; ++w) {
+            for (uint32_t w = 0; w < kW; ++w) {
                 const uint32_t c = whist[w][tid];
                 whist[w][tid] = total;
                 total += c;
@@ -503,7 +535,7 @@ __device__ void sort_composites(uint32_t* A, uint32_t* B, uint32_t m, uint32_t (
             uint32_t base = x - total;
             for (uint32_t w = 0; w < wave; ++w) base += tmp[w];
 #pragma unroll
-            for (uint32_t w = 0; w < kWaves; ++w) whist[w][tid] += base;
+            for (uint32_t w = 0; w < kW; ++w) whist[w][tid] += base;
         }
         __syncthreads();
         for (uint32_t c = 0; c < per_wave; c += 64) {
@@ -532,22 +564,23 @@ __device__ void sort_composites(uint32_t* A, uint32_t* B, uint32_t m, uint32_t (
 // in id order by counting its smaller ids.  Returns false, with A untouched,
 // when the limits do not hold.  start/cursor: kSortRange words of LDS each.
 constexpr uint32_t kSortRange = 8192, kGroupCap = 64;
+template <uint32_t kT = kThreads>
 __device__ bool sort_counting(uint32_t* A, uint32_t* B, uint32_t m, uint32_t kmin, uint32_t* start,
                               uint32_t* cursor, uint32_t* tmp) {
     const uint32_t tid = threadIdx.x;
     uint32_t kmax = 0;
-    for (uint32_t q = tid; q < m; q += kThreads) kmax = max(kmax, 0xffffu - (A[q] >> 16));
-    kmax = block_max(kmax, tmp);
+    for (uint32_t q = tid; q < m; q += kT) kmax = max(kmax, 0xffffu - (A[q] >> 16));
+    kmax = block_max<kT>(kmax, tmp);
     if (m == 0) return true;
     if (kmax < kmin || kmax - kmin >= kSortRange) return false;
     const uint32_t range = kmax - kmin + 1;
-    for (uint32_t i = tid; i < range; i += kThreads) start[i] = 0;
+    for (uint32_t i = tid; i < range; i += kT) start[i] = 0;
     __syncthreads();
-    for (uint32_t q = tid; q < m; q += kThreads) atomicAdd(&start[0xffffu - (A[q] >> 16) - kmin], 1u);
+    for (uint32_t q = tid; q < m; q += kT) atomicAdd(&start[0xffffu - (A[q] >> 16) - kmin], 1u);
     __syncthreads();
     // each thread owns a run of bins, thread 0 the top ones
-    const uint32_t per = (range + kThreads - 1) / kThreads;
-    const uint32_t first = (kThreads - 1 - tid) * per;
+    const uint32_t per = (range + kT - 1) / kT;
+    const uint32_t first = (kT - 1 - tid) * per;
     uint32_t sum = 0, big = 0;
     for (uint32_t i = 0; i < per; ++i) {
         const uint32_t b = first + i;
@@ -556,9 +589,9 @@ __device__ bool sort_counting(uint32_t* A, uint32_t* B, uint32_t m, uint32_t kmi
             big = max(big, start[b]);
         }
     }
-    big = block_max(big, tmp);
+    big = block_max<kT>(big, tmp);
     if (big > kGroupCap) return false;
-    uint32_t run = block_exclusive_scan(sum, tmp) + sum;
+    uint32_t run = block_exclusive_scan<kT>(sum, tmp) + sum;
     for (uint32_t i = 0; i < per; ++i) {
         const uint32_t b = first + i;
         if (b < range) {
@@ -568,12 +601,12 @@ __device__ bool sort_counting(uint32_t* A, uint32_t* B, uint32_t m, uint32_t kmi
         }
     }
     __syncthreads();
-    for (uint32_t q = tid; q < m; q += kThreads) {
+    for (uint32_t q = tid; q < m; q += kT) {
         const uint32_t e = A[q];
         B[atomicAdd(&cursor[0xffffu - (e >> 16) - kmin], 1u)] = e;
     }
     __syncthreads();
-    for (uint32_t q = tid; q < m; q += kThreads) {
+    for (uint32_t q = tid; q < m; q += kT) {
         const uint32_t e = B[q];
         const uint32_t b = 0xffffu - (e >> 16) - kmin;
         const uint32_t gs = start[b], gc = cursor[b] - gs;
@@ -639,7 +672,7 @@ __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
         lv[u] = ok ? a.g_lo[static_cast<size_t>(h * S) * 256 + i] : 0u;
     }
     uint32_t packed[kRun / 2];
-    load_run(a, h, begin, packed);
+    load_run<kRun>(a, h, begin, packed);
     if (tid < 256) hist[0][tid] = hist[1][tid] = 0;
     __syncthreads();
 #pragma unroll
@@ -786,6 +819,254 @@ __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
             info[2] = m ? 0xffffu - (sort_lds[0] >> 16) : 0u;  // largest key of the slice
             info[3] = kstar;
         }
+    }
+}
+
+// ---- 2'. per-head select (n <= kHeadMaxN) --------------------------------------
+// One 1024-thread workgroup per head, 32 consecutive ids per thread (one
+// membership word), after the count launch, which also left every score's
+// order key in the workspace: k from every head's count, the k-th key from
+// the head's high-byte histograms and a low-byte histogram of its bucket, the
+// ties taken (lowest ids first), then membership and the ids in id order, or,
+// for rank order, the selection (k <= kHeadMaxK) stable-sorted by key in LDS.
+// Every head-wide step is a workgroup step, so plan, select and rank need no
+// launch boundaries between them.
+static_assert(kHeadMaxN / 64 <= kHThreads, "one head-0 tile maximum per thread");
+static_assert(kMaxHeads * (kHeadMaxN / kSlice) <= kHThreads, "one slice count per thread");
+static_assert(kSortRange % kHThreads == 0, "whole key bins per thread");
+
+// Stable placement of the m composites in A ((0xffff - key) << 16 | id, in
+// id order, all keys in [kstar, kstar + kSortRange)) by key, from their key
+// histogram `start`: exclusive suffix scan (larger keys
+// first), scatter into the key groups through B, then each group placed in
+// id order by counting its smaller ids.  Returns false, with A untouched,
+// when a group exceeds kGroupCap (many equal keys); the caller then sorts A
+// otherwise.  cursor: kSortRange words.
+__device__ bool place_by_histogram(uint32_t* A, uint32_t* B, uint32_t m, uint32_t kstar,
+                                   uint32_t* start, uint32_t* cursor, uint32_t* tmp,
+                                   uint32_t* flag) {
+    constexpr uint32_t kPer = kSortRange / kHThreads;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t first = (kHThreads - 1 - tid) * kPer;  // thread 0 owns the top bins
+    uint32_t c[kPer], sum = 0, big = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+        c[i] = start[first + i];
+        sum += c[i];
+        big = max(big, c[i]);
+    }
+    if (big > kGroupCap) *flag = 1;  // read after the scan's barriers
+    const uint32_t scan = block_exclusive_scan<kHThreads>(sum, tmp);
+    if (*flag) return false;
+    uint32_t run = scan + sum;
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+        run -= c[i];
+        start[first + i] = run;
+        cursor[first + i] = run;
+    }
+    __syncthreads();
+    for (uint32_t q = tid; q < m; q += kHThreads) {
+        const uint32_t e = A[q];
+        B[atomicAdd(&cursor[0xffffu - (e >> 16) - kstar], 1u)] = e;
+    }
+    __syncthreads();
+    // each element's rank in its group by id; a thread's kPerThread elements
+    // are handled side by side so their LDS round trips overlap, and the
+    // first 8 members of every group are read in one batch (groups are short)
+    constexpr uint32_t kPerThread = kHeadMaxK / kHThreads;
+    uint32_t e[kPerThread], gs[kPerThread], gc[kPerThread], r[kPerThread];
+#pragma unroll
+    for (uint32_t u = 0; u < kPerThread; ++u) {
+        const uint32_t q = tid + u * kHThreads;
+        e[u] = q < m ? B[q] : 0u;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kPerThread; ++u) {
+        const uint32_t bin = min(0xffffu - (e[u] >> 16) - kstar, kSortRange - 1);
+        gs[u] = start[bin];
+        gc[u] = tid + u * kHThreads < m ? cursor[bin] - gs[u] : 0u;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kPerThread; ++u) {
+        r[u] = 0;
+        uint32_t v[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) v[i] = B[gs[u] + min(i, gc[u] ? gc[u] - 1 : 0u)];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i)
+            r[u] += i < gc[u] && (v[i] & 0xffffu) < (e[u] & 0xffffu) ? 1u : 0u;
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kPerThread; ++u)
+        for (uint32_t i = 8; i < gc[u]; ++i)  // long groups
+            r[u] += (B[gs[u] + i] & 0xffffu) < (e[u] & 0xffffu) ? 1u : 0u;
+#pragma unroll
+    for (uint32_t u = 0; u < kPerThread; ++u)
+        if (tid + u * kHThreads < m) A[gs[u] + r[u]] = e[u];
+    __syncthreads();
+    return true;
+}
+
+template <bool kRankOrder>
+__global__ void __launch_bounds__(kHThreads) head_select_kernel(SelectArgs a) {
+    __shared__ uint32_t hist[2][256];
+    __shared__ uint32_t head_count[kMaxHeads], head_bad[kMaxHeads];
+    __shared__ uint32_t tmp[kHWaves];
+    __shared__ uint32_t sh[8];
+    __shared__ uint32_t sort_lds[kRankOrder ? 2 * kHeadMaxK : 1];
+    __shared__ uint32_t tables[kRankOrder ? 2 * kSortRange : 1];
+    __shared__ uint32_t whist[kRankOrder ? kHWaves : 1][256];
+    enum { kCode, kK, kBucket, kAbove, kBucket2, kAbove2, kFlag };
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t h = blockIdx.x, S = a.S, n = a.n, groups = a.heads * S;
+    const uint32_t begin = tid * kHRun, words = (n + 31) / 32;
+
+    // every global read is issued up front: head-0 tile maxima, all slice
+    // counts and flags, this head's slice histograms and this thread's keys
+    uint32_t best = tid < a.partials ? a.partial[tid] : 0u;
+    const uint32_t cnt = tid < groups ? a.g_count[tid] : 0u;
+    const uint32_t bad = tid < groups ? a.g_bad[tid] : 0u;
+    constexpr uint32_t kBinLoads = (kHeadMaxN / kSlice) * 256 / kHThreads;  // 2
+    uint32_t hv[kBinLoads];
+#pragma unroll
+    for (uint32_t u = 0; u < kBinLoads; ++u) {
+        const uint32_t i = tid + u * kHThreads;
+        hv[u] = i < S * 256 ? a.g_hi[static_cast<size_t>(h * S) * 256 + i] : 0u;
+    }
+    uint32_t keys[kHRun / 2];
+    const uint16_t* krow = a.g_key16 + static_cast<size_t>(h) * a.key_stride;
+#pragma unroll
+    for (uint32_t v = 0; v < kHRun / 8; ++v) {
+        uint4 x = make_uint4(0u, 0u, 0u, 0u);
+        if (begin + 8 * v < a.key_stride) x = *reinterpret_cast<const uint4*>(krow + begin + 8 * v);
+        keys[4 * v] = x.x; keys[4 * v + 1] = x.y; keys[4 * v + 2] = x.z; keys[4 * v + 3] = x.w;
+    }
+
+    if (tid < 256) hist[0][tid] = hist[1][tid] = 0;
+    if (tid < a.heads) head_count[tid] = head_bad[tid] = 0;
+    if constexpr (kRankOrder) {
+        for (uint32_t i = tid; i < kSortRange; i += kHThreads) tables[i] = 0;
+        if (tid == 0) sh[kFlag] = 0;
+    }
+    __syncthreads();
+    if (tid < groups) {
+        atomicAdd(&head_count[tid / S], cnt);
+        atomicOr(&head_bad[tid / S], bad);
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kBinLoads; ++u)
+        if (hv[u]) atomicAdd(&hist[0][(tid + u * kHThreads) & 255u], hv[u]);
+    best = block_max<kHThreads>(best, tmp);  // its barrier also publishes the sums above
+    const float thr = threshold_from_key(best, (a.flags & HS_SELECT_SCALE_RAW) != 0, a.alpha);
+    if (wave == 0) {
+        uint32_t k = 0;
+        const int code = derive_k(a, head_count, head_bad, thr, k);
+        if (lane == 0) {
+            sh[kCode] = static_cast<uint32_t>(code);
+            sh[kK] = k;
+            if (h == 0) {
+                a.plan->code = code;
+                a.plan->k = code == HS_OK ? k : 0u;
+                a.status->code = code;
+                a.status->k = code == HS_OK ? k : 0u;
+                a.status->head0_max_key = best;
+            }
+        }
+        if (code == HS_OK && k > 0) find_bucket(hist[0], k, &sh[kBucket], &sh[kAbove]);
+    }
+    if (h == 0 && tid < a.heads && a.counts_out) a.counts_out[tid] = head_count[tid];
+    __syncthreads();
+    const int code = static_cast<int>(sh[kCode]);
+    const uint32_t k = sh[kK];
+    if (code != HS_OK) return;
+    if (k == 0) {
+        if (a.member && tid < words) a.member[static_cast<size_t>(h) * words + tid] = 0u;
+        return;
+    }
+
+    // low byte of the k-th key
+    const uint32_t hi = sh[kBucket] & 255u, above_hi = sh[kAbove];
+#pragma unroll
+    for (uint32_t j = 0; j < kHRun; ++j) {
+        const uint32_t key = half_at(keys, j);
+        if (begin + j < n && (key >> 8) == hi) atomicAdd(&hist[1][key & 255u], 1u);
+    }
+    __syncthreads();
+    find_bucket(hist[1], k - above_hi, &sh[kBucket2], &sh[kAbove2]);
+    __syncthreads();
+    const uint32_t lo = sh[kBucket2] & 255u;
+    const uint32_t kstar = (hi << 8) | lo;
+    const uint32_t c_above = above_hi + sh[kAbove2];
+    const uint32_t c_equal = hist[1][lo];
+    const uint32_t t_need = k - c_above;  // ties taken, lowest ids first (>= 1)
+    // boundary tie (gqa_policy.cpp:65): the (k+1)-th element exists with
+    // equal bits; equal keys mean equal bits except -0 / +0 (key 0x8000).
+    const bool cut_tie = k < n && c_above + c_equal > k;
+    if (tid == 0 && cut_tie && kstar != 0x8000u) atomicAdd(&a.status->boundary_tied_heads, 1u);
+    const bool zero_cut = cut_tie && kstar == 0x8000u;
+
+    // this thread's keys above K* and ties, as bit masks over its 32 ids
+    uint32_t above_mask = 0, tie_mask = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kHRun; ++j) {
+        const uint32_t key = half_at(keys, j);
+        const bool in = begin + j < n;
+        above_mask |= (in && key > kstar ? 1u : 0u) << j;
+        tie_mask |= (in && key == kstar ? 1u : 0u) << j;
+    }
+    // one scan of both counts (each total <= 32768 fits its 16 bits): the ties
+    // taken before this thread are min(ties before it, t_need)
+    const uint32_t my_ties = static_cast<uint32_t>(__popc(tie_mask));
+    const uint32_t both = block_exclusive_scan<kHThreads>(
+        (static_cast<uint32_t>(__popc(above_mask)) << 16) | my_ties, tmp);
+    const uint32_t tie_start = both & 0xffffu;
+    const uint32_t my_taken = tie_start >= t_need ? 0u : std::min(my_ties, t_need - tie_start);
+    uint32_t pos = (both >> 16) + std::min(tie_start, t_need);
+    uint32_t bits32 = above_mask, rest = tie_mask;
+    for (uint32_t t = 0; t < my_taken; ++t) {  // the lowest-id ties first
+        const uint32_t low = rest & (0u - rest);
+        bits32 |= low;
+        rest ^= low;
+    }
+    if (zero_cut) {
+        // the ties ranked t_need-1 and t_need: compare their raw bits
+        const uint16_t* row = a.scores + static_cast<size_t>(h) * a.stride;
+        uint32_t m = tie_mask;
+        for (uint32_t r = tie_start; m != 0; ++r) {
+            const uint32_t j = static_cast<uint32_t>(__ffs(m)) - 1;
+            m &= m - 1;
+            if (r + 1 == t_need || r == t_need) {
+                uint32_t bits = row[begin + j];
+                if (a.flags & HS_SELECT_SCALE_RAW) bits = scale_raw(bits);
+                note_zero_tie(a, h, bits, r == t_need);
+            }
+        }
+    }
+    uint32_t* out = a.ids + static_cast<size_t>(h) * a.ids_stride;
+    bool wide = false;  // a selected key beyond the counting table
+#pragma unroll
+    for (uint32_t j = 0; j < kHRun; ++j) {
+        if ((bits32 >> j) & 1u) {
+            if (!kRankOrder) {
+                out[pos] = begin + j;
+            } else {
+                const uint32_t key = half_at(keys, j);
+                sort_lds[pos] = ((0xffffu - key) << 16) | (begin + j);
+                if (key - kstar < kSortRange) atomicAdd(&tables[key - kstar], 1u);
+                else wide = true;
+            }
+            ++pos;
+        }
+    }
+    if (a.member && tid < words) a.member[static_cast<size_t>(h) * words + tid] = bits32;
+    if constexpr (kRankOrder) {
+        const uint32_t m = std::min(k, kHeadMaxK);
+        if (__syncthreads_or(wide) ||
+            !place_by_histogram(sort_lds, sort_lds + kHeadMaxK, m, kstar, tables,
+                                tables + kSortRange, tmp, &sh[kFlag]))
+            sort_composites<kHThreads>(sort_lds, sort_lds + kHeadMaxK, m, whist, tmp);
+        for (uint32_t r = tid; r < m; r += kHThreads) out[r] = sort_lds[r] & 0xffffu;
     }
 }
 
@@ -1020,6 +1301,8 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
     args.g_m = reinterpret_cast<uint32_t*>(ws + p.off_m);
     args.kcap = p.kcap;
     args.g_tie = reinterpret_cast<unsigned long long*>(ws + p.off_tie);
+    args.g_key16 = p.key_stride ? reinterpret_cast<uint16_t*>(ws + p.off_key16) : nullptr;
+    args.key_stride = p.key_stride;
     args.cap = p.cap;
     args.ids = ids;
     args.ids_stride = static_cast<uint32_t>(ids_stride);
@@ -1034,6 +1317,18 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
     }
     const dim3 grid(p.groups), block(kThreads);
     hipLaunchKernelGGL(count_kernel, grid, block, 0, stream, args);
+    const bool id_order = (flags & HS_SELECT_ID_ORDER) != 0;
+    if (n <= kHeadMaxN && (id_order || kmax <= kHeadMaxK)) {
+        // one workgroup per head finishes the selection
+        if (id_order)
+            hipLaunchKernelGGL(head_select_kernel<false>, dim3(heads), dim3(kHThreads), 0, stream,
+                               args);
+        else
+            hipLaunchKernelGGL(head_select_kernel<true>, dim3(heads), dim3(kHThreads), 0, stream,
+                               args);
+        const hipError_t st = hipGetLastError();
+        return st == hipSuccess ? HS_OK : hip_fail(st, "select launch");
+    }
     hipLaunchKernelGGL(plan_kernel, grid, block, 0, stream, args);
     if (flags & HS_SELECT_ID_ORDER) {
         hipLaunchKernelGGL(slice_select_kernel<false>, grid, block, 0, stream, args);
