@@ -93,9 +93,10 @@ int hs_gqa_score(const uint16_t *q_dev, const uint16_t *keys_dev,
  * initialisation needed).
  * head0_partial_dev: NULL, or the per-tile maxima from hs_gqa_score over
  * the same raw scores (skips one pass over head 0).
- * One call is 3 launches on `stream` (4 in rank order, +1 without
- * head0_partial_dev); calls sharing a workspace must be ordered on one
- * stream. */
+ * One call is 2 launches on `stream` when n <= 32768 (and, in rank
+ * order, floor(n*ratio) <= 8192), otherwise 3 (4 in rank order); +1
+ * without head0_partial_dev.  Calls sharing a workspace must be ordered on
+ * one stream. */
 enum {
     HS_SELECT_SCALE_RAW = 1u,
     HS_SELECT_FP32_COUNTS = 2u,
