@@ -35,6 +35,7 @@ HS_SELECT_SCALE_RAW = 1
 HS_SELECT_FP32_COUNTS = 2
 HS_SELECT_REQUIRE_K = 4
 HS_SELECT_ID_ORDER = 8
+HS_SELECT_COVER = 16
 
 ERROR_NAMES = {
     HS_ERR_ARGUMENT: "argument",

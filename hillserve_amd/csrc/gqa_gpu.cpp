@@ -229,6 +229,65 @@ GQASelection select_gqa_scores(const std::vector<std::uint16_t>& score, std::siz
     return r;
 }
 
+// ---- history cover ---------------------------------------------------------------
+
+GQAHistoryCover history_cover_gqa(const std::vector<std::uint16_t>& raw, std::size_t h,
+                                  std::size_t capacity, std::uint64_t position, float alpha,
+                                  bool fp32_counts, float cap_ratio) {
+    // policy/full_gqa_runtime.cpp:309-311
+    const std::size_t cap = std::min<std::size_t>(
+        position, static_cast<std::size_t>(std::floor(double(position + 1) * double(cap_ratio))));
+    if (!(position && position < capacity && raw.size() == h * capacity && cap && h > 0 &&
+          h <= 128 && std::isfinite(alpha) && alpha >= 0 && cap_ratio > 0 && cap_ratio <= 1))
+        throw std::runtime_error("payload prefetch historical cap/range mismatch");
+    if (position > 131072 || capacity > std::numeric_limits<std::uint32_t>::max())
+        throw std::invalid_argument("history cover: more than 131072 candidates (beyond this build)");
+    Scratch& s = scratch();
+    void* stream = nullptr;
+    const std::size_t n = static_cast<std::size_t>(position);
+    const std::size_t words = (n + 31) / 32;
+    auto* scores_dev = s.in.as<std::uint16_t>(h * capacity);
+    auto* ids_dev = s.ids.as<std::uint32_t>(h * cap);
+    auto* counts_dev = s.counts.as<std::uint32_t>(h);
+    auto* member_dev = s.member.as<std::uint32_t>(h * words);
+    auto* status_dev = s.status.as<hs_status_t>(1);
+    void* ws = s.ws.ensure(hs_gqa_select_workspace_bytes(static_cast<std::uint32_t>(h),
+                                                         static_cast<std::uint32_t>(n)));
+    upload(scores_dev, raw.data(), raw.size() * 2, stream);
+    api_check(hs_gqa_select(scores_dev, static_cast<std::uint32_t>(h), capacity,
+                            static_cast<std::uint32_t>(n), alpha, cap_ratio,
+                            HS_SELECT_SCALE_RAW | HS_SELECT_COVER |
+                                (fp32_counts ? HS_SELECT_FP32_COUNTS : 0u),
+                            nullptr, ids_dev, cap, counts_dev, member_dev, status_dev, ws, stream));
+    const hs_status_t st = read_status(status_dev, stream);
+    switch (st.code) {
+        case HS_OK: break;
+        case HS_ERR_THRESHOLD:
+            throw std::runtime_error("prefetch threshold upper-bound requires finite historical threshold");
+        case HS_ERR_COUNT:
+            throw std::runtime_error("prefetch count upper-bound exceeds original F16 range");
+        case HS_ERR_MEAN: throw std::runtime_error("prefetch mean upper-bound invalid");
+        default: throw DeviceError(st.code, "history cover device status");
+    }
+    GQAHistoryCover r;
+    r.bound = st.k;
+    std::vector<std::uint32_t> ids(h * cap), member(h * words);
+    download(ids.data(), ids_dev, ids.size() * 4, stream);
+    download(member.data(), member_dev, member.size() * 4, stream);
+    sync(stream);
+    r.per_head_ids.resize(h);
+    for (std::size_t head = 0; head < h; ++head)
+        r.per_head_ids[head].assign(ids.begin() + head * cap, ids.begin() + head * cap + r.bound);
+    // :338-340 sorted union, from the membership bitmaps
+    for (std::size_t w = 0; w < words; ++w) {
+        std::uint32_t any = 0;
+        for (std::size_t head = 0; head < h; ++head) any |= member[head * words + w];
+        for (; any; any &= any - 1)
+            r.physical_ids.push_back(w * 32 + static_cast<std::uint32_t>(__builtin_ctz(any)));
+    }
+    return r;
+}
+
 // ---- union and pack --------------------------------------------------------------
 
 namespace {

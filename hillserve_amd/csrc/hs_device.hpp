@@ -51,6 +51,9 @@ __device__ __forceinline__ uint32_t scale_raw(uint32_t raw) {
     return f2h(__builtin_fmaf(e, kRecip, q0)) | sign;
 }
 
+__device__ __forceinline__ bool is_nan_half(uint32_t bits) {
+    return (bits & 0x7c00u) == 0x7c00u && (bits & 0x03ffu) != 0;
+}
 __device__ __forceinline__ bool finite_half(uint32_t bits) {
     return (bits & 0x7c00u) != 0x7c00u;
 }

@@ -115,7 +115,8 @@ score_kernel(const uint32_t* __restrict__ q32, const uint16_t* __restrict__ keys
             o[3 * static_cast<size_t>(out_stride)] = static_cast<uint16_t>(s3);
         }
         if (head0_partial != nullptr && head_kv == 0) {
-            const uint32_t best = wave_max_u32(token < n ? order_key(s0) : 0u);
+            // NaN is skipped, like std::max over the scores
+            const uint32_t best = wave_max_u32(token < n && !is_nan_half(s0) ? order_key(s0) : 0u);
             if (lane == 0) head0_partial[id >> 3] = best;
         }
     };

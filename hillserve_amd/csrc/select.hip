@@ -135,13 +135,14 @@ struct SelectArgs {
     hs_status_t* status;
 };
 
-// Per 64-element tile of head 0: maximum order key of the input scores
-// (0 = nothing).  Scaling is monotone, so raw keys serve the scaled maximum.
+// Per 64-element tile of head 0: maximum order key of the non-NaN input
+// scores (0 = nothing).  Scaling is monotone, so raw keys serve the scaled maximum.
 __global__ void __launch_bounds__(256)
 head0_max_kernel(const uint16_t* __restrict__ scores, uint32_t n, uint32_t* __restrict__ partial) {
     const uint32_t tile = blockIdx.x * 4 + (threadIdx.x >> 6);
     const uint32_t i = tile * 64 + (threadIdx.x & 63u);
-    const uint32_t key = i < n ? order_key(scores[i]) : 0u;
+    const uint32_t bits = i < n ? scores[i] : 0u;
+    const uint32_t key = i < n && !is_nan_half(bits) ? order_key(bits) : 0u;
     const uint32_t best = wave_max_u32(key);
     if ((threadIdx.x & 63u) == 0 && tile * 64 < n) partial[tile] = best;
 }
@@ -323,6 +324,8 @@ __global__ void __launch_bounds__(kThreads) count_kernel(SelectArgs a) {
     hist_clear(whist);
     best = block_max(best, tmp);  // its barrier also orders the histogram clear
     const float thr = threshold_from_key(best, (a.flags & HS_SELECT_SCALE_RAW) != 0, a.alpha);
+    // the history cover does not reject nonfinite scores (NaN counts as below)
+    const bool cover = (a.flags & HS_SELECT_COVER) != 0;
     uint32_t count = 0, bad = 0;
     uint32_t keyw[kRun / 2] = {};
 #pragma unroll
@@ -330,7 +333,7 @@ __global__ void __launch_bounds__(kThreads) count_kernel(SelectArgs a) {
         const uint32_t b = half_at(packed, j);
         keyw[j >> 1] |= order_key(b) << ((j & 1u) * 16u);
         if (begin + j < a.n) {
-            if (!finite_half(b)) {
+            if (!cover && !finite_half(b)) {
                 bad = 1;
             } else {
                 count += h2f(b) >= thr ? 1u : 0u;
@@ -365,6 +368,31 @@ __device__ int derive_k(const SelectArgs& a, const uint32_t* head_count, const u
     const bool fp32_counts = (a.flags & HS_SELECT_FP32_COUNTS) != 0;
     int code = HS_OK;
     k = 0;
+    if (a.flags & HS_SELECT_COVER) {
+        // history cover bound (policy/full_gqa_runtime.cpp:317-331): every
+        // count gets the current token's possible +1, the mean must be >= 1,
+        // and the cap is that of n + 1 columns
+        if (!isfinite(thr)) return HS_ERR_THRESHOLD;
+        float total = 0.0f;
+        for (uint32_t first = 0; first < a.heads && code == HS_OK; first += 64) {
+            const uint32_t hh = first + lane;
+            const bool valid = hh < a.heads;
+            const float c = valid ? static_cast<float>(head_count[hh] + 1u) : 0.0f;
+            const float rounded = fp32_counts ? c : h2f(f2h(c));
+            if (__ballot(valid && !isfinite(rounded))) code = HS_ERR_COUNT;
+            total += wave_sum_f32(valid ? rounded : 0.0f);
+        }
+        if (code != HS_OK) return code;
+        const float q = __fdiv_rn(total, static_cast<float>(a.heads));
+        const float mean = fp32_counts ? q : h2f(f2h(q));
+        if (!isfinite(mean) || !(mean >= 1.0f)) return HS_ERR_MEAN;
+        uint64_t cap_k = static_cast<uint64_t>(
+            floor(static_cast<double>(a.n + 1u) * static_cast<double>(a.ratio)));
+        cap_k = cap_k < a.n ? cap_k : a.n;
+        const uint64_t kk = static_cast<uint64_t>(mean);
+        k = static_cast<uint32_t>(kk < cap_k ? kk : cap_k);
+        return HS_OK;
+    }
     if (head_bad[0]) return HS_ERR_NONFINITE;
     if (!isfinite(thr)) return HS_ERR_THRESHOLD;
     float total = 0.0f;
@@ -1271,10 +1299,14 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
     if (!std::isfinite(alpha) || alpha < 0 || !std::isfinite(ratio) || ratio <= 0 || ratio > 1)
         return reject("GQA selector numeric parameters");
     if (flags & ~uint32_t(HS_SELECT_SCALE_RAW | HS_SELECT_FP32_COUNTS | HS_SELECT_REQUIRE_K |
-                          HS_SELECT_ID_ORDER))
+                          HS_SELECT_ID_ORDER | HS_SELECT_COVER))
         return reject("select: unknown flags");
+    // the history cover caps at the selection over n + 1 columns
+    const bool cover = (flags & HS_SELECT_COVER) != 0;
     const uint64_t kmax = std::min<uint64_t>(
-        n, static_cast<uint64_t>(std::floor(static_cast<double>(n) * static_cast<double>(ratio))));
+        n, static_cast<uint64_t>(std::floor(static_cast<double>(cover ? n + 1ull : n) *
+                                            static_cast<double>(ratio))));
+    if (cover && kmax == 0) return reject("payload prefetch historical cap/range mismatch");
     if (ids_stride < kmax || ids_stride > 0xffffffffu)
         return reject("select: ids_stride below the largest possible k");
     // A workspace of select_workspace_bytes(heads, n) covers every ratio.

@@ -12,7 +12,7 @@ import math
 
 import torch
 
-from . import (HS_SELECT_FP32_COUNTS, HS_SELECT_ID_ORDER, HS_SELECT_REQUIRE_K, HS_SELECT_SCALE_RAW, HsError, check,
+from . import (HS_SELECT_COVER, HS_SELECT_FP32_COUNTS, HS_SELECT_ID_ORDER, HS_SELECT_REQUIRE_K, HS_SELECT_SCALE_RAW, HsError, check,
                lib)
 
 H, KH, D = 32, 8, 128
@@ -83,15 +83,18 @@ def select_workspace_bytes(heads, n):
 
 
 def select(scores, heads, stride, n, alpha, ratio, *, scale_raw=False, fp32_counts=False,
-           require_k=False, id_order=False, head0_partial=None, ids=None, ids_stride=None, counts=None,
-           member=None, status=None, ws=None, stream=None):
+           require_k=False, id_order=False, cover=False, head0_partial=None, ids=None,
+           ids_stride=None, counts=None, member=None, status=None, ws=None, stream=None):
     """select_gqa_scores on device.  Returns (ids, counts, member, status).
 
     ids per head are in rank order (key desc, id asc), or ascending id order
-    with id_order=True (same set, no rank sort)."""
+    with id_order=True (same set, no rank sort).  cover=True selects the
+    history cover of prefetch_payload (policy/full_gqa_runtime.cpp:299-344)
+    over the n historical columns; status["k"] is then the cover bound."""
     _need_cuda(scores)
     dev = scores.device
-    kmax = min(n, math.floor(float(n) * float(ctypes.c_float(ratio).value)))
+    cols = n + 1 if cover else n
+    kmax = min(n, math.floor(float(cols) * float(ctypes.c_float(ratio).value)))
     if ids_stride is None:
         ids_stride = max(1, kmax)
     if ids is None:
@@ -103,7 +106,8 @@ def select(scores, heads, stride, n, alpha, ratio, *, scale_raw=False, fp32_coun
     if ws is None:
         ws = workspace(select_workspace_bytes(heads, n), dev)
     flags = ((HS_SELECT_SCALE_RAW if scale_raw else 0) | (HS_SELECT_FP32_COUNTS if fp32_counts else 0)
-             | (HS_SELECT_REQUIRE_K if require_k else 0) | (HS_SELECT_ID_ORDER if id_order else 0))
+             | (HS_SELECT_REQUIRE_K if require_k else 0) | (HS_SELECT_ID_ORDER if id_order else 0)
+             | (HS_SELECT_COVER if cover else 0))
     check(lib().hs_gqa_select(_p(scores), heads, stride, n, alpha, ratio, flags,
                               _p(head0_partial), _p(ids), ids_stride, _p(counts), _p(member),
                               _p(status), _p(ws), _s(stream)))

@@ -67,7 +67,8 @@ int hs_full_gqa_pipeline(const void *query_dev, const void *keys_dev,
  * zero keys (no access).  pool_rows is ignored when rows_dev is NULL.  Scores written to
  * scores_dev[h*score_stride + t] for t < tokens; 1 <= tokens <= 65536.
  * head0_partial_dev (nullable, ceil(tokens/64) uint32) receives the order
- * key maximum of head-0 raw scores per 64-token tile, for hs_gqa_select. */
+ * key maximum of the non-NaN head-0 raw scores per 64-token tile (0 when the
+ * tile has none), for hs_gqa_select. */
 int hs_gqa_score(const uint16_t *q_dev, const uint16_t *keys_dev,
                  size_t key_stride_words, const int32_t *rows_dev,
                  uint32_t pool_rows, uint32_t tokens, uint16_t *scores_dev,
@@ -83,12 +84,23 @@ int hs_gqa_score(const uint16_t *q_dev, const uint16_t *keys_dev,
  * is the reference's fp32_counts; HS_SELECT_REQUIRE_K rejects k == 0;
  * HS_SELECT_ID_ORDER lists each head's selection in ascending id order (the
  * same set; skips the rank sort).
+ * HS_SELECT_COVER selects the history cover of prefetch_payload
+ * (policy/full_gqa_runtime.cpp:299-344) instead: the n columns are the
+ * history (n = position), each head's count is 1 + #{scaled >= thr} (room
+ * for the current token not yet scored), cap = min(n, floor((n+1)*ratio)),
+ * k = min(cap, trunc(mean)) is the cover bound, and nonfinite scores are not
+ * rejected (NaN is skipped by the head-0 maximum and compares false).  Its
+ * errors: HS_ERR_ARGUMENT when cap == 0, HS_ERR_THRESHOLD (nonfinite
+ * threshold), HS_ERR_COUNT (a count beyond the F16 range), HS_ERR_MEAN (mean
+ * bound nonfinite or below 1).  The cover of every head contains every
+ * historical id that head's final selection over n + 1 columns can pick.
  * Outputs: ids_dev [heads][ids_stride] uint32 in rank order (key desc, id
  * asc) unless HS_SELECT_ID_ORDER, counts_dev [heads] uint32, status_dev
  * (k, tied heads, code), and
  * optionally member_dev [heads][ceil(n/32)] uint32 bitmaps of the selected
  * ids (input of hs_gqa_sparse_attention).  ids_stride must be >= the
- * largest possible k = min(n, floor(n*ratio)).  workspace_dev holds
+ * largest possible k = min(n, floor(n*ratio)) (HS_SELECT_COVER:
+ * min(n, floor((n+1)*ratio))).  workspace_dev holds
  * hs_gqa_select_workspace_bytes(heads, n) bytes of scratch (no
  * initialisation needed).
  * head0_partial_dev: NULL, or the per-tile maxima from hs_gqa_score over
@@ -101,7 +113,8 @@ enum {
     HS_SELECT_SCALE_RAW = 1u,
     HS_SELECT_FP32_COUNTS = 2u,
     HS_SELECT_REQUIRE_K = 4u,
-    HS_SELECT_ID_ORDER = 8u
+    HS_SELECT_ID_ORDER = 8u,
+    HS_SELECT_COVER = 16u
 };
 size_t hs_gqa_select_workspace_bytes(uint32_t heads, uint32_t n);
 int hs_gqa_select(const uint16_t *scores_dev, uint32_t heads, size_t stride,

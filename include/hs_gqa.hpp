@@ -7,6 +7,8 @@
 //        -> hillserve::gpu::FullGqaGpuScorer::score
 //   hillserve::policy::select_gqa_scores (policy/gqa_policy.hpp:14-21)
 //        -> hillserve::gpu::select_gqa_scores
+//   FullGqaRuntimePolicy::prefetch_payload's cover selection
+//   (policy/full_gqa_runtime.cpp:299-344) -> hillserve::gpu::history_cover_gqa
 //   hillserve::gqa_physical_union / pack_gqa_workspace (runtime/gqa_pack.hpp:12-58)
 //        -> hillserve::gpu::gqa_physical_union / pack_gqa_workspace
 //   hillserve::FpgaScoreBackend::score_raw_gqa (smartssd/adapter.hpp:73-76)
@@ -81,6 +83,24 @@ struct GQASelection {
 GQASelection select_gqa_scores(const std::vector<std::uint16_t>& scaled_scores, std::size_t heads,
                                std::size_t stride, std::size_t valid_tokens, float alpha,
                                float cap_ratio, bool fp32_counts = false);
+
+// The history cover that FullGqaRuntimePolicy::prefetch_payload selects
+// before the current token is scored (policy/full_gqa_runtime.cpp:299-344):
+// raw_scores F16 [heads][capacity] (host) whose columns t < position are the
+// history; each head's first `bound` ids of (key desc, id asc) over the
+// scaled scores, and their sorted union.  bound = min(min(position,
+// floor((position+1)*cap_ratio)), trunc(mean of F16(1 + count_h))), so every
+// head's final selection over position + 1 columns keeps its historical ids
+// inside its cover.  Failures throw std::runtime_error with the reference's
+// need() texts.
+struct GQAHistoryCover {
+    std::vector<std::vector<std::uint64_t>> per_head_ids;  // rank order
+    std::vector<std::uint64_t> physical_ids;               // sorted union
+    std::size_t bound = 0;
+};
+GQAHistoryCover history_cover_gqa(const std::vector<std::uint16_t>& raw_scores, std::size_t heads,
+                                  std::size_t capacity, std::uint64_t position, float alpha,
+                                  bool fp32_counts = false, float cap_ratio = 0.2f);
 
 // Sorted unique ids over the 32 heads; duplicates within a head or ids >=
 // visible throw std::invalid_argument.

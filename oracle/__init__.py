@@ -56,6 +56,9 @@ class Port:
                                  _P, _SZ, _P, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]
         L.hso_select_k.argtypes = [_P, _SZ, _SZ, _SZ, ctypes.c_float, ctypes.c_float,
                                    ctypes.c_int, ctypes.POINTER(_SZ)]
+        L.hso_history_cover.argtypes = [_P, _SZ, _SZ, _SZ, ctypes.c_float, ctypes.c_float,
+                                        ctypes.c_int, _P, _SZ, ctypes.POINTER(_SZ), _P,
+                                        ctypes.POINTER(_SZ)]
         L.hso_physical_union.argtypes = [_P, _P, _SZ, _SZ, _P, ctypes.POINTER(_SZ)]
         L.hso_pack.argtypes = [_P, _P, _SZ, _P, _SZ, _P, _SZ, _P, _SZ, _P, _P, _P]
         L.hso_gather_rows.argtypes = [_P, _P, _P, _SZ, _P, _P]
@@ -108,6 +111,21 @@ class Port:
                                ctypes.c_float(ratio), int(fp32_counts), _ptr(ids), width,
                                _ptr(counts), ctypes.byref(k2), ctypes.byref(tied))
         return rc, k2.value, ids[:, : k2.value], counts, tied.value
+
+    def history_cover(self, raw, heads, stride, position, alpha, ratio=0.2, fp32_counts=False):
+        """prefetch_payload's cover (policy/full_gqa_runtime.cpp:299-344) of the
+        RAW scores -> (rc, bound, ids[heads][bound] u32, physical u32)."""
+        raw = np.ascontiguousarray(raw, dtype=np.uint16)
+        width = max(1, position)
+        ids = np.zeros((heads, width), dtype=np.uint32)
+        physical = np.zeros(width, dtype=np.uint32)
+        bound, np_out = _SZ(0), _SZ(0)
+        rc = self.L.hso_history_cover(_ptr(raw), heads, stride, position, ctypes.c_float(alpha),
+                                      ctypes.c_float(ratio), int(fp32_counts), _ptr(ids), width,
+                                      ctypes.byref(bound), _ptr(physical), ctypes.byref(np_out))
+        if rc:
+            return rc, 0, None, None
+        return rc, bound.value, ids[:, : bound.value], physical[: np_out.value]
 
     def physical_union(self, ids_rows, visible):
         stride = max(1, max(len(r) for r in ids_rows))

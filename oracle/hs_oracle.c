@@ -225,6 +225,115 @@ int hso_select(const uint16_t *scaled, size_t heads, size_t stride, size_t n,
     return HSO_OK;
 }
 
+/* ---- history cover (policy/full_gqa_runtime.cpp:299-344) ---------------- */
+
+int hso_history_cover(const uint16_t *raw, size_t heads, size_t stride,
+                      size_t position, float alpha, float ratio, int fp32_counts,
+                      uint32_t *ids, size_t ids_stride, size_t *bound_out,
+                      uint32_t *physical, size_t *physical_n)
+{
+    /* :309-311 cap over position + 1 columns; position < capacity */
+    if (!raw || heads == 0 || heads > 128 || position == 0 || position >= stride)
+        return HSO_ERR_SHAPE;
+    size_t cap = (size_t)floor((double)(position + 1) * (double)ratio);
+    if (position < cap)
+        cap = position;
+    if (cap == 0)
+        return HSO_ERR_SHAPE;
+    /* :312 scaling */
+    uint16_t *scaled = (uint16_t *)malloc(sizeof(uint16_t) * heads * stride);
+    if (!scaled)
+        return HSO_ERR_SHAPE;
+    for (size_t i = 0; i < heads * stride; ++i)
+        scaled[i] = hso_scale_one(raw[i]);
+    /* :313-314 head-0 maximum as std::max(maximum, x): NaN never replaces it */
+    float maximum = -INFINITY;
+    for (size_t t = 0; t < position; ++t) {
+        const float x = hso_half_value(scaled[t]);
+        if (maximum < x)
+            maximum = x;
+    }
+    /* :315-316 threshold */
+    const float threshold = hso_half_value(hso_half_bits(maximum - alpha));
+    int rc = HSO_OK;
+    if (!is_finite_f(threshold))
+        rc = HSO_ERR_THRESHOLD;
+    /* :317-324 counts with one possible current token each */
+    float count_sum = 0.0f;
+    for (size_t h = 0; rc == HSO_OK && h < heads; ++h) {
+        uint64_t count = 1;
+        for (size_t t = 0; t < position; ++t)
+            count += hso_half_value(scaled[h * stride + t]) >= threshold;
+        const float rounded = fp32_counts ? (float)count
+                                          : hso_half_value(hso_half_bits((float)count));
+        if (!is_finite_f(rounded))
+            rc = HSO_ERR_COUNT;
+        count_sum += rounded;
+    }
+    size_t bound = 0;
+    if (rc == HSO_OK) {
+        /* :325-327 mean bound, :328 bound */
+        const float mean = fp32_counts
+                               ? count_sum / (float)heads
+                               : hso_half_value(hso_half_bits(count_sum / (float)heads));
+        if (!is_finite_f(mean) || !(mean >= 1.0f))
+            rc = HSO_ERR_MEAN;
+        else
+            bound = (size_t)mean < cap ? (size_t)mean : cap;
+    }
+    if (rc == HSO_OK && ids && ids_stride < bound)
+        rc = HSO_ERR_SHAPE;
+    if (rc != HSO_OK) {
+        free(scaled);
+        return rc;
+    }
+    /* :329-337 per head, the first `bound` of (key desc, id asc): stable
+     * counting sort on the order key, ids visited ascending */
+    uint32_t *start = (uint32_t *)malloc(sizeof(uint32_t) * 65536);
+    unsigned char *used = (unsigned char *)calloc(position, 1);
+    if (!start || !used) {
+        free(start);
+        free(used);
+        free(scaled);
+        return HSO_ERR_SHAPE;
+    }
+    for (size_t h = 0; h < heads; ++h) {
+        const uint16_t *row = scaled + h * stride;
+        memset(start, 0, sizeof(uint32_t) * 65536);
+        for (size_t t = 0; t < position; ++t)
+            start[hso_order_key(row[t])]++;
+        uint32_t running = 0;
+        for (int key = 65535; key >= 0; --key) {
+            const uint32_t c = start[key];
+            start[key] = running;
+            running += c;
+        }
+        for (size_t t = 0; t < position; ++t) {
+            const uint32_t p = start[hso_order_key(row[t])]++;
+            if (p < bound) {
+                if (ids)
+                    ids[h * ids_stride + p] = (uint32_t)t;
+                used[t] = 1;
+            }
+        }
+    }
+    /* :338-340 the sorted union */
+    size_t np = 0;
+    for (size_t t = 0; t < position; ++t)
+        if (used[t]) {
+            if (physical)
+                physical[np] = (uint32_t)t;
+            ++np;
+        }
+    if (physical_n)
+        *physical_n = np;
+    *bound_out = bound;
+    free(start);
+    free(used);
+    free(scaled);
+    return HSO_OK;
+}
+
 /* ---- union and pack (runtime/gqa_pack.hpp:12-58) ------------------------ */
 
 int hso_physical_union(const uint32_t *ids, const size_t *lens,

@@ -25,6 +25,14 @@
  *   hso_select           : known answers of tests/gqa_policy_tests.cpp:46-79
  *       and tests/quality_alpha_tests.cpp:32-77, brute-force std-sort order,
  *       and the compiled reference select_gqa_scores.
+ *   hso_history_cover    : the reference's own guarantee (full_gqa_prefetch_
+ *       tests.cpp:150-258): for any current-token scores, the final
+ *       selection over position + 1 columns (hso_select, pinned above) keeps
+ *       its historical ids inside the cover; bound == cap when the threshold
+ *       admits everything and bound == m + 1 when exactly m historical
+ *       tokens per head reach it; error cases of :310-327.  The reference
+ *       function itself (full_gqa_runtime.cpp) needs the absent
+ *       nlohmann/json.hpp and is not compiled.
  *   hso_physical_union / hso_pack / hso_gather_rows : tests/gqa_pack_tests.cpp
  *       known values, and the compiled reference pack_gqa_workspace.
  *   hso_attention_f64    : parity unpinned against the reference (its
@@ -109,6 +117,19 @@ int hso_pack(const uint32_t *ids, const size_t *lens, size_t ids_stride,
 void hso_gather_rows(const uint16_t *prefetched, const uint16_t *misses,
                      const int32_t *map, size_t count, uint16_t *k_out,
                      uint16_t *v_out);
+
+/* History cover of prefetch_payload, policy/full_gqa_runtime.cpp:299-344.
+ *   raw          F16 raw scores [heads][stride]; columns t < position are the
+ *                history (position < stride, room for the current token)
+ *   ids          [heads][ids_stride] the first `bound` of (key desc, id asc)
+ *   bound_out    min(min(position, floor((position+1)*ratio)), trunc(mean))
+ *   physical     sorted union of all heads' ids (position entries max)
+ * Returns HSO_ERR_SHAPE (cap 0 / shapes), HSO_ERR_THRESHOLD, HSO_ERR_COUNT
+ * or HSO_ERR_MEAN like the reference's need() checks. */
+int hso_history_cover(const uint16_t *raw, size_t heads, size_t stride,
+                      size_t position, float alpha, float ratio, int fp32_counts,
+                      uint32_t *ids, size_t ids_stride, size_t *bound_out,
+                      uint32_t *physical, size_t *physical_n);
 
 /* Dense-reference decode attention restricted to a selection, FP64.
  * Semantics of patches/llama-b6000-external-attention-device.patch:49-66:

@@ -494,6 +494,56 @@ void pack_contracts() {
 
 }  // namespace
 
+// ---- history cover (policy/full_gqa_runtime.cpp:299-344) ------------------------
+// The checks of tests/full_gqa_prefetch_tests.cpp:196-233 on the selection part:
+// bound-sized per-head covers of historical ids, a sorted union, the sparse
+// threshold bound m + 1, and the final selection over position + 1 columns
+// inside the cover whatever the current token scores.
+void cover_contracts() {
+    const std::size_t H = 32, capacity = 3000, position = 2500;
+    std::uint32_t state = 0x2468ace1u;
+    auto next = [&] { state ^= state << 13; state ^= state >> 17; state ^= state << 5; return state; };
+    std::vector<std::uint16_t> raw(H * capacity, half_bits(0.f));
+    for (auto& r : raw) r = half_bits(float(int(next() % 2001) - 1000) / 16.f);
+    for (float alpha : {0.5f, 3.f}) {
+        const auto cover = history_cover_gqa(raw, H, capacity, position, alpha);
+        const std::size_t cap = std::min<std::size_t>(position, std::size_t(std::floor(double(position + 1) * double(.2f))));
+        check(cover.bound >= 1 && cover.bound <= cap, "cover bound within the cap");
+        std::vector<unsigned char> used(position, 0);
+        for (const auto& ids : cover.per_head_ids) {
+            check(ids.size() == cover.bound, "every head's cover holds bound ids");
+            for (auto id : ids) { check(id < position, "cover never holds current or future KV"); used[id] = 1; }
+        }
+        std::vector<std::uint64_t> expect;
+        for (std::size_t t = 0; t < position; ++t) if (used[t]) expect.push_back(t);
+        check(cover.physical_ids == expect, "physical cover is the sorted union");
+        for (float current : {0.f, 900.f, -900.f}) {
+            auto final_raw = raw;
+            for (std::size_t h = 0; h < H; ++h) final_raw[h * capacity + position] = half_bits(current + float(h));
+            std::vector<std::uint16_t> scaled(final_raw.size());
+            for (std::size_t i = 0; i < scaled.size(); ++i) scaled[i] = half_bits(half_value(final_raw[i]) / std::sqrt(128.f));
+            const auto sel = select_gqa_scores(scaled, H, capacity, position + 1, alpha, .2f);
+            for (std::size_t h = 0; h < H; ++h)
+                for (auto id : sel.ids[h])
+                    if (id < position)
+                        check(std::find(cover.per_head_ids[h].begin(), cover.per_head_ids[h].end(), id) !=
+                                  cover.per_head_ids[h].end(),
+                              "threshold-count bounded history covers final ordered selection");
+        }
+    }
+    // constructed sparse threshold: 5 historical tokens per head near the top
+    std::vector<std::uint16_t> sparse(H * capacity, half_bits(-500.f));
+    for (std::size_t h = 0; h < H; ++h)
+        for (std::size_t j = 0; j < 5; ++j) sparse[h * capacity + 40 + 300 * j + h] = half_bits(500.f + float(j));
+    const auto small = history_cover_gqa(sparse, H, capacity, position, 1.f);
+    check(small.bound == 6, "F16 threshold-count upper bound includes unknown current contribution");
+    rejects([&] { history_cover_gqa(raw, H, capacity, 1, 1.f); }, "cap 0 rejected");
+    rejects([&] { history_cover_gqa(raw, H, capacity, capacity, 1.f); }, "no room for the current token");
+    auto inf = raw;
+    inf[7] = 0x7c00u;
+    rejects([&] { history_cover_gqa(inf, H, capacity, position, 1.f); }, "nonfinite historical threshold");
+}
+
 int main() {
     int devices = 0;
     if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0) {
@@ -505,6 +555,7 @@ int main() {
         scorer_contracts();
         kernel_contracts();
         pack_contracts();
+        cover_contracts();
         std::cout << "{\"status\":\"passed\",\"cases\":" << cases
                   << ",\"bitwise_scores_compared\":" << comparisons << "}" << std::endl;
         return 0;

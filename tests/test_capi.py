@@ -58,7 +58,7 @@ def test_select_rejects_bad_parameters(hs):
     assert call(ratio=0.0) == hs.HS_ERR_ARGUMENT
     assert call(ratio=1.5) == hs.HS_ERR_ARGUMENT
     assert call(ids_stride=11) == hs.HS_ERR_ARGUMENT  # floor(64*0.2f) = 12
-    assert call(flags=16) == hs.HS_ERR_ARGUMENT
+    assert call(flags=32) == hs.HS_ERR_ARGUMENT
     assert call(scores=None) == hs.HS_ERR_ARGUMENT
 
 
@@ -98,7 +98,7 @@ def test_cpp_adapters_exported(hs):
                          capture_output=True, text=True, check=True).stdout
     for name in ("hillserve::gpu::FullGqaGpuScorer::score(", "hillserve::gpu::select_gqa_scores(",
                  "hillserve::gpu::gqa_physical_union(", "hillserve::gpu::pack_gqa_workspace(",
-                 "hillserve::gpu::GpuScoreBackend::score_raw_gqa("):
+                 "hillserve::gpu::GpuScoreBackend::score_raw_gqa(", "hillserve::gpu::history_cover_gqa("):
         assert name in out, name
 
 
