@@ -68,6 +68,37 @@ class Status(ctypes.Structure):
     ]
 
 
+class ScoreJob(ctypes.Structure):
+    """hs_score_job_t of include/hs_gpu.h."""
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("keys", ctypes.c_void_p),
+        ("scores", ctypes.c_void_p),
+        ("head0_partial", ctypes.c_void_p),
+        ("key_stride_words", ctypes.c_uint32),
+        ("tokens", ctypes.c_uint32),
+        ("score_stride", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
+class SelectJob(ctypes.Structure):
+    """hs_select_job_t of include/hs_gpu.h."""
+    _fields_ = [
+        ("scores", ctypes.c_void_p),
+        ("head0_partial", ctypes.c_void_p),
+        ("ids", ctypes.c_void_p),
+        ("counts", ctypes.c_void_p),
+        ("member", ctypes.c_void_p),
+        ("status", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("stride", ctypes.c_uint32),
+        ("n", ctypes.c_uint32),
+        ("ids_stride", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
 _P = ctypes.c_void_p
 _SZ = ctypes.c_size_t
 _U32 = ctypes.c_uint32
@@ -80,8 +111,10 @@ SIGNATURES = {
     "hs_last_error": (ctypes.c_char_p, []),
     "hs_full_gqa_pipeline": (_I, [_P, _P, _P, _U32, _P]),
     "hs_gqa_score": (_I, [_P, _P, _SZ, _P, _U32, _U32, _P, _SZ, _P, _P]),
+    "hs_gqa_score_batched": (_I, [_P, _U32, _P]),
     "hs_gqa_select_workspace_bytes": (_SZ, [_U32, _U32]),
     "hs_gqa_select": (_I, [_P, _U32, _SZ, _U32, _F, _F, _U32, _P, _P, _SZ, _P, _P, _P, _P, _P]),
+    "hs_gqa_select_batched": (_I, [_P, _U32, _U32, _F, _F, _U32, _P]),
     "hs_gqa_union_workspace_bytes": (_SZ, [_U32]),
     "hs_gqa_physical_union": (_I, [_P, _P, _SZ, _U32, _P, _P, _P, _P, _P]),
     "hs_gqa_pack": (_I, [_P, _U32, _P, _U32, _P, _P, _SZ, _P, _U32, _U32, _P, _P, _P, _P, _P]),

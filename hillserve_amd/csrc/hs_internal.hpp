@@ -32,11 +32,16 @@ int launch_score(const uint16_t* q, const uint16_t* keys, size_t stride_words,
                  const int32_t* rows, uint32_t pool_rows, uint32_t tokens, uint16_t* scores,
                  size_t score_stride, uint32_t* head0_partial, hipStream_t stream);
 
+int launch_score_batched(const hs_score_job_t* jobs, uint32_t count, hipStream_t stream);
+
 size_t select_workspace_bytes(uint32_t heads, uint32_t n);
 int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_t n,
                   float alpha, float ratio, uint32_t flags, const uint32_t* head0_partial,
                   uint32_t* ids, size_t ids_stride, uint32_t* counts, uint32_t* member,
                   hs_status_t* status, void* workspace, hipStream_t stream);
+
+int launch_select_batched(const hs_select_job_t* jobs, uint32_t count, uint32_t heads,
+                          float alpha, float ratio, uint32_t flags, hipStream_t stream);
 
 size_t attention_workspace_bytes(uint32_t n);
 int launch_attention(const float* q, const uint8_t* pool, size_t row_bytes,

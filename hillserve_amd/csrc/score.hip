@@ -42,37 +42,57 @@ __device__ __forceinline__ float hi_half(uint32_t w) { return h2f(w >> 16); }
 // LDS slot (in 16 B units) of chunk c of tile token t.
 __device__ __forceinline__ uint32_t slot(uint32_t t, uint32_t c) { return t * kChunks + (c ^ (t & 15u)); }
 
-template <bool kRows>
+// One scoring job: a query, its keys and where the scores go.  A launch
+// covers one job or, batched, up to kMaxBatch of them; job j owns the
+// (token tile, KV head) ids [first_id, first_id + tiles_j * 8) of the launch.
+struct ScoreJob {
+    const uint32_t* q32;  // F16 pairs: head h channel c at q32[(h*128 + c)/2]
+    const uint16_t* keys;
+    uint16_t* out;
+    uint32_t* head0_partial;
+    uint32_t stride_words, n, out_stride, first_id;
+};
+constexpr uint32_t kMaxBatch = 16;
+struct ScoreJobs {
+    ScoreJob job[kMaxBatch];
+    uint32_t count, total_ids;
+};
+
+template <bool kRows, bool kBatch>
 __global__ void __launch_bounds__(kWavesPerBlock * 64)
-score_kernel(const uint32_t* __restrict__ q32, const uint16_t* __restrict__ keys,
-             uint32_t stride_words, const int32_t* __restrict__ rows, uint32_t pool_rows,
-             uint32_t n, uint16_t* __restrict__ out, uint32_t out_stride,
-             uint32_t* __restrict__ head0_partial) {
+score_kernel(const ScoreJobs jobs, const int32_t* __restrict__ rows, uint32_t pool_rows) {
     __shared__ uint4 lds[kWavesPerBlock][kTileTokens * kChunks];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     uint4* region = lds[w];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + w);
     const uint32_t waves = gridDim.x * kWavesPerBlock;
-    const uint32_t tiles = ((n + kTileTokens - 1) / kTileTokens) * 8;  // (token tile, KV head)
+    const uint32_t tiles = jobs.total_ids;  // (token tile, KV head) pairs of all jobs
 
-    // Row index of token (tile >> 3) * 64 + lane, or ~0 when it reads as zero keys
-    // (past n, or a mapped row outside the pool).
-    auto row_of = [&](uint32_t id) -> uint32_t {
-        const uint32_t token = (id >> 3) * kTileTokens + lane;
-        if (token >= n) return 0xffffffffu;
+    // job of a launch-wide id (wave-uniform)
+    auto job_of = [&](uint32_t id) -> uint32_t {
+        if (!kBatch) return 0;
+        uint32_t j = 0;
+        for (uint32_t i = 1; i < jobs.count; ++i) j = id >= jobs.job[i].first_id ? i : j;
+        return j;
+    };
+    // Row index of token (tile >> 3) * 64 + lane of the job, or ~0 when it
+    // reads as zero keys (past n, or a mapped row outside the pool).
+    auto row_of = [&](const ScoreJob& jb, uint32_t id) -> uint32_t {
+        const uint32_t token = ((id - jb.first_id) >> 3) * kTileTokens + lane;
+        if (token >= jb.n) return 0xffffffffu;
         if (!kRows) return token;
         const uint32_t r = static_cast<uint32_t>(rows[token]);
         return r < pool_rows ? r : 0xffffffffu;
     };
     // Instruction j: lane reads chunk (lane & 15) of tile token 4j + (lane >> 4).
-    auto load = [&](uint32_t id, uint32_t my_row, uint4 (&v)[16]) {
-        const uint16_t* base = keys + (id & 7u) * 128u + (lane & 15u) * 8u;
+    auto load = [&](const ScoreJob& jb, uint32_t id, uint32_t my_row, uint4 (&v)[16]) {
+        const uint16_t* base = jb.keys + ((id - jb.first_id) & 7u) * 128u + (lane & 15u) * 8u;
 #pragma unroll
         for (uint32_t j = 0; j < 16; ++j) {
             const uint32_t r = __shfl(my_row, 4 * j + (lane >> 4), 64);
             v[j] = r != 0xffffffffu
-                       ? *reinterpret_cast<const uint4*>(base + static_cast<size_t>(r) * stride_words)
+                       ? *reinterpret_cast<const uint4*>(base + static_cast<size_t>(r) * jb.stride_words)
                        : make_uint4(0u, 0u, 0u, 0u);
         }
     };
@@ -80,10 +100,13 @@ score_kernel(const uint32_t* __restrict__ q32, const uint16_t* __restrict__ keys
 #pragma unroll
         for (uint32_t j = 0; j < 16; ++j) region[slot(4 * j + (lane >> 4), lane & 15u)] = v[j];
     };
-    auto compute = [&](uint32_t id) {
-        const uint32_t head_kv = id & 7u;  // wave-uniform
-        // q32 holds F16 pairs; head h channel c lives in q32[(h*128 + c)/2].
-        const uint32_t* qh = q32 + head_kv * 4 * 64;
+    auto compute = [&](const ScoreJob& jb, uint32_t id) {
+        const uint32_t local = id - jb.first_id;
+        const uint32_t head_kv = local & 7u;  // wave-uniform
+        // Q is never written by the kernel: reading it through the constant
+        // address space lets every Q operand come from a scalar load
+        using ConstU32 = const __attribute__((address_space(4))) uint32_t;
+        ConstU32* qh = (ConstU32*)(jb.q32) + head_kv * 4 * 64;
         float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
         for (uint32_t j = 0; j < 16; ++j) {
@@ -105,40 +128,58 @@ score_kernel(const uint32_t* __restrict__ q32, const uint16_t* __restrict__ keys
                 a3 = __builtin_fmaf(hi_half(q3), khi, a3);
             }
         }
-        const uint32_t token = (id >> 3) * kTileTokens + lane;
+        const uint32_t token = (local >> 3) * kTileTokens + lane;
         const uint32_t s0 = f2h(a0), s1 = f2h(a1), s2 = f2h(a2), s3 = f2h(a3);
-        if (token < n) {
-            uint16_t* o = out + static_cast<size_t>(head_kv * 4) * out_stride + token;
+        if (token < jb.n) {
+            uint16_t* o = jb.out + static_cast<size_t>(head_kv * 4) * jb.out_stride + token;
             o[0] = static_cast<uint16_t>(s0);
-            o[out_stride] = static_cast<uint16_t>(s1);
-            o[2 * static_cast<size_t>(out_stride)] = static_cast<uint16_t>(s2);
-            o[3 * static_cast<size_t>(out_stride)] = static_cast<uint16_t>(s3);
+            o[jb.out_stride] = static_cast<uint16_t>(s1);
+            o[2 * static_cast<size_t>(jb.out_stride)] = static_cast<uint16_t>(s2);
+            o[3 * static_cast<size_t>(jb.out_stride)] = static_cast<uint16_t>(s3);
         }
-        if (head0_partial != nullptr && head_kv == 0) {
+        if (jb.head0_partial != nullptr && head_kv == 0) {
             // NaN is skipped, like std::max over the scores
-            const uint32_t best = wave_max_u32(token < n && !is_nan_half(s0) ? order_key(s0) : 0u);
-            if (lane == 0) head0_partial[id >> 3] = best;
+            const uint32_t best =
+                wave_max_u32(token < jb.n && !is_nan_half(s0) ? order_key(s0) : 0u);
+            if (lane == 0) jb.head0_partial[local >> 3] = best;
         }
     };
 
     uint4 v[16];
     uint32_t id = wave;
     if (id >= tiles) return;
-    uint32_t next_row = row_of(id);
-    load(id, next_row, v);
-    if (id + waves < tiles) next_row = row_of(id + waves);
+    ScoreJob cur = jobs.job[job_of(id)];
+    uint32_t next_row = row_of(cur, id);
+    load(cur, id, next_row, v);
+    ScoreJob nxt = cur;
+    if (id + waves < tiles) {
+        nxt = jobs.job[job_of(id + waves)];
+        next_row = row_of(nxt, id + waves);
+    }
     while (id < tiles) {
         const uint32_t next = id + waves;
         stash(v);
         __builtin_amdgcn_wave_barrier();
+        const ScoreJob here = cur;
         if (next < tiles) {
-            load(next, next_row, v);
-            if (next + waves < tiles) next_row = row_of(next + waves);
+            load(nxt, next, next_row, v);
+            cur = nxt;
+            if (next + waves < tiles) {
+                nxt = jobs.job[job_of(next + waves)];
+                next_row = row_of(nxt, next + waves);
+            }
         }
-        compute(id);
+        compute(here, id);
         __builtin_amdgcn_wave_barrier();
         id = next;
     }
+}
+
+// 8 waves per CU (two per SIMD, 128 KiB of LDS), each streaming its share of
+// the (token tile, KV head) pairs.
+uint32_t score_grid(uint32_t ids) {
+    const uint32_t max_blocks = (8u / kWavesPerBlock) * static_cast<uint32_t>(device_cu_count());
+    return std::min<uint32_t>((ids + kWavesPerBlock - 1) / kWavesPerBlock, max_blocks);
 }
 
 }  // namespace
@@ -156,27 +197,56 @@ int launch_score(const uint16_t* q, const uint16_t* keys, size_t stride_words,
         return reject("score: keys must be 16-byte aligned");
     if ((reinterpret_cast<uintptr_t>(q) & 3u) != 0)
         return reject("score: query must be 4-byte aligned");
-    // 8 waves per CU (two per SIMD, 128 KiB of LDS), each streaming its share
-    // of (token tile, KV head) pairs
-    const uint32_t tiles = ((tokens + kTileTokens - 1) / kTileTokens) * 8;
-    const uint32_t max_blocks = (8u / kWavesPerBlock) * static_cast<uint32_t>(device_cu_count());
-    const uint32_t grid = std::min<uint32_t>((tiles + kWavesPerBlock - 1) / kWavesPerBlock, max_blocks);
-    const uint32_t* q32 = reinterpret_cast<const uint32_t*>(q);
+    ScoreJobs jobs{};
+    jobs.count = 1;
+    jobs.job[0] = ScoreJob{reinterpret_cast<const uint32_t*>(q), keys, scores, head0_partial,
+                           static_cast<uint32_t>(stride_words), tokens,
+                           static_cast<uint32_t>(score_stride), 0u};
+    jobs.total_ids = ((tokens + kTileTokens - 1) / kTileTokens) * 8;  // (token tile, KV head)
+    const dim3 grid(score_grid(jobs.total_ids)), block(kWavesPerBlock * 64);
     if (rows)
-        hipLaunchKernelGGL(score_kernel<true>, dim3(grid), dim3(kWavesPerBlock * 64), 0, stream, q32, keys,
-                           static_cast<uint32_t>(stride_words), rows, pool_rows, tokens, scores,
-                           static_cast<uint32_t>(score_stride), head0_partial);
+        hipLaunchKernelGGL((score_kernel<true, false>), grid, block, 0, stream, jobs, rows, pool_rows);
     else
-        hipLaunchKernelGGL(score_kernel<false>, dim3(grid), dim3(kWavesPerBlock * 64), 0, stream, q32, keys,
-                           static_cast<uint32_t>(stride_words), rows, 0u, tokens, scores,
-                           static_cast<uint32_t>(score_stride), head0_partial);
+        hipLaunchKernelGGL((score_kernel<false, false>), grid, block, 0, stream, jobs, rows, 0u);
     const hipError_t status = hipGetLastError();
     return status == hipSuccess ? HS_OK : hip_fail(status, "score launch");
+}
+
+int launch_score_batched(const hs_score_job_t* jobs, uint32_t count, hipStream_t stream) {
+    if (!jobs || count == 0 || count > kMaxBatch) return reject("score batch: 1..16 jobs");
+    ScoreJobs table{};
+    table.count = count;
+    uint32_t first = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const hs_score_job_t& j = jobs[i];
+        if (!j.q || !j.keys || !j.scores) return reject("score batch: null pointer");
+        if (j.key_stride_words != 1024 && j.key_stride_words != 2048)
+            return reject("score batch: key stride must be 1024 or 2048 F16 words");
+        if (j.tokens == 0 || j.tokens > 65536) return reject("score batch: tokens must be 1..65536");
+        if (j.score_stride < j.tokens) return reject("score batch: score stride must be >= tokens");
+        if ((reinterpret_cast<uintptr_t>(j.keys) & 15u) || (reinterpret_cast<uintptr_t>(j.q) & 3u))
+            return reject("score batch: keys must be 16-byte and queries 4-byte aligned");
+        table.job[i] = ScoreJob{reinterpret_cast<const uint32_t*>(j.q), j.keys, j.scores,
+                                j.head0_partial, j.key_stride_words, j.tokens, j.score_stride,
+                                first};
+        first += ((j.tokens + kTileTokens - 1) / kTileTokens) * 8;
+    }
+    table.total_ids = first;
+    hipLaunchKernelGGL((score_kernel<false, true>), dim3(score_grid(first)),
+                       dim3(kWavesPerBlock * 64), 0, stream, table, nullptr, 0u);
+    const hipError_t status = hipGetLastError();
+    return status == hipSuccess ? HS_OK : hip_fail(status, "score batch launch");
 }
 
 }  // namespace hs
 
 extern "C" {
+
+int hs_gqa_score_batched(const hs_score_job_t* jobs, uint32_t count, void* stream) {
+    hs::clear_error();
+    return hs::launch_score_batched(jobs, count, hs::as_stream(stream));
+}
+
 
 int hs_gqa_score(const uint16_t* q_dev, const uint16_t* keys_dev, size_t key_stride_words,
                  const int32_t* rows_dev, uint32_t pool_rows, uint32_t tokens,

@@ -79,16 +79,19 @@ struct SelectPlan {
     uint32_t kcap = 0;  // per-head capacity of the rank-sorted lists (>= k)
 };
 
-SelectPlan plan_select(uint32_t heads, uint32_t n, uint32_t kmax) {
+__host__ __device__ constexpr size_t round256(size_t bytes) { return (bytes + 255) & ~size_t(255); }
+
+// Workspace layout of one selection (host and device agree on it).
+__host__ __device__ SelectPlan plan_select(uint32_t heads, uint32_t n, uint32_t kmax) {
     SelectPlan p;
     p.S = (n + kSlice - 1) / kSlice;
     p.groups = heads * p.S;
     p.partials = (n + 63) / 64;
-    p.cap = std::max<uint32_t>(1u, std::min(kSlice, kmax));
+    p.cap = kmax < kSlice ? (kmax > 1u ? kmax : 1u) : kSlice;
     size_t at = 0;
     auto take = [&](size_t bytes) {
         const size_t here = at;
-        at += align256(bytes);
+        at += round256(bytes);
         return here;
     };
     p.off_plan = take(sizeof(SelectPlanDev));
@@ -97,7 +100,7 @@ SelectPlan plan_select(uint32_t heads, uint32_t n, uint32_t kmax) {
     p.off_bad = take(sizeof(uint32_t) * p.groups);
     p.off_hi = take(sizeof(uint32_t) * 256 * p.groups);
     p.off_lo = take(sizeof(uint32_t) * 256 * p.groups);
-    p.kcap = std::max<uint32_t>(1u, kmax);
+    p.kcap = kmax > 1u ? kmax : 1u;
     p.off_sort = take(sizeof(uint32_t) * size_t(heads) * p.kcap);
     p.off_keys = take(sizeof(uint16_t) * size_t(heads) * p.kcap);
     p.off_m = take(sizeof(uint32_t) * 4 * p.groups);
@@ -106,6 +109,14 @@ SelectPlan plan_select(uint32_t heads, uint32_t n, uint32_t kmax) {
     p.off_key16 = take(sizeof(uint16_t) * size_t(heads) * p.key_stride);
     p.total = at;
     return p;
+}
+
+// Largest possible k: min(n, floor(n*ratio)), over n + 1 columns for the
+// history cover.
+__host__ __device__ inline uint32_t kmax_of(uint32_t n, float ratio, uint32_t flags) {
+    const uint64_t cols = (flags & HS_SELECT_COVER) ? uint64_t(n) + 1 : uint64_t(n);
+    const uint64_t k = static_cast<uint64_t>(floor(static_cast<double>(cols) * static_cast<double>(ratio)));
+    return static_cast<uint32_t>(k < n ? k : n);
 }
 
 struct SelectArgs {
@@ -135,16 +146,77 @@ struct SelectArgs {
     hs_status_t* status;
 };
 
+// One selection of a launch: a batched launch runs up to kMaxBatch of them
+// (the decode sequences of a batch), one per blockIdx.y, sharing heads, alpha,
+// ratio and flags; every job has its own workspace.
+constexpr uint32_t kMaxBatch = 16;
+struct SelectJob {
+    const uint16_t* scores;
+    const uint32_t* partial;  // head-0 tile maxima, or null: computed into the workspace
+    uint32_t* ids;
+    uint32_t* counts;
+    uint32_t* member;
+    hs_status_t* status;
+    char* ws;
+    uint32_t stride, n, ids_stride;
+};
+struct SelectJobs {
+    SelectJob job[kMaxBatch];
+    uint32_t count, heads, flags;
+    float alpha, ratio;
+};
+
+// The SelectArgs view of job j: its workspace slices follow plan_select.
+__host__ __device__ inline SelectArgs job_args(const SelectJobs& js, uint32_t j) {
+    const SelectJob& jb = js.job[j];
+    const uint32_t kmax = kmax_of(jb.n, js.ratio, js.flags);
+    const SelectPlan p = plan_select(js.heads, jb.n, kmax);
+    char* ws = jb.ws;
+    SelectArgs a;
+    a.scores = jb.scores;
+    a.heads = js.heads;
+    a.stride = jb.stride;
+    a.n = jb.n;
+    a.S = p.S;
+    a.alpha = js.alpha;
+    a.ratio = js.ratio;
+    a.flags = js.flags;
+    a.partial = jb.partial ? jb.partial : reinterpret_cast<const uint32_t*>(ws + p.off_partial);
+    a.partials = p.partials;
+    a.plan = reinterpret_cast<SelectPlanDev*>(ws + p.off_plan);
+    a.g_count = reinterpret_cast<uint32_t*>(ws + p.off_count);
+    a.g_bad = reinterpret_cast<uint32_t*>(ws + p.off_bad);
+    a.g_hi = reinterpret_cast<uint32_t*>(ws + p.off_hi);
+    a.g_lo = reinterpret_cast<uint32_t*>(ws + p.off_lo);
+    a.g_sort = reinterpret_cast<uint32_t*>(ws + p.off_sort);
+    a.g_keys = reinterpret_cast<uint16_t*>(ws + p.off_keys);
+    a.g_m = reinterpret_cast<uint32_t*>(ws + p.off_m);
+    a.kcap = p.kcap;
+    a.g_tie = reinterpret_cast<unsigned long long*>(ws + p.off_tie);
+    a.g_key16 = p.key_stride ? reinterpret_cast<uint16_t*>(ws + p.off_key16) : nullptr;
+    a.key_stride = p.key_stride;
+    a.cap = p.cap;
+    a.ids = jb.ids;
+    a.ids_stride = jb.ids_stride;
+    a.counts_out = jb.counts;
+    a.member = jb.member;
+    a.status = jb.status;
+    return a;
+}
+
 // Per 64-element tile of head 0: maximum order key of the non-NaN input
 // scores (0 = nothing).  Scaling is monotone, so raw keys serve the scaled maximum.
-__global__ void __launch_bounds__(256)
-head0_max_kernel(const uint16_t* __restrict__ scores, uint32_t n, uint32_t* __restrict__ partial) {
+__global__ void __launch_bounds__(256) head0_max_kernel(const SelectJobs js) {
+    const SelectJob& jb = js.job[blockIdx.y];
+    if (jb.partial) return;  // the scorer's tile maxima serve
+    const SelectArgs a = job_args(js, blockIdx.y);
+    uint32_t* own = const_cast<uint32_t*>(a.partial);
     const uint32_t tile = blockIdx.x * 4 + (threadIdx.x >> 6);
     const uint32_t i = tile * 64 + (threadIdx.x & 63u);
-    const uint32_t bits = i < n ? scores[i] : 0u;
-    const uint32_t key = i < n && !is_nan_half(bits) ? order_key(bits) : 0u;
+    const uint32_t bits = i < a.n ? a.scores[i] : 0u;
+    const uint32_t key = i < a.n && !is_nan_half(bits) ? order_key(bits) : 0u;
     const uint32_t best = wave_max_u32(key);
-    if ((threadIdx.x & 63u) == 0 && tile * 64 < n) partial[tile] = best;
+    if ((threadIdx.x & 63u) == 0 && tile * 64 < a.n) own[tile] = best;
 }
 
 // Threshold from the head-0 maximum key: thr = f32(F16(f32(max) - alpha)).
@@ -312,11 +384,14 @@ __device__ __forceinline__ uint32_t partial_max(const SelectArgs& a) {
 }
 
 // ---- 1. count ---------------------------------------------------------------
-__global__ void __launch_bounds__(kThreads) count_kernel(SelectArgs a) {
+__global__ void __launch_bounds__(kThreads) count_kernel(const SelectJobs js) {
     __shared__ uint32_t whist[kHistWords];
     __shared__ uint32_t tmp[kWaves];
+    const SelectArgs a = job_args(js, blockIdx.y);
     const uint32_t tid = threadIdx.x;
-    const uint32_t g = blockIdx.x, h = g / a.S, s = g - h * a.S;
+    const uint32_t g = blockIdx.x;
+    if (g >= a.heads * a.S) return;  // a shorter job of the batch
+    const uint32_t h = g / a.S, s = g - h * a.S;
     const uint32_t begin = s * kSlice + tid * kRun;
     uint32_t best = partial_max(a);
     uint32_t packed[kRun / 2];
@@ -937,7 +1012,7 @@ __device__ bool place_by_histogram(uint32_t* A, uint32_t* B, uint32_t m, uint32_
 }
 
 template <bool kRankOrder>
-__global__ void __launch_bounds__(kHThreads) head_select_kernel(SelectArgs a) {
+__global__ void __launch_bounds__(kHThreads) head_select_kernel(const SelectJobs js) {
     __shared__ uint32_t hist[2][256];
     __shared__ uint32_t head_count[kMaxHeads], head_bad[kMaxHeads];
     __shared__ uint32_t tmp[kHWaves];
@@ -946,6 +1021,7 @@ __global__ void __launch_bounds__(kHThreads) head_select_kernel(SelectArgs a) {
     __shared__ uint32_t tables[kRankOrder ? 2 * kSortRange : 1];
     __shared__ uint32_t whist[kRankOrder ? kHWaves : 1][256];
     enum { kCode, kK, kBucket, kAbove, kBucket2, kAbove2, kFlag };
+    const SelectArgs a = job_args(js, blockIdx.y);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t h = blockIdx.x, S = a.S, n = a.n, groups = a.heads * S;
     const uint32_t begin = tid * kHRun, words = (n + 31) / 32;
@@ -1288,92 +1364,138 @@ __global__ void __launch_bounds__(kThreads) rank_kernel(SelectArgs a) {
 
 size_t select_workspace_bytes(uint32_t heads, uint32_t n) { return plan_select(heads, n, n).total; }
 
+namespace {
+
+constexpr uint32_t kAllFlags = HS_SELECT_SCALE_RAW | HS_SELECT_FP32_COUNTS | HS_SELECT_REQUIRE_K |
+                               HS_SELECT_ID_ORDER | HS_SELECT_COVER;
+
+int check_common(uint32_t heads, float alpha, float ratio, uint32_t flags) {
+    if (heads == 0 || heads > kMaxHeads) return reject("GQA selector shape: heads must be 1..128");
+    if (!std::isfinite(alpha) || alpha < 0 || !std::isfinite(ratio) || ratio <= 0 || ratio > 1)
+        return reject("GQA selector numeric parameters");
+    if (flags & ~kAllFlags) return reject("select: unknown flags");
+    return HS_OK;
+}
+
+// Host checks of one job; on success fills the job's kernel record.
+int check_job(const uint16_t* scores, size_t stride, uint32_t n, const uint32_t* head0_partial,
+              uint32_t* ids, size_t ids_stride, uint32_t* counts, uint32_t* member,
+              hs_status_t* status, void* workspace, float ratio, uint32_t flags, SelectJob& out) {
+    if (!scores || !ids || !status || !workspace) return reject("select: null pointer");
+    if (n == 0 || n > kMaxN) return reject("GQA selector shape: n must be 1..131072");
+    if (stride < n || stride > 0xffffffffu) return reject("GQA selector shape: stride < n");
+    // the history cover caps at the selection over n + 1 columns
+    const uint32_t kmax = kmax_of(n, ratio, flags);
+    if ((flags & HS_SELECT_COVER) && kmax == 0)
+        return reject("payload prefetch historical cap/range mismatch");
+    if (ids_stride < kmax || ids_stride > 0xffffffffu)
+        return reject("select: ids_stride below the largest possible k");
+    out = SelectJob{scores, head0_partial, ids, counts, member, status,
+                    static_cast<char*>(workspace), static_cast<uint32_t>(stride), n,
+                    static_cast<uint32_t>(ids_stride)};
+    return HS_OK;
+}
+
+// The per-head path covers the job: n <= 32768 and, in rank order, a cap
+// whose selection fits the LDS sort.
+bool per_head_path(uint32_t n, float ratio, uint32_t flags) {
+    return n <= kHeadMaxN &&
+           ((flags & HS_SELECT_ID_ORDER) || kmax_of(n, ratio, flags) <= kHeadMaxK);
+}
+
+// Launches for the checked jobs of `js`.  Batches whose jobs all take the
+// per-head path run as one launch per phase; otherwise each job runs alone.
+int launch_jobs(const SelectJobs& js, hipStream_t stream) {
+    uint32_t max_partials = 0, max_groups = 0;
+    bool any_own_partial = false, all_per_head = true;
+    for (uint32_t j = 0; j < js.count; ++j) {
+        const SelectPlan p = plan_select(js.heads, js.job[j].n, kmax_of(js.job[j].n, js.ratio, js.flags));
+        max_partials = std::max(max_partials, p.partials);
+        max_groups = std::max(max_groups, p.groups);
+        any_own_partial |= js.job[j].partial == nullptr;
+        all_per_head &= per_head_path(js.job[j].n, js.ratio, js.flags);
+    }
+    if (!all_per_head && js.count > 1) {
+        for (uint32_t j = 0; j < js.count; ++j) {
+            SelectJobs one = js;
+            one.count = 1;
+            one.job[0] = js.job[j];
+            const int rc = launch_jobs(one, stream);
+            if (rc != HS_OK) return rc;
+        }
+        return HS_OK;
+    }
+    if (any_own_partial)
+        hipLaunchKernelGGL(head0_max_kernel, dim3((max_partials + 3) / 4, js.count), dim3(256), 0,
+                           stream, js);
+    hipLaunchKernelGGL(count_kernel, dim3(max_groups, js.count), dim3(kThreads), 0, stream, js);
+    const bool id_order = (js.flags & HS_SELECT_ID_ORDER) != 0;
+    if (all_per_head) {
+        // one workgroup per (head, job) finishes the selection
+        if (id_order)
+            hipLaunchKernelGGL(head_select_kernel<false>, dim3(js.heads, js.count), dim3(kHThreads),
+                               0, stream, js);
+        else
+            hipLaunchKernelGGL(head_select_kernel<true>, dim3(js.heads, js.count), dim3(kHThreads),
+                               0, stream, js);
+    } else {
+        // one large job: the slice launch chain
+        const SelectArgs args = job_args(js, 0);
+        const dim3 grid(max_groups), block(kThreads);
+        hipLaunchKernelGGL(plan_kernel, grid, block, 0, stream, args);
+        if (id_order) {
+            hipLaunchKernelGGL(slice_select_kernel<false>, grid, block, 0, stream, args);
+        } else {
+            hipLaunchKernelGGL(slice_select_kernel<true>, grid, block, 0, stream, args);
+            // k <= kmax: the staged variant serves every head whose selection fits LDS
+            if (kmax_of(js.job[0].n, js.ratio, js.flags) <= kRankCap)
+                hipLaunchKernelGGL(rank_kernel<true>, grid, block, 0, stream, args);
+            else
+                hipLaunchKernelGGL(rank_kernel<false>, grid, block, 0, stream, args);
+        }
+    }
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hip_fail(st, "select launch");
+}
+
+}  // namespace
+
 int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_t n, float alpha,
                   float ratio, uint32_t flags, const uint32_t* head0_partial, uint32_t* ids,
                   size_t ids_stride, uint32_t* counts, uint32_t* member, hs_status_t* status,
                   void* workspace, hipStream_t stream) {
-    if (!scores || !ids || !status || !workspace) return reject("select: null pointer");
-    if (heads == 0 || heads > kMaxHeads) return reject("GQA selector shape: heads must be 1..128");
-    if (n == 0 || n > kMaxN) return reject("GQA selector shape: n must be 1..131072");
-    if (stride < n || stride > 0xffffffffu) return reject("GQA selector shape: stride < n");
-    if (!std::isfinite(alpha) || alpha < 0 || !std::isfinite(ratio) || ratio <= 0 || ratio > 1)
-        return reject("GQA selector numeric parameters");
-    if (flags & ~uint32_t(HS_SELECT_SCALE_RAW | HS_SELECT_FP32_COUNTS | HS_SELECT_REQUIRE_K |
-                          HS_SELECT_ID_ORDER | HS_SELECT_COVER))
-        return reject("select: unknown flags");
-    // the history cover caps at the selection over n + 1 columns
-    const bool cover = (flags & HS_SELECT_COVER) != 0;
-    const uint64_t kmax = std::min<uint64_t>(
-        n, static_cast<uint64_t>(std::floor(static_cast<double>(cover ? n + 1ull : n) *
-                                            static_cast<double>(ratio))));
-    if (cover && kmax == 0) return reject("payload prefetch historical cap/range mismatch");
-    if (ids_stride < kmax || ids_stride > 0xffffffffu)
-        return reject("select: ids_stride below the largest possible k");
-    // A workspace of select_workspace_bytes(heads, n) covers every ratio.
-    const SelectPlan p = plan_select(heads, n, static_cast<uint32_t>(kmax));
-    char* ws = static_cast<char*>(workspace);
-    SelectArgs args;
-    args.scores = scores;
-    args.heads = heads;
-    args.stride = static_cast<uint32_t>(stride);
-    args.n = n;
-    args.S = p.S;
-    args.alpha = alpha;
-    args.ratio = ratio;
-    args.flags = flags;
-    args.partial = head0_partial;
-    args.partials = p.partials;
-    args.plan = reinterpret_cast<SelectPlanDev*>(ws + p.off_plan);
-    args.g_count = reinterpret_cast<uint32_t*>(ws + p.off_count);
-    args.g_bad = reinterpret_cast<uint32_t*>(ws + p.off_bad);
-    args.g_hi = reinterpret_cast<uint32_t*>(ws + p.off_hi);
-    args.g_lo = reinterpret_cast<uint32_t*>(ws + p.off_lo);
-    args.g_sort = reinterpret_cast<uint32_t*>(ws + p.off_sort);
-    args.g_keys = reinterpret_cast<uint16_t*>(ws + p.off_keys);
-    args.g_m = reinterpret_cast<uint32_t*>(ws + p.off_m);
-    args.kcap = p.kcap;
-    args.g_tie = reinterpret_cast<unsigned long long*>(ws + p.off_tie);
-    args.g_key16 = p.key_stride ? reinterpret_cast<uint16_t*>(ws + p.off_key16) : nullptr;
-    args.key_stride = p.key_stride;
-    args.cap = p.cap;
-    args.ids = ids;
-    args.ids_stride = static_cast<uint32_t>(ids_stride);
-    args.counts_out = counts;
-    args.member = member;
-    args.status = status;
-    if (!head0_partial) {
-        uint32_t* own = reinterpret_cast<uint32_t*>(ws + p.off_partial);
-        hipLaunchKernelGGL(head0_max_kernel, dim3((p.partials + 3) / 4), dim3(256), 0, stream,
-                           scores, n, own);
-        args.partial = own;
+    int rc = check_common(heads, alpha, ratio, flags);
+    if (rc != HS_OK) return rc;
+    SelectJobs js{};
+    js.count = 1;
+    js.heads = heads;
+    js.flags = flags;
+    js.alpha = alpha;
+    js.ratio = ratio;
+    rc = check_job(scores, stride, n, head0_partial, ids, ids_stride, counts, member, status,
+                   workspace, ratio, flags, js.job[0]);
+    if (rc != HS_OK) return rc;
+    return launch_jobs(js, stream);
+}
+
+int launch_select_batched(const hs_select_job_t* jobs, uint32_t count, uint32_t heads,
+                          float alpha, float ratio, uint32_t flags, hipStream_t stream) {
+    if (!jobs || count == 0 || count > kMaxBatch) return reject("select batch: 1..16 jobs");
+    int rc = check_common(heads, alpha, ratio, flags);
+    if (rc != HS_OK) return rc;
+    SelectJobs js{};
+    js.count = count;
+    js.heads = heads;
+    js.flags = flags;
+    js.alpha = alpha;
+    js.ratio = ratio;
+    for (uint32_t j = 0; j < count; ++j) {
+        const hs_select_job_t& q = jobs[j];
+        rc = check_job(q.scores, q.stride, q.n, q.head0_partial, q.ids, q.ids_stride, q.counts,
+                       q.member, q.status, q.workspace, ratio, flags, js.job[j]);
+        if (rc != HS_OK) return rc;
     }
-    const dim3 grid(p.groups), block(kThreads);
-    hipLaunchKernelGGL(count_kernel, grid, block, 0, stream, args);
-    const bool id_order = (flags & HS_SELECT_ID_ORDER) != 0;
-    if (n <= kHeadMaxN && (id_order || kmax <= kHeadMaxK)) {
-        // one workgroup per head finishes the selection
-        if (id_order)
-            hipLaunchKernelGGL(head_select_kernel<false>, dim3(heads), dim3(kHThreads), 0, stream,
-                               args);
-        else
-            hipLaunchKernelGGL(head_select_kernel<true>, dim3(heads), dim3(kHThreads), 0, stream,
-                               args);
-        const hipError_t st = hipGetLastError();
-        return st == hipSuccess ? HS_OK : hip_fail(st, "select launch");
-    }
-    hipLaunchKernelGGL(plan_kernel, grid, block, 0, stream, args);
-    if (flags & HS_SELECT_ID_ORDER) {
-        hipLaunchKernelGGL(slice_select_kernel<false>, grid, block, 0, stream, args);
-    } else {
-        hipLaunchKernelGGL(slice_select_kernel<true>, grid, block, 0, stream, args);
-        // k <= kmax: the staged variant serves every head whose selection fits LDS
-        if (kmax <= kRankCap)
-            hipLaunchKernelGGL(rank_kernel<true>, grid, block, 0, stream, args);
-        else
-            hipLaunchKernelGGL(rank_kernel<false>, grid, block, 0, stream, args);
-    }
-    const hipError_t st = hipGetLastError();
-    return st == hipSuccess ? HS_OK : hip_fail(st, "select launch");
+    return launch_jobs(js, stream);
 }
 
 }  // namespace hs
@@ -1393,6 +1515,13 @@ int hs_gqa_select(const uint16_t* scores_dev, uint32_t heads, size_t stride, uin
     return hs::launch_select(scores_dev, heads, stride, n, alpha, ratio, flags, head0_partial_dev,
                              ids_dev, ids_stride, counts_dev, member_dev, status_dev,
                              workspace_dev, hs::as_stream(stream));
+}
+
+int hs_gqa_select_batched(const hs_select_job_t* jobs, uint32_t count, uint32_t heads,
+                          float alpha, float ratio, uint32_t flags, void* stream) {
+    hs::clear_error();
+    return hs::launch_select_batched(jobs, count, heads, alpha, ratio, flags,
+                                     hs::as_stream(stream));
 }
 
 }  // extern "C"

@@ -78,6 +78,29 @@ def score(q16, keys, tokens, key_stride_words=1024, rows=None, out=None, score_s
 
 # ---- selection ---------------------------------------------------------------
 
+def score_batched(jobs, stream=None):
+    """Score up to 16 (q16, keys, tokens) jobs in one launch.
+
+    jobs: sequence of dicts with q16, keys, tokens and optional
+    key_stride_words (1024), out, score_stride, head0_partial.  Returns the
+    list of score tensors [32, score_stride]."""
+    from . import ScoreJob
+    table = (ScoreJob * max(1, len(jobs)))()
+    outs = []
+    for i, j in enumerate(jobs):
+        _need_cuda(j["q16"], j["keys"])
+        tokens = int(j["tokens"])
+        stride = int(j.get("score_stride") or tokens)
+        out = j.get("out")
+        if out is None:
+            out = torch.empty((32, stride), dtype=torch.float16, device=j["keys"].device)
+        outs.append(out)
+        table[i] = ScoreJob(_p(j["q16"]), _p(j["keys"]), _p(out), _p(j.get("head0_partial")),
+                            int(j.get("key_stride_words", 1024)), tokens, stride, 0)
+    check(lib().hs_gqa_score_batched(ctypes.cast(table, ctypes.c_void_p), len(jobs), _s(stream)))
+    return outs
+
+
 def select_workspace_bytes(heads, n):
     return lib().hs_gqa_select_workspace_bytes(heads, n)
 
@@ -112,6 +135,40 @@ def select(scores, heads, stride, n, alpha, ratio, *, scale_raw=False, fp32_coun
                               _p(head0_partial), _p(ids), ids_stride, _p(counts), _p(member),
                               _p(status), _p(ws), _s(stream)))
     return ids, counts, member, status
+
+
+def select_batched(jobs, heads, alpha, ratio, *, scale_raw=False, fp32_counts=False,
+                   require_k=False, id_order=False, cover=False, stream=None):
+    """Up to 16 selections sharing heads/alpha/ratio/flags in one batch.
+
+    jobs: dicts with scores [heads, stride] and n, optional head0_partial,
+    member (int32 [heads, ceil(n/32)]).  Returns a list of
+    (ids, counts, member, status) per job."""
+    from . import SelectJob
+    table = (SelectJob * max(1, len(jobs)))()
+    results = []
+    for i, j in enumerate(jobs):
+        scores, n = j["scores"], int(j["n"])
+        _need_cuda(scores)
+        dev = scores.device
+        stride = int(j.get("stride") or scores.shape[-1])
+        cols = n + 1 if cover else n
+        kmax = min(n, math.floor(float(cols) * float(ctypes.c_float(ratio).value)))
+        ids_stride = max(1, kmax)
+        ids = torch.empty((heads, ids_stride), dtype=torch.int32, device=dev)
+        counts = torch.empty(heads, dtype=torch.int32, device=dev)
+        status = new_status(dev)
+        ws = workspace(select_workspace_bytes(heads, n), dev)
+        member = j.get("member")
+        results.append((ids, counts, member, status, ws))
+        table[i] = SelectJob(_p(scores), _p(j.get("head0_partial")), _p(ids), _p(counts),
+                             _p(member), _p(status), _p(ws), stride, n, ids_stride, 0)
+    flags = ((HS_SELECT_SCALE_RAW if scale_raw else 0) | (HS_SELECT_FP32_COUNTS if fp32_counts else 0)
+             | (HS_SELECT_REQUIRE_K if require_k else 0) | (HS_SELECT_ID_ORDER if id_order else 0)
+             | (HS_SELECT_COVER if cover else 0))
+    check(lib().hs_gqa_select_batched(ctypes.cast(table, ctypes.c_void_p), len(jobs), heads,
+                                      alpha, ratio, flags, _s(stream)))
+    return [r[:4] for r in results]
 
 
 # ---- union / pack / gather -------------------------------------------------------

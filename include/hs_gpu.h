@@ -75,6 +75,23 @@ int hs_gqa_score(const uint16_t *q_dev, const uint16_t *keys_dev,
                  size_t score_stride, uint32_t *head0_partial_dev,
                  void *stream);
 
+/* Batched scorer: up to 16 independent scoring jobs (one query each, its own
+ * keys, token count and outputs; the decode sequences of a batch) in one
+ * launch, each with hs_gqa_score's semantics and limits (no row map).  The
+ * jobs share the launch's waves, so short sequences do not leave the device
+ * idle.  Job order does not matter. */
+typedef struct {
+    const uint16_t *q;          /* F16 [32][128], 4-byte aligned            */
+    const uint16_t *keys;       /* keys + t*key_stride_words, 16-byte aligned */
+    uint16_t *scores;           /* F16 [32][score_stride]                   */
+    uint32_t *head0_partial;    /* nullable, ceil(tokens/64) tile maxima    */
+    uint32_t key_stride_words;  /* 1024 or 2048                             */
+    uint32_t tokens;            /* 1..65536                                 */
+    uint32_t score_stride;      /* >= tokens                                */
+    uint32_t reserved;          /* 0                                        */
+} hs_score_job_t;
+int hs_gqa_score_batched(const hs_score_job_t *jobs, uint32_t count, void *stream);
+
 /* ---- (2) selection -------------------------------------------------------
  * select_gqa_scores (policy/gqa_policy.cpp:47-70) on device.
  * scores_dev F16 [heads][stride]; first n columns are candidates (heads
@@ -122,6 +139,25 @@ int hs_gqa_select(const uint16_t *scores_dev, uint32_t heads, size_t stride,
                   const uint32_t *head0_partial_dev, uint32_t *ids_dev,
                   size_t ids_stride, uint32_t *counts_dev, uint32_t *member_dev,
                   hs_status_t *status_dev, void *workspace_dev, void *stream);
+
+/* Batched selection: up to 16 independent selections (the decode sequences
+ * of a batch: each its own scores, n, outputs and workspace of
+ * hs_gqa_select_workspace_bytes(heads, n)) sharing heads, alpha, ratio and
+ * flags, each with hs_gqa_select's semantics.  When every job has n <= 32768
+ * (and, in rank order, floor(n*ratio) <= 8192) one launch per phase serves
+ * the whole batch; otherwise the jobs run one after another. */
+typedef struct {
+    const uint16_t *scores;          /* F16 [heads][stride]                  */
+    const uint32_t *head0_partial;   /* nullable tile maxima (hs_gqa_score)  */
+    uint32_t *ids;                   /* [heads][ids_stride]                  */
+    uint32_t *counts;                /* nullable [heads]                     */
+    uint32_t *member;                /* nullable [heads][ceil(n/32)]         */
+    hs_status_t *status;
+    void *workspace;
+    uint32_t stride, n, ids_stride, reserved;
+} hs_select_job_t;
+int hs_gqa_select_batched(const hs_select_job_t *jobs, uint32_t count, uint32_t heads,
+                          float alpha, float ratio, uint32_t flags, void *stream);
 
 /* ---- (3) union / gather / pack ------------------------------------------
  * gqa_physical_union (runtime/gqa_pack.hpp:12-22): 32 id lists
