@@ -30,6 +30,7 @@ HS_ERR_DUPLICATE = 7
 HS_ERR_MISSING = 8
 HS_ERR_HIP = 9
 HS_ERR_UNSUPPORTED = 10
+HS_ERR_OVERFLOW = 11
 
 HS_SELECT_SCALE_RAW = 1
 HS_SELECT_FP32_COUNTS = 2
@@ -48,6 +49,7 @@ ERROR_NAMES = {
     HS_ERR_MISSING: "missing KV row",
     HS_ERR_HIP: "HIP runtime",
     HS_ERR_UNSUPPORTED: "unsupported",
+    HS_ERR_OVERFLOW: "F16 overflow",
 }
 
 
@@ -115,6 +117,8 @@ SIGNATURES = {
     "hs_gqa_select_workspace_bytes": (_SZ, [_U32, _U32]),
     "hs_gqa_select": (_I, [_P, _U32, _SZ, _U32, _F, _F, _U32, _P, _P, _SZ, _P, _P, _P, _P, _P]),
     "hs_gqa_select_batched": (_I, [_P, _U32, _U32, _F, _F, _U32, _P]),
+    "hs_rehearsal_workspace_bytes": (_SZ, [_U32]),
+    "hs_rehearsal_query": (_I, [_P, _P, _P, _U32, _F, _F, _P, _P, _P, _P]),
     "hs_gqa_union_workspace_bytes": (_SZ, [_U32]),
     "hs_gqa_physical_union": (_I, [_P, _P, _SZ, _U32, _P, _P, _P, _P, _P]),
     "hs_gqa_pack": (_I, [_P, _U32, _P, _U32, _P, _P, _SZ, _P, _U32, _U32, _P, _P, _P, _P, _P]),

@@ -50,7 +50,8 @@ DEVICE = [
     "-munsafe-fp-atomics",
 ]
 
-HIP_SOURCES = ["score.hip", "select.hip", "attention.hip", "pack.hip", "runtime.hip"]
+HIP_SOURCES = ["score.hip", "select.hip", "attention.hip", "pack.hip", "rehearsal.hip",
+               "runtime.hip"]
 HOST_SOURCES = ["gqa_gpu.cpp"]
 
 

@@ -171,6 +171,26 @@ def select_batched(jobs, heads, alpha, ratio, *, scale_raw=False, fp32_counts=Fa
     return [r[:4] for r in results]
 
 
+def rehearsal_query(hidden, wq, positions, eps=1e-5, theta=500000.0, out=None, status=True,
+                    stream=None):
+    """Rehearsal query of a batch (<= 16 sequences) on MFMA.
+
+    hidden: bfloat16 [batch, 4096]; wq: bfloat16 [4096, 4096] (out, in);
+    positions: host ints.  Returns (q16 [batch, 32, 128], status or None)."""
+    _need_cuda(hidden, wq)
+    batch = hidden.shape[0]
+    pos = (ctypes.c_uint32 * max(1, batch))(*[int(p) for p in positions])
+    if out is None:
+        out = torch.empty((batch, 32, 128), dtype=torch.float16, device=hidden.device)
+    st = ws = None
+    if status:
+        st = torch.zeros((batch, 4), dtype=torch.int32, device=hidden.device)
+        ws = workspace(lib().hs_rehearsal_workspace_bytes(batch), hidden.device)
+    check(lib().hs_rehearsal_query(_p(hidden), _p(wq), ctypes.cast(pos, ctypes.c_void_p), batch,
+                                   eps, theta, _p(out), _p(st), _p(ws), _s(stream)))
+    return out, st
+
+
 # ---- union / pack / gather -------------------------------------------------------
 
 def physical_union(ids, lens, ids_stride, visible, stream=None):

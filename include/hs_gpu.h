@@ -33,7 +33,8 @@ enum {
     HS_ERR_DUPLICATE = 7,    /* duplicate/future id (gqa_pack.hpp:17,33)     */
     HS_ERR_MISSING = 8,      /* selected id without KV row (gqa_pack.hpp:44) */
     HS_ERR_HIP = 9,          /* HIP runtime call failed                      */
-    HS_ERR_UNSUPPORTED = 10  /* valid for the reference, beyond this build   */
+    HS_ERR_UNSUPPORTED = 10, /* valid for the reference, beyond this build   */
+    HS_ERR_OVERFLOW = 11     /* finite value beyond F16 (full_gqa_runtime.cpp:63) */
 };
 
 /* Device-side result of one selection; written by hs_gqa_select*. */
@@ -158,6 +159,23 @@ typedef struct {
 } hs_select_job_t;
 int hs_gqa_select_batched(const hs_select_job_t *jobs, uint32_t count, uint32_t heads,
                           float alpha, float ratio, uint32_t flags, void *stream);
+
+/* Rehearsal query (patches/llama-b6000-early-rehearsal.patch:17-27, then
+ * query_f16 of policy/full_gqa_runtime.cpp:61-64) for up to 16 sequences:
+ *   q_b = F16_RNE(RoPE(Wq . (hidden_b / sqrt(mean(hidden_b^2) + eps)), pos_b))
+ * hidden_dev BF16 [batch][4096]; wq_dev BF16 [4096 out][4096 in] row-major
+ * (ggml's Wq); RoPE on adjacent channel pairs of each 128-channel head with
+ * angle pos_b * theta^(-2i/128) (ggml NORM rope); positions: HOST array of
+ * batch entries; q_dev F16 [batch][32][128], the scorer's query layout.  The
+ * product runs on MFMA (BF16 operands, FP32 accumulation).  status_dev
+ * (nullable, [batch]) gets HS_ERR_NONFINITE for a nonfinite value and
+ * HS_ERR_OVERFLOW for one beyond F16, as query_f16 rejects them; it needs
+ * workspace_dev of hs_rehearsal_workspace_bytes(batch) bytes. */
+size_t hs_rehearsal_workspace_bytes(uint32_t batch);
+int hs_rehearsal_query(const uint16_t *hidden_dev, const uint16_t *wq_dev,
+                       const uint32_t *positions, uint32_t batch, float eps, float theta,
+                       uint16_t *q_dev, hs_status_t *status_dev, void *workspace_dev,
+                       void *stream);
 
 /* ---- (3) union / gather / pack ------------------------------------------
  * gqa_physical_union (runtime/gqa_pack.hpp:12-22): 32 id lists
