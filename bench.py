@@ -55,7 +55,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bounded CPU-baseline sample duration")
     p.add_argument("--layer-steps", type=int, default=20)
-    p.add_argument("--only", choices=["score", "select", "select_id", "layer"], default=None,
+    p.add_argument("--only", choices=["score", "select", "select_id", "layer", "batch"], default=None,
                    help="profiling aid: run just one kernel family over the 30 layers "
                         "(prints its own timing line, not the benchmark JSON)")
     return p.parse_args()
@@ -126,6 +126,103 @@ def pmc_traffic():
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", path.read_text())
     return int(m.group(1)) if m else None
+
+
+BATCH = 16
+REHEARSAL_FLOPS = 2 * BATCH * 4096 * 4096
+REHEARSAL_BYTES = 4096 * 4096 * 2 + 2 * BATCH * 4096 * 2  # Wq + hidden + q
+
+
+def batch_leg(args, hs, ops, torch, stream, dev):
+    """16 decode sequences (N_i in 8192..32768, multiples of 64).
+    One step = rehearsal query (RMS norm, BF16 Wq on MFMA, RoPE) for the
+    batch, batched ordered-FP32 scoring of every sequence's keys, batched
+    rank-order selection.  The C entry points are called directly with
+    prebuilt job tables, so the timed loop is device work only."""
+    import ctypes
+    import numpy as np
+    g = np.random.default_rng(7)
+    ns = [int(x) * 64 for x in g.integers(8192 // 64, 32768 // 64 + 1, size=BATCH)]
+    keys = [torch.empty(n * 1024, dtype=torch.float16, device=dev) for n in ns]
+    for i, (k, n) in enumerate(zip(keys, ns)):
+        ops.fill_rope_keys(k, n, 1024, 8, seed=7000 + i, theta=500000.0)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    hidden = torch.randn((BATCH, 4096), generator=gen, device=dev).to(torch.bfloat16)
+    wq = (torch.randn((4096, 4096), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    q = torch.empty((BATCH, 32, 128), dtype=torch.float16, device=dev)
+    rstatus = torch.zeros((BATCH, 4), dtype=torch.int32, device=dev)
+    L = hs.lib()
+    rws = ops.workspace(L.hs_rehearsal_workspace_bytes(BATCH), dev)
+    positions = (ctypes.c_uint32 * BATCH)(*ns)  # the current token follows the history
+    scores = [torch.empty((32, n), dtype=torch.float16, device=dev) for n in ns]
+    partials = [torch.empty((n + 63) // 64, dtype=torch.int32, device=dev) for n in ns]
+    kmaxes = [math.floor(n * float(np.float32(RATIO))) for n in ns]
+    ids = [torch.empty((32, k), dtype=torch.int32, device=dev) for k in kmaxes]
+    counts = [torch.empty(32, dtype=torch.int32, device=dev) for _ in ns]
+    statuses = [ops.new_status(dev) for _ in ns]
+    wss = [ops.workspace(ops.select_workspace_bytes(32, n), dev) for n in ns]
+    score_table = (hs.ScoreJob * BATCH)()
+    sel_table = (hs.SelectJob * BATCH)()
+    vp = lambda t: t.data_ptr()
+    for i, n in enumerate(ns):
+        score_table[i] = hs.ScoreJob(vp(q[i]), vp(keys[i]), vp(scores[i]), vp(partials[i]), 1024, n,
+                                     n, 0)
+        sel_table[i] = hs.SelectJob(vp(scores[i]), vp(partials[i]), vp(ids[i]), vp(counts[i]), None,
+                                    vp(statuses[i]), vp(wss[i]), n, n, kmaxes[i], 0)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    score_p, sel_p = ctypes.cast(score_table, ctypes.c_void_p), ctypes.cast(sel_table, ctypes.c_void_p)
+
+    def rehearsal():
+        hs.check(L.hs_rehearsal_query(vp(hidden), vp(wq), ctypes.cast(positions, ctypes.c_void_p),
+                                      BATCH, 1e-5, 500000.0, vp(q), vp(rstatus), vp(rws), sp))
+
+    def scoring():
+        hs.check(L.hs_gqa_score_batched(score_p, BATCH, sp))
+
+    def step():
+        rehearsal()
+        scoring()
+        hs.check(L.hs_gqa_select_batched(sel_p, BATCH, 32, ALPHA, RATIO, hs.HS_SELECT_SCALE_RAW, sp))
+
+    def timed(fn, reps):
+        b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        b.record(stream)
+        for _ in range(reps):
+            fn()
+        e.record(stream)
+        torch.cuda.synchronize()
+        return 1e3 * b.elapsed_time(e) / reps
+
+    for _ in range(max(2, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    st = [ops.read_status(x) for x in statuses]
+    assert all(x["code"] == 0 and 0 < x["k"] <= k for x, k in zip(st, kmaxes)), st
+    assert int(rstatus[:, 0].abs().sum()) == 0
+    reps = max(10, args.steps)
+    step_us = timed(step, reps)
+    rehearsal_us = timed(rehearsal, reps)
+    score_us = timed(scoring, reps)
+    total = sum(ns)
+    score_bytes = sum(n * 2112 + 8192 for n in ns)
+    out = {
+        "workload": "configs[3]: 16 sequences, rehearsal query on MFMA + batched score + "
+                    "batched rank-order select",
+        "sequences": BATCH, "tokens": ns, "total_keys": total,
+        "us_per_step": step_us, "keys_per_s": total / (step_us * 1e-6),
+        "rehearsal_us": rehearsal_us,
+        "rehearsal_mfma_util": REHEARSAL_FLOPS / (rehearsal_us * 1e-6) / 2.5e15,
+        "rehearsal_gbps": REHEARSAL_BYTES / (rehearsal_us * 1e-6) / 1e9,
+        "score_batched_us": score_us,
+        "score_batched_gbps": score_bytes / (score_us * 1e-6) / 1e9,
+    }
+    log(f"configs[3]: {step_us:.1f} us/step for {total} keys over {BATCH} sequences = "
+        f"{out['keys_per_s']/1e9:.2f} G keys/s; rehearsal {rehearsal_us:.2f} us "
+        f"({out['rehearsal_gbps']:.0f} GB/s, MFMA {100*out['rehearsal_mfma_util']:.2f} %), "
+        f"batched score {score_us:.1f} us ({out['score_batched_gbps']:.0f} GB/s)")
+    del keys
+    return out
 
 
 def profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status, ws, kmax):
@@ -201,6 +298,9 @@ def main():
             ops.select(raw, 32, N, N, ALPHA, RATIO, scale_raw=True, head0_partial=partial,
                        ids=ids, ids_stride=kmax, counts=counts, status=status, ws=ws)
 
+    if args.only == "batch":
+        batch_leg(args, hs, ops, torch, stream, dev)
+        return 0
     if args.only in ("score", "select", "select_id"):
         return profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status,
                             ws, kmax)
@@ -279,6 +379,10 @@ def main():
     log(f"configs[2]: {layer_us:.1f} us/layer, {layer_gbs:.0f} GB/s algorithmic "
         f"(union {utokens} (id,KV-head) rows of the last layer)")
 
+    # ---- batched rehearsal + scoring + selection ----------------------
+    del pools
+    batch = batch_leg(args, hs, ops, torch, stream, dev)
+
     # ---- CPU baseline on a bounded sample ----------------------------------------
     k_sample = torch.empty(N * 1024, dtype=torch.float16, device=dev)
     ops.fill_rope_keys(k_sample, N, 1024, 8, seed=1000, theta=500000.0)
@@ -319,6 +423,7 @@ def main():
             "achieved_gbps": layer_gbs, "frac_of_hbm_peak": layer_gbs / HBM_PEAK_GBS,
             "union_rows": utokens,
         },
+        "batch_step": batch,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

@@ -73,30 +73,28 @@ __global__ void __launch_bounds__(kSplits * 64) rehearsal_kernel(const Rehearsal
     const uint16_t* hrow = a.hidden + static_cast<size_t>(live ? r : 0u) * kModel + k0;
     if (tid < 16) bad[tid] = 0;
 
+    // every load of the K slice is issued before the first product: with 8
+    // waves per CU the whole of Wq is in flight at once
+    uint4 wb[kSteps], hb[kSteps];
+#pragma unroll
+    for (uint32_t s = 0; s < kSteps; ++s) {
+        wb[s] = *reinterpret_cast<const uint4*>(wrow + s * kMfmaK);
+        hb[s] = live ? *reinterpret_cast<const uint4*>(hrow + s * kMfmaK)
+                     : make_uint4(0u, 0u, 0u, 0u);
+    }
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     float ss = 0.0f;
 #pragma unroll
-    for (uint32_t half = 0; half < 2; ++half) {
-        uint4 wb[kSteps / 2], hb[kSteps / 2];
+    for (uint32_t s = 0; s < kSteps; ++s) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hb[s]),
+                                                      __builtin_bit_cast(bf16x8, wb[s]), acc, 0,
+                                                      0, 0);
+        const uint32_t hw[4] = {hb[s].x, hb[s].y, hb[s].z, hb[s].w};
 #pragma unroll
-        for (uint32_t s = 0; s < kSteps / 2; ++s) {
-            const uint32_t step = half * (kSteps / 2) + s;
-            wb[s] = *reinterpret_cast<const uint4*>(wrow + step * kMfmaK);
-            hb[s] = live ? *reinterpret_cast<const uint4*>(hrow + step * kMfmaK)
-                         : make_uint4(0u, 0u, 0u, 0u);
-        }
-#pragma unroll
-        for (uint32_t s = 0; s < kSteps / 2; ++s) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hb[s]),
-                                                          __builtin_bit_cast(bf16x8, wb[s]), acc,
-                                                          0, 0, 0);
-            const uint32_t hw[4] = {hb[s].x, hb[s].y, hb[s].z, hb[s].w};
-#pragma unroll
-            for (uint32_t c = 0; c < 4; ++c) {
-                const float lo = bf16_lo(hw[c]), hi = bf16_hi(hw[c]);
-                ss = __builtin_fmaf(lo, lo, ss);  // bf16 squares are exact in FP32
-                ss = __builtin_fmaf(hi, hi, ss);
-            }
+        for (uint32_t c = 0; c < 4; ++c) {
+            const float lo = bf16_lo(hw[c]), hi = bf16_hi(hw[c]);
+            ss = __builtin_fmaf(lo, lo, ss);  // bf16 squares are exact in FP32
+            ss = __builtin_fmaf(hi, hi, ss);
         }
     }
     // lane holds D[4*grp + i][r] of this K slice; squares of row r over 4 groups
