@@ -31,6 +31,7 @@ HS_ERR_MISSING = 8
 HS_ERR_HIP = 9
 HS_ERR_UNSUPPORTED = 10
 HS_ERR_OVERFLOW = 11
+HS_ERR_CORRUPT = 12
 
 HS_SELECT_SCALE_RAW = 1
 HS_SELECT_FP32_COUNTS = 2
@@ -50,6 +51,7 @@ ERROR_NAMES = {
     HS_ERR_HIP: "HIP runtime",
     HS_ERR_UNSUPPORTED: "unsupported",
     HS_ERR_OVERFLOW: "F16 overflow",
+    HS_ERR_CORRUPT: "corrupt cold record",
 }
 
 
@@ -119,6 +121,11 @@ SIGNATURES = {
     "hs_gqa_select_batched": (_I, [_P, _U32, _U32, _F, _F, _U32, _P]),
     "hs_rehearsal_workspace_bytes": (_SZ, [_U32]),
     "hs_rehearsal_query": (_I, [_P, _P, _P, _U32, _F, _F, _P, _P, _P, _P]),
+    "hs_kv_store_bytes": (_U64, [_U32, _U32]),
+    "hs_kv_store_init": (_I, [_P, _U64, _U32, _U32]),
+    "hs_kv_store_append": (_I, [_P, _U32, _U32, _P, _U32]),
+    "hs_kv_cold_fetch_workspace_bytes": (_SZ, [_U32]),
+    "hs_kv_cold_fetch": (_I, [_P, _U32, _P, _U32, _P, _P, _P, _P]),
     "hs_gqa_union_workspace_bytes": (_SZ, [_U32]),
     "hs_gqa_physical_union": (_I, [_P, _P, _SZ, _U32, _P, _P, _P, _P, _P]),
     "hs_gqa_pack": (_I, [_P, _U32, _P, _U32, _P, _P, _SZ, _P, _U32, _U32, _P, _P, _P, _P, _P]),

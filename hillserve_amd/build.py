@@ -51,7 +51,7 @@ DEVICE = [
 ]
 
 HIP_SOURCES = ["score.hip", "select.hip", "attention.hip", "pack.hip", "rehearsal.hip",
-               "runtime.hip"]
+               "kv_store.hip", "runtime.hip"]
 HOST_SOURCES = ["gqa_gpu.cpp"]
 
 

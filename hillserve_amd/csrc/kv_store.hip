@@ -1,0 +1,220 @@
+// Cold tier: SegmentedKVStore v1 images in host memory, read by the GPU.
+//
+// Format (storage/segmented_store.cpp:18-38, the file the reference keeps on
+// SSD, kept here in pinned host memory so the GPU reads it over the host
+// link):
+//   page 0 (4096 B): u64 magic 0x48534b5653454731 ("HSKVSEG1"), version 1,
+//                    request, layers, positions (capacity), record bytes
+//                    (4096), stride (4128), extent; the rest zero
+//   record (layer l, position p) at 4096 + (l*capacity + p)*4128:
+//                    {u64 digest, u64 position, u64 request, u32 layer,
+//                     u32 version = 1} then the 4096 B KV row
+//   digest = FNV-1a 64 of the row (storage/file_store.cpp:12-16)
+//   extent = the record region rounded up to 4096 B
+// The reference's fetch (segmented_store.cpp:85-95, and the prefetch reader
+// of policy/full_gqa_runtime.cpp:398-409) refuses a record whose identity or
+// digest does not match.  hs_kv_cold_fetch does the same on the device:
+//   cold_copy_kernel:   one wave per record copies it from host memory with
+//                       coalesced 16 B reads into the device staging rows and
+//                       checks the header identity;
+//   cold_digest_kernel: one lane per record hashes its staged row in byte
+//                       order (FNV-1a is sequential within a record) and
+//                       compares the digest;
+//   cold_status_kernel: folds the per-record flags into the status.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+
+#include "hs_device.hpp"
+#include "hs_internal.hpp"
+
+namespace hs {
+namespace {
+
+constexpr uint64_t kMagic = 0x48534b5653454731ull;
+constexpr uint64_t kFnvSeed = 14695981039346656037ull, kFnvPrime = 1099511628211ull;
+constexpr uint32_t kRow = 4096, kHeader = 32, kStride = kRow + kHeader;
+constexpr uint32_t kMaxLayers = 128, kMaxPositions = 66048;  // segmented_store.cpp:31
+
+uint64_t extent_of(uint32_t layers, uint32_t capacity) {
+    return (4096ull + uint64_t(layers) * capacity * kStride + 4095) / 4096 * 4096;
+}
+uint64_t record_offset(uint32_t layer, uint32_t capacity, uint32_t position) {
+    return 4096ull + (uint64_t(layer) * capacity + position) * kStride;
+}
+uint64_t fnv1a(const uint8_t* p, size_t n) {
+    uint64_t h = kFnvSeed;
+    for (size_t i = 0; i < n; ++i) h = (h ^ p[i]) * kFnvPrime;
+    return h;
+}
+
+struct RecordHeader {
+    uint64_t digest, position, request;
+    uint32_t layer, version;
+};
+static_assert(sizeof(RecordHeader) == kHeader, "32-byte record header");
+
+// One wave per record: payload 4096 B = 64 lanes x 4 x 16 B, header by 2 lanes.
+__global__ void __launch_bounds__(256)
+cold_copy_kernel(const uint8_t* __restrict__ image, uint32_t layer, uint32_t capacity,
+                 uint64_t request, const uint32_t* __restrict__ positions, uint32_t count,
+                 uint8_t* __restrict__ out, uint64_t* __restrict__ digests,
+                 uint32_t* __restrict__ flags) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t i = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (i >= count) return;
+    const uint32_t p = positions[i];
+    if (p >= capacity) {  // nothing to read
+        if (lane == 0) {
+            flags[i] = 1u;
+            digests[i] = 0;
+        }
+        return;
+    }
+    const uint8_t* rec = image + 4096ull + (uint64_t(layer) * capacity + p) * kStride;
+    uint4 v[4];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j)
+        v[j] = *reinterpret_cast<const uint4*>(rec + kHeader + j * 1024 + lane * 16);
+    uint4 hdr = make_uint4(0u, 0u, 0u, 0u);
+    if (lane < 2) hdr = *reinterpret_cast<const uint4*>(rec + lane * 16);
+    uint8_t* dst = out + uint64_t(i) * kRow;
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(dst + j * 1024 + lane * 16) = v[j];
+    // lane 0: digest, position; lane 1: request, layer | version << 32
+    const uint64_t a = (uint64_t(hdr.y) << 32) | hdr.x, b = (uint64_t(hdr.w) << 32) | hdr.z;
+    const uint64_t request_in = __shfl(a, 1, 64), ident = __shfl(b, 1, 64);
+    if (lane == 0) {
+        const bool ok = b == p && request_in == request && uint32_t(ident) == layer &&
+                        uint32_t(ident >> 32) == 1u;
+        flags[i] = ok ? 0u : 1u;
+        digests[i] = a;
+    }
+}
+
+// One lane per record: FNV-1a 64 over the staged row, in byte order.
+__global__ void __launch_bounds__(256)
+cold_digest_kernel(const uint8_t* __restrict__ rows, const uint64_t* __restrict__ digests,
+                   uint32_t count, uint32_t* __restrict__ flags) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= count) return;
+    const uint4* row = reinterpret_cast<const uint4*>(rows + uint64_t(i) * kRow);
+    uint64_t h = kFnvSeed;
+    for (uint32_t c = 0; c < kRow / 16; ++c) {
+        const uint4 w = row[c];
+        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k)
+#pragma unroll
+            for (uint32_t b = 0; b < 4; ++b) h = (h ^ ((words[k] >> (8 * b)) & 0xffu)) * kFnvPrime;
+    }
+    if (h != digests[i]) flags[i] |= 2u;
+}
+
+// Status: code HS_ERR_CORRUPT when any record failed, k = failed records.
+__global__ void __launch_bounds__(256)
+cold_status_kernel(const uint32_t* __restrict__ flags, uint32_t count, hs_status_t* status) {
+    __shared__ uint32_t bad;
+    if (threadIdx.x == 0) bad = 0;
+    __syncthreads();
+    uint32_t mine = 0;
+    for (uint32_t i = threadIdx.x; i < count; i += 256) mine += flags[i] ? 1u : 0u;
+    if (mine) atomicAdd(&bad, mine);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        hs_status_t s{};
+        s.code = bad ? HS_ERR_CORRUPT : HS_OK;
+        s.k = bad;
+        *status = s;
+    }
+}
+
+}  // namespace
+
+size_t cold_fetch_workspace_bytes(uint32_t count) {
+    const size_t n = count ? count : 1;
+    return align256(sizeof(uint64_t) * n) + align256(sizeof(uint32_t) * n);
+}
+
+int launch_cold_fetch(const void* image, uint32_t layer, const uint32_t* positions,
+                      uint32_t count, uint8_t* out, hs_status_t* status, void* workspace,
+                      hipStream_t stream) {
+    if (!image || !positions || !out || !status || !workspace) return reject("cold fetch: null pointer");
+    if (count == 0) return reject("cold fetch: count must be >= 1");
+    if ((reinterpret_cast<uintptr_t>(image) | reinterpret_cast<uintptr_t>(out)) & 15u)
+        return reject("cold fetch: image and out must be 16-byte aligned");
+    // the image header is host memory: geometry comes from it, as the
+    // reference's reader takes it from the file's first page
+    uint64_t h[8];
+    std::memcpy(h, image, sizeof h);
+    if (h[0] != kMagic || h[1] != 1 || h[5] != kRow || h[6] != kStride || h[3] == 0 ||
+        h[3] > kMaxLayers || h[4] == 0 || h[4] > kMaxPositions || h[7] != extent_of(h[3], h[4]))
+        return reject("cold fetch: not a SegmentedKVStore v1 image of 4096 B records");
+    if (layer >= h[3]) return reject("cold fetch: layer beyond the image");
+    uint64_t* digests = static_cast<uint64_t*>(workspace);
+    uint32_t* flags = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) +
+                                                  align256(sizeof(uint64_t) * count));
+    hipLaunchKernelGGL(cold_copy_kernel, dim3((count + 3) / 4), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(image), layer, static_cast<uint32_t>(h[4]),
+                       h[2], positions, count, out, digests, flags);
+    hipLaunchKernelGGL(cold_digest_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, out,
+                       digests, count, flags);
+    hipLaunchKernelGGL(cold_status_kernel, dim3(1), dim3(256), 0, stream, flags, count, status);
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hip_fail(st, "cold fetch launch");
+}
+
+}  // namespace hs
+
+extern "C" {
+
+uint64_t hs_kv_store_bytes(uint32_t layers, uint32_t capacity) {
+    if (layers == 0 || layers > hs::kMaxLayers || capacity == 0 || capacity > hs::kMaxPositions)
+        return 0;
+    return hs::extent_of(layers, capacity);
+}
+
+int hs_kv_store_init(void* image, uint64_t request, uint32_t layers, uint32_t capacity) {
+    hs::clear_error();
+    if (!image) return hs::reject("kv store: null image");
+    const uint64_t extent = hs_kv_store_bytes(layers, capacity);
+    if (!extent) return hs::reject("bounded segmented geometry/quota");
+    std::memset(image, 0, extent);
+    uint64_t h[8] = {hs::kMagic, 1, request, layers, capacity, hs::kRow, hs::kStride, extent};
+    std::memcpy(image, h, sizeof h);
+    return HS_OK;
+}
+
+int hs_kv_store_append(void* image, uint32_t layer, uint32_t first, const uint8_t* rows,
+                       uint32_t count) {
+    hs::clear_error();
+    if (!image || !rows || count == 0) return hs::reject("kv store: null image/rows or count 0");
+    uint64_t h[8];
+    std::memcpy(h, image, sizeof h);
+    if (h[0] != hs::kMagic || h[1] != 1) return hs::reject("kv store: not a v1 image");
+    if (layer >= h[3] || first > h[4] || count > h[4] - first)
+        return hs::reject("append capacity");
+    auto* base = static_cast<uint8_t*>(image);
+    for (uint32_t i = 0; i < count; ++i) {
+        const uint8_t* row = rows + uint64_t(i) * hs::kRow;
+        hs::RecordHeader hdr{hs::fnv1a(row, hs::kRow), uint64_t(first) + i, h[2], layer, 1};
+        uint8_t* rec = base + hs::record_offset(layer, static_cast<uint32_t>(h[4]), first + i);
+        std::memcpy(rec, &hdr, sizeof hdr);
+        std::memcpy(rec + hs::kHeader, row, hs::kRow);
+    }
+    return HS_OK;
+}
+
+size_t hs_kv_cold_fetch_workspace_bytes(uint32_t count) {
+    return hs::cold_fetch_workspace_bytes(count);
+}
+
+int hs_kv_cold_fetch(const void* image, uint32_t layer, const uint32_t* positions_dev,
+                     uint32_t count, uint8_t* out_dev, hs_status_t* status_dev,
+                     void* workspace_dev, void* stream) {
+    hs::clear_error();
+    return hs::launch_cold_fetch(image, layer, positions_dev, count, out_dev, status_dev,
+                                 workspace_dev, hs::as_stream(stream));
+}
+
+}  // extern "C"

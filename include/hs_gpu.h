@@ -34,7 +34,8 @@ enum {
     HS_ERR_MISSING = 8,      /* selected id without KV row (gqa_pack.hpp:44) */
     HS_ERR_HIP = 9,          /* HIP runtime call failed                      */
     HS_ERR_UNSUPPORTED = 10, /* valid for the reference, beyond this build   */
-    HS_ERR_OVERFLOW = 11     /* finite value beyond F16 (full_gqa_runtime.cpp:63) */
+    HS_ERR_OVERFLOW = 11,    /* finite value beyond F16 (full_gqa_runtime.cpp:63) */
+    HS_ERR_CORRUPT = 12      /* cold record identity/digest (segmented_store.cpp:92-94) */
 };
 
 /* Device-side result of one selection; written by hs_gqa_select*. */
@@ -176,6 +177,34 @@ int hs_rehearsal_query(const uint16_t *hidden_dev, const uint16_t *wq_dev,
                        const uint32_t *positions, uint32_t batch, float eps, float theta,
                        uint16_t *q_dev, hs_status_t *status_dev, void *workspace_dev,
                        void *stream);
+
+/* ---- cold tier -------------------------------------------------------------
+ * SegmentedKVStore v1 images (storage/segmented_store.cpp:18-38): a 4096 B
+ * header page (u64 magic "HSKVSEG1", version 1, request, layers, positions,
+ * record bytes 4096, stride 4128, extent), then per (layer, position) a
+ * 32 B header {u64 FNV-1a digest of the row, u64 position, u64 request,
+ * u32 layer, u32 version 1} and the 4096 B KV row, at 4096 +
+ * (layer*positions + position)*4128; the extent is rounded up to 4096 B.
+ * hs_kv_store_bytes gives the extent (0 for a geometry the reference
+ * refuses: layers 1..128, positions 1..66048); hs_kv_store_init and
+ * hs_kv_store_append build an image in host memory (the reference's append,
+ * :77-82, with the digests computed on the host).  Keep the image in pinned
+ * host memory (hipHostMalloc) for the GPU to read it. */
+uint64_t hs_kv_store_bytes(uint32_t layers, uint32_t positions);
+int hs_kv_store_init(void *image, uint64_t request, uint32_t layers, uint32_t positions);
+int hs_kv_store_append(void *image, uint32_t layer, uint32_t first, const uint8_t *rows,
+                       uint32_t count);
+/* The device read of the cold rows of one layer (SegmentedKVStore::fetch,
+ * segmented_store.cpp:85-95): positions_dev [count] -> out_dev [count][4096]
+ * read straight from the pinned image over the host link, every record's
+ * identity (position, request, layer, version) and FNV-1a digest checked on
+ * the device.  status_dev: code HS_ERR_CORRUPT and k = number of bad
+ * records, else HS_OK.  The header page is read by the host call.
+ * workspace: hs_kv_cold_fetch_workspace_bytes(count).  3 launches. */
+size_t hs_kv_cold_fetch_workspace_bytes(uint32_t count);
+int hs_kv_cold_fetch(const void *image, uint32_t layer, const uint32_t *positions_dev,
+                     uint32_t count, uint8_t *out_dev, hs_status_t *status_dev,
+                     void *workspace_dev, void *stream);
 
 /* ---- (3) union / gather / pack ------------------------------------------
  * gqa_physical_union (runtime/gqa_pack.hpp:12-22): 32 id lists

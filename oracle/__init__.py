@@ -59,6 +59,12 @@ class Port:
         L.hso_history_cover.argtypes = [_P, _SZ, _SZ, _SZ, ctypes.c_float, ctypes.c_float,
                                         ctypes.c_int, _P, _SZ, ctypes.POINTER(_SZ), _P,
                                         ctypes.POINTER(_SZ)]
+        L.hso_fnv1a64.restype = ctypes.c_uint64
+        L.hso_fnv1a64.argtypes = [_P, _SZ]
+        L.hso_kv_store_extent.restype = ctypes.c_uint64
+        L.hso_kv_store_extent.argtypes = [_SZ, _SZ]
+        L.hso_kv_store_header.argtypes = [_P, ctypes.c_uint64, _SZ, _SZ]
+        L.hso_kv_record.argtypes = [_P, _P, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32]
         L.hso_physical_union.argtypes = [_P, _P, _SZ, _SZ, _P, ctypes.POINTER(_SZ)]
         L.hso_pack.argtypes = [_P, _P, _SZ, _P, _SZ, _P, _SZ, _P, _SZ, _P, _P, _P]
         L.hso_gather_rows.argtypes = [_P, _P, _P, _SZ, _P, _P]
@@ -126,6 +132,23 @@ class Port:
         if rc:
             return rc, 0, None, None
         return rc, bound.value, ids[:, : bound.value], physical[: np_out.value]
+
+    def fnv1a64(self, data):
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        return self.L.hso_fnv1a64(_ptr(data), data.size)
+
+    def kv_store_image(self, request, layers, positions, layer, rows, first=0):
+        """SegmentedKVStore image bytes with rows at positions first.. of layer."""
+        rows = np.ascontiguousarray(rows, dtype=np.uint8).reshape(-1, 4096)
+        image = np.zeros(self.L.hso_kv_store_extent(layers, positions), dtype=np.uint8)
+        self.L.hso_kv_store_header(_ptr(image), request, layers, positions)
+        rec = np.zeros(4128, dtype=np.uint8)
+        for i, row in enumerate(rows):
+            p = first + i
+            self.L.hso_kv_record(_ptr(rec), _ptr(np.ascontiguousarray(row)), p, request, layer)
+            off = 4096 + (layer * positions + p) * 4128
+            image[off:off + 4128] = rec
+        return image
 
     def physical_union(self, ids_rows, visible):
         stride = max(1, max(len(r) for r in ids_rows))
@@ -222,11 +245,32 @@ class Ref:
                                    ctypes.POINTER(_SZ)]
         L.hsref_physical_union.argtypes = [_P, _P, _SZ, _SZ, _P, ctypes.POINTER(_SZ)]
         L.hsref_pack.argtypes = [_P, _P, _SZ, _P, _SZ, _P, _SZ, _P, _SZ, _P, _P, _P]
+        L.hsref_checksum.restype = ctypes.c_uint64
+        L.hsref_checksum.argtypes = [_P, _SZ]
+        L.hsref_segmented_write.argtypes = [ctypes.c_char_p, ctypes.c_uint64, _SZ, ctypes.c_uint64,
+                                            _SZ, _P, _SZ, ctypes.POINTER(ctypes.c_uint64)]
         self.L = L
         self._scorers = {}
 
     def error(self):
         return self.L.hsref_last_error().decode()
+
+    def checksum(self, data):
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        return self.L.hsref_checksum(_ptr(data), data.size)
+
+    def segmented_file(self, path, request, layers, positions, layer, rows):
+        """Bytes of a SegmentedKVStore file holding rows [count][4096] at
+        positions 0.. of `layer` (the reference's own writer)."""
+        rows = np.ascontiguousarray(rows, dtype=np.uint8)
+        extent = ctypes.c_uint64(0)
+        rc = self.L.hsref_segmented_write(str(path).encode(), request, layers, positions, layer,
+                                          _ptr(rows), rows.size // 4096, ctypes.byref(extent))
+        if rc:
+            raise RuntimeError(self.error())
+        data = np.fromfile(str(path), dtype=np.uint8)
+        assert data.size == extent.value
+        return data
 
     def scorer(self, threads=1, impl=0):
         key = (threads, impl)

@@ -334,6 +334,55 @@ int hso_history_cover(const uint16_t *raw, size_t heads, size_t stride,
     return HSO_OK;
 }
 
+/* ---- cold tier format (storage/segmented_store.cpp:18-38, file_store.cpp:12) */
+
+uint64_t hso_fnv1a64(const uint8_t *p, size_t n)
+{
+    uint64_t h = 14695981039346656037ULL;
+    for (size_t i = 0; i < n; ++i) {
+        h ^= p[i];
+        h *= 1099511628211ULL;
+    }
+    return h;
+}
+
+static void put_u64(uint8_t *dst, uint64_t v)
+{
+    for (int b = 0; b < 8; ++b)
+        dst[b] = (uint8_t)(v >> (8 * b));
+}
+
+uint64_t hso_kv_store_extent(size_t layers, size_t positions)
+{
+    return (4096u + (uint64_t)layers * positions * 4128u + 4095u) / 4096u * 4096u;
+}
+
+void hso_kv_store_header(uint8_t *page, uint64_t request, size_t layers, size_t positions)
+{
+    memset(page, 0, 4096);
+    put_u64(page + 0, 0x48534b5653454731ULL);
+    put_u64(page + 8, 1);
+    put_u64(page + 16, request);
+    put_u64(page + 24, layers);
+    put_u64(page + 32, positions);
+    put_u64(page + 40, 4096);
+    put_u64(page + 48, 4128);
+    put_u64(page + 56, hso_kv_store_extent(layers, positions));
+}
+
+void hso_kv_record(uint8_t *out, const uint8_t *row, uint64_t position, uint64_t request,
+                   uint32_t layer)
+{
+    put_u64(out + 0, hso_fnv1a64(row, 4096));
+    put_u64(out + 8, position);
+    put_u64(out + 16, request);
+    for (int b = 0; b < 4; ++b) {
+        out[24 + b] = (uint8_t)(layer >> (8 * b));
+        out[28 + b] = (uint8_t)(1u >> (8 * b));
+    }
+    memcpy(out + 32, row, 4096);
+}
+
 /* ---- union and pack (runtime/gqa_pack.hpp:12-58) ------------------------ */
 
 int hso_physical_union(const uint32_t *ids, const size_t *lens,

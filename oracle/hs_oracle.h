@@ -33,6 +33,9 @@
  *       tokens per head reach it; error cases of :310-327.  The reference
  *       function itself (full_gqa_runtime.cpp) needs the absent
  *       nlohmann/json.hpp and is not compiled.
+ *   hso_fnv1a64 / hso_kv_store_header / hso_kv_record : published FNV-1a 64
+ *       test vectors, the compiled reference checksum(), and byte equality
+ *       with a file written by the compiled reference SegmentedKVStore.
  *   hso_physical_union / hso_pack / hso_gather_rows : tests/gqa_pack_tests.cpp
  *       known values, and the compiled reference pack_gqa_workspace.
  *   hso_attention_f64    : parity unpinned against the reference (its
@@ -130,6 +133,15 @@ int hso_history_cover(const uint16_t *raw, size_t heads, size_t stride,
                       size_t position, float alpha, float ratio, int fp32_counts,
                       uint32_t *ids, size_t ids_stride, size_t *bound_out,
                       uint32_t *physical, size_t *physical_n);
+
+/* Cold tier format (storage/segmented_store.cpp:18-38, file_store.cpp:12):
+ * FNV-1a 64; the 4096 B header page; one 4128 B record (32 B header + row)
+ * at 4096 + (layer*positions + position)*4128 of the image. */
+uint64_t hso_fnv1a64(const uint8_t *p, size_t n);
+uint64_t hso_kv_store_extent(size_t layers, size_t positions);
+void hso_kv_store_header(uint8_t *page, uint64_t request, size_t layers, size_t positions);
+void hso_kv_record(uint8_t *out, const uint8_t *row, uint64_t position, uint64_t request,
+                   uint32_t layer);
 
 /* Dense-reference decode attention restricted to a selection, FP64.
  * Semantics of patches/llama-b6000-external-attention-device.patch:49-66:

@@ -12,10 +12,14 @@
 //   select_gqa_scores                policy/gqa_policy.hpp:19-21
 //   gqa_physical_union               runtime/gqa_pack.hpp:12-22
 //   pack_gqa_workspace               runtime/gqa_pack.hpp:26-58
+//   checksum                         storage/file_store.hpp:13
+//   SegmentedKVStore (create, append) storage/segmented_store.hpp:8-30
 #include "policy/full_gqa_cpu.hpp"
 #include "policy/gqa_policy.hpp"
 #include "policy/host_policy.hpp"
 #include "runtime/gqa_pack.hpp"
+#include "storage/file_store.hpp"
+#include "storage/segmented_store.hpp"
 
 #include <cmath>
 #include <cstdint>
@@ -144,6 +148,25 @@ int hsref_pack(const std::uint32_t* ids, const std::size_t* lens, std::size_t id
         std::vector<std::uint64_t> phys(physical, physical + np);
         std::vector<std::uint8_t> bytes(payload, payload + np * 4096);
         hillserve::pack_gqa_workspace(sel, pos, phys, bytes, count, k, v, mask);
+        return 0;
+    } catch (const std::exception& e) {
+        return fail(e, 1);
+    }
+}
+
+std::uint64_t hsref_checksum(const void* data, std::size_t n) { return hillserve::checksum(data, n); }
+
+// Creates a SegmentedKVStore file at `path` and appends `count` 4096 B rows
+// at positions 0.. of `layer`; returns its extent in *extent.
+int hsref_segmented_write(const char* path, std::uint64_t request, std::size_t layers,
+                          std::uint64_t positions, std::size_t layer, const std::uint8_t* rows,
+                          std::size_t count, std::uint64_t* extent) {
+    try {
+        hillserve::SegmentedKVStore store(path, request, layers, positions, 4096,
+                                          9ULL * 1024 * 1024 * 1024);
+        std::vector<std::uint8_t> data(rows, rows + count * 4096);
+        if (count) store.append(layer, 0, data);
+        *extent = store.extent_bytes();
         return 0;
     } catch (const std::exception& e) {
         return fail(e, 1);
