@@ -35,6 +35,8 @@ constexpr uint64_t kMagic = 0x48534b5653454731ull;
 constexpr uint64_t kFnvSeed = 14695981039346656037ull, kFnvPrime = 1099511628211ull;
 constexpr uint32_t kRow = 4096, kHeader = 32, kStride = kRow + kHeader;
 constexpr uint32_t kMaxLayers = 128, kMaxPositions = 66048;  // segmented_store.cpp:31
+constexpr uint32_t kPad = 0xffffffffu;  // a position list's padding entry: no record
+constexpr uint32_t kPadFlag = 4u;
 
 uint64_t extent_of(uint32_t layers, uint32_t capacity) {
     return (4096ull + uint64_t(layers) * capacity * kStride + 4095) / 4096 * 4096;
@@ -64,9 +66,9 @@ cold_copy_kernel(const uint8_t* __restrict__ image, uint32_t layer, uint32_t cap
     const uint32_t i = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (i >= count) return;
     const uint32_t p = positions[i];
-    if (p >= capacity) {  // nothing to read
+    if (p == kPad || p >= capacity) {  // padding entry, or nothing to read
         if (lane == 0) {
-            flags[i] = 1u;
+            flags[i] = p == kPad ? kPadFlag : 1u;
             digests[i] = 0;
         }
         return;
@@ -97,7 +99,7 @@ __global__ void __launch_bounds__(256)
 cold_digest_kernel(const uint8_t* __restrict__ rows, const uint64_t* __restrict__ digests,
                    uint32_t count, uint32_t* __restrict__ flags) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= count) return;
+    if (i >= count || (flags[i] & kPadFlag)) return;
     const uint4* row = reinterpret_cast<const uint4*>(rows + uint64_t(i) * kRow);
     uint64_t h = kFnvSeed;
     for (uint32_t c = 0; c < kRow / 16; ++c) {
@@ -118,7 +120,7 @@ cold_status_kernel(const uint32_t* __restrict__ flags, uint32_t count, hs_status
     if (threadIdx.x == 0) bad = 0;
     __syncthreads();
     uint32_t mine = 0;
-    for (uint32_t i = threadIdx.x; i < count; i += 256) mine += flags[i] ? 1u : 0u;
+    for (uint32_t i = threadIdx.x; i < count; i += 256) mine += (flags[i] & 3u) ? 1u : 0u;
     if (mine) atomicAdd(&bad, mine);
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -127,6 +129,67 @@ cold_status_kernel(const uint32_t* __restrict__ flags, uint32_t count, hs_status
         s.k = bad;
         *status = s;
     }
+}
+
+// Cold plan of one sequence (n <= 32768, one 1024-thread workgroup, one
+// membership word per thread): the tokens selected by any head whose row is
+// cold, ascending, padded with kPad to `list_size`; the row map of every
+// token (its hot-pool slot, staging_base + its cold-list index, or -1 for a
+// cold token nobody selected); and the cold count.
+__global__ void __launch_bounds__(1024)
+cold_plan_kernel(const uint32_t* __restrict__ member, uint32_t heads, uint32_t n,
+                 const int32_t* __restrict__ slot, uint32_t staging_base, uint32_t list_size,
+                 uint32_t* __restrict__ positions, int32_t* __restrict__ rows,
+                 uint32_t* __restrict__ count_out) {
+    __shared__ uint32_t wsum[16];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t words = (n + 31) / 32;
+    uint32_t any = 0, cold = 0;
+    if (tid < words) {
+        for (uint32_t h = 0; h < heads; ++h) any |= member[static_cast<size_t>(h) * words + tid];
+#pragma unroll 4
+        for (uint32_t j = 0; j < 32; ++j) {
+            const uint32_t p = tid * 32 + j;
+            if (p < n && slot[p] < 0) cold |= 1u << j;
+        }
+    }
+    const uint32_t take = any & cold;
+    // exclusive scan of the per-thread counts
+    const uint32_t c = static_cast<uint32_t>(__popc(take));
+    uint32_t x = c;
+#pragma unroll
+    for (uint32_t off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < 16; ++w) {
+        before += w < wave ? wsum[w] : 0u;
+        total += wsum[w];
+    }
+    uint32_t at = before + x - c;
+    if (tid < words) {
+        for (uint32_t j = 0; j < 32; ++j) {
+            const uint32_t p = tid * 32 + j;
+            if (p >= n) break;
+            if (!((cold >> j) & 1u)) {
+                rows[p] = slot[p];
+            } else if ((take >> j) & 1u) {
+                // a list shorter than the cold count drops the excess (the
+                // count tells the caller); no write goes past list_size
+                if (at < list_size) positions[at] = p;
+                rows[p] = at < list_size ? static_cast<int32_t>(staging_base + at) : -1;
+                ++at;
+            } else {
+                rows[p] = -1;
+            }
+        }
+    }
+    for (uint32_t i = total + tid; i < list_size; i += 1024) positions[i] = kPad;
+    if (tid == 0) *count_out = total;
 }
 
 }  // namespace
@@ -164,9 +227,31 @@ int launch_cold_fetch(const void* image, uint32_t layer, const uint32_t* positio
     return st == hipSuccess ? HS_OK : hip_fail(st, "cold fetch launch");
 }
 
+int launch_cold_plan(const uint32_t* member, uint32_t heads, uint32_t n, const int32_t* slot,
+                     uint32_t staging_base, uint32_t list_size, uint32_t* positions,
+                     int32_t* rows, uint32_t* count, hipStream_t stream) {
+    if (!member || !slot || !positions || !rows || !count) return reject("cold plan: null pointer");
+    if (heads == 0 || heads > 128 || n == 0 || n > 32768) return reject("cold plan: heads 1..128, n 1..32768");
+    if (list_size == 0 || staging_base > 0x7fffffffu - list_size)
+        return reject("cold plan: list size / staging base");
+    hipLaunchKernelGGL(cold_plan_kernel, dim3(1), dim3(1024), 0, stream, member, heads, n, slot,
+                       staging_base, list_size, positions, rows, count);
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hip_fail(st, "cold plan launch");
+}
+
 }  // namespace hs
 
 extern "C" {
+
+int hs_gqa_cold_plan(const uint32_t* member_dev, uint32_t heads, uint32_t n,
+                     const int32_t* slot_dev, uint32_t staging_base, uint32_t list_size,
+                     uint32_t* positions_dev, int32_t* rows_dev, uint32_t* count_dev,
+                     void* stream) {
+    hs::clear_error();
+    return hs::launch_cold_plan(member_dev, heads, n, slot_dev, staging_base, list_size,
+                                positions_dev, rows_dev, count_dev, hs::as_stream(stream));
+}
 
 uint64_t hs_kv_store_bytes(uint32_t layers, uint32_t capacity) {
     if (layers == 0 || layers > hs::kMaxLayers || capacity == 0 || capacity > hs::kMaxPositions)

@@ -198,13 +198,33 @@ int hs_kv_store_append(void *image, uint32_t layer, uint32_t first, const uint8_
  * segmented_store.cpp:85-95): positions_dev [count] -> out_dev [count][4096]
  * read straight from the pinned image over the host link, every record's
  * identity (position, request, layer, version) and FNV-1a digest checked on
- * the device.  status_dev: code HS_ERR_CORRUPT and k = number of bad
- * records, else HS_OK.  The header page is read by the host call.
+ * the device.  A position of 0xffffffff is padding: no record is read and
+ * its output row is left as it was.  status_dev: code HS_ERR_CORRUPT and k
+ * = number of bad records, else HS_OK.  The header page is read by the host
+ * call.
  * workspace: hs_kv_cold_fetch_workspace_bytes(count).  3 launches. */
 size_t hs_kv_cold_fetch_workspace_bytes(uint32_t count);
 int hs_kv_cold_fetch(const void *image, uint32_t layer, const uint32_t *positions_dev,
                      uint32_t count, uint8_t *out_dev, hs_status_t *status_dev,
                      void *workspace_dev, void *stream);
+
+/* Cold plan of one sequence after its selection (the hot/prefetched/cold
+ * split of FullGqaRuntimePolicy::fetch, policy/full_gqa_runtime.cpp:
+ * 640-660, for device consumers): member_dev [heads][ceil(n/32)] bitmaps,
+ * slot_dev [n] = hot-pool row of each token or -1 when its row is cold.
+ * Writes positions_dev [list_size]: the tokens any head selected whose row
+ * is cold, ascending, padded with 0xffffffff (ready for hs_kv_cold_fetch
+ * with count = list_size); rows_dev [n]: slot for hot tokens,
+ * staging_base + list index for selected cold tokens (rows fetched into
+ * pool rows staging_base.., so attention reads hot and cold rows through
+ * one row map), -1 for cold tokens nobody selected; *count_dev: the number
+ * of cold rows.  n <= 32768; list_size >= the number of cold tokens (a
+ * shorter list drops the excess rows, mapped to -1; *count_dev still
+ * counts them). */
+int hs_gqa_cold_plan(const uint32_t *member_dev, uint32_t heads, uint32_t n,
+                     const int32_t *slot_dev, uint32_t staging_base, uint32_t list_size,
+                     uint32_t *positions_dev, int32_t *rows_dev, uint32_t *count_dev,
+                     void *stream);
 
 /* ---- (3) union / gather / pack ------------------------------------------
  * gqa_physical_union (runtime/gqa_pack.hpp:12-22): 32 id lists

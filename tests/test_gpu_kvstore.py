@@ -73,3 +73,55 @@ def test_bad_header_refused(hs):
     image.numpy()[0] ^= 1  # magic
     with pytest.raises(hs.HsError):
         cold_fetch(hs, image, 0, [0])
+
+
+def test_cold_plan_and_padded_fetch(hs):
+    # selection bitmaps of 4 heads over n tokens, half the 64-token blocks hot
+    g = rng(4)
+    n, heads = 4000, 4
+    words = (n + 31) // 32
+    member = g.integers(0, 2**32, size=(heads, words), dtype=np.uint64).astype(np.uint32)
+    member &= g.integers(0, 2**32, size=(heads, words), dtype=np.uint64).astype(np.uint32)
+    member[:, -1] &= (1 << (n - 32 * (words - 1))) - 1
+    hot_blocks = g.permutation((n + 63) // 64)[: (n + 63) // 128]
+    slot = np.full(n, -1, dtype=np.int32)
+    next_slot = 0
+    for b in sorted(hot_blocks):
+        for t in range(b * 64, min(n, b * 64 + 64)):
+            slot[t] = next_slot
+            next_slot += 1
+    cold_tokens = int((slot < 0).sum())
+    staging_base = next_slot
+    L = hs.lib()
+    md = torch.from_numpy(member.view(np.int32)).cuda()
+    sd = torch.from_numpy(slot).cuda()
+    pos = torch.empty(cold_tokens, dtype=torch.int32, device="cuda")
+    rows = torch.empty(n, dtype=torch.int32, device="cuda")
+    count = torch.empty(1, dtype=torch.int32, device="cuda")
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    hs.check(L.hs_gqa_cold_plan(vp(md), heads, n, vp(sd), staging_base, cold_tokens, vp(pos),
+                                vp(rows), vp(count), st))
+    any_sel = np.zeros(n, dtype=bool)
+    for h in range(heads):
+        bits = np.unpackbits(member[h].view(np.uint8), bitorder="little")[:n].astype(bool)
+        any_sel |= bits
+    want = np.nonzero(any_sel & (slot < 0))[0]
+    got_pos = pos.cpu().numpy().view(np.uint32)
+    assert int(count.item()) == want.size
+    assert np.array_equal(got_pos[: want.size], want)
+    assert np.all(got_pos[want.size:] == 0xFFFFFFFF)
+    want_rows = np.where(slot >= 0, slot, -1)
+    want_rows[want] = staging_base + np.arange(want.size)
+    assert np.array_equal(rows.cpu().numpy(), want_rows)
+    # the padded list fetches exactly the listed cold records
+    data = g.integers(0, 256, size=(n, 4096), dtype=np.uint8)
+    image = pinned_image(hs, 9, 1, n, 0, data)
+    out = torch.zeros((cold_tokens, 4096), dtype=torch.uint8, device="cuda")
+    status = hs.ops.new_status("cuda")
+    ws = hs.ops.workspace(L.hs_kv_cold_fetch_workspace_bytes(cold_tokens), "cuda")
+    hs.check(L.hs_kv_cold_fetch(vp(image), 0, vp(pos), cold_tokens, vp(out), vp(status), vp(ws), st))
+    assert hs.ops.read_status(status)["code"] == 0
+    o = out.cpu().numpy()
+    assert np.array_equal(o[: want.size], data[want])
+    assert not o[want.size:].any()  # padding rows untouched
