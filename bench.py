@@ -55,7 +55,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bounded CPU-baseline sample duration")
     p.add_argument("--layer-steps", type=int, default=20)
-    p.add_argument("--only", choices=["score", "select", "select_id", "layer", "batch"], default=None,
+    p.add_argument("--only", choices=["score", "select", "select_id", "layer", "batch", "tier"],
+                   default=None,
                    help="profiling aid: run just one kernel family over the 30 layers "
                         "(prints its own timing line, not the benchmark JSON)")
     return p.parse_args()
@@ -225,6 +226,190 @@ def batch_leg(args, hs, ops, torch, stream, dev):
     return out
 
 
+TIER_SEQS, TIER_N, TIER_PHYS = 8, 32768, 2
+
+
+def tier_leg(args, hs, ops, torch, stream, dev):
+    """8 sequences x N = 32768, half of the 64-token blocks hot
+    (seeded permutation).  Hot rows sit in an HBM pool followed by staging
+    rows; cold rows sit in a pinned SegmentedKVStore image per sequence.  The
+    keys of every token stay in HBM for scoring (the cold-key scoring owner
+    is the GPU: the reference's raw-K score file, held in HBM).  Per layer, on
+    the main stream: batched score, batched id-order selection, cold plan per
+    sequence; on a side stream: the cold fetch of that layer (identity and
+    FNV-1a checked), overlapped with the next layer's score and selection;
+    attention of the layer runs on the main stream once its cold rows are in.
+    A step is 30 layers over TIER_PHYS distinct physical layers."""
+    import ctypes
+    import numpy as np
+    L = hs.lib()
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    g = np.random.default_rng(11)
+    blocks = TIER_N // 64
+    hot_blocks = [np.sort(g.permutation(blocks)[: blocks // 2]) for _ in range(TIER_SEQS)]
+    hot_rows = (blocks // 2) * 64
+    cold_rows = TIER_N - hot_rows
+    side = torch.cuda.Stream(device=dev)
+    log(f"configs[4]: building {TIER_SEQS} x {TIER_PHYS} layers of hot pools, keys and pinned "
+        f"cold images ({TIER_SEQS * TIER_PHYS * TIER_N * 4128 / 2**30:.1f} GiB pinned)")
+    seqs = []
+    for s_i in range(TIER_SEQS):
+        slot = np.full(TIER_N, -1, dtype=np.int32)
+        for j, b in enumerate(hot_blocks[s_i]):
+            slot[b * 64:(b + 1) * 64] = np.arange(j * 64, (j + 1) * 64, dtype=np.int32)
+        extent = L.hs_kv_store_bytes(TIER_PHYS, TIER_N)
+        image = torch.empty(extent, dtype=torch.uint8, pin_memory=True)
+        hs.check(L.hs_kv_store_init(vp(image), 5000 + s_i, TIER_PHYS, TIER_N))
+        layers = []
+        for l in range(TIER_PHYS):
+            rows = torch.empty((TIER_N, 2048), dtype=torch.float16, device=dev)  # K | V per token
+            ops.fill_rope_keys(rows, TIER_N, 2048, 8, seed=9000 + 10 * s_i + l, theta=500000.0)
+            v = torch.empty((TIER_N, 1024), dtype=torch.float16, device=dev)
+            ops.fill_gaussian(v, seed=9500 + 10 * s_i + l)
+            rows[:, 1024:] = v
+            keys = rows[:, :1024].contiguous()  # every token's K, for scoring
+            slot_dev = torch.from_numpy(slot).to(dev)
+            pool = torch.empty((hot_rows + cold_rows, 2048), dtype=torch.float16, device=dev)
+            hot_ids = torch.from_numpy(np.nonzero(slot >= 0)[0]).to(dev)
+            pool[:hot_rows] = rows[hot_ids]
+            host_rows = rows.view(torch.uint8).cpu().numpy()
+            hs.check(L.hs_kv_store_append(vp(image), l, 0,
+                                          host_rows.ctypes.data_as(ctypes.c_void_p), TIER_N))
+            words = (TIER_N + 31) // 32
+            q = torch.empty(4096, dtype=torch.float16, device=dev)
+            ops.fill_gaussian(q, seed=9800 + 10 * s_i + l)
+            q32 = torch.empty((32, 128), dtype=torch.float32, device=dev).normal_(
+                generator=torch.Generator(device=dev).manual_seed(s_i * 10 + l))
+            kmax = math.floor(TIER_N * float(np.float32(RATIO)))
+            layers.append(dict(
+                keys=keys, q=q, q32=q32, pool=pool, slot=slot_dev,
+                scores=torch.empty((32, TIER_N), dtype=torch.float16, device=dev),
+                partial=torch.empty(TIER_N // 64, dtype=torch.int32, device=dev),
+                ids=torch.empty((32, kmax), dtype=torch.int32, device=dev), kmax=kmax,
+                counts=torch.empty(32, dtype=torch.int32, device=dev),
+                member=torch.empty((32, words), dtype=torch.int32, device=dev),
+                status=ops.new_status(dev),
+                ws=ops.workspace(ops.select_workspace_bytes(32, TIER_N), dev),
+                pos=torch.empty(cold_rows, dtype=torch.int32, device=dev),
+                rowmap=torch.empty(TIER_N, dtype=torch.int32, device=dev),
+                count=torch.empty(1, dtype=torch.int32, device=dev),
+                cstatus=ops.new_status(dev),
+                cws=ops.workspace(L.hs_kv_cold_fetch_workspace_bytes(cold_rows), dev),
+                out=torch.empty((32, 128), dtype=torch.float32, device=dev),
+                aws=ops.workspace(ops.attention_workspace_bytes(TIER_N), dev)))
+            del rows, v, host_rows
+        seqs.append(dict(image=image, layers=layers))
+    torch.cuda.synchronize()
+    sp, sside = ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p(side.cuda_stream)
+    score_tabs, sel_tabs = [], []
+    for l in range(TIER_PHYS):
+        st_ = (hs.ScoreJob * TIER_SEQS)()
+        lt_ = (hs.SelectJob * TIER_SEQS)()
+        for s_i, sq in enumerate(seqs):
+            d = sq["layers"][l]
+            st_[s_i] = hs.ScoreJob(d["q"].data_ptr(), d["keys"].data_ptr(), d["scores"].data_ptr(),
+                                   d["partial"].data_ptr(), 1024, TIER_N, TIER_N, 0)
+            lt_[s_i] = hs.SelectJob(d["scores"].data_ptr(), d["partial"].data_ptr(), d["ids"].data_ptr(),
+                                    d["counts"].data_ptr(), d["member"].data_ptr(),
+                                    d["status"].data_ptr(), d["ws"].data_ptr(), TIER_N, TIER_N,
+                                    d["kmax"], 0)
+        score_tabs.append(ctypes.cast(st_, ctypes.c_void_p))
+        sel_tabs.append(ctypes.cast(lt_, ctypes.c_void_p))
+        score_tabs.append(st_)  # keep the tables alive
+        sel_tabs.append(lt_)
+    score_ptr = [score_tabs[2 * l] for l in range(TIER_PHYS)]
+    sel_ptr = [sel_tabs[2 * l] for l in range(TIER_PHYS)]
+
+    def front(l):  # main stream: score, select, cold plan of layer l
+        p = l % TIER_PHYS
+        hs.check(L.hs_gqa_score_batched(score_ptr[p], TIER_SEQS, sp))
+        hs.check(L.hs_gqa_select_batched(sel_ptr[p], TIER_SEQS, 32, ALPHA, RATIO,
+                                         hs.HS_SELECT_SCALE_RAW | hs.HS_SELECT_ID_ORDER, sp))
+        for sq in seqs:
+            d = sq["layers"][p]
+            hs.check(L.hs_gqa_cold_plan(vp(d["member"]), 32, TIER_N, vp(d["slot"]), hot_rows,
+                                        cold_rows, vp(d["pos"]), vp(d["rowmap"]), vp(d["count"]), sp))
+
+    def cold(l, strm):
+        p = l % TIER_PHYS
+        for sq in seqs:
+            d = sq["layers"][p]
+            staging = d["pool"][hot_rows:]
+            hs.check(L.hs_kv_cold_fetch(vp(sq["image"]), p, vp(d["pos"]), cold_rows, vp(staging),
+                                        vp(d["cstatus"]), vp(d["cws"]), strm))
+
+    def attend(l):
+        p = l % TIER_PHYS
+        for sq in seqs:
+            d = sq["layers"][p]
+            hs.check(L.hs_gqa_sparse_attention(vp(d["q32"]), vp(d["pool"]), 4096, vp(d["rowmap"]),
+                                               hot_rows + cold_rows, vp(d["member"]), TIER_N,
+                                               vp(d["out"]), vp(d["aws"]), sp))
+
+    def step(with_cold=True):
+        pending = None
+        for l in range(LAYERS):
+            front(l)
+            ev = torch.cuda.Event()
+            ev.record(stream)
+            if with_cold:
+                side.wait_event(ev)
+                cold(l, sside)
+                done = torch.cuda.Event()
+                done.record(side)
+            if pending is not None:
+                if with_cold:
+                    stream.wait_event(pending[1])
+                attend(pending[0])
+            pending = (l, done if with_cold else None)
+        if with_cold:
+            stream.wait_event(pending[1])
+        attend(pending[0])
+
+    def cold_only():
+        for l in range(LAYERS):
+            cold(l, sp)
+
+    def timed(fn, reps):
+        b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        b.record(stream)
+        for _ in range(reps):
+            fn()
+        e.record(stream)
+        torch.cuda.synchronize()
+        return b.elapsed_time(e) / reps
+
+    step()
+    torch.cuda.synchronize()
+    for sq in seqs:
+        for d in sq["layers"]:
+            assert ops.read_status(d["status"])["code"] == 0
+            assert ops.read_status(d["cstatus"])["code"] == 0, ops.read_status(d["cstatus"])
+    counts = [int(d["count"].item()) for sq in seqs for d in sq["layers"]]
+    reps = 2
+    step_ms = timed(step, reps)
+    main_ms = timed(lambda: step(False), reps)
+    cold_ms = timed(cold_only, reps)
+    cold_bytes = sum(counts) / len(counts) * TIER_SEQS * LAYERS * 4128
+    overlap = max(0.0, min(1.0, (main_ms + cold_ms - step_ms) / cold_ms))
+    out = {
+        "workload": "configs[4]: 8 sequences x N=32768, 50% of 64-token blocks in HBM, cold rows in "
+                    "pinned SegmentedKVStore images, 30 layers per step",
+        "cold_key_scoring": "GPU: every token's K is HBM-resident (the raw-K score file held in HBM); "
+                            "cold 4096 B rows come over the host link for the selected tokens",
+        "ms_per_step": step_ms, "main_stream_ms": main_ms, "cold_fetch_ms": cold_ms,
+        "overlap_fraction": overlap, "cold_rows_per_seq_layer": sum(counts) / len(counts),
+        "cold_link_gbps": cold_bytes / (cold_ms * 1e-3) / 1e9,
+    }
+    log(f"configs[4]: {step_ms:.1f} ms/step (main stream alone {main_ms:.1f} ms, cold fetch alone "
+        f"{cold_ms:.1f} ms = {out['cold_link_gbps']:.1f} GB/s over the host link, "
+        f"{out['cold_rows_per_seq_layer']:.0f} cold rows per sequence-layer); overlap "
+        f"fraction {overlap:.3f}")
+    del seqs
+    return out
+
+
 def profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status, ws, kmax):
     """Back-to-back launches of one kernel family over the 30 layers."""
     def run():
@@ -300,6 +485,9 @@ def main():
 
     if args.only == "batch":
         batch_leg(args, hs, ops, torch, stream, dev)
+        return 0
+    if args.only == "tier":
+        tier_leg(args, hs, ops, torch, stream, dev)
         return 0
     if args.only in ("score", "select", "select_id"):
         return profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status,
@@ -382,6 +570,7 @@ def main():
     # ---- batched rehearsal + scoring + selection ----------------------
     del pools
     batch = batch_leg(args, hs, ops, torch, stream, dev)
+    tier = tier_leg(args, hs, ops, torch, stream, dev)
 
     # ---- CPU baseline on a bounded sample ----------------------------------------
     k_sample = torch.empty(N * 1024, dtype=torch.float16, device=dev)
@@ -424,6 +613,7 @@ def main():
             "union_rows": utokens,
         },
         "batch_step": batch,
+        "tier_step": tier,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
