@@ -4,9 +4,13 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <unistd.h>
+
 #include <algorithm>
+#include <cerrno>
 #include <chrono>
 #include <cmath>
+#include <cstring>
 #include <limits>
 #include <mutex>
 
@@ -401,13 +405,91 @@ void pack_gqa_workspace(const std::vector<std::vector<std::uint64_t>>& ids,
     sync(stream);
 }
 
+// ---- chunked stream planner (smartssd/stream_layout.hpp:18-51) --------------------
+
+std::vector<DirectChunkPlan> plan_raw_gqa_stream(const std::vector<ScoreFileRegion>& regions,
+                                                 std::size_t chunk_tokens) {
+    constexpr std::size_t kKeyBytes = kKvHeads * kDim * 2, kBlockBytes = 64 * kKeyBytes;
+    if (regions.empty() || chunk_tokens == 0 || chunk_tokens > 32768 || chunk_tokens % 64)
+        throw std::invalid_argument("CSS requires nonempty64-token regions and64<=chunk<=32768");
+    std::size_t total = 0;
+    for (const auto& r : regions) {
+        if (r.fd < 0 || r.bytes == 0 || r.offset % 4096 || r.bytes % kBlockBytes ||
+            r.offset > std::numeric_limits<std::uint64_t>::max() - r.bytes)
+            throw std::invalid_argument("CSS region must be aligned exact64-token raw GQA blocks");
+        if (r.bytes / kKeyBytes > 32768 - total) throw std::length_error("CSS pilot exceeds32768 cold tokens");
+        total += r.bytes / kKeyBytes;
+    }
+    std::vector<DirectChunkPlan> plan;
+    std::size_t region = 0;
+    std::uint64_t used = 0;  // bytes of `region` already planned
+    for (std::size_t first = 0; first < total; first += chunk_tokens) {
+        DirectChunkPlan chunk;
+        chunk.token_offset = first;
+        chunk.tokens = std::min(chunk_tokens, total - first);
+        std::size_t left = chunk.tokens * kKeyBytes, dest = 0;
+        while (left) {
+            const ScoreFileRegion& r = regions[region];
+            const std::size_t take = static_cast<std::size_t>(std::min<std::uint64_t>(left, r.bytes - used));
+            const std::uint64_t at = r.offset + used;
+            DirectChunkRead* last = chunk.reads.empty() ? nullptr : &chunk.reads.back();
+            if (last && last->fd == r.fd && last->offset + last->bytes == at)
+                last->bytes += take;  // contiguous in the same file: one read
+            else
+                chunk.reads.push_back(DirectChunkRead{r.fd, at, take, dest});
+            left -= take;
+            dest += take;
+            used += take;
+            if (used == r.bytes) {
+                ++region;
+                used = 0;
+            }
+        }
+        plan.push_back(std::move(chunk));
+    }
+    return plan;
+}
+
 // ---- score backend ---------------------------------------------------------------
+
+// Grow-only pinned host allocation (device-readable).
+class PinnedBuffer {
+public:
+    PinnedBuffer() = default;
+    PinnedBuffer(const PinnedBuffer&) = delete;
+    PinnedBuffer& operator=(const PinnedBuffer&) = delete;
+    ~PinnedBuffer() {
+        if (ptr_) (void)hipHostFree(ptr_);
+    }
+    void* ensure(std::size_t bytes) {
+        if (bytes > size_) {
+            if (ptr_) hip_check(hipHostFree(ptr_), "hipHostFree");
+            ptr_ = nullptr;
+            size_ = 0;
+            hip_check(hipHostMalloc(&ptr_, bytes, hipHostMallocDefault), "hipHostMalloc");
+            size_ = bytes;
+        }
+        return ptr_;
+    }
+    void* device() {
+        void* d = nullptr;
+        hip_check(hipHostGetDevicePointer(&d, ptr_, 0), "hipHostGetDevicePointer");
+        return d;
+    }
+    std::size_t size() const noexcept { return size_; }
+
+private:
+    void* ptr_ = nullptr;
+    std::size_t size_ = 0;
+};
 
 struct GpuScoreBackend::Impl {
     std::string abi;
     void* stream = nullptr;
     std::mutex invocation;
     DeviceBuffer query, keys, scores;
+    PinnedBuffer stage[2], host_scores[2];
+    DeviceBuffer stream_scores[2];
 };
 
 GpuScoreBackend::GpuScoreBackend(std::string abi, void* stream) : impl_(std::make_unique<Impl>()) {
@@ -459,6 +541,119 @@ DeviceScores GpuScoreBackend::score_raw_gqa(const std::vector<std::uint16_t>& q,
     if (!std::all_of(result.values.begin(), result.values.end(), finite_half))
         throw std::runtime_error("nonfinite raw GQA score");  // smartssd/xrt_backend.cpp:381
     return result;
+}
+
+FileScoreStreamReport GpuScoreBackend::score_file_regions_raw_gqa_stream(
+    const std::vector<std::uint16_t>& q, const std::vector<ScoreFileRegion>& regions,
+    std::size_t qh, std::size_t kh, std::size_t d, std::size_t chunk_tokens,
+    const FileScoreCallback& callback) {
+    std::lock_guard<std::mutex> call(impl_->invocation);
+    if (qh != 32 || kh != 8 || d != 128)
+        throw std::invalid_argument("raw GQA requires explicit V2/V3 ABI and Q32/KV8/D128,1<=N<=32768");
+    if (q.size() != kHeads * kDim) throw std::invalid_argument("raw GQA query vector size");
+    if (!callback) throw std::invalid_argument("CSS requires a chunk callback");
+    const auto plan = plan_raw_gqa_stream(regions, chunk_tokens);
+    constexpr std::size_t kKeyBytes = kKvHeads * kDim * 2;
+    auto stamp = [] {
+        return static_cast<std::uint64_t>(std::chrono::duration_cast<std::chrono::nanoseconds>(
+                                              Clock::now().time_since_epoch())
+                                              .count());
+    };
+    FileScoreStreamReport report;
+    const auto start = Clock::now();
+    const std::size_t key_bytes = chunk_tokens * kKeyBytes, score_bytes = kHeads * chunk_tokens * 2;
+    report.buffers_reused = impl_->stage[0].size() >= key_bytes;
+    auto* q_dev = impl_->query.as<std::uint16_t>(q.size());
+    for (int b = 0; b < 2; ++b) {
+        impl_->stage[b].ensure(key_bytes);
+        impl_->host_scores[b].ensure(score_bytes);
+        impl_->stream_scores[b].ensure(score_bytes);
+    }
+    report.allocation_ms = ms_since(start);
+    report.device_buffer_bytes = 2 * score_bytes + q.size() * 2;
+    report.host_score_buffer_bytes = 2 * score_bytes;
+    const auto qstart = Clock::now();
+    upload(q_dev, q.data(), q.size() * 2, impl_->stream);
+    sync(impl_->stream);
+    report.query_h2d_ms = ms_since(qstart);
+    report.query_h2d_bytes = q.size() * 2;
+
+    auto read_chunk = [&](const DirectChunkPlan& c, int slot, FileScoreChunkInfo& info) {
+        auto* dst = static_cast<std::uint8_t*>(impl_->stage[slot].ensure(key_bytes));
+        info.read_started_ns = stamp();
+        const auto t = Clock::now();
+        for (const auto& r : c.reads) {
+            std::size_t done = 0;
+            while (done < r.bytes) {
+                const ssize_t got = pread(r.fd, dst + r.destination_offset + done, r.bytes - done,
+                                          static_cast<off_t>(r.offset + done));
+                if (got < 0 && errno == EINTR) continue;
+                if (got <= 0) throw std::runtime_error("CSS direct read failed; no fallback");
+                done += static_cast<std::size_t>(got);
+                ++info.file_read_operations;
+            }
+            info.file_read_bytes += r.bytes;
+        }
+        info.file_read_ms = ms_since(t);
+        info.read_finished_ns = stamp();
+    };
+    std::vector<hipEvent_t> done(plan.size(), nullptr);
+    std::vector<FileScoreChunkInfo> infos(plan.size());
+    auto deliver = [&](std::size_t i) {
+        FileScoreChunkInfo& info = infos[i];
+        hip_check(hipEventSynchronize(done[i]), "hipEventSynchronize");
+        info.kernel_finished_ns = info.scores_CPU_ready_ns = stamp();
+        info.launch_wait_ms = (info.kernel_finished_ns - info.kernel_started_ns) / 1e6;
+        (void)hipEventDestroy(done[i]);
+        done[i] = nullptr;
+        const auto* values = static_cast<const std::uint16_t*>(impl_->host_scores[i % 2].ensure(score_bytes));
+        FileScoreChunk chunk;
+        chunk.values.assign(values, values + kHeads * info.tokens);
+        if (!std::all_of(chunk.values.begin(), chunk.values.end(), finite_half))
+            throw std::runtime_error("nonfinite raw GQA score");  // smartssd/xrt_backend.cpp:381
+        info.callback_started_ns = stamp();
+        chunk.info = info;
+        const auto t = Clock::now();
+        callback(chunk);
+        info.callback_ms = ms_since(t);
+        info.callback_finished_ns = stamp();
+        report.file_read_bytes += info.file_read_bytes;
+        report.score_d2h_bytes += info.score_d2h_bytes;
+        report.chunks.push_back(info);
+    };
+    try {
+        if (!plan.empty()) read_chunk(plan[0], 0, infos[0]);
+        for (std::size_t i = 0; i < plan.size(); ++i) {
+            const int slot = static_cast<int>(i % 2);
+            FileScoreChunkInfo& info = infos[i];
+            info.token_offset = plan[i].token_offset;
+            info.tokens = plan[i].tokens;
+            info.buffer_slot = static_cast<std::size_t>(slot);
+            info.score_d2h_bytes = kHeads * info.tokens * 2;
+            auto* s_dev = impl_->stream_scores[slot].as<std::uint16_t>(kHeads * chunk_tokens);
+            info.kernel_started_ns = stamp();
+            // the scorer reads this chunk's keys straight from pinned host memory
+            api_check(hs_gqa_score(q_dev, static_cast<const std::uint16_t*>(impl_->stage[slot].device()),
+                                   1024, nullptr, 0, static_cast<std::uint32_t>(info.tokens), s_dev,
+                                   info.tokens, nullptr, impl_->stream));
+            download(impl_->host_scores[slot].ensure(score_bytes), s_dev, info.score_d2h_bytes,
+                     impl_->stream);
+            hip_check(hipEventCreateWithFlags(&done[i], hipEventDisableTiming), "hipEventCreate");
+            hip_check(hipEventRecord(done[i], as_stream(impl_->stream)), "hipEventRecord");
+            // while chunk i is scored: deliver chunk i-1, then read chunk i+1
+            // into the buffer chunk i-1 used
+            if (i > 0) deliver(i - 1);
+            if (i + 1 < plan.size()) read_chunk(plan[i + 1], 1 - slot, infos[i + 1]);
+        }
+        if (!plan.empty()) deliver(plan.size() - 1);
+    } catch (...) {
+        (void)hipStreamSynchronize(as_stream(impl_->stream));
+        for (auto& e : done)
+            if (e) (void)hipEventDestroy(e);
+        throw;
+    }
+    report.total_ms = ms_since(start);
+    return report;
 }
 
 DeviceScores GpuScoreBackend::score(const std::vector<std::uint16_t>&,

@@ -13,6 +13,11 @@
 //        -> hillserve::gpu::gqa_physical_union / pack_gqa_workspace
 //   hillserve::FpgaScoreBackend::score_raw_gqa (smartssd/adapter.hpp:73-76)
 //        -> hillserve::gpu::GpuScoreBackend::score_raw_gqa
+//   hillserve::FpgaScoreBackend::score_file_regions_raw_gqa_stream
+//   (smartssd/adapter.hpp:67-71) and plan_raw_gqa_stream
+//   (smartssd/stream_layout.hpp:18-51)
+//        -> hillserve::gpu::GpuScoreBackend::score_file_regions_raw_gqa_stream
+//           and hillserve::gpu::plan_raw_gqa_stream
 // The host-vector overloads copy in, run on the device and copy out
 // (synchronous, like the reference calls); the *_device members take device
 // pointers and only enqueue on the object's stream.
@@ -23,6 +28,7 @@
 #pragma once
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -125,6 +131,55 @@ struct DeviceScores {
     ScoreDeviceTimings timings;
 };
 
+// ---- chunked streaming of raw-K file regions (smartssd/adapter.hpp:22-55) ----
+// A region is a page-aligned run of whole 64-token raw-K blocks (2048 B per
+// token) in a caller-owned file descriptor.
+struct ScoreFileRegion {
+    int fd = -1;
+    std::uint64_t offset = 0, bytes = 0;
+    bool capture_mapping_evidence = false;
+};
+struct DirectChunkRead {
+    int fd = -1;
+    std::uint64_t offset = 0;
+    std::size_t bytes = 0, destination_offset = 0;
+};
+struct DirectChunkPlan {
+    std::size_t token_offset = 0, tokens = 0;
+    std::vector<DirectChunkRead> reads;
+};
+// Chunks of chunk_tokens over the concatenated regions (the last may be
+// shorter); every read is page aligned, adjacent pieces of one descriptor
+// coalesce, a region crossing a chunk boundary splits.  Throws
+// std::invalid_argument / std::length_error on the layouts the reference
+// planner refuses (at most 32768 tokens in all).
+std::vector<DirectChunkPlan> plan_raw_gqa_stream(const std::vector<ScoreFileRegion>& regions,
+                                                 std::size_t chunk_tokens);
+
+// A streamed chunk is head-major [32 query heads][tokens]; token_offset
+// indexes the concatenation of the input regions.  Callback references
+// expire when it returns.  Times are steady_clock nanoseconds / ms.
+struct FileScoreChunkInfo {
+    std::size_t token_offset = 0, tokens = 0, buffer_slot = 0;
+    std::uint64_t file_read_bytes = 0, score_d2h_bytes = 0, file_read_operations = 0;
+    std::uint64_t read_started_ns = 0, read_finished_ns = 0;
+    std::uint64_t kernel_started_ns = 0, kernel_finished_ns = 0;
+    std::uint64_t scores_CPU_ready_ns = 0, callback_started_ns = 0, callback_finished_ns = 0;
+    double file_read_ms = 0, launch_wait_ms = 0, callback_ms = 0;
+};
+struct FileScoreChunk {
+    FileScoreChunkInfo info;
+    std::vector<std::uint16_t> values;
+};
+using FileScoreCallback = std::function<void(const FileScoreChunk&)>;
+struct FileScoreStreamReport {
+    std::vector<FileScoreChunkInfo> chunks;
+    double allocation_ms = 0, query_h2d_ms = 0, total_ms = 0;
+    std::uint64_t file_read_bytes = 0, query_h2d_bytes = 0, score_d2h_bytes = 0;
+    std::size_t device_buffer_bytes = 0, host_score_buffer_bytes = 0;
+    bool buffers_reused = false;
+};
+
 // The explicit full-dimension GQA ABI of the score backend: Q[32,128],
 // K[token,8,128], S[32,token].  abi "HS_FULL_GQA_PIPELINE_F16_V3" enforces
 // 64 <= n <= 32768, n % 64 == 0; "HS_FULL_GQA_F16_V2" accepts 1..32768
@@ -138,6 +193,15 @@ public:
     DeviceScores score_raw_gqa(const std::vector<std::uint16_t>& q,
                                const std::vector<std::uint16_t>& k, std::size_t query_heads,
                                std::size_t kv_heads, std::size_t tokens, std::size_t channels);
+    // Chunked streaming score of raw-K file regions: each chunk is read by
+    // the host into one of two page-aligned pinned buffers while the GPU
+    // scores the previous one straight from pinned memory (over the host
+    // link); scores come back per chunk through `callback`, in order.  Same
+    // shape rules as score_raw_gqa (Q32/KV8/D128); nonfinite scores throw.
+    FileScoreStreamReport score_file_regions_raw_gqa_stream(
+        const std::vector<std::uint16_t>& q, const std::vector<ScoreFileRegion>& regions,
+        std::size_t query_heads, std::size_t kv_heads, std::size_t channels,
+        std::size_t chunk_tokens, const FileScoreCallback& callback);
     // The per-query-head partial layout is not served (as the reference's
     // GQA-only images): throws std::invalid_argument.
     DeviceScores score(const std::vector<std::uint16_t>& q, const std::vector<std::uint16_t>& k,

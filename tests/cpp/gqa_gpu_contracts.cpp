@@ -8,6 +8,9 @@
 // Exit status: 0 passed, 1 failed, 77 no GPU visible (nothing run).
 #include <hip/hip_runtime_api.h>
 
+#include <fcntl.h>
+#include <unistd.h>
+
 #include <algorithm>
 #include <array>
 #include <cmath>
@@ -494,6 +497,86 @@ void pack_contracts() {
 
 }  // namespace
 
+// ---- chunked stream planner (tests/css_stream_layout_tests.cpp:13-44) ------------
+// The reference's known answers for plan_raw_gqa_stream; CPU only.
+void stream_layout_contracts() {
+    constexpr std::size_t block = 64 * 8 * 128 * 2;
+    auto plan = plan_raw_gqa_stream({{3, 0, block, false}, {3, 3 * block, block, false}, {3, 7 * block, block, false}}, 128);
+    check(plan.size() == 2 && plan[0].tokens == 128 && plan[1].tokens == 64, "tail shape");
+    check(plan[1].token_offset == 128 && plan[0].reads.size() == 2, "cold index map");
+    check(plan[0].reads[1].offset == 3 * block && plan[0].reads[1].destination_offset == block, "noncontiguous direct placement");
+    check(plan[1].reads[0].offset == 7 * block && plan[1].reads[0].destination_offset == 0, "tail original identity");
+    plan = plan_raw_gqa_stream({{3, block, block, false}, {3, 2 * block, 4 * block, false}}, 128);
+    check(plan.size() == 3 && plan[0].reads.size() == 1 && plan[0].reads[0].bytes == 2 * block, "coalescing");
+    check(plan[1].reads[0].offset == 3 * block && plan[2].reads[0].offset == 5 * block, "split coverage");
+    std::size_t read_bytes = 0;
+    for (const auto& chunk : plan) {
+        std::size_t dest = 0;
+        for (const auto& read : chunk.reads) {
+            check(read.destination_offset == dest && read.offset % 4096 == 0 && read.bytes % 4096 == 0, "direct alignment/coverage");
+            dest += read.bytes;
+        }
+        check(dest == chunk.tokens * 8 * 128 * 2, "chunk exact coverage");
+        read_bytes += dest;
+    }
+    check(read_bytes == 5 * block, "total byte coverage");
+    plan = plan_raw_gqa_stream({{3, 0, block, false}, {4, block, block, false}}, 128);
+    check(plan[0].reads.size() == 2, "different fd must not coalesce");
+    rejects([&] { plan_raw_gqa_stream({}, 64); }, "empty regions");
+    rejects([&] { plan_raw_gqa_stream({{3, 0, block, false}}, 0); }, "chunk 0");
+    rejects([&] { plan_raw_gqa_stream({{3, 0, block, false}}, 65); }, "chunk not 64-aligned");
+    rejects([&] { plan_raw_gqa_stream({{3, 0, block, false}}, 32832); }, "chunk beyond 32768");
+    rejects([&] { plan_raw_gqa_stream({{-1, 0, block, false}}, 64); }, "bad fd");
+    rejects([&] { plan_raw_gqa_stream({{3, 1, block, false}}, 64); }, "unaligned offset");
+    rejects([&] { plan_raw_gqa_stream({{3, 0, block - 4096, false}}, 64); }, "partial block");
+    rejects([&] { plan_raw_gqa_stream({{3, 0, 0, false}}, 64); }, "empty region");
+    rejects([&] { plan_raw_gqa_stream({{3, 0, 513 * block, false}}, 64); }, "beyond 32768 tokens");
+    rejects([&] { plan_raw_gqa_stream({{3, std::numeric_limits<std::uint64_t>::max() - 4095, block, false}}, 64); }, "offset overflow");
+}
+
+// GPU streaming of file regions: the chunks concatenate to the one-shot
+// score_raw_gqa of the same keys, bit for bit, in plan order.
+void stream_score_contracts() {
+    constexpr std::size_t block = 64 * 8 * 128 * 2, blocks = 24;
+    char path[] = "/tmp/hs_css_XXXXXX";
+    const int fd = mkstemp(path);
+    check(fd >= 0, "temporary raw-K file");
+    unlink(path);
+    std::uint32_t state = 0x13579bdfu;
+    auto next = [&] { state ^= state << 13; state ^= state >> 17; state ^= state << 5; return state; };
+    std::vector<std::uint16_t> file(blocks * block / 2);
+    for (auto& w : file) w = half_bits(float(int(next() % 4001) - 2000) / 512.f);
+    check(pwrite(fd, file.data(), file.size() * 2, 0) == static_cast<ssize_t>(file.size() * 2), "write raw-K file");
+    const std::vector<ScoreFileRegion> regions{{fd, 0, block, false}, {fd, 3 * block, block, false},
+                                               {fd, 7 * block, 9 * block, false}, {fd, 20 * block, 2 * block, false}};
+    std::vector<std::uint16_t> concat;
+    for (const auto& r : regions)
+        concat.insert(concat.end(), file.begin() + r.offset / 2, file.begin() + (r.offset + r.bytes) / 2);
+    const std::size_t tokens = concat.size() / 1024;
+    std::vector<std::uint16_t> q(32 * 128);
+    for (auto& w : q) w = half_bits(float(int(next() % 2001) - 1000) / 256.f);
+    GpuScoreBackend v2("HS_FULL_GQA_F16_V2");
+    const auto whole = v2.score_raw_gqa(q, concat, 32, 8, tokens, 128).values;
+    for (std::size_t chunk : {64u, 192u, 4096u}) {
+        std::vector<std::uint16_t> got(32 * tokens, 0);
+        std::size_t expect_offset = 0, calls = 0;
+        auto report = v2.score_file_regions_raw_gqa_stream(q, regions, 32, 8, 128, chunk, [&](const FileScoreChunk& c) {
+            check(c.info.token_offset == expect_offset, "chunks arrive in plan order");
+            check(c.values.size() == 32 * c.info.tokens, "head-major chunk size");
+            for (std::size_t h = 0; h < 32; ++h)
+                for (std::size_t t = 0; t < c.info.tokens; ++t)
+                    got[h * tokens + c.info.token_offset + t] = c.values[h * c.info.tokens + t];
+            expect_offset += c.info.tokens;
+            ++calls;
+        });
+        check(expect_offset == tokens && calls == (tokens + chunk - 1) / chunk, "every token once");
+        check(report.file_read_bytes == tokens * 2048 && report.chunks.size() == calls, "stream accounting");
+        check(got == whole, "streamed chunks equal the one-shot scores");
+        comparisons += got.size();
+    }
+    close(fd);
+}
+
 // ---- history cover (policy/full_gqa_runtime.cpp:299-344) ------------------------
 // The checks of tests/full_gqa_prefetch_tests.cpp:196-233 on the selection part:
 // bound-sized per-head covers of historical ids, a sorted union, the sparse
@@ -545,6 +628,12 @@ void cover_contracts() {
 }
 
 int main() {
+    try {
+        stream_layout_contracts();  // host-only contracts run with or without a GPU
+    } catch (const std::exception& e) {
+        std::cerr << e.what() << std::endl;
+        return 1;
+    }
     int devices = 0;
     if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0) {
         std::cout << "{\"status\":\"skipped\",\"reason\":\"no GPU visible\"}" << std::endl;
@@ -556,6 +645,7 @@ int main() {
         kernel_contracts();
         pack_contracts();
         cover_contracts();
+        stream_score_contracts();
         std::cout << "{\"status\":\"passed\",\"cases\":" << cases
                   << ",\"bitwise_scores_compared\":" << comparisons << "}" << std::endl;
         return 0;
