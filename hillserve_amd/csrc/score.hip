@@ -14,14 +14,17 @@
 //    the 4 query heads of that KV head.  Its Q operands (4 x 128 channels) are
 //    wave-uniform and come through the scalar unit, so every ordered FMA is
 //    one v_fma_mix_f32 with Q from an SGPR and K from a VGPR.
-//  * Keys are fetched coalesced: load instruction j covers tokens 4j..4j+3 of
-//    the tile, 16 lanes per 256 B head row, i.e. 8 whole 128 B lines per
-//    instruction.  The wave transposes the tile through its own 16 KiB LDS
-//    region (XOR-swizzled 16 B chunks: conflict-free writes and reads) so that
-//    afterwards lane t holds token t's 128 channels in order.
-//  * Waves are independent pipelines: the next tile's loads are issued right
-//    after the current tile is parked in LDS, so they overlap its compute.
-//    8 waves per CU keep ~32 MB of keys in flight across the chip.
+//  * The pipeline unit is half a tile (channels 0-63, then 64-127): load
+//    instruction j covers tokens 8j..8j+7, 8 lanes per 128 B half row, i.e.
+//    8 whole lines per instruction, with no branch between the requests.  The
+//    wave transposes the half tile through its own 8 KiB LDS region
+//    (XOR-swizzled 16 B chunks: conflict-free writes and reads) so that lane t
+//    then holds token t's 64 channels in order; the 4 chains run on across
+//    the two halves.
+//  * Waves are independent pipelines: the next half's loads are issued right
+//    after the current half is parked in LDS, so they overlap its compute,
+//    and a half tile is the most compute left once the last loads land.
+//    16 waves per CU keep the whole key set in flight at N = 32768.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -38,9 +41,6 @@ constexpr uint32_t kChunks = 16;  // 16-byte chunks per 128-channel F16 head row
 
 __device__ __forceinline__ float lo_half(uint32_t w) { return h2f(w & 0xffffu); }
 __device__ __forceinline__ float hi_half(uint32_t w) { return h2f(w >> 16); }
-
-// LDS slot (in 16 B units) of chunk c of tile token t.
-__device__ __forceinline__ uint32_t slot(uint32_t t, uint32_t c) { return t * kChunks + (c ^ (t & 15u)); }
 
 // One scoring job: a query, its keys and where the scores go.  A launch
 // covers one job or, batched, up to kMaxBatch of them; job j owns the
@@ -61,7 +61,8 @@ struct ScoreJobs {
 template <bool kRows, bool kBatch>
 __global__ void __launch_bounds__(kWavesPerBlock * 64)
 score_kernel(const ScoreJobs jobs, const int32_t* __restrict__ rows, uint32_t pool_rows) {
-    __shared__ uint4 lds[kWavesPerBlock][kTileTokens * kChunks];
+    constexpr uint32_t kHalf = kChunks / 2;  // 16 B chunks of one half row (64 channels)
+    __shared__ uint4 lds[kWavesPerBlock][kTileTokens * kHalf];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     uint4* region = lds[w];
@@ -69,15 +70,12 @@ score_kernel(const ScoreJobs jobs, const int32_t* __restrict__ rows, uint32_t po
     const uint32_t waves = gridDim.x * kWavesPerBlock;
     const uint32_t tiles = jobs.total_ids;  // (token tile, KV head) pairs of all jobs
 
-    // job of a launch-wide id (wave-uniform)
     auto job_of = [&](uint32_t id) -> uint32_t {
         if (!kBatch) return 0;
         uint32_t j = 0;
         for (uint32_t i = 1; i < jobs.count; ++i) j = id >= jobs.job[i].first_id ? i : j;
-        return j;
+        return __builtin_amdgcn_readfirstlane(j);
     };
-    // Row index of token (tile >> 3) * 64 + lane of the job, or ~0 when it
-    // reads as zero keys (past n, or a mapped row outside the pool).
     auto row_of = [&](const ScoreJob& jb, uint32_t id) -> uint32_t {
         const uint32_t token = ((id - jb.first_id) >> 3) * kTileTokens + lane;
         if (token >= jb.n) return 0xffffffffu;
@@ -85,39 +83,57 @@ score_kernel(const ScoreJobs jobs, const int32_t* __restrict__ rows, uint32_t po
         const uint32_t r = static_cast<uint32_t>(rows[token]);
         return r < pool_rows ? r : 0xffffffffu;
     };
-    // Instruction j: lane reads chunk (lane & 15) of tile token 4j + (lane >> 4).
-    auto load = [&](const ScoreJob& jb, uint32_t id, uint32_t my_row, uint4 (&v)[16]) {
-        const uint16_t* base = jb.keys + ((id - jb.first_id) & 7u) * 128u + (lane & 15u) * 8u;
+    // Half h of the tile: instruction j reads chunk 8h + (lane & 7) of token
+    // 8j + (lane >> 3), i.e. 8 whole 128 B lines per instruction.
+    auto load = [&](const ScoreJob& jb, uint32_t id, uint32_t h, uint32_t my_row, uint4 (&v)[kHalf]) {
+        const uint32_t local = id - jb.first_id;
+        const uint16_t* base = jb.keys + (local & 7u) * 128u + h * 64u + (lane & 7u) * 8u;
+        uint32_t r[kHalf];
 #pragma unroll
-        for (uint32_t j = 0; j < 16; ++j) {
-            const uint32_t r = __shfl(my_row, 4 * j + (lane >> 4), 64);
-            v[j] = r != 0xffffffffu
-                       ? *reinterpret_cast<const uint4*>(base + static_cast<size_t>(r) * jb.stride_words)
-                       : make_uint4(0u, 0u, 0u, 0u);
+        for (uint32_t j = 0; j < kHalf; ++j) {
+            if (kRows) {
+                r[j] = __shfl(my_row, 8 * j + (lane >> 3), 64);
+            } else {
+                const uint32_t t = (local >> 3) * kTileTokens + 8 * j + (lane >> 3);
+                r[j] = t < jb.n ? t : 0xffffffffu;
+            }
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kHalf; ++j) {
+            const bool ok = r[j] != 0xffffffffu;
+            const uint4 x = *reinterpret_cast<const uint4*>(
+                base + static_cast<size_t>(ok ? r[j] : 0u) * jb.stride_words);
+            v[j] = ok ? x : make_uint4(0u, 0u, 0u, 0u);
         }
     };
-    auto stash = [&](const uint4 (&v)[16]) {
+    auto hslot = [](uint32_t t, uint32_t c) { return t * kHalf + (c ^ (t & 7u)); };
+    auto stash = [&](const uint4 (&v)[kHalf]) {
 #pragma unroll
-        for (uint32_t j = 0; j < 16; ++j) region[slot(4 * j + (lane >> 4), lane & 15u)] = v[j];
+        for (uint32_t j = 0; j < kHalf; ++j) region[hslot(8 * j + (lane >> 3), lane & 7u)] = v[j];
     };
-    auto compute = [&](const ScoreJob& jb, uint32_t id) {
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    // channels 64h .. 64h+63 of the 4 ordered chains
+    auto compute = [&](const ScoreJob& jb, uint32_t id, uint32_t h) {
         const uint32_t local = id - jb.first_id;
         const uint32_t head_kv = local & 7u;  // wave-uniform
-        // Q is never written by the kernel: reading it through the constant
-        // address space lets every Q operand come from a scalar load
         using ConstU32 = const __attribute__((address_space(4))) uint32_t;
-        ConstU32* qh = (ConstU32*)(jb.q32) + head_kv * 4 * 64;
-        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        // a wave-uniform pointer: the job's query is read with scalar loads
+        const uint64_t qa = reinterpret_cast<uint64_t>(jb.q32);
+        // (readfirstlane returns int: widen each half through uint32_t, or a
+        // low word with bit 31 set would sign-extend over the high word)
+        const uint32_t q_hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(uint32_t(qa >> 32)));
+        const uint32_t q_lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(uint32_t(qa)));
+        const uint64_t qu = (static_cast<uint64_t>(q_hi) << 32) | static_cast<uint64_t>(q_lo);
+        ConstU32* qh = (ConstU32*)(reinterpret_cast<const uint32_t*>(qu)) + head_kv * 4 * 64 + h * 32;
 #pragma unroll
-        for (uint32_t j = 0; j < 16; ++j) {
-            const uint4 k4 = region[slot(lane, j)];
+        for (uint32_t j = 0; j < kHalf; ++j) {
+            const uint4 k4 = region[hslot(lane, j)];
             const uint32_t kw[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
             for (uint32_t p = 0; p < 4; ++p) {
-                const uint32_t c2 = j * 4 + p;  // channel pair index
+                const uint32_t c2 = j * 4 + p;
                 const float klo = lo_half(kw[p]), khi = hi_half(kw[p]);
-                const uint32_t q0 = qh[c2], q1 = qh[64 + c2], q2 = qh[128 + c2],
-                               q3 = qh[192 + c2];
+                const uint32_t q0 = qh[c2], q1 = qh[64 + c2], q2 = qh[128 + c2], q3 = qh[192 + c2];
                 a0 = __builtin_fmaf(lo_half(q0), klo, a0);
                 a1 = __builtin_fmaf(lo_half(q1), klo, a1);
                 a2 = __builtin_fmaf(lo_half(q2), klo, a2);
@@ -128,6 +144,10 @@ score_kernel(const ScoreJobs jobs, const int32_t* __restrict__ rows, uint32_t po
                 a3 = __builtin_fmaf(hi_half(q3), khi, a3);
             }
         }
+    };
+    auto finish = [&](const ScoreJob& jb, uint32_t id) {
+        const uint32_t local = id - jb.first_id;
+        const uint32_t head_kv = local & 7u;
         const uint32_t token = (local >> 3) * kTileTokens + lane;
         const uint32_t s0 = f2h(a0), s1 = f2h(a1), s2 = f2h(a2), s3 = f2h(a3);
         if (token < jb.n) {
@@ -138,47 +158,51 @@ score_kernel(const ScoreJobs jobs, const int32_t* __restrict__ rows, uint32_t po
             o[3 * static_cast<size_t>(jb.out_stride)] = static_cast<uint16_t>(s3);
         }
         if (jb.head0_partial != nullptr && head_kv == 0) {
-            // NaN is skipped, like std::max over the scores
             const uint32_t best =
                 wave_max_u32(token < jb.n && !is_nan_half(s0) ? order_key(s0) : 0u);
             if (lane == 0) jb.head0_partial[local >> 3] = best;
         }
+        a0 = a1 = a2 = a3 = 0.0f;
     };
 
-    uint4 v[16];
+    // Pipeline unit: half a tile.  While one half is computed, the next is
+    // in flight; the tile's 4 chains run on across its two halves.
+    uint4 v[kHalf];
     uint32_t id = wave;
     if (id >= tiles) return;
     ScoreJob cur = jobs.job[job_of(id)];
-    uint32_t next_row = row_of(cur, id);
-    load(cur, id, next_row, v);
-    ScoreJob nxt = cur;
-    if (id + waves < tiles) {
-        nxt = jobs.job[job_of(id + waves)];
-        next_row = row_of(nxt, id + waves);
-    }
-    while (id < tiles) {
-        const uint32_t next = id + waves;
+    uint32_t row = row_of(cur, id);
+    load(cur, id, 0, row, v);
+    while (true) {
         stash(v);
         __builtin_amdgcn_wave_barrier();
-        const ScoreJob here = cur;
-        if (next < tiles) {
-            load(nxt, next, next_row, v);
-            cur = nxt;
-            if (next + waves < tiles) {
-                nxt = jobs.job[job_of(next + waves)];
-                next_row = row_of(nxt, next + waves);
-            }
-        }
-        compute(here, id);
+        load(cur, id, 1, row, v);
+        compute(cur, id, 0);
         __builtin_amdgcn_wave_barrier();
+        stash(v);
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t next = id + waves;
+        ScoreJob nxt = cur;
+        uint32_t nrow = 0;
+        if (next < tiles) {
+            nxt = jobs.job[job_of(next)];
+            nrow = row_of(nxt, next);
+            load(nxt, next, 0, nrow, v);
+        }
+        compute(cur, id, 1);
+        finish(cur, id);
+        __builtin_amdgcn_wave_barrier();
+        if (next >= tiles) break;
         id = next;
+        cur = nxt;
+        row = nrow;
     }
 }
 
-// 8 waves per CU (two per SIMD, 128 KiB of LDS), each streaming its share of
-// the (token tile, KV head) pairs.
+// 16 waves per CU (four per SIMD, 8 KiB of LDS each), each streaming its
+// share of the (token tile, KV head) pairs: at N = 32768 one pair per wave.
 uint32_t score_grid(uint32_t ids) {
-    const uint32_t max_blocks = (8u / kWavesPerBlock) * static_cast<uint32_t>(device_cu_count());
+    const uint32_t max_blocks = (16u / kWavesPerBlock) * static_cast<uint32_t>(device_cu_count());
     return std::min<uint32_t>((ids + kWavesPerBlock - 1) / kWavesPerBlock, max_blocks);
 }
 
