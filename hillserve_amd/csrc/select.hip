@@ -326,20 +326,42 @@ __device__ __forceinline__ void load_run(const SelectArgs& a, uint32_t h, uint32
                                          uint32_t (&packed)[kR / 2]) {
     static_assert(kR % 8 == 0, "runs are whole 16-byte words");
     const uint16_t* row = a.scores + static_cast<size_t>(h) * a.stride;
-    const bool vec = (reinterpret_cast<uintptr_t>(row) & 15u) == 0 && begin + kR <= a.n;
+    const uint32_t n = a.n;
+    // 16-byte loads when the row is aligned (uniform over the workgroup);
+    // every load is straight-line, its address clamped into the row
+    const bool vec = (reinterpret_cast<uintptr_t>(row) & 15u) == 0 && n >= 8;
+    if (vec) {
 #pragma unroll
-    for (uint32_t v = 0; v < kR / 8; ++v) {
-        uint32_t* w = packed + 4 * v;
-        const uint32_t at = begin + 8 * v;
-        if (vec) {
-            const uint4 x = *reinterpret_cast<const uint4*>(row + at);
-            w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
-        } else {
+        for (uint32_t v = 0; v < kR / 8; ++v) {
+            const uint32_t at = begin + 8 * v;
+            const bool full = at + 8 <= n;
+            const uint4 x = *reinterpret_cast<const uint4*>(row + (full ? at : 0u));
+            uint32_t* w = packed + 4 * v;
+            w[0] = full ? x.x : 0u; w[1] = full ? x.y : 0u;
+            w[2] = full ? x.z : 0u; w[3] = full ? x.w : 0u;
+        }
+        if (begin + kR > n && begin < n) {  // the row's last, partial word
+#pragma unroll
+            for (uint32_t v = 0; v < kR / 8; ++v) {
+                const uint32_t at = begin + 8 * v;
+                if (at < n && at + 8 > n) {
+#pragma unroll
+                    for (uint32_t c = 0; c < 4; ++c) {
+                        const uint32_t lo = at + 2 * c < n ? row[at + 2 * c] : 0u;
+                        const uint32_t hi = at + 2 * c + 1 < n ? row[at + 2 * c + 1] : 0u;
+                        packed[4 * v + c] = lo | (hi << 16);
+                    }
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (uint32_t v = 0; v < kR / 8; ++v) {
 #pragma unroll
             for (uint32_t c = 0; c < 4; ++c) {
-                const uint32_t lo = at + 2 * c < a.n ? row[at + 2 * c] : 0u;
-                const uint32_t hi = at + 2 * c + 1 < a.n ? row[at + 2 * c + 1] : 0u;
-                w[c] = lo | (hi << 16);
+                const uint32_t e = begin + 8 * v + 2 * c;
+                const uint32_t lo = row[e < n ? e : n - 1u], hi = row[e + 1 < n ? e + 1 : n - 1u];
+                packed[4 * v + c] = (e < n ? lo : 0u) | ((e + 1 < n ? hi : 0u) << 16);
             }
         }
     }
@@ -368,15 +390,21 @@ __device__ __forceinline__ uint32_t hist_total(const uint32_t* whist, uint32_t b
     return c;
 }
 
+// p[i] for i < n (n >= 1), else 0, with no branch around the load: the
+// index is clamped into range and the value selected afterwards, so all the
+// loads of a phase are in flight together instead of each waiting for the
+// last at a branch join.
+__device__ __forceinline__ uint32_t load_or_zero(const uint32_t* p, uint32_t i, uint32_t n) {
+    const uint32_t x = p[i < n ? i : n - 1u];
+    return i < n ? x : 0u;
+}
+
 // Maximum of the head-0 per-tile maxima (at most kMaxN / 64 of them).
 __device__ __forceinline__ uint32_t partial_max(const SelectArgs& a) {
     constexpr uint32_t kLoads = kMaxN / 64 / kThreads;
     uint32_t v[kLoads];
 #pragma unroll
-    for (uint32_t u = 0; u < kLoads; ++u) {
-        const uint32_t i = threadIdx.x + u * kThreads;
-        v[u] = i < a.partials ? a.partial[i] : 0u;
-    }
+    for (uint32_t u = 0; u < kLoads; ++u) v[u] = load_or_zero(a.partial, threadIdx.x + u * kThreads, a.partials);
     uint32_t best = 0;
 #pragma unroll
     for (uint32_t u = 0; u < kLoads; ++u) best = v[u] > best ? v[u] : best;
@@ -521,13 +549,13 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
 #pragma unroll
     for (uint32_t u = 0; u < kCountLoads; ++u) {  // heads * S slice counts
         const uint32_t i = tid + u * kThreads;
-        cnt[u] = i < groups ? a.g_count[i] : 0u;
-        bad[u] = i < groups ? a.g_bad[i] : 0u;
+        cnt[u] = load_or_zero(a.g_count, i, groups);
+        bad[u] = load_or_zero(a.g_bad, i, groups);
     }
 #pragma unroll
     for (uint32_t u = 0; u < kBinLoads; ++u) {  // this head's S * 256 bins
         const uint32_t i = tid + u * kThreads;
-        hi_part[u] = i < S * 256 ? a.g_hi[static_cast<size_t>(h * S) * 256 + i] : 0u;
+        hi_part[u] = load_or_zero(a.g_hi + static_cast<size_t>(h * S) * 256, i, S * 256);
     }
     uint32_t packed[kRun / 2];
     const uint32_t begin = s * kSlice + tid * kRun;
@@ -770,9 +798,8 @@ __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
 #pragma unroll
     for (uint32_t u = 0; u < kBinLoads; ++u) {
         const uint32_t i = tid + u * kThreads;
-        const bool ok = i < S * 256;
-        hv[u] = ok ? a.g_hi[static_cast<size_t>(h * S) * 256 + i] : 0u;
-        lv[u] = ok ? a.g_lo[static_cast<size_t>(h * S) * 256 + i] : 0u;
+        hv[u] = load_or_zero(a.g_hi + static_cast<size_t>(h * S) * 256, i, S * 256);
+        lv[u] = load_or_zero(a.g_lo + static_cast<size_t>(h * S) * 256, i, S * 256);
     }
     uint32_t packed[kRun / 2];
     load_run<kRun>(a, h, begin, packed);
@@ -938,79 +965,6 @@ static_assert(kHeadMaxN / 64 <= kHThreads, "one head-0 tile maximum per thread")
 static_assert(kMaxHeads * (kHeadMaxN / kSlice) <= kHThreads, "one slice count per thread");
 static_assert(kSortRange % kHThreads == 0, "whole key bins per thread");
 
-// Stable placement of the m composites in A ((0xffff - key) << 16 | id, in
-// id order, all keys in [kstar, kstar + kSortRange)) by key, from their key
-// histogram `start`: exclusive suffix scan (larger keys
-// first), scatter into the key groups through B, then each group placed in
-// id order by counting its smaller ids.  Returns false, with A untouched,
-// when a group exceeds kGroupCap (many equal keys); the caller then sorts A
-// otherwise.  cursor: kSortRange words.
-__device__ bool place_by_histogram(uint32_t* A, uint32_t* B, uint32_t m, uint32_t kstar,
-                                   uint32_t* start, uint32_t* cursor, uint32_t* tmp,
-                                   uint32_t* flag) {
-    constexpr uint32_t kPer = kSortRange / kHThreads;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t first = (kHThreads - 1 - tid) * kPer;  // thread 0 owns the top bins
-    uint32_t c[kPer], sum = 0, big = 0;
-#pragma unroll
-    for (uint32_t i = 0; i < kPer; ++i) {
-        c[i] = start[first + i];
-        sum += c[i];
-        big = max(big, c[i]);
-    }
-    if (big > kGroupCap) *flag = 1;  // read after the scan's barriers
-    const uint32_t scan = block_exclusive_scan<kHThreads>(sum, tmp);
-    if (*flag) return false;
-    uint32_t run = scan + sum;
-#pragma unroll
-    for (uint32_t i = 0; i < kPer; ++i) {
-        run -= c[i];
-        start[first + i] = run;
-        cursor[first + i] = run;
-    }
-    __syncthreads();
-    for (uint32_t q = tid; q < m; q += kHThreads) {
-        const uint32_t e = A[q];
-        B[atomicAdd(&cursor[0xffffu - (e >> 16) - kstar], 1u)] = e;
-    }
-    __syncthreads();
-    // each element's rank in its group by id; a thread's kPerThread elements
-    // are handled side by side so their LDS round trips overlap, and the
-    // first 8 members of every group are read in one batch (groups are short)
-    constexpr uint32_t kPerThread = kHeadMaxK / kHThreads;
-    uint32_t e[kPerThread], gs[kPerThread], gc[kPerThread], r[kPerThread];
-#pragma unroll
-    for (uint32_t u = 0; u < kPerThread; ++u) {
-        const uint32_t q = tid + u * kHThreads;
-        e[u] = q < m ? B[q] : 0u;
-    }
-#pragma unroll
-    for (uint32_t u = 0; u < kPerThread; ++u) {
-        const uint32_t bin = min(0xffffu - (e[u] >> 16) - kstar, kSortRange - 1);
-        gs[u] = start[bin];
-        gc[u] = tid + u * kHThreads < m ? cursor[bin] - gs[u] : 0u;
-    }
-#pragma unroll
-    for (uint32_t u = 0; u < kPerThread; ++u) {
-        r[u] = 0;
-        uint32_t v[8];
-#pragma unroll
-        for (uint32_t i = 0; i < 8; ++i) v[i] = B[gs[u] + min(i, gc[u] ? gc[u] - 1 : 0u)];
-#pragma unroll
-        for (uint32_t i = 0; i < 8; ++i)
-            r[u] += i < gc[u] && (v[i] & 0xffffu) < (e[u] & 0xffffu) ? 1u : 0u;
-    }
-#pragma unroll
-    for (uint32_t u = 0; u < kPerThread; ++u)
-        for (uint32_t i = 8; i < gc[u]; ++i)  // long groups
-            r[u] += (B[gs[u] + i] & 0xffffu) < (e[u] & 0xffffu) ? 1u : 0u;
-#pragma unroll
-    for (uint32_t u = 0; u < kPerThread; ++u)
-        if (tid + u * kHThreads < m) A[gs[u] + r[u]] = e[u];
-    __syncthreads();
-    return true;
-}
-
 template <bool kRankOrder>
 __global__ void __launch_bounds__(kHThreads) head_select_kernel(const SelectJobs js) {
     __shared__ uint32_t hist[2][256];
@@ -1028,23 +982,26 @@ __global__ void __launch_bounds__(kHThreads) head_select_kernel(const SelectJobs
 
     // every global read is issued up front: head-0 tile maxima, all slice
     // counts and flags, this head's slice histograms and this thread's keys
-    uint32_t best = tid < a.partials ? a.partial[tid] : 0u;
-    const uint32_t cnt = tid < groups ? a.g_count[tid] : 0u;
-    const uint32_t bad = tid < groups ? a.g_bad[tid] : 0u;
+    uint32_t best = load_or_zero(a.partial, tid, a.partials);
+    const uint32_t cnt = load_or_zero(a.g_count, tid, groups);
+    const uint32_t bad = load_or_zero(a.g_bad, tid, groups);
     constexpr uint32_t kBinLoads = (kHeadMaxN / kSlice) * 256 / kHThreads;  // 2
     uint32_t hv[kBinLoads];
 #pragma unroll
     for (uint32_t u = 0; u < kBinLoads; ++u) {
         const uint32_t i = tid + u * kHThreads;
-        hv[u] = i < S * 256 ? a.g_hi[static_cast<size_t>(h * S) * 256 + i] : 0u;
+        hv[u] = load_or_zero(a.g_hi + static_cast<size_t>(h * S) * 256, i, S * 256);
     }
+    // (key_stride: n rounded up to 8, so at least 8)
     uint32_t keys[kHRun / 2];
     const uint16_t* krow = a.g_key16 + static_cast<size_t>(h) * a.key_stride;
 #pragma unroll
     for (uint32_t v = 0; v < kHRun / 8; ++v) {
-        uint4 x = make_uint4(0u, 0u, 0u, 0u);
-        if (begin + 8 * v < a.key_stride) x = *reinterpret_cast<const uint4*>(krow + begin + 8 * v);
-        keys[4 * v] = x.x; keys[4 * v + 1] = x.y; keys[4 * v + 2] = x.z; keys[4 * v + 3] = x.w;
+        const uint32_t at = begin + 8 * v;
+        const bool in = at < a.key_stride;
+        const uint4 x = *reinterpret_cast<const uint4*>(krow + (in ? at : a.key_stride - 8));
+        keys[4 * v] = in ? x.x : 0u; keys[4 * v + 1] = in ? x.y : 0u;
+        keys[4 * v + 2] = in ? x.z : 0u; keys[4 * v + 3] = in ? x.w : 0u;
     }
 
     if (tid < 256) hist[0][tid] = hist[1][tid] = 0;
@@ -1089,20 +1046,30 @@ __global__ void __launch_bounds__(kHThreads) head_select_kernel(const SelectJobs
         return;
     }
 
-    // low byte of the k-th key
+    // K*'s low byte from a histogram of this head's keys counted from the
+    // bucket's base: in rank order kSortRange keys, whose counts the placement
+    // below reuses; in id order the bucket's 256.  A key past the rank-order
+    // table sends the placement to the radix sort.
     const uint32_t hi = sh[kBucket] & 255u, above_hi = sh[kAbove];
+    const uint32_t base = hi << 8;
+    constexpr uint32_t kSpan = kRankOrder ? kSortRange : 256u;
+    uint32_t* table = kRankOrder ? tables : hist[1];
+    bool wide = false;
 #pragma unroll
     for (uint32_t j = 0; j < kHRun; ++j) {
-        const uint32_t key = half_at(keys, j);
-        if (begin + j < n && (key >> 8) == hi) atomicAdd(&hist[1][key & 255u], 1u);
+        const uint32_t d = half_at(keys, j) - base;  // wraps below the bucket
+        const bool in = begin + j < n;
+        if (in && d < kSpan) atomicAdd(&table[d], 1u);
+        if (kRankOrder) wide |= in && d >= kSpan && d < 0x10000u;
     }
+    if (kRankOrder && wide) sh[kFlag] = 1u;
     __syncthreads();
-    find_bucket(hist[1], k - above_hi, &sh[kBucket2], &sh[kAbove2]);
+    find_bucket(table, k - above_hi, &sh[kBucket2], &sh[kAbove2]);
     __syncthreads();
     const uint32_t lo = sh[kBucket2] & 255u;
-    const uint32_t kstar = (hi << 8) | lo;
+    const uint32_t kstar = base | lo;
     const uint32_t c_above = above_hi + sh[kAbove2];
-    const uint32_t c_equal = hist[1][lo];
+    const uint32_t c_equal = table[lo];
     const uint32_t t_need = k - c_above;  // ties taken, lowest ids first (>= 1)
     // boundary tie (gqa_policy.cpp:65): the (k+1)-th element exists with
     // equal bits; equal keys mean equal bits except -0 / +0 (key 0x8000).
@@ -1111,14 +1078,18 @@ __global__ void __launch_bounds__(kHThreads) head_select_kernel(const SelectJobs
     const bool zero_cut = cut_tie && kstar == 0x8000u;
 
     // this thread's keys above K* and ties, as bit masks over its 32 ids
+    // (bit j = id begin + j, shifted in from the top id down)
+    const uint32_t valid = begin + kHRun <= n ? 0xffffffffu
+                                               : (begin < n ? (1u << (n - begin)) - 1u : 0u);
     uint32_t above_mask = 0, tie_mask = 0;
 #pragma unroll
-    for (uint32_t j = 0; j < kHRun; ++j) {
-        const uint32_t key = half_at(keys, j);
-        const bool in = begin + j < n;
-        above_mask |= (in && key > kstar ? 1u : 0u) << j;
-        tie_mask |= (in && key == kstar ? 1u : 0u) << j;
+    for (int j = kHRun - 1; j >= 0; --j) {
+        const uint32_t key = half_at(keys, static_cast<uint32_t>(j));
+        above_mask = (above_mask << 1) + (key > kstar ? 1u : 0u);
+        tie_mask = (tie_mask << 1) + (key == kstar ? 1u : 0u);
     }
+    above_mask &= valid;
+    tie_mask &= valid;
     // one scan of both counts (each total <= 32768 fits its 16 bits): the ties
     // taken before this thread are min(ties before it, t_need)
     const uint32_t my_ties = static_cast<uint32_t>(__popc(tie_mask));
@@ -1147,30 +1118,88 @@ __global__ void __launch_bounds__(kHThreads) head_select_kernel(const SelectJobs
             }
         }
     }
-    uint32_t* out = a.ids + static_cast<size_t>(h) * a.ids_stride;
-    bool wide = false;  // a selected key beyond the counting table
-#pragma unroll
-    for (uint32_t j = 0; j < kHRun; ++j) {
-        if ((bits32 >> j) & 1u) {
-            if (!kRankOrder) {
-                out[pos] = begin + j;
-            } else {
-                const uint32_t key = half_at(keys, j);
-                sort_lds[pos] = ((0xffffu - key) << 16) | (begin + j);
-                if (key - kstar < kSortRange) atomicAdd(&tables[key - kstar], 1u);
-                else wide = true;
-            }
-            ++pos;
-        }
-    }
     if (a.member && tid < words) a.member[static_cast<size_t>(h) * words + tid] = bits32;
-    if constexpr (kRankOrder) {
-        const uint32_t m = std::min(k, kHeadMaxK);
-        if (__syncthreads_or(wide) ||
-            !place_by_histogram(sort_lds, sort_lds + kHeadMaxK, m, kstar, tables,
-                                tables + kSortRange, tmp, &sh[kFlag]))
-            sort_composites<kHThreads>(sort_lds, sort_lds + kHeadMaxK, m, whist, tmp);
-        for (uint32_t r = tid; r < m; r += kHThreads) out[r] = sort_lds[r] & 0xffffu;
+    uint32_t* out = a.ids + static_cast<size_t>(h) * a.ids_stride;
+    if constexpr (!kRankOrder) {
+        for (uint32_t sel = bits32; sel != 0; sel &= sel - 1)
+            out[pos++] = begin + static_cast<uint32_t>(__ffs(sel)) - 1;
+    } else {
+        // Rank order (k <= kHeadMaxK here): a counting sort by key over the
+        // table's bins, larger keys first.  Bins above K*'s hold every key,
+        // K*'s bin the t_need ties taken, lower bins nothing.  Thread t owns
+        // kPer consecutive bins, thread 0 the top ones.
+        const uint32_t m = k;
+        const uint32_t tie_bin = kstar - base;
+        uint32_t* cursor = tables + kSortRange;
+        constexpr uint32_t kPer = kSortRange / kHThreads;
+        const uint32_t first = (kHThreads - 1 - tid) * kPer;
+        uint32_t c[kPer], sum = 0, big = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < kPer; ++i) {
+            const uint32_t bin = first + i;
+            c[i] = bin > tie_bin ? table[bin] : (bin == tie_bin ? t_need : 0u);
+            sum += c[i];
+            big = max(big, c[i]);
+        }
+        if (big > kGroupCap) sh[kFlag] = 1u;  // read after the scan's barriers
+        const uint32_t higher = block_exclusive_scan<kHThreads>(sum, tmp);
+        uint32_t* B = sort_lds;
+        if (sh[kFlag] == 0) {
+            uint32_t run = higher + sum;
+#pragma unroll
+            for (uint32_t i = 0; i < kPer; ++i) {
+                run -= c[i];
+                table[first + i] = run;  // the bin's first position
+                cursor[first + i] = run;
+            }
+            if (tid < 8) B[m + tid] = 0xffffffffu;  // past every composite
+            __syncthreads();
+            // each selected composite ((0xffff - key) << 16 | id) into its key's group
+#pragma unroll
+            for (uint32_t j = 0; j < kHRun; ++j) {
+                if ((bits32 >> j) & 1u) {
+                    const uint32_t key = half_at(keys, j);
+                    B[atomicAdd(&cursor[key - base], 1u)] = ((0xffffu - key) << 16) | (begin + j);
+                }
+            }
+            __syncthreads();
+            // a composite's place in its group is the number of its group's
+            // composites below it; the reads run on past the group, where
+            // every composite (later groups: smaller keys; the padding) is larger
+            constexpr uint32_t kPerThread = kHeadMaxK / kHThreads;
+#pragma unroll
+            for (uint32_t u = 0; u < kPerThread; ++u) {
+                const uint32_t q = tid + u * kHThreads;
+                if (q < m) {
+                    const uint32_t e = B[q];
+                    const uint32_t bin = 0xffffu - (e >> 16) - base;
+                    const uint32_t gs = table[bin], gc = cursor[bin] - gs;
+                    uint32_t r = 0;
+                    for (uint32_t i = 0; i < gc; i += 8) {
+                        uint32_t v[8];
+#pragma unroll
+                        for (uint32_t t = 0; t < 8; ++t) v[t] = B[gs + i + t];
+#pragma unroll
+                        for (uint32_t t = 0; t < 8; ++t) r += v[t] < e ? 1u : 0u;
+                    }
+                    out[gs + r] = e & 0xffffu;
+                }
+            }
+        } else {
+            // a long run of equal keys or a key range past the table: stable
+            // radix sort of the composites written in id order
+            uint32_t* A = sort_lds;
+#pragma unroll
+            for (uint32_t j = 0; j < kHRun; ++j) {
+                if ((bits32 >> j) & 1u) {
+                    const uint32_t key = half_at(keys, j);
+                    A[pos++] = ((0xffffu - key) << 16) | (begin + j);
+                }
+            }
+            __syncthreads();
+            sort_composites<kHThreads>(A, A + kHeadMaxK, m, whist, tmp);
+            for (uint32_t r = tid; r < m; r += kHThreads) out[r] = A[r] & 0xffffu;
+        }
     }
 }
 

@@ -120,6 +120,47 @@ def test_zero_key_boundary_bits(hs, port):
         check_against_port(hs, port, s, 1, n, n, 10.0, ratio)
 
 
+def order_keys(bits):
+    b = np.asarray(bits, dtype=np.uint32)
+    return np.where(b & 0x8000, (~b) & 0xFFFF, b | 0x8000)
+
+
+@pytest.mark.parametrize("case", ["counting", "wide_range", "long_run"])
+def test_rank_order_placement_paths(hs, port, case):
+    # The per-head rank order places the selection by a counting sort over
+    # the 8192 keys from K*'s 256-key bucket upward, and falls back to a radix
+    # sort when a selected key lies past them or more than 64 selected keys
+    # are equal.  Each case is checked (on the oracle's selection) to take
+    # the path it names.
+    g = rng({"counting": 21, "wide_range": 22, "long_run": 23}[case])
+    heads, n = 4, 32768
+    if case == "wide_range":
+        # 30 % of the tokens spread over every positive normal key, the rest
+        # -1: the selected quarter spans about 25000 keys
+        s = np.full((heads, n), hb(-1.0), dtype=np.uint16)
+        spread = g.random((heads, n)) < 0.3
+        s[spread] = g.integers(0x0400, 0x7BFF, size=int(spread.sum())).astype(np.uint16)
+        alpha, ratio = 70000.0, 0.25
+    else:
+        s = f16_bits(g.standard_normal((heads, n)) * 2.0)
+        if case == "long_run":
+            s[:, 1000:1100] = hb(9.5)  # 100 equal keys at the top of every head
+        alpha, ratio = 5.0, 0.2
+    rc, k, ids, _, _ = port.select(s, heads, n, n, alpha, ratio)
+    assert rc == 0 and k <= 8192
+    keys = order_keys(s[np.arange(heads)[:, None], ids])
+    kstar = keys.min(axis=1)
+    span = keys.max(axis=1) - (kstar & 0xFF00)
+    run = max(np.unique(row, return_counts=True)[1].max() for row in keys)
+    if case == "counting":
+        assert (span < 8192).all() and run <= 64
+    elif case == "wide_range":
+        assert (span >= 8192).any()
+    else:
+        assert (span < 8192).all() and run > 64
+    check_against_port(hs, port, s, heads, n, n, alpha, ratio)
+
+
 def test_large_k_global_sort(hs, port):
     n = 40000
     g = rng(9)
