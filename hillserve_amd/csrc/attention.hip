@@ -243,23 +243,35 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
 }
 
 // Merge the per-chunk (m, l, o) records of each query head.  Grid (32 query
-// heads, 4 groups of 32 channels): a workgroup computes the chunk weights
-// exp(m_i - max m) and their l sum, then 16 rows of 32 threads each sum the
-// weighted o of every 16th chunk (8 records requested together per thread)
-// and the 16 partial sums are added in LDS.
+// heads, 4 groups of 32 channels).  Every record value a workgroup needs is
+// requested up front, since none depends on another: the o values of this
+// thread's channel over every 16th chunk, and one chunk's (m, l) per thread.
+// Then the chunk weights exp(m_i - max m) and their l sum, 16 rows of 32
+// threads each summing the weighted o of their chunks, and the 16 partial
+// sums added in LDS.
 constexpr uint32_t kMaxChunks = 65536 / kChunk;
 constexpr uint32_t kCombineThreads = 512;
+constexpr uint32_t kCombineRows = 16;  // chunks r, r + 16, ... per row of 32 threads
 static_assert(kMaxChunks <= kCombineThreads, "one chunk weight per thread");
 __global__ void __launch_bounds__(kCombineThreads)
 attn_combine_kernel(const float* __restrict__ part, uint32_t chunks, float* __restrict__ out) {
     __shared__ float weight[kMaxChunks];
     __shared__ float red[8];
-    __shared__ float acc16[16][33];
+    __shared__ float acc16[kCombineRows][33];
     const uint32_t h = blockIdx.x, g = h >> 2, j = h & 3u, tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = tid >> 6;
     const float* recs = part + static_cast<size_t>(g) * chunks * 4 * kRecord + j * kRecord;
-    const float m = tid < chunks ? recs[tid * 4 * kRecord] : -INFINITY;
-    const float l = tid < chunks ? recs[tid * 4 * kRecord + 1] : 0.0f;
+    const uint32_t c = tid & 31u, r = tid >> 5, ch = blockIdx.y * 32 + c;
+    const uint32_t last = chunks - 1;  // reads past the last chunk are clamped to it
+    constexpr uint32_t kFirst = 16;    // o values per thread in the first batch
+    float v[kFirst];
+#pragma unroll
+    for (uint32_t u = 0; u < kFirst; ++u)
+        v[u] = recs[min(r + kCombineRows * u, last) * 4 * kRecord + 2 + ch];
+    const float* mine = recs + min(tid, last) * 4 * kRecord;
+    const float m_rec = mine[0], l_rec = mine[1];
+    const float m = tid < chunks ? m_rec : -INFINITY;
+    const float l = tid < chunks ? l_rec : 0.0f;
     float top = wave_max_f32(m);
     if (lane == 0) red[wave] = top;
     __syncthreads();
@@ -267,7 +279,7 @@ attn_combine_kernel(const float* __restrict__ part, uint32_t chunks, float* __re
 #pragma unroll
     for (uint32_t w = 1; w < 8; ++w) top = fmaxf(top, red[w]);
     const float w_self = (m == -INFINITY || top == -INFINITY) ? 0.0f : __expf(m - top);
-    if (tid < chunks) weight[tid] = w_self;
+    weight[tid] = w_self;
     __syncthreads();
     const float lsum = wave_sum_f32(l * w_self);
     __syncthreads();  // every wave has read red[] before it is reused
@@ -276,28 +288,22 @@ attn_combine_kernel(const float* __restrict__ part, uint32_t chunks, float* __re
     float L = 0.0f;
 #pragma unroll
     for (uint32_t w = 0; w < 8; ++w) L += red[w];
-    const uint32_t c = tid & 31u, r = tid >> 5, ch = blockIdx.y * 32 + c;
     float a = 0.0f;
-    constexpr uint32_t kLoads = 8;
-    for (uint32_t i0 = r; i0 < chunks; i0 += 16 * kLoads) {
-        float v[kLoads];
 #pragma unroll
-        for (uint32_t u = 0; u < kLoads; ++u) {
-            const uint32_t i = i0 + 16 * u;
-            v[u] = i < chunks ? recs[i * 4 * kRecord + 2 + ch] : 0.0f;
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < kLoads; ++u) {
-            const uint32_t i = i0 + 16 * u;
-            if (i < chunks && weight[i] != 0.0f) a = __builtin_fmaf(v[u], weight[i], a);
-        }
+    for (uint32_t u = 0; u < kFirst; ++u) {
+        const uint32_t i = r + kCombineRows * u;
+        if (i < chunks && weight[i] != 0.0f) a = __builtin_fmaf(v[u], weight[i], a);
+    }
+    for (uint32_t i = r + kCombineRows * kFirst; i < chunks; i += kCombineRows) {  // n > 32768
+        const float x = recs[i * 4 * kRecord + 2 + ch];
+        if (weight[i] != 0.0f) a = __builtin_fmaf(x, weight[i], a);
     }
     acc16[r][c] = a;
     __syncthreads();
     if (tid < 32) {
         float sum = 0.0f;
 #pragma unroll
-        for (uint32_t k = 0; k < 16; ++k) sum += acc16[k][tid];
+        for (uint32_t k = 0; k < kCombineRows; ++k) sum += acc16[k][tid];
         out[h * 128 + ch] = L > 0.0f ? sum / L : 0.0f;
     }
 }

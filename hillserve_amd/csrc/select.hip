@@ -448,12 +448,14 @@ __global__ void __launch_bounds__(kThreads) count_kernel(const SelectJobs js) {
     if (a.g_key16 && begin < a.key_stride)
         *reinterpret_cast<uint4*>(a.g_key16 + static_cast<size_t>(h) * a.key_stride + begin) =
             make_uint4(keyw[0], keyw[1], keyw[2], keyw[3]);
-    count = block_sum(count, tmp);
-    bad = block_max(bad, tmp);
+    // one reduction of both: the slice's count (<= kSlice) in the low 16
+    // bits, its threads' nonfinite flags summed above them
+    static_assert(kSlice < 65536 && kThreads < 65536, "count and flags share a word");
+    const uint32_t both = block_sum((bad << 16) | count, tmp);
     if (tid < 256) a.g_hi[static_cast<size_t>(g) * 256 + tid] = hist_total(whist, tid);
     if (tid == 0) {
-        a.g_count[g] = count;
-        a.g_bad[g] = bad;
+        a.g_count[g] = both & 0xffffu;
+        a.g_bad[g] = both >> 16 ? 1u : 0u;
     }
     // the tie records the next launch accumulates into start from zero here
     if (g == 0) {
@@ -1054,15 +1056,26 @@ __global__ void __launch_bounds__(kHThreads) head_select_kernel(const SelectJobs
     const uint32_t base = hi << 8;
     constexpr uint32_t kSpan = kRankOrder ? kSortRange : 256u;
     uint32_t* table = kRankOrder ? tables : hist[1];
-    bool wide = false;
+    uint32_t top = 0;  // the largest key counted from the base (rank order)
+    if (begin + kHRun <= n) {  // every thread but a row's last, partial one
 #pragma unroll
-    for (uint32_t j = 0; j < kHRun; ++j) {
-        const uint32_t d = half_at(keys, j) - base;  // wraps below the bucket
-        const bool in = begin + j < n;
-        if (in && d < kSpan) atomicAdd(&table[d], 1u);
-        if (kRankOrder) wide |= in && d >= kSpan && d < 0x10000u;
+        for (uint32_t j = 0; j < kHRun; ++j) {
+            const uint32_t key = half_at(keys, j);
+            const uint32_t d = key - base;  // wraps below the bucket
+            if (d < kSpan) atomicAdd(&table[d], 1u);
+            if (kRankOrder) top = max(top, key);
+        }
+    } else {
+#pragma unroll
+        for (uint32_t j = 0; j < kHRun; ++j) {
+            const uint32_t key = half_at(keys, j);
+            const uint32_t d = key - base;
+            const bool in = begin + j < n;
+            if (in && d < kSpan) atomicAdd(&table[d], 1u);
+            if (kRankOrder && in) top = max(top, key);
+        }
     }
-    if (kRankOrder && wide) sh[kFlag] = 1u;
+    if (kRankOrder && top >= base + kSpan) sh[kFlag] = 1u;
     __syncthreads();
     find_bucket(table, k - above_hi, &sh[kBucket2], &sh[kAbove2]);
     __syncthreads();
