@@ -14,7 +14,9 @@ Also reported on the same line:
                 buffer) right after the timed steps, on the same stream.
   layer_step    configs[2]: one full sparse layer (score over the hot pool ->
                 select at the cap -> sparse attention), microseconds per layer
-                over 30 distinct hot pools, and its algorithmic HBM rate.
+                over 30 distinct hot pools held as K and V arrays (and, for
+                comparison, as 4096 B KV records), and its algorithmic HBM
+                rate.
   cpu_baseline  the reference's own CPU path (FullGqaCpuScorer + scaling +
                 select_gqa_scores, compiled from the reference sources into
                 oracle/_ref) on a bounded sample, timed on this host.
@@ -334,17 +336,20 @@ def tier_leg(args, hs, ops, torch, stream, dev):
         p = l % TIER_PHYS
         for sq in seqs:
             d = sq["layers"][p]
-            staging = d["pool"][hot_rows:]
+            staging = d["pool"][hot_rows:]  # 4096 B records: V 2048 B after K
             hs.check(L.hs_kv_cold_fetch(vp(sq["image"]), p, vp(d["pos"]), cold_rows, vp(staging),
+                                        ctypes.c_void_p(staging.data_ptr() + 2048), 4096,
                                         vp(d["cstatus"]), vp(d["cws"]), strm))
 
     def attend(l):
         p = l % TIER_PHYS
         for sq in seqs:
             d = sq["layers"][p]
-            hs.check(L.hs_gqa_sparse_attention(vp(d["q32"]), vp(d["pool"]), 4096, vp(d["rowmap"]),
-                                               hot_rows + cold_rows, vp(d["member"]), TIER_N,
-                                               vp(d["out"]), vp(d["aws"]), sp))
+            hs.check(L.hs_gqa_sparse_attention(vp(d["q32"]), vp(d["pool"]),
+                                               ctypes.c_void_p(d["pool"].data_ptr() + 2048), 4096,
+                                               vp(d["rowmap"]), hot_rows + cold_rows,
+                                               vp(d["member"]), TIER_N, vp(d["out"]), vp(d["aws"]),
+                                               sp))
 
     def step(with_cold=True):
         pending = None
@@ -524,51 +529,72 @@ def main():
         f"score kernel {avg_score_us:.2f} us avg = {score_gbs:.0f} GB/s")
 
     # ---- full sparse layer over 30 hot pools ---------------------
-    log("allocating 30 hot pools of 32768 x 4096 B (3.8 GB)")
+    # The hot pool as a K array and a V array (2048 B rows each, the layout
+    # this framework keeps in HBM: the scorer streams K contiguously), and,
+    # for comparison, as the reference's 4096 B KV records.
     del keys
-    pools = [torch.empty(N * 2048, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
     q32s = [torch.empty((32, 128), dtype=torch.float32, device=dev) for _ in range(LAYERS)]
     for layer in range(LAYERS):
-        # K halves RoPE-structured, V halves Gaussian
-        ops.fill_rope_keys(pools[layer], N, 2048, 8, seed=2000 + layer, theta=500000.0)
-        v_view = pools[layer].view(N, 2048)[:, 1024:]
-        tmp = torch.empty((N, 1024), dtype=torch.float16, device=dev)
-        ops.fill_gaussian(tmp, seed=3000 + layer)
-        v_view.copy_(tmp)
         q32s[layer].normal_(generator=torch.Generator(device=dev).manual_seed(layer))
-    del tmp
     out = torch.empty((32, 128), dtype=torch.float32, device=dev)
     lws = ops.workspace(ops.decode_layer_workspace_bytes(N), dev)
-    torch.cuda.synchronize()
 
-    def layer_pass():
+    def layer_leg(split):
+        log(f"configs[2]: 30 hot pools of 32768 x 4096 B (3.8 GB) as "
+            f"{'K and V arrays' if split else '4096 B KV records'}")
+        k_pools, v_pools = [], []
         for layer in range(LAYERS):
-            ops.decode_layer(qs[layer], q32s[layer], pools[layer], N, ALPHA, RATIO, scores=raw,
-                             ids=ids, ids_stride=kmax, counts=counts, out=out, status=status,
-                             ws=lws)
+            # K RoPE-structured, V Gaussian
+            if split:
+                kp = torch.empty(N * 1024, dtype=torch.float16, device=dev)
+                vpool = torch.empty(N * 1024, dtype=torch.float16, device=dev)
+                ops.fill_rope_keys(kp, N, 1024, 8, seed=2000 + layer, theta=500000.0)
+                ops.fill_gaussian(vpool, seed=3000 + layer)
+            else:
+                kp = torch.empty(N * 2048, dtype=torch.float16, device=dev)
+                ops.fill_rope_keys(kp, N, 2048, 8, seed=2000 + layer, theta=500000.0)
+                tmp = torch.empty((N, 1024), dtype=torch.float16, device=dev)
+                ops.fill_gaussian(tmp, seed=3000 + layer)
+                kp.view(N, 2048)[:, 1024:].copy_(tmp)
+                vpool = None
+            k_pools.append(kp)
+            v_pools.append(vpool)
+        torch.cuda.synchronize()
+        row_bytes = 2048 if split else 4096
 
-    layer_pass()
-    st = ops.read_status(status)
-    assert st["code"] == 0 and st["k"] == kmax, st
-    # member bitmaps of the last layer sit at the workspace's member slice
-    member_off = ((N + 63) // 64 * 4 + 255) // 256 * 256
-    member = lws[member_off: member_off + 32 * ((N + 31) // 32) * 4].view(torch.int32)
-    ubytes, utokens = union_bytes(hs, member, N)
-    b3, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    b3.record(stream)
-    for _ in range(args.layer_steps):
+        def layer_pass():
+            for layer in range(LAYERS):
+                ops.decode_layer(qs[layer], q32s[layer], k_pools[layer], N, ALPHA, RATIO,
+                                 scores=raw, ids=ids, ids_stride=kmax, counts=counts, out=out,
+                                 status=status, ws=lws, v_pool=v_pools[layer], row_bytes=row_bytes)
+
         layer_pass()
-    e3.record(stream)
-    torch.cuda.synchronize()
-    layer_us = 1e3 * b3.elapsed_time(e3) / (args.layer_steps * LAYERS)
+        st = ops.read_status(status)
+        assert st["code"] == 0 and st["k"] == kmax, st
+        # member bitmaps of the last layer sit at the workspace's member slice
+        member_off = ((N + 63) // 64 * 4 + 255) // 256 * 256
+        member = lws[member_off: member_off + 32 * ((N + 31) // 32) * 4].view(torch.int32)
+        ubytes, utokens = union_bytes(hs, member, N)
+        b3, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        b3.record(stream)
+        for _ in range(args.layer_steps):
+            layer_pass()
+        e3.record(stream)
+        torch.cuda.synchronize()
+        us = 1e3 * b3.elapsed_time(e3) / (args.layer_steps * LAYERS)
+        del k_pools, v_pools
+        return us, ubytes, utokens
+
+    rec_us, _, _ = layer_leg(split=False)
+    layer_us, ubytes, utokens = layer_leg(split=True)
     layer_bytes = SCORE_BYTES + 2 * 32 * N * 2 + 4 * 32 * kmax + ubytes + 8192 + 16384
     layer_gbs = layer_bytes / (layer_us * 1e-6) / 1e9
-    log(f"configs[2]: {layer_us:.1f} us/layer, {layer_gbs:.0f} GB/s algorithmic "
-        f"(union {utokens} (id,KV-head) rows of the last layer)")
+    log(f"configs[2]: {layer_us:.1f} us/layer with K and V arrays ({rec_us:.1f} us with 4096 B "
+        f"KV records), {layer_gbs:.0f} GB/s algorithmic (union {utokens} (id,KV-head) rows of "
+        f"the last layer)")
 
     # ---- batched rehearsal + scoring + selection ----------------------
-    del pools
     batch = batch_leg(args, hs, ops, torch, stream, dev)
     tier = tier_leg(args, hs, ops, torch, stream, dev)
 
@@ -608,7 +634,9 @@ def main():
         },
         "layer_step": {
             "workload": "configs[2]: score over hot pool + select at cap + sparse attention",
-            "us_per_layer": layer_us, "algorithmic_bytes": layer_bytes,
+            "pool_layout": "K and V arrays, 2048 B rows each",
+            "us_per_layer": layer_us, "us_per_layer_kv_records": rec_us,
+            "algorithmic_bytes": layer_bytes,
             "achieved_gbps": layer_gbs, "frac_of_hbm_peak": layer_gbs / HBM_PEAK_GBS,
             "union_rows": utokens,
         },

@@ -125,16 +125,16 @@ SIGNATURES = {
     "hs_kv_store_init": (_I, [_P, _U64, _U32, _U32]),
     "hs_kv_store_append": (_I, [_P, _U32, _U32, _P, _U32]),
     "hs_kv_cold_fetch_workspace_bytes": (_SZ, [_U32]),
-    "hs_kv_cold_fetch": (_I, [_P, _U32, _P, _U32, _P, _P, _P, _P]),
+    "hs_kv_cold_fetch": (_I, [_P, _U32, _P, _U32, _P, _P, _SZ, _P, _P, _P]),
     "hs_gqa_cold_plan": (_I, [_P, _U32, _U32, _P, _U32, _U32, _P, _P, _P, _P]),
     "hs_gqa_union_workspace_bytes": (_SZ, [_U32]),
     "hs_gqa_physical_union": (_I, [_P, _P, _SZ, _U32, _P, _P, _P, _P, _P]),
-    "hs_gqa_pack": (_I, [_P, _U32, _P, _U32, _P, _P, _SZ, _P, _U32, _U32, _P, _P, _P, _P, _P]),
+    "hs_gqa_pack": (_I, [_P, _P, _SZ, _U32, _P, _U32, _P, _P, _SZ, _P, _U32, _U32, _P, _P, _P, _P, _P]),
     "hs_gqa_gather_rows": (_I, [_P, _U32, _P, _U32, _P, _U32, _P, _P, _P, _P]),
     "hs_gqa_attention_workspace_bytes": (_SZ, [_U32]),
-    "hs_gqa_sparse_attention": (_I, [_P, _P, _SZ, _P, _U32, _P, _U32, _P, _P, _P]),
+    "hs_gqa_sparse_attention": (_I, [_P, _P, _P, _SZ, _P, _U32, _P, _U32, _P, _P, _P]),
     "hs_decode_layer_workspace_bytes": (_SZ, [_U32]),
-    "hs_decode_layer": (_I, [_P, _P, _P, _P, _U32, _U32, _F, _F, _U32, _P, _P, _SZ, _P, _P, _P, _P, _P]),
+    "hs_decode_layer": (_I, [_P, _P, _P, _P, _SZ, _P, _U32, _U32, _F, _F, _U32, _P, _P, _SZ, _P, _P, _P, _P, _P]),
     "hs_selftest_f16_checksums": (_I, [_P, _P]),
     "hs_selftest_scale_table": (_I, [_P, _P]),
     "hs_fill_gaussian_f16": (_I, [_P, _SZ, _U64, _F, _P]),

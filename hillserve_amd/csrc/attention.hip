@@ -1,5 +1,10 @@
 // Kernel #4 — sparse decode attention over the selection, read straight from
-// the HBM hot pool (no packed K/V/mask materialisation).
+// the HBM hot pool (no packed K/V/mask materialisation).  The pool is a K
+// array and a V array with one row stride: row r's K (F16 [8][128], 2048 B)
+// at k_pool + r * row_bytes and its V at v_pool + r * row_bytes.  The
+// reference's 4096 B KV records are the interleaved case (pool, pool + 2048,
+// 4096); separate K and V arrays (2048 B rows) let the scorer stream K
+// contiguously.
 //
 // Semantics: the external-KV decode attention of
 // patches/llama-b6000-external-attention-device.patch:49-66 (kq = K.q,
@@ -13,11 +18,11 @@
 //    compacts the union in id order, and reads each selected (id, g) K row
 //    and V row exactly once for all of its query heads -> HBM bytes =
 //    sum_g |U_g|*512.  The 8 waves read the 8 heads' segments of the same
-//    4 KiB pool rows at about the same time.
+//    pool rows at about the same time.
 //  * one pass: 16 lanes per id, 16 B (8 channels) per lane, so every K and
-//    V access is a contiguous 256 B run; the K and V halves of a row (same
-//    4 KiB pool row) are requested together, which streams ~1.4x faster
-//    than a K pass followed by a V pass.  Scores are reduced over the 16
+//    V access is a contiguous 256 B run; a row's K and V segments are
+//    requested together, which streams ~1.4x faster than a K pass followed
+//    by a V pass.  Scores are reduced over the 16
 //    lanes with 4 DPP adds per head, softmax is online (rescaled once per
 //    batch of rows), and p*V accumulates in registers.  Loads run one batch
 //    ahead of their use.
@@ -72,7 +77,8 @@ __device__ __forceinline__ float row_sum16(float v) {
 template <bool kRows>
 __global__ void __launch_bounds__(kThreads)
 attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ pool,
-                    uint32_t row_bytes, const int32_t* __restrict__ rows, uint32_t pool_rows,
+                    uint32_t row_bytes, int64_t v_delta, const int32_t* __restrict__ rows,
+                    uint32_t pool_rows,
                     const uint32_t* __restrict__ member, uint32_t n, uint32_t chunks,
                     float* __restrict__ part) {
     constexpr uint32_t kBatch = 2;  // rows per batch of a 16-lane group (K + V); 2 batches in flight
@@ -119,7 +125,9 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
     for (uint32_t j = 0; j < 4; ++j)
 #pragma unroll
         for (uint32_t e = 0; e < 8; ++e) qr[j][e] = q[(4 * g + j) * 128 + part16 * 8 + e];
-    const uint32_t koff = g * 256 + part16 * 16, voff = 2048 + koff;
+    // a row's V segment sits v_delta bytes from its K segment
+    const uint32_t koff = g * 256 + part16 * 16;
+    const int64_t voff = v_delta + koff;
     float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float o[4][8];
@@ -315,24 +323,28 @@ size_t attention_workspace_bytes(uint32_t n) {
     return align256(sizeof(float) * 8 * chunks * 4 * kRecord);
 }
 
-int launch_attention(const float* q, const uint8_t* pool, size_t row_bytes, const int32_t* rows,
-                     uint32_t pool_rows, const uint32_t* member, uint32_t n, float* out,
-                     void* workspace, hipStream_t stream) {
-    if (!q || !pool || !member || !out || !workspace) return reject("attention: null pointer");
+int launch_attention(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
+                     size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
+                     const uint32_t* member, uint32_t n, float* out, void* workspace,
+                     hipStream_t stream) {
+    if (!q || !k_pool || !v_pool || !member || !out || !workspace)
+        return reject("attention: null pointer");
     if (n == 0 || n > 65536) return reject("attention: n must be 1..65536");
-    if (row_bytes < 4096 || row_bytes % 16 != 0 || row_bytes > (1u << 20))
-        return reject("attention: row_bytes must be >= 4096 and a multiple of 16");
-    if (reinterpret_cast<uintptr_t>(pool) & 15u) return reject("attention: pool not 16-byte aligned");
+    if (row_bytes < 2048 || row_bytes % 16 != 0 || row_bytes > (1u << 20))
+        return reject("attention: row_bytes must be 2048..1 MiB and a multiple of 16");
+    if ((reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool)) & 15u)
+        return reject("attention: K and V pools must be 16-byte aligned");
+    const int64_t v_delta = reinterpret_cast<intptr_t>(v_pool) - reinterpret_cast<intptr_t>(k_pool);
     const uint32_t chunks = (n + kChunk - 1) / kChunk;
     float* part = static_cast<float*>(workspace);
     if (rows)
         hipLaunchKernelGGL(attn_partial_kernel<true>, dim3(chunks), dim3(kThreads), 0, stream, q,
-                           pool, static_cast<uint32_t>(row_bytes), rows, pool_rows, member, n,
-                           chunks, part);
+                           k_pool, static_cast<uint32_t>(row_bytes), v_delta, rows, pool_rows,
+                           member, n, chunks, part);
     else
         hipLaunchKernelGGL(attn_partial_kernel<false>, dim3(chunks), dim3(kThreads), 0, stream,
-                           q, pool, static_cast<uint32_t>(row_bytes), rows, 0u, member, n,
-                           chunks, part);
+                           q, k_pool, static_cast<uint32_t>(row_bytes), v_delta, rows, 0u, member,
+                           n, chunks, part);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(32, 4), dim3(kCombineThreads), 0, stream, part, chunks,
                        out);
     const hipError_t st = hipGetLastError();
@@ -347,13 +359,15 @@ size_t hs_gqa_attention_workspace_bytes(uint32_t n) {
     return hs::attention_workspace_bytes(n ? n : 1);
 }
 
-int hs_gqa_sparse_attention(const float* q_dev, const uint8_t* pool_dev, size_t row_bytes,
+int hs_gqa_sparse_attention(const float* q_dev, const uint8_t* k_pool_dev,
+                            const uint8_t* v_pool_dev, size_t row_bytes,
                             const int32_t* row_of_id_dev, uint32_t pool_rows,
                             const uint32_t* member_dev, uint32_t n, float* out_dev,
                             void* workspace_dev, void* stream) {
     hs::clear_error();
-    return hs::launch_attention(q_dev, pool_dev, row_bytes, row_of_id_dev, pool_rows, member_dev,
-                                n, out_dev, workspace_dev, hs::as_stream(stream));
+    return hs::launch_attention(q_dev, k_pool_dev, v_pool_dev, row_bytes, row_of_id_dev,
+                                pool_rows, member_dev, n, out_dev, workspace_dev,
+                                hs::as_stream(stream));
 }
 
 }  // extern "C"

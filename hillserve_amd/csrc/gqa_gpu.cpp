@@ -390,7 +390,9 @@ void pack_gqa_workspace(const std::vector<std::vector<std::uint64_t>>& ids,
     upload(ids_dev, flat.data(), flat.size() * 4, stream);
     upload(lens_dev, lens.data(), 32 * 4, stream);
     upload(pos_dev, positions.data(), positions.size() * 8, stream);
-    api_check(hs_gqa_pack(pool_dev, static_cast<std::uint32_t>(physical.size()), map_dev,
+    // the payload holds the reference's 4096 B KV records: V 2048 B after K
+    api_check(hs_gqa_pack(pool_dev, pool_dev + 2048, 4096,
+                          static_cast<std::uint32_t>(physical.size()), map_dev,
                           static_cast<std::uint32_t>(max_id), ids_dev, lens_dev, width, pos_dev,
                           static_cast<std::uint32_t>(positions.size()),
                           static_cast<std::uint32_t>(count), k_dev, v_dev, mask_dev, status_dev,

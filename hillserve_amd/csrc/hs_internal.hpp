@@ -44,9 +44,9 @@ int launch_select_batched(const hs_select_job_t* jobs, uint32_t count, uint32_t 
                           float alpha, float ratio, uint32_t flags, hipStream_t stream);
 
 size_t attention_workspace_bytes(uint32_t n);
-int launch_attention(const float* q, const uint8_t* pool, size_t row_bytes,
-                     const int32_t* rows, uint32_t pool_rows, const uint32_t* member,
-                     uint32_t n, float* out,
-                     void* workspace, hipStream_t stream);
+int launch_attention(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
+                     size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
+                     const uint32_t* member, uint32_t n, float* out, void* workspace,
+                     hipStream_t stream);
 
 }  // namespace hs

@@ -15,11 +15,14 @@
 // of policy/full_gqa_runtime.cpp:398-409) refuses a record whose identity or
 // digest does not match.  hs_kv_cold_fetch does the same on the device:
 //   cold_copy_kernel:   one wave per record copies it from host memory with
-//                       coalesced 16 B reads into the device staging rows and
-//                       checks the header identity;
-//   cold_digest_kernel: one lane per record hashes its staged row in byte
-//                       order (FNV-1a is sequential within a record) and
-//                       compares the digest;
+//                       coalesced 16 B reads into the device staging rows
+//                       (its K half to k_out + i * row_bytes, its V half to
+//                       v_out + i * row_bytes; the record layout itself is
+//                       (out, out + 2048, 4096)) and checks the header
+//                       identity;
+//   cold_digest_kernel: one lane per record hashes its staged K then V half
+//                       in byte order (FNV-1a is sequential within a record)
+//                       and compares the digest;
 //   cold_status_kernel: folds the per-record flags into the status.
 #include <hip/hip_runtime.h>
 
@@ -60,8 +63,8 @@ static_assert(sizeof(RecordHeader) == kHeader, "32-byte record header");
 __global__ void __launch_bounds__(256)
 cold_copy_kernel(const uint8_t* __restrict__ image, uint32_t layer, uint32_t capacity,
                  uint64_t request, const uint32_t* __restrict__ positions, uint32_t count,
-                 uint8_t* __restrict__ out, uint64_t* __restrict__ digests,
-                 uint32_t* __restrict__ flags) {
+                 uint8_t* k_out, uint32_t row_bytes, int64_t v_delta,
+                 uint64_t* __restrict__ digests, uint32_t* __restrict__ flags) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t i = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (i >= count) return;
@@ -80,9 +83,10 @@ cold_copy_kernel(const uint8_t* __restrict__ image, uint32_t layer, uint32_t cap
         v[j] = *reinterpret_cast<const uint4*>(rec + kHeader + j * 1024 + lane * 16);
     uint4 hdr = make_uint4(0u, 0u, 0u, 0u);
     if (lane < 2) hdr = *reinterpret_cast<const uint4*>(rec + lane * 16);
-    uint8_t* dst = out + uint64_t(i) * kRow;
+    uint8_t* dst = k_out + uint64_t(i) * row_bytes;  // K half (bytes 0..2047 of the row)
 #pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(dst + j * 1024 + lane * 16) = v[j];
+    for (uint32_t j = 0; j < 4; ++j)
+        *reinterpret_cast<uint4*>(dst + (j < 2 ? 0 : v_delta - 2048) + j * 1024 + lane * 16) = v[j];
     // lane 0: digest, position; lane 1: request, layer | version << 32
     const uint64_t a = (uint64_t(hdr.y) << 32) | hdr.x, b = (uint64_t(hdr.w) << 32) | hdr.z;
     const uint64_t request_in = __shfl(a, 1, 64), ident = __shfl(b, 1, 64);
@@ -94,16 +98,18 @@ cold_copy_kernel(const uint8_t* __restrict__ image, uint32_t layer, uint32_t cap
     }
 }
 
-// One lane per record: FNV-1a 64 over the staged row, in byte order.
+// One lane per record: FNV-1a 64 over the staged row (K half, then V half),
+// in byte order.
 __global__ void __launch_bounds__(256)
-cold_digest_kernel(const uint8_t* __restrict__ rows, const uint64_t* __restrict__ digests,
-                   uint32_t count, uint32_t* __restrict__ flags) {
+cold_digest_kernel(const uint8_t* k_rows, uint32_t row_bytes, int64_t v_delta,
+                   const uint64_t* __restrict__ digests, uint32_t count,
+                   uint32_t* __restrict__ flags) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i >= count || (flags[i] & kPadFlag)) return;
-    const uint4* row = reinterpret_cast<const uint4*>(rows + uint64_t(i) * kRow);
+    const uint8_t* k = k_rows + uint64_t(i) * row_bytes;
     uint64_t h = kFnvSeed;
     for (uint32_t c = 0; c < kRow / 16; ++c) {
-        const uint4 w = row[c];
+        const uint4 w = *reinterpret_cast<const uint4*>(k + (c < 128 ? 0 : v_delta - 2048) + c * 16);
         const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (uint32_t k = 0; k < 4; ++k)
@@ -200,12 +206,17 @@ size_t cold_fetch_workspace_bytes(uint32_t count) {
 }
 
 int launch_cold_fetch(const void* image, uint32_t layer, const uint32_t* positions,
-                      uint32_t count, uint8_t* out, hs_status_t* status, void* workspace,
-                      hipStream_t stream) {
-    if (!image || !positions || !out || !status || !workspace) return reject("cold fetch: null pointer");
+                      uint32_t count, uint8_t* k_out, uint8_t* v_out, size_t row_bytes,
+                      hs_status_t* status, void* workspace, hipStream_t stream) {
+    if (!image || !positions || !k_out || !v_out || !status || !workspace)
+        return reject("cold fetch: null pointer");
     if (count == 0) return reject("cold fetch: count must be >= 1");
-    if ((reinterpret_cast<uintptr_t>(image) | reinterpret_cast<uintptr_t>(out)) & 15u)
-        return reject("cold fetch: image and out must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(image) | reinterpret_cast<uintptr_t>(k_out) |
+         reinterpret_cast<uintptr_t>(v_out)) & 15u)
+        return reject("cold fetch: image, K and V rows must be 16-byte aligned");
+    if (row_bytes < 2048 || row_bytes % 16 != 0 || row_bytes > (1u << 20))
+        return reject("cold fetch: row_bytes must be 2048..1 MiB and a multiple of 16");
+    const int64_t v_delta = reinterpret_cast<intptr_t>(v_out) - reinterpret_cast<intptr_t>(k_out);
     // the image header is host memory: geometry comes from it, as the
     // reference's reader takes it from the file's first page
     uint64_t h[8];
@@ -219,9 +230,10 @@ int launch_cold_fetch(const void* image, uint32_t layer, const uint32_t* positio
                                                   align256(sizeof(uint64_t) * count));
     hipLaunchKernelGGL(cold_copy_kernel, dim3((count + 3) / 4), dim3(256), 0, stream,
                        static_cast<const uint8_t*>(image), layer, static_cast<uint32_t>(h[4]),
-                       h[2], positions, count, out, digests, flags);
-    hipLaunchKernelGGL(cold_digest_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, out,
-                       digests, count, flags);
+                       h[2], positions, count, k_out, static_cast<uint32_t>(row_bytes), v_delta,
+                       digests, flags);
+    hipLaunchKernelGGL(cold_digest_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, k_out,
+                       static_cast<uint32_t>(row_bytes), v_delta, digests, count, flags);
     hipLaunchKernelGGL(cold_status_kernel, dim3(1), dim3(256), 0, stream, flags, count, status);
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "cold fetch launch");
@@ -295,11 +307,11 @@ size_t hs_kv_cold_fetch_workspace_bytes(uint32_t count) {
 }
 
 int hs_kv_cold_fetch(const void* image, uint32_t layer, const uint32_t* positions_dev,
-                     uint32_t count, uint8_t* out_dev, hs_status_t* status_dev,
-                     void* workspace_dev, void* stream) {
+                     uint32_t count, uint8_t* k_out_dev, uint8_t* v_out_dev, size_t row_bytes,
+                     hs_status_t* status_dev, void* workspace_dev, void* stream) {
     hs::clear_error();
-    return hs::launch_cold_fetch(image, layer, positions_dev, count, out_dev, status_dev,
-                                 workspace_dev, hs::as_stream(stream));
+    return hs::launch_cold_fetch(image, layer, positions_dev, count, k_out_dev, v_out_dev,
+                                 row_bytes, status_dev, workspace_dev, hs::as_stream(stream));
 }
 
 }  // extern "C"

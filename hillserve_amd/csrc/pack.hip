@@ -7,8 +7,10 @@
 //  * hs_gqa_pack: runtime/gqa_pack.hpp:26-58, byte for byte: K
 //    [slot][Qhead][128], V transposed [Qhead][128][slot], mask
 //    [Qhead][qpad][slot] = 0 where id <= position[q], -inf elsewhere, zero
-//    K/V padding.  Rows come from the device hot pool (4096 B: K[8][128] then
-//    V[8][128]) through an optional id -> row map.
+//    K/V padding.  Rows come from the device hot pool (row r's K[8][128] at
+//    k_pool + r * row_bytes, its V[8][128] at v_pool + r * row_bytes; the
+//    reference's 4096 B records are k_pool = pool, v_pool = pool + 2048)
+//    through an optional id -> row map.
 //  * hs_gqa_gather_rows: runtime/gqa_prefetch_cuda.cu:12-22 (row map
 //    >=0 prefetched, <=-2 miss row, -1 zero).
 // K and V for a (head, 64-slot) block are staged in LDS so both the K rows
@@ -95,8 +97,10 @@ union_write_kernel(const uint32_t* __restrict__ seen, uint32_t visible,
 
 // Source of one (slot, head) pair of the packed layout.
 struct PoolSource {
-    const uint8_t* pool;
+    const uint8_t* pool;   // K rows
     uint32_t pool_rows;
+    uint32_t row_bytes;
+    int64_t v_delta;       // a row's V segment sits v_delta bytes from its K segment
     const int32_t* row_of_id;
     uint32_t max_id;
     const uint32_t* ids;
@@ -147,7 +151,7 @@ pack_kernel(PoolSource ps, MapSource ms, const uint64_t* __restrict__ positions,
                         raise(status, HS_ERR_MISSING);
                         id = 0xffffffffu;
                     } else {
-                        src = ps.pool + static_cast<size_t>(row) * 4096;
+                        src = ps.pool + static_cast<size_t>(row) * ps.row_bytes;
                     }
                 }
             } else {
@@ -168,13 +172,15 @@ pack_kernel(PoolSource ps, MapSource ms, const uint64_t* __restrict__ positions,
     }
     __syncthreads();
     // K rows: 64 slots x 16 x 16 B; V half rows staged for the transpose.
+    // (prefetched and miss rows are 4096 B records: V 2048 B after K)
+    const int64_t v_delta = kPack ? ps.v_delta : 2048;
     for (uint32_t i = tid; i < 64 * 16; i += 256) {
         const uint32_t s = i >> 4, c = i & 15u;
         const uint8_t* src = src_row[s];
         uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
         if (src) {
             kw = reinterpret_cast<const uint4*>(src + kv * 256)[c];
-            vw = reinterpret_cast<const uint4*>(src + 2048 + kv * 256)[c];
+            vw = reinterpret_cast<const uint4*>(src + v_delta + kv * 256)[c];
         }
         vtile[s][c] = vw;
         if (s0 + s < count)
@@ -237,23 +243,28 @@ int hs_gqa_physical_union(const uint32_t* ids_dev, const uint32_t* lens_dev, siz
     return st == hipSuccess ? HS_OK : hs::hip_fail(st, "union launch");
 }
 
-int hs_gqa_pack(const uint8_t* pool_dev, uint32_t pool_rows, const int32_t* row_of_id_dev,
-                uint32_t max_id,
+int hs_gqa_pack(const uint8_t* k_pool_dev, const uint8_t* v_pool_dev, size_t row_bytes,
+                uint32_t pool_rows, const int32_t* row_of_id_dev, uint32_t max_id,
                 const uint32_t* ids_dev, const uint32_t* lens_dev, size_t ids_stride,
                 const uint64_t* positions_dev, uint32_t nq, uint32_t count, uint16_t* k_dev,
                 uint16_t* v_dev, float* mask_dev, hs_status_t* status_dev, void* stream) {
     hs::clear_error();
-    if (!pool_dev || !ids_dev || !lens_dev || !positions_dev || !k_dev || !v_dev || !mask_dev ||
-        !status_dev)
+    if (!k_pool_dev || !v_pool_dev || !ids_dev || !lens_dev || !positions_dev || !k_dev ||
+        !v_dev || !mask_dev || !status_dev)
         return hs::reject("GQA packing: null pointer");
     if (nq == 0 || nq > 256 || count == 0 || count > hs::kMaxVisible)
         return hs::reject("GQA packing shape");
     if (ids_stride > 0xffffffffu) return hs::reject("GQA packing: ids_stride too large");
-    if (reinterpret_cast<uintptr_t>(pool_dev) & 15u) return hs::reject("GQA packing: pool alignment");
+    if ((reinterpret_cast<uintptr_t>(k_pool_dev) | reinterpret_cast<uintptr_t>(v_pool_dev)) & 15u)
+        return hs::reject("GQA packing: pool alignment");
+    if (row_bytes < 2048 || row_bytes % 16 != 0 || row_bytes > (1u << 20))
+        return hs::reject("GQA packing: row_bytes must be 2048..1 MiB and a multiple of 16");
     hipStream_t s = hs::as_stream(stream);
     // extent = positions[nq-1] + 1 is read on the device; bound it by max_id.
-    hs::PoolSource ps{pool_dev, pool_rows, row_of_id_dev, max_id, ids_dev, lens_dev,
-                      static_cast<uint32_t>(ids_stride)};
+    const int64_t v_delta =
+        reinterpret_cast<intptr_t>(v_pool_dev) - reinterpret_cast<intptr_t>(k_pool_dev);
+    hs::PoolSource ps{k_pool_dev, pool_rows, static_cast<uint32_t>(row_bytes), v_delta,
+                      row_of_id_dev, max_id, ids_dev, lens_dev, static_cast<uint32_t>(ids_stride)};
     hipLaunchKernelGGL(hs::fill_u32_kernel, dim3(1), dim3(256), 0, s,
                        reinterpret_cast<uint32_t*>(status_dev), 4u, 0u);
     hs::MapSource ms{nullptr, nullptr, nullptr};

@@ -151,33 +151,36 @@ const char* hs_last_error(void) { return hs::g_last_error.c_str(); }
 
 size_t hs_decode_layer_workspace_bytes(uint32_t n) { return hs::plan_layer(n ? n : 1).total; }
 
-int hs_decode_layer(const uint16_t* q16_dev, const float* q32_dev, const uint8_t* pool_dev,
-                    const int32_t* row_of_id_dev, uint32_t pool_rows, uint32_t n, float alpha,
-                    float ratio,
-                    uint32_t flags, uint16_t* scores_dev, uint32_t* ids_dev, size_t ids_stride,
+int hs_decode_layer(const uint16_t* q16_dev, const float* q32_dev, const uint8_t* k_pool_dev,
+                    const uint8_t* v_pool_dev, size_t row_bytes, const int32_t* row_of_id_dev,
+                    uint32_t pool_rows, uint32_t n, float alpha, float ratio, uint32_t flags,
+                    uint16_t* scores_dev, uint32_t* ids_dev, size_t ids_stride,
                     uint32_t* counts_dev, float* out_dev, hs_status_t* status_dev,
                     void* workspace_dev, void* stream) {
     hs::clear_error();
-    if (!q16_dev || !q32_dev || !pool_dev || !scores_dev || !ids_dev || !out_dev || !status_dev ||
-        !workspace_dev)
+    if (!q16_dev || !q32_dev || !k_pool_dev || !v_pool_dev || !scores_dev || !ids_dev ||
+        !out_dev || !status_dev || !workspace_dev)
         return hs::reject("decode layer: null pointer");
     if (n == 0 || n > 65536) return hs::reject("decode layer: n must be 1..65536");
     if (flags & ~uint32_t(HS_SELECT_FP32_COUNTS)) return hs::reject("decode layer: unknown flags");
+    // the scorer streams K rows of 1024 or 2048 words
+    if (row_bytes != 2048 && row_bytes != 4096)
+        return hs::reject("decode layer: row_bytes must be 2048 (K and V arrays) or 4096 (KV records)");
     hipStream_t s = hs::as_stream(stream);
     const hs::LayerPlan p = hs::plan_layer(n);
     char* ws = static_cast<char*>(workspace_dev);
     uint32_t* partial = reinterpret_cast<uint32_t*>(ws + p.off_partial);
     uint32_t* member = reinterpret_cast<uint32_t*>(ws + p.off_member);
-    int rc = hs::launch_score(q16_dev, reinterpret_cast<const uint16_t*>(pool_dev), 2048,
-                              row_of_id_dev, pool_rows, n, scores_dev, n, partial, s);
+    int rc = hs::launch_score(q16_dev, reinterpret_cast<const uint16_t*>(k_pool_dev),
+                              row_bytes / 2, row_of_id_dev, pool_rows, n, scores_dev, n, partial, s);
     if (rc != HS_OK) return rc;
     rc = hs::launch_select(scores_dev, 32, n, n, alpha, ratio,
                            flags | HS_SELECT_SCALE_RAW | HS_SELECT_REQUIRE_K | HS_SELECT_ID_ORDER,
                            partial, ids_dev,
                            ids_stride, counts_dev, member, status_dev, ws + p.off_select, s);
     if (rc != HS_OK) return rc;
-    return hs::launch_attention(q32_dev, pool_dev, 4096, row_of_id_dev, pool_rows, member, n,
-                                out_dev, ws + p.off_attn, s);
+    return hs::launch_attention(q32_dev, k_pool_dev, v_pool_dev, row_bytes, row_of_id_dev,
+                                pool_rows, member, n, out_dev, ws + p.off_attn, s);
 }
 
 int hs_selftest_f16_checksums(uint64_t* checksums_dev, void* stream) {

@@ -204,9 +204,22 @@ def physical_union(ids, lens, ids_stride, visible, stream=None):
     return out, out_n, status
 
 
+def _kv_pool(pool, v_pool, row_bytes):
+    """(K base, V base, row bytes, rows) of a hot pool: one tensor of the
+    reference's 4096 B KV records (v_pool None), or K and V row arrays."""
+    if v_pool is None:
+        if row_bytes != 4096:
+            raise ValueError("a single pool tensor holds 4096 B KV records")
+        return (_p(pool), ctypes.c_void_p(pool.data_ptr() + 2048), 4096,
+                pool.numel() * pool.element_size() // 4096)
+    rows = min(pool.numel() * pool.element_size(), v_pool.numel() * v_pool.element_size())
+    return _p(pool), _p(v_pool), row_bytes, rows // row_bytes
+
+
 def pack(pool, ids, lens, ids_stride, positions, count, row_of_id=None, max_id=None,
-         stream=None):
-    """pack_gqa_workspace from the device hot pool -> (K, V, mask, status)."""
+         v_pool=None, row_bytes=4096, stream=None):
+    """pack_gqa_workspace from the device hot pool -> (K, V, mask, status).
+    pool: 4096 B KV records, or with v_pool the K and V row arrays."""
     dev = pool.device
     nq = positions.numel()
     qpad = (nq + 63) // 64 * 64
@@ -214,10 +227,10 @@ def pack(pool, ids, lens, ids_stride, positions, count, row_of_id=None, max_id=N
     v = torch.empty(count * H * D, dtype=torch.float16, device=dev)
     mask = torch.empty(H * qpad * count, dtype=torch.float32, device=dev)
     status = new_status(dev)
-    pool_rows = pool.numel() * pool.element_size() // 4096
+    kp, vp, row_bytes, pool_rows = _kv_pool(pool, v_pool, row_bytes)
     if max_id is None:
         max_id = row_of_id.numel() if row_of_id is not None else pool_rows
-    check(lib().hs_gqa_pack(_p(pool), pool_rows, _p(row_of_id), max_id, _p(ids), _p(lens),
+    check(lib().hs_gqa_pack(kp, vp, row_bytes, pool_rows, _p(row_of_id), max_id, _p(ids), _p(lens),
                             ids_stride,
                             _p(positions), nq, count, _p(k), _p(v), _p(mask), _p(status),
                             _s(stream)))
@@ -241,17 +254,19 @@ def attention_workspace_bytes(n):
     return lib().hs_gqa_attention_workspace_bytes(n)
 
 
-def sparse_attention(q32, pool, n, member, rows=None, row_bytes=4096, out=None, ws=None,
-                     pool_rows=None, stream=None):
-    _need_cuda(q32, pool, member)
+def sparse_attention(q32, pool, n, member, rows=None, out=None, ws=None, pool_rows=None,
+                     v_pool=None, row_bytes=4096, stream=None):
+    """pool: 4096 B KV records, or with v_pool the K and V row arrays."""
+    _need_cuda(q32, pool, member, v_pool)
     dev = pool.device
     if out is None:
         out = torch.empty((H, D), dtype=torch.float32, device=dev)
     if ws is None:
         ws = workspace(attention_workspace_bytes(n), dev)
+    kp, vp, row_bytes, rows_in_pool = _kv_pool(pool, v_pool, row_bytes)
     if pool_rows is None:
-        pool_rows = pool.numel() * pool.element_size() // row_bytes
-    check(lib().hs_gqa_sparse_attention(_p(q32), _p(pool), row_bytes, _p(rows), pool_rows,
+        pool_rows = rows_in_pool
+    check(lib().hs_gqa_sparse_attention(_p(q32), kp, vp, row_bytes, _p(rows), pool_rows,
                                         _p(member), n, _p(out), _p(ws), _s(stream)))
     return out
 
@@ -262,8 +277,10 @@ def decode_layer_workspace_bytes(n):
 
 def decode_layer(q16, q32, pool, n, alpha, ratio, *, rows=None, fp32_counts=False, scores=None,
                  ids=None, ids_stride=None, counts=None, out=None, status=None, ws=None,
-                 pool_rows=None, stream=None):
-    """score -> select -> sparse attention for one layer (all on device)."""
+                 pool_rows=None, v_pool=None, row_bytes=4096, stream=None):
+    """score -> select -> sparse attention for one layer (all on device).
+    pool: 4096 B KV records, or with v_pool the K and V arrays (row_bytes
+    2048: the scorer streams K contiguously)."""
     dev = pool.device
     kmax = min(n, math.floor(float(n) * float(ctypes.c_float(ratio).value)))
     if ids_stride is None:
@@ -280,12 +297,38 @@ def decode_layer(q16, q32, pool, n, alpha, ratio, *, rows=None, fp32_counts=Fals
         status = new_status(dev)
     if ws is None:
         ws = workspace(decode_layer_workspace_bytes(n), dev)
+    kp, vp, row_bytes, rows_in_pool = _kv_pool(pool, v_pool, row_bytes)
     if pool_rows is None:
-        pool_rows = pool.numel() * pool.element_size() // 4096
-    check(lib().hs_decode_layer(_p(q16), _p(q32), _p(pool), _p(rows), pool_rows, n, alpha, ratio,
+        pool_rows = rows_in_pool
+    check(lib().hs_decode_layer(_p(q16), _p(q32), kp, vp, row_bytes, _p(rows), pool_rows, n,
+                                alpha, ratio,
                                 HS_SELECT_FP32_COUNTS if fp32_counts else 0, _p(scores), _p(ids),
                                 ids_stride, _p(counts), _p(out), _p(status), _p(ws), _s(stream)))
     return scores, ids, counts, out, status
+
+
+def kv_cold_fetch(image, layer, positions, k_out, *, v_out=None, row_bytes=4096, status=None,
+                  ws=None, stream=None):
+    """Device read of cold records (hs_kv_cold_fetch) from a pinned
+    SegmentedKVStore image: record i's K half to row i of k_out and its V
+    half to row i of v_out (v_out None: k_out holds 4096 B records)."""
+    _need_cuda(positions, k_out, v_out)
+    if image.is_cuda or not image.is_pinned():
+        raise ValueError("the store image must be pinned host memory")
+    count = positions.numel()
+    if v_out is None:
+        if row_bytes != 4096:
+            raise ValueError("a single output tensor holds 4096 B KV records")
+        kp, vp = _p(k_out), ctypes.c_void_p(k_out.data_ptr() + 2048)
+    else:
+        kp, vp = _p(k_out), _p(v_out)
+    if status is None:
+        status = new_status(k_out.device)
+    if ws is None:
+        ws = workspace(lib().hs_kv_cold_fetch_workspace_bytes(count), k_out.device)
+    check(lib().hs_kv_cold_fetch(ctypes.c_void_p(image.data_ptr()), layer, _p(positions), count,
+                                 kp, vp, row_bytes, _p(status), _p(ws), _s(stream)))
+    return status
 
 
 # ---- device checks and synthetic data -------------------------------------------------

@@ -195,8 +195,10 @@ int hs_kv_store_init(void *image, uint64_t request, uint32_t layers, uint32_t po
 int hs_kv_store_append(void *image, uint32_t layer, uint32_t first, const uint8_t *rows,
                        uint32_t count);
 /* The device read of the cold rows of one layer (SegmentedKVStore::fetch,
- * segmented_store.cpp:85-95): positions_dev [count] -> out_dev [count][4096]
- * read straight from the pinned image over the host link, every record's
+ * segmented_store.cpp:85-95): record i of positions_dev [count] -> its K
+ * half (2048 B) at k_out_dev + i*row_bytes and its V half at v_out_dev +
+ * i*row_bytes (the record's own layout: v_out_dev = k_out_dev + 2048,
+ * row_bytes 4096), read straight from the pinned image over the host link, every record's
  * identity (position, request, layer, version) and FNV-1a digest checked on
  * the device.  A position of 0xffffffff is padding: no record is read and
  * its output row is left as it was.  status_dev: code HS_ERR_CORRUPT and k
@@ -205,8 +207,8 @@ int hs_kv_store_append(void *image, uint32_t layer, uint32_t first, const uint8_
  * workspace: hs_kv_cold_fetch_workspace_bytes(count).  3 launches. */
 size_t hs_kv_cold_fetch_workspace_bytes(uint32_t count);
 int hs_kv_cold_fetch(const void *image, uint32_t layer, const uint32_t *positions_dev,
-                     uint32_t count, uint8_t *out_dev, hs_status_t *status_dev,
-                     void *workspace_dev, void *stream);
+                     uint32_t count, uint8_t *k_out_dev, uint8_t *v_out_dev, size_t row_bytes,
+                     hs_status_t *status_dev, void *workspace_dev, void *stream);
 
 /* Cold plan of one sequence after its selection (the hot/prefetched/cold
  * split of FullGqaRuntimePolicy::fetch, policy/full_gqa_runtime.cpp:
@@ -239,15 +241,18 @@ int hs_gqa_physical_union(const uint32_t *ids_dev, const uint32_t *lens_dev,
                           void *stream);
 
 /* pack_gqa_workspace (runtime/gqa_pack.hpp:26-58) from the device hot pool.
- * pool_dev rows of 4096 B (F16 K[8][128] then V[8][128]); row_of_id_dev
+ * Hot pool: row r's F16 K[8][128] at k_pool_dev + r*row_bytes and its F16
+ * V[8][128] at v_pool_dev + r*row_bytes (the reference's 4096 B KV records:
+ * v_pool_dev = k_pool_dev + 2048, row_bytes 4096; separate K and V arrays:
+ * row_bytes 2048).  row_of_id_dev
  * (nullable = identity, max_id entries) maps token id -> pool row; a row
  * outside [0, pool_rows) is absent (HS_ERR_MISSING in the status).
  * ids_dev/lens_dev as above (lens <= count, nonzero), positions_dev [nq]
  * ascending query positions (1 <= nq <= 256).  Writes K F16[count][32][128],
  * V F16[32][128][count], mask F32[32][qpad][count], qpad = ceil(nq/64)*64;
  * byte-identical to the reference, zero/-inf padding included. */
-int hs_gqa_pack(const uint8_t *pool_dev, uint32_t pool_rows,
-                const int32_t *row_of_id_dev, uint32_t max_id,
+int hs_gqa_pack(const uint8_t *k_pool_dev, const uint8_t *v_pool_dev, size_t row_bytes,
+                uint32_t pool_rows, const int32_t *row_of_id_dev, uint32_t max_id,
                 const uint32_t *ids_dev,
                 const uint32_t *lens_dev, size_t ids_stride,
                 const uint64_t *positions_dev, uint32_t nq, uint32_t count,
@@ -268,27 +273,31 @@ int hs_gqa_gather_rows(const uint16_t *prefetched_dev,
 
 /* ---- (4) sparse decode attention ----------------------------------------
  * Decode attention of patches/llama-b6000-external-attention-device.patch:
- * 49-66 over the selection, read straight from the hot pool (no pack):
+ * 49-66 over the selection, read straight from the hot pool (no pack; K
+ * and V rows as for hs_gqa_pack, row_bytes 2048..1 MiB):
  * s = (q_h . K_id) / sqrt(128), p = softmax(s), o_h = sum p V_id.  Each
  * (id, KV head) row is read once for the union of its 4 query heads.
  * q_dev F32 [32][128]; member_dev from hs_gqa_select ([32][ceil(n/32)]);
  * out_dev F32 [32][128].  With row_of_id_dev, rows outside [0, pool_rows)
  * contribute nothing.  workspace: hs_gqa_attention_workspace_bytes. */
 size_t hs_gqa_attention_workspace_bytes(uint32_t n);
-int hs_gqa_sparse_attention(const float *q_dev, const uint8_t *pool_dev,
-                            size_t row_bytes, const int32_t *row_of_id_dev,
+int hs_gqa_sparse_attention(const float *q_dev, const uint8_t *k_pool_dev,
+                            const uint8_t *v_pool_dev, size_t row_bytes,
+                            const int32_t *row_of_id_dev,
                             uint32_t pool_rows, const uint32_t *member_dev,
                             uint32_t n,
                             float *out_dev, void *workspace_dev, void *stream);
 
 /* ---- fused layer step ----------------------------------------------------
- * One sparse decode layer: score (rehearsal q16 over the hot pool's K
- * halves) -> select (scaled, alpha, ratio; ids in ascending id order) ->
- * sparse attention (q32).
- * pool rows 4096 B.  workspace: hs_decode_layer_workspace_bytes. */
+ * One sparse decode layer: score (rehearsal q16 over the hot pool's K rows)
+ * -> select (scaled, alpha, ratio; ids in ascending id order) -> sparse
+ * attention (q32).  Hot pool as for hs_gqa_pack, with row_bytes 2048 (K and
+ * V arrays: the scorer streams K contiguously) or 4096 (the reference's KV
+ * records).  workspace: hs_decode_layer_workspace_bytes. */
 size_t hs_decode_layer_workspace_bytes(uint32_t n);
 int hs_decode_layer(const uint16_t *q16_dev, const float *q32_dev,
-                    const uint8_t *pool_dev, const int32_t *row_of_id_dev,
+                    const uint8_t *k_pool_dev, const uint8_t *v_pool_dev, size_t row_bytes,
+                    const int32_t *row_of_id_dev,
                     uint32_t pool_rows, uint32_t n, float alpha, float ratio, uint32_t flags,
                     uint16_t *scores_dev, uint32_t *ids_dev, size_t ids_stride,
                     uint32_t *counts_dev, float *out_dev,

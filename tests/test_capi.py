@@ -78,15 +78,25 @@ def test_pack_union_gather_reject_bad_shapes(hs):
     L = hs.lib()
     assert L.hs_gqa_physical_union(fake, fake, 8, 0, fake, fake, fake, fake, None) == hs.HS_ERR_ARGUMENT
     assert L.hs_gqa_physical_union(fake, fake, 8, 66049, fake, fake, fake, fake, None) == hs.HS_ERR_ARGUMENT
-    assert L.hs_gqa_pack(fake, 1, None, 1, fake, fake, 8, fake, 0, 32, fake, fake, fake, fake,
-                         None) == hs.HS_ERR_ARGUMENT  # nq == 0
-    assert L.hs_gqa_pack(fake, 1, None, 1, fake, fake, 8, fake, 257, 32, fake, fake, fake, fake,
-                         None) == hs.HS_ERR_ARGUMENT  # nq > 256
-    assert L.hs_gqa_pack(fake, 1, None, 1, fake, fake, 8, fake, 1, 0, fake, fake, fake, fake,
-                         None) == hs.HS_ERR_ARGUMENT  # count == 0
+    pack = lambda nq, count, row_bytes=4096: L.hs_gqa_pack(
+        fake, fake, row_bytes, 1, None, 1, fake, fake, 8, fake, nq, count, fake, fake, fake, fake,
+        None)
+    assert pack(0, 32) == hs.HS_ERR_ARGUMENT  # nq == 0
+    assert pack(257, 32) == hs.HS_ERR_ARGUMENT  # nq > 256
+    assert pack(1, 0) == hs.HS_ERR_ARGUMENT  # count == 0
+    assert pack(1, 32, row_bytes=1024) == hs.HS_ERR_ARGUMENT  # a row holds 2048 B of K
     assert L.hs_gqa_gather_rows(fake, 1, fake, 1, fake, 0, fake, fake, fake, None) == hs.HS_ERR_ARGUMENT
-    assert L.hs_gqa_sparse_attention(fake, fake, 1000, None, 0, fake, 64, fake, fake,
+    for row_bytes in (1000, 2056 - 1, 1 << 21):  # below 2048, not a multiple of 16, above 1 MiB
+        assert L.hs_gqa_sparse_attention(fake, fake, fake, row_bytes, None, 0, fake, 64, fake,
+                                         fake, None) == hs.HS_ERR_ARGUMENT
+    misaligned = ctypes.c_void_p(0x1008)
+    assert L.hs_gqa_sparse_attention(fake, fake, misaligned, 2048, None, 0, fake, 64, fake, fake,
                                      None) == hs.HS_ERR_ARGUMENT
+    # the scorer streams K rows of 2048 or 4096 B only
+    assert L.hs_decode_layer(fake, fake, fake, fake, 3072, None, 0, 64, 1.0, 0.2, 0, fake, fake,
+                             16, fake, fake, fake, fake, None) == hs.HS_ERR_ARGUMENT
+    assert L.hs_kv_cold_fetch(fake, 0, fake, 1, fake, fake, 1024, fake, fake,
+                              None) == hs.HS_ERR_ARGUMENT
 
 
 CONTRACTS = Path(__file__).resolve().parent / "cpp" / "gqa_gpu_contracts"

@@ -55,3 +55,33 @@ def test_row_map_and_peaked_softmax(hs, port):
                                   to_dev(member.reshape(-1)), rows=to_dev(perm))
     ref = port.attention(q, pool.view(np.uint8).reshape(-1), ids, rows=perm)
     assert rel_err(out.cpu().numpy().astype(np.float64), ref) <= TOL
+
+
+@pytest.mark.parametrize("mapped", [False, True])
+def test_split_kv_arrays_equal_records(hs, port, mapped):
+    # The hot pool as a K array and a V array (2048 B rows) reads the same
+    # rows as the reference's 4096 B KV records: the output is the same bit
+    # for bit, and within the tolerance of the oracle.
+    n = 6000
+    g = rng(90 + mapped)
+    k = rope_keys(n, 9)
+    v = f16_bits(g.standard_normal((n, 8, 128)))
+    records = pool_rows(k, v)
+    rows = None
+    if mapped:
+        perm = g.permutation(n).astype(np.int32)
+        records = records[np.argsort(perm)]  # row perm[id] holds id
+        rows = to_dev(perm)
+    k_rows = np.ascontiguousarray(records[:, :1024])
+    v_rows = np.ascontiguousarray(records[:, 1024:])
+    q = (g.standard_normal((32, 128)) * 2.0).astype(np.float32)
+    ids = [np.sort(g.choice(n, size=900, replace=False)) for _ in range(32)]
+    member = to_dev(member_words(ids, n).reshape(-1))
+    qd = torch.from_numpy(q).cuda()
+    a = hs.ops.sparse_attention(qd, to_dev(records.reshape(-1)), n, member, rows=rows)
+    b = hs.ops.sparse_attention(qd, to_dev(k_rows.reshape(-1)), n, member, rows=rows,
+                                v_pool=to_dev(v_rows.reshape(-1)), row_bytes=2048)
+    assert torch.equal(a, b)
+    ref = port.attention(q, records.view(np.uint8).reshape(-1), ids,
+                         rows=None if rows is None else perm)
+    assert rel_err(b.cpu().numpy().astype(np.float64), ref) <= TOL

@@ -24,26 +24,28 @@ def pinned_image(hs, request, layers, positions, layer, rows):
     return image
 
 
-def cold_fetch(hs, image, layer, positions):
-    L = hs.lib()
+def cold_fetch(hs, image, layer, positions, split=False):
+    """Fetched records as [count][4096] bytes; with split, fetched into a K
+    array and a V array of 2048 B rows and joined again here."""
     pos = torch.tensor(positions, dtype=torch.int32, device="cuda")
-    out = torch.empty((len(positions), 4096), dtype=torch.uint8, device="cuda")
-    status = hs.ops.new_status("cuda")
-    ws = hs.ops.workspace(L.hs_kv_cold_fetch_workspace_bytes(len(positions)), "cuda")
-    hs.check(L.hs_kv_cold_fetch(ctypes.c_void_p(image.data_ptr()), layer,
-                                ctypes.c_void_p(pos.data_ptr()), len(positions),
-                                ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(status.data_ptr()),
-                                ctypes.c_void_p(ws.data_ptr()),
-                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    if split:
+        k_out = torch.empty((len(positions), 2048), dtype=torch.uint8, device="cuda")
+        v_out = torch.empty((len(positions), 2048), dtype=torch.uint8, device="cuda")
+        status = hs.ops.kv_cold_fetch(image, layer, pos, k_out, v_out=v_out, row_bytes=2048)
+        out = torch.cat([k_out, v_out], dim=1)
+    else:
+        out = torch.empty((len(positions), 4096), dtype=torch.uint8, device="cuda")
+        status = hs.ops.kv_cold_fetch(image, layer, pos, out)
     return out.cpu().numpy(), hs.ops.read_status(status)
 
 
-def test_rows_round_trip(hs):
+@pytest.mark.parametrize("split", [False, True])
+def test_rows_round_trip(hs, split):
     g = rng(1)
     rows = g.integers(0, 256, size=(300, 4096), dtype=np.uint8)
     image = pinned_image(hs, 77, 3, 512, 2, rows)
     positions = [int(x) for x in g.integers(0, 300, size=1000)]
-    out, st = cold_fetch(hs, image, 2, positions)
+    out, st = cold_fetch(hs, image, 2, positions, split=split)
     assert st["code"] == 0 and st["k"] == 0
     assert np.array_equal(out, rows[positions])
 
@@ -54,11 +56,13 @@ def test_corruption_detected(hs):
     image = pinned_image(hs, 5, 2, 64, 1, rows)
     raw = image.numpy()
     rec = lambda p: 4096 + (1 * 64 + p) * 4128
-    raw[rec(3) + 32 + 1000] ^= 0x40          # payload byte: digest mismatch
+    raw[rec(3) + 32 + 1000] ^= 0x40          # K half payload byte: digest mismatch
+    raw[rec(5) + 32 + 3000] ^= 0x01          # V half payload byte
     raw[rec(9) + 16] ^= 1                     # request field
     raw[rec(12) + 24] ^= 1                    # layer field
-    out, st = cold_fetch(hs, image, 1, list(range(64)))
-    assert st["code"] == hs.HS_ERR_CORRUPT and st["k"] == 3
+    for split in (False, True):  # the digest covers the K and the V half
+        out, st = cold_fetch(hs, image, 1, list(range(64)), split=split)
+        assert st["code"] == hs.HS_ERR_CORRUPT and st["k"] == 4
     # a record never appended (version 0) and a position past the capacity
     blank = pinned_image(hs, 5, 2, 64, 1, rows[:10])
     _, st = cold_fetch(hs, blank, 1, [0, 1, 20])
@@ -119,8 +123,7 @@ def test_cold_plan_and_padded_fetch(hs):
     image = pinned_image(hs, 9, 1, n, 0, data)
     out = torch.zeros((cold_tokens, 4096), dtype=torch.uint8, device="cuda")
     status = hs.ops.new_status("cuda")
-    ws = hs.ops.workspace(L.hs_kv_cold_fetch_workspace_bytes(cold_tokens), "cuda")
-    hs.check(L.hs_kv_cold_fetch(vp(image), 0, vp(pos), cold_tokens, vp(out), vp(status), vp(ws), st))
+    hs.ops.kv_cold_fetch(image, 0, pos, out, status=status)
     assert hs.ops.read_status(status)["code"] == 0
     o = out.cpu().numpy()
     assert np.array_equal(o[: want.size], data[want])

@@ -68,3 +68,25 @@ def test_layer_zero_selection_is_an_error(hs):
     *_, status = hs.ops.decode_layer(to_dev(q16), torch.from_numpy(q32).cuda(),
                                      to_dev(pool.reshape(-1)), n, 0.5, 0.2)
     assert hs.ops.read_status(status)["code"] == hs.HS_ERR_ZERO_SELECTION
+
+
+def test_layer_split_kv_arrays_equal_records(hs):
+    # score over the K array's 2048 B rows and attention over the K and V
+    # arrays: scores, ids, counts and output equal the 4096 B record layout's
+    n = 32768
+    g = rng(4242)
+    k = rope_keys(n, 4243)
+    v = f16_bits(g.standard_normal((n, 8, 128)))
+    records = pool_rows(k, v)
+    q16 = f16_bits(g.standard_normal((32, 128)))
+    q32 = torch.from_numpy(g.standard_normal((32, 128)).astype(np.float32)).cuda()
+    a = hs.ops.decode_layer(to_dev(q16), q32, to_dev(records.reshape(-1)), n, 5.0, 0.2)
+    b = hs.ops.decode_layer(to_dev(q16), q32, to_dev(np.ascontiguousarray(records[:, :1024])), n,
+                            5.0, 0.2, v_pool=to_dev(np.ascontiguousarray(records[:, 1024:])),
+                            row_bytes=2048)
+    sa, sb = hs.ops.read_status(a[4]), hs.ops.read_status(b[4])
+    assert sa == sb and sa["code"] == 0
+    kk = sa["k"]
+    assert torch.equal(a[0], b[0])
+    assert torch.equal(a[1][:, :kk], b[1][:, :kk])
+    assert torch.equal(a[2], b[2]) and torch.equal(a[3], b[3])

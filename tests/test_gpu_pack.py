@@ -19,14 +19,21 @@ def dev_ids(selected):
     return to_dev(ids), to_dev(lens), stride
 
 
-def gpu_pack(hs, selected, queries, physical, payload, count, extra_rows=0):
+def gpu_pack(hs, selected, queries, physical, payload, count, extra_rows=0, split=False):
     ids, lens, stride = dev_ids(selected)
     row_of_id = np.full(max(int(np.max(physical)) + 1, 1) + extra_rows, -1, dtype=np.int32)
     row_of_id[np.asarray(physical, dtype=np.int64)] = np.arange(len(physical), dtype=np.int32)
-    pool = torch.from_numpy(np.ascontiguousarray(payload)).cuda()
     pos = torch.tensor(np.asarray(queries, dtype=np.uint64).view(np.int64), device="cuda")
-    k, v, mask, status = hs.ops.pack(pool, ids, lens, stride, pos, count,
-                                     row_of_id=to_dev(row_of_id))
+    records = np.ascontiguousarray(payload, dtype=np.uint8).reshape(-1, 4096)
+    if split:  # the hot pool as a K array and a V array of 2048 B rows
+        kp = torch.from_numpy(np.ascontiguousarray(records[:, :2048])).cuda()
+        vp = torch.from_numpy(np.ascontiguousarray(records[:, 2048:])).cuda()
+        k, v, mask, status = hs.ops.pack(kp, ids, lens, stride, pos, count,
+                                         row_of_id=to_dev(row_of_id), v_pool=vp, row_bytes=2048)
+    else:
+        pool = torch.from_numpy(records).cuda()
+        k, v, mask, status = hs.ops.pack(pool, ids, lens, stride, pos, count,
+                                         row_of_id=to_dev(row_of_id))
     st = hs.ops.read_status(status)
     return st, from_dev(k), from_dev(v), mask.cpu().numpy()
 
@@ -48,7 +55,8 @@ def test_pack_known_values(hs, port):
 def test_pack_random(hs, port, trial):
     g = rng(781 + trial)
     n, slots, rows, payload, selected, queries = random_trial(g, trial)
-    st, k, v, mask = gpu_pack(hs, selected, queries, rows, payload, slots)
+    # every other trial reads a hot pool of separate K and V arrays
+    st, k, v, mask = gpu_pack(hs, selected, queries, rows, payload, slots, split=trial % 2 == 1)
     rc, pk, pv, pmask = port.pack(selected, queries, rows, payload, slots)
     assert st["code"] == 0 and rc == 0
     assert np.array_equal(k, pk) and np.array_equal(v, pv)
