@@ -19,13 +19,12 @@
 //    and V row exactly once for all of its query heads -> HBM bytes =
 //    sum_g |U_g|*512.  The 8 waves read the 8 heads' segments of the same
 //    pool rows at about the same time.
-//  * one pass: 16 lanes per id, 16 B (8 channels) per lane, so every K and
-//    V access is a contiguous 256 B run; a row's K and V segments are
-//    requested together, which streams ~1.4x faster than a K pass followed
-//    by a V pass.  Scores are reduced over the 16
-//    lanes with 4 DPP adds per head, softmax is online (rescaled once per
-//    batch of rows), and p*V accumulates in registers.  Loads run one batch
-//    ahead of their use.
+//  * one pass over tiles of 16 union rows: a row's K and V segments are
+//    requested together (which streamed ~1.4x faster than a K pass followed
+//    by a V pass), the next tile before the current one is used.  Scores
+//    come from MFMA (q split into F16 hi and lo parts, FP32 products and
+//    sums), softmax is online per tile with a wave-uniform running maximum,
+//    and p*V accumulates in FP32 registers.
 //  * the (m, l, o[128]) partials of all chunks are merged by attn_combine.
 #include <hip/hip_runtime.h>
 
@@ -43,13 +42,6 @@ constexpr uint32_t kThreads = 512; // 8 waves: one per KV head
 constexpr uint32_t kRecord = 2 + 128;
 constexpr float kScale = 0.088388347648318440550f;  // 1/sqrt(128)
 
-__device__ __forceinline__ void unpack8(const uint4 w, float* f) {
-    f[0] = h2f(w.x & 0xffffu); f[1] = h2f(w.x >> 16);
-    f[2] = h2f(w.y & 0xffffu); f[3] = h2f(w.y >> 16);
-    f[4] = h2f(w.z & 0xffffu); f[5] = h2f(w.z >> 16);
-    f[6] = h2f(w.w & 0xffffu); f[7] = h2f(w.w >> 16);
-}
-
 // Sum over the 16 lanes of a DPP row (one 16-lane group), returned to every
 // lane with the same bits: quad xor 1, quad xor 2, then the row mirror
 // (quad a <-> 3-a) and the half-row mirror (quad a <-> a^1).  Each step adds
@@ -66,14 +58,44 @@ __device__ __forceinline__ float row_sum16(float v) {
     return v;
 }
 
+template <int kCtrl>
+__device__ __forceinline__ float dpp_max(float v) {
+    return fmaxf(v, dpp_f32<kCtrl>(v));
+}
+// Maximum over the 16 lanes of a DPP row, the same bits in every lane.
+__device__ __forceinline__ float row_max16(float v) {
+    v = dpp_max<0xB1>(v);
+    v = dpp_max<0x4E>(v);
+    v = dpp_max<0x140>(v);
+    v = dpp_max<0x141>(v);
+    return v;
+}
+__device__ __forceinline__ float first_lane(float v) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
 // One pass over the selected rows.  A workgroup owns kChunk consecutive ids
-// and all 8 KV heads, one wave per KV head, so the K and V segments of the
-// 8 heads in one 4 KiB pool row are requested close together in time.  In a
-// wave, 16 lanes take one (id, g) row at a time with 8 channels per lane; K
-// and V are requested together, the next batch of rows before the current
-// one is used.  Each 16-lane group keeps an online softmax state (m, l, o)
-// per query head, rescaled once per batch; the 4 groups of the wave are
-// merged with cross-lane moves and the wave writes the chunk's record.
+// and all 8 KV heads, one wave per KV head, so the 8 heads' segments of the
+// same pool rows are requested close together in time.  A wave walks its
+// union in tiles of 16 rows, the next tile's K and V requested before the
+// current tile is used:
+//  * scores on MFMA: S = Q . K^T with v_mfma_f32_16x16x32_f16, A = the 4
+//    query rows of the wave (rows 4..15 zero), B = K^T of the tile (lane l
+//    supplies channels 32s + 8(l/16) .. +7 of row l%16 at step s: 16
+//    contiguous bytes).  q is split into F16 hi = f16(q) and lo =
+//    f16(q - hi), two products per step, so the scores carry ~22 bits of q;
+//    products and sums are FP32.  Lanes 0..15 then hold S[0..3][row l];
+//  * softmax per tile: the tile's maximum per head (DPP over those 16
+//    lanes) updates the wave-uniform running maximum; o and the lanes'
+//    partial sums are rescaled only when it rises; p = exp(s - m) goes to
+//    LDS (16 B per row);
+//  * p * V on VALU: lane (row group l/16, channel group l%16) adds 4 rows of
+//    the tile for its 8 channels and 4 heads.
+// At the end the 4 row groups' o are added (they share m) and the wave
+// writes the chunk's record.
 template <bool kRows>
 __global__ void __launch_bounds__(kThreads)
 attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ pool,
@@ -81,9 +103,9 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
                     uint32_t pool_rows,
                     const uint32_t* __restrict__ member, uint32_t n, uint32_t chunks,
                     float* __restrict__ part) {
-    constexpr uint32_t kBatch = 2;  // rows per batch of a 16-lane group (K + V); 2 batches in flight
     __shared__ uint32_t sel_row[8][kChunk];
     __shared__ uint8_t sel_mask[8][kChunk];
+    __shared__ float4 ptile[8][16];
 
     const uint32_t chunk = blockIdx.x;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -117,131 +139,150 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
         total += static_cast<uint32_t>(__popcll(any));
     }
     __builtin_amdgcn_wave_barrier();
+    float* rec = part + (static_cast<size_t>(g) * chunks + chunk) * 4 * kRecord;
+    const uint32_t r16 = lane & 15u, q16 = lane >> 4;
+    if (total == 0) {  // no selected row: an empty record, and no row is read
+        if (lane < 16) {
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+#pragma unroll
+                for (uint32_t c = 0; c < 8; ++c) rec[j * kRecord + 2 + r16 * 8 + c] = 0.0f;
+                if (lane == 0) {
+                    rec[j * kRecord + 0] = -INFINITY;
+                    rec[j * kRecord + 1] = 0.0f;
+                }
+            }
+        }
+        return;
+    }
 
-    // ---- one pass: scores, online softmax, p * V -----------------------------
-    const uint32_t grp = lane >> 4, part16 = lane & 15u;  // 4 groups per wave
-    float qr[4][8];
+    // A operands: this wave's query rows, hi and lo parts (lanes with
+    // l%16 >= 4 hold the zero rows)
+    half8 ahi[4], alo[4];
 #pragma unroll
-    for (uint32_t j = 0; j < 4; ++j)
+    for (uint32_t s = 0; s < 4; ++s) {
 #pragma unroll
-        for (uint32_t e = 0; e < 8; ++e) qr[j][e] = q[(4 * g + j) * 128 + part16 * 8 + e];
-    // a row's V segment sits v_delta bytes from its K segment
-    const uint32_t koff = g * 256 + part16 * 16;
-    const int64_t voff = v_delta + koff;
-    float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t e = 0; e < 8; ++e) {
+            const float qv = q[(4 * g + (r16 & 3u)) * 128 + 32 * s + 8 * q16 + e];  // in range
+            const float x = r16 < 4 ? qv : 0.0f;
+            const _Float16 hi = static_cast<_Float16>(x);
+            ahi[s][e] = hi;
+            alo[s][e] = static_cast<_Float16>(x - static_cast<float>(hi));
+        }
+    }
+    const uint32_t head_off = g * 256;  // the wave's KV head within a row
+    // tile t: K rows 16t + l%16 (MFMA B layout) and V rows 16t + l/16 + 4i
+    // (16 B per lane at channel group l%16); rows past the union re-read its
+    // last row and are masked out
+    auto load_tile = [&](uint32_t t, uint4 (&kw)[4], uint4 (&vw)[4]) {
+        const uint32_t ek = min(16 * t + r16, total - 1);
+        const uint8_t* krow = pool + static_cast<size_t>(sel_row[g][ek]) * row_bytes + head_off +
+                              16 * q16;
+#pragma unroll
+        for (uint32_t s = 0; s < 4; ++s) kw[s] = *reinterpret_cast<const uint4*>(krow + 64 * s);
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t ev = min(16 * t + q16 + 4 * i, total - 1);
+            const uint8_t* vrow = pool + static_cast<size_t>(sel_row[g][ev]) * row_bytes;
+            vw[i] = *reinterpret_cast<const uint4*>(vrow + v_delta + head_off + 16 * r16);
+        }
+    };
+    float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // wave-uniform
+    float lsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // lanes 0..15: their rows' p sums
     float o[4][8];
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j)
 #pragma unroll
         for (uint32_t c = 0; c < 8; ++c) o[j][c] = 0.0f;
 
-    // rows e = e0 + 4u (u < kBatch) form a batch of this group
-    auto load_batch = [&](uint32_t e0, uint4 (&kw)[kBatch], uint4 (&vw)[kBatch]) {
+    auto use_tile = [&](uint32_t t, const uint4 (&kw)[4], const uint4 (&vw)[4]) {
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u) {
-            // past the end, the last row is read again and masked out below;
-            // straight-line loads let the next batch stay in flight
-            const size_t r = sel_row[g][min(e0 + 4 * u, total - 1)];
-            const uint8_t* row = pool + r * row_bytes;
-            kw[u] = *reinterpret_cast<const uint4*>(row + koff);
-            vw[u] = *reinterpret_cast<const uint4*>(row + voff);
+        for (uint32_t s = 0; s < 4; ++s) {
+            const half8 kb = __builtin_bit_cast(half8, kw[s]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[s], kb, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[s], kb, acc, 0, 0, 0);
         }
-    };
-    auto use_batch = [&](uint32_t e0, const uint4 (&kw)[kBatch], const uint4 (&vw)[kBatch]) {
-        float s[kBatch][4];
-        float bm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        // lanes 0..15: row 16t + l of the union, heads 0..3
+        const uint32_t e = 16 * t + r16;
+        const uint32_t mk_at = sel_mask[g][min(e, total - 1)];
+        const uint32_t mk = (q16 == 0 && e < total) ? mk_at : 0u;
+        float sc[4];
 #pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u) {
-            const uint32_t e = e0 + 4 * u;
-            float kf[8];
-            unpack8(kw[u], kf);
-            float d[4];
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) {
-                float acc = 0.0f;
-#pragma unroll
-                for (uint32_t c = 0; c < 8; ++c) acc = __builtin_fmaf(qr[j][c], kf[c], acc);
-                d[j] = acc;
-            }
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) d[j] = row_sum16(d[j]);
-            const uint32_t mk_at = sel_mask[g][min(e, total - 1)];
-            const uint32_t mk = e < total ? mk_at : 0u;
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) {
-                s[u][j] = ((mk >> j) & 1u) ? d[j] * kScale : -INFINITY;
-                bm[j] = fmaxf(bm[j], s[u][j]);
-            }
-        }
+        for (uint32_t j = 0; j < 4; ++j) sc[j] = ((mk >> j) & 1u) ? acc[j] * kScale : -INFINITY;
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
-            const float mn = fmaxf(m[j], bm[j]);
-            // scale 0 while head j has no selected row (m = -inf)
-            const float scale = m[j] == -INFINITY ? 0.0f : __expf(m[j] - mn);
-            l[j] *= scale;
+            const float mn = fmaxf(m[j], first_lane(row_max16(sc[j])));
+            if (mn > m[j]) {  // wave-uniform
+                // scale 0 while head j had no selected row (m = -inf)
+                const float scale = m[j] == -INFINITY ? 0.0f : __expf(m[j] - mn);
+                lsum[j] *= scale;
 #pragma unroll
-            for (uint32_t c = 0; c < 8; ++c) o[j][c] *= scale;
-            m[j] = mn;
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u) {
-            float vf[8];
-            unpack8(vw[u], vf);
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) {
-                const float p = s[u][j] == -INFINITY ? 0.0f : __expf(s[u][j] - m[j]);
-                l[j] += p;
-#pragma unroll
-                for (uint32_t c = 0; c < 8; ++c) o[j][c] = __builtin_fmaf(p, vf[c], o[j][c]);
+                for (uint32_t c = 0; c < 8; ++c) o[j][c] *= scale;
+                m[j] = mn;
             }
         }
+        float p[4];
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            p[j] = sc[j] == -INFINITY ? 0.0f : __expf(sc[j] - m[j]);
+            lsum[j] += p[j];
+        }
+        if (q16 == 0) ptile[g][r16] = make_float4(p[0], p[1], p[2], p[3]);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const float4 pp = ptile[g][q16 + 4 * i];
+            const uint32_t vwords[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
+#pragma unroll
+            for (uint32_t c2 = 0; c2 < 4; ++c2) {
+                const float v0 = h2f(vwords[c2] & 0xffffu), v1 = h2f(vwords[c2] >> 16);
+                o[0][2 * c2] = __builtin_fmaf(pp.x, v0, o[0][2 * c2]);
+                o[1][2 * c2] = __builtin_fmaf(pp.y, v0, o[1][2 * c2]);
+                o[2][2 * c2] = __builtin_fmaf(pp.z, v0, o[2][2 * c2]);
+                o[3][2 * c2] = __builtin_fmaf(pp.w, v0, o[3][2 * c2]);
+                o[0][2 * c2 + 1] = __builtin_fmaf(pp.x, v1, o[0][2 * c2 + 1]);
+                o[1][2 * c2 + 1] = __builtin_fmaf(pp.y, v1, o[1][2 * c2 + 1]);
+                o[2][2 * c2 + 1] = __builtin_fmaf(pp.z, v1, o[2][2 * c2 + 1]);
+                o[3][2 * c2 + 1] = __builtin_fmaf(pp.w, v1, o[3][2 * c2 + 1]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // the tile's p are read before the next tile writes
     };
-    constexpr uint32_t kStep = 4 * kBatch;
-    // All 4 groups of a wave step together, over pairs of batches (the loop
-    // bound is wave-uniform; an odd batch count ends with one fully masked
-    // batch).  Each batch is requested, unconditionally, before the previous
-    // one is used, and no exit test sits between a batch's loads and its use,
-    // so the compiler keeps the loads where they are and the wait before each
-    // use leaves the next batch in flight.
-    uint4 ka[kBatch], va[kBatch], kb[kBatch], vb[kBatch];
-    const uint32_t pairs = (total + 2 * kStep - 1) / (2 * kStep);
-    load_batch(grp, ka, va);
-    for (uint32_t p = 0; p < pairs; ++p) {
-        const uint32_t b0 = p * 2 * kStep + grp;
-        load_batch(b0 + kStep, kb, vb);
+    // Pairs of tiles (the loop bound is wave-uniform; an odd tile count ends
+    // with one fully masked tile).  Each tile is requested, unconditionally,
+    // before the previous one is used, and no exit test sits between a
+    // tile's loads and its use, so the waits before each use leave the next
+    // tile in flight.
+    uint4 ka[4], va[4], kb[4], vb[4];
+    const uint32_t tiles = (total + 15) / 16;
+    const uint32_t pairs = (tiles + 1) / 2;
+    load_tile(0, ka, va);
+    for (uint32_t pi = 0; pi < pairs; ++pi) {
+        load_tile(2 * pi + 1, kb, vb);
         __builtin_amdgcn_sched_barrier(0);
-        use_batch(b0, ka, va);
-        load_batch(b0 + 2 * kStep, ka, va);
+        use_tile(2 * pi, ka, va);
+        load_tile(2 * pi + 2, ka, va);
         __builtin_amdgcn_sched_barrier(0);
-        use_batch(b0 + kStep, kb, vb);
+        use_tile(2 * pi + 1, kb, vb);
     }
 
-    // ---- merge the 4 groups of the wave (lanes l, l^16, l^32, l^48) ----------
+    // ---- the 4 row groups share m: add their o; l from the row lanes ------
 #pragma unroll
-    for (uint32_t off = 16; off < 64; off <<= 1) {
+    for (uint32_t off = 16; off < 64; off <<= 1)
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-            const float mo = __shfl_xor(m[j], off, 64), lo = __shfl_xor(l[j], off, 64);
-            const float mn = fmaxf(m[j], mo);
-            const float a = (m[j] == -INFINITY) ? 0.0f : __expf(m[j] - mn);
-            const float b = (mo == -INFINITY) ? 0.0f : __expf(mo - mn);
-            l[j] = l[j] * a + lo * b;
+        for (uint32_t j = 0; j < 4; ++j)
 #pragma unroll
-            for (uint32_t c = 0; c < 8; ++c) {
-                const float oo = __shfl_xor(o[j][c], off, 64);
-                o[j][c] = o[j][c] * a + oo * b;
-            }
-            m[j] = mn;
-        }
-    }
+            for (uint32_t c = 0; c < 8; ++c) o[j][c] += __shfl_xor(o[j][c], off, 64);
+    float l[4];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) l[j] = first_lane(row_sum16(lsum[j]));
     // ---- this chunk's (m, l, o[128]) record per query head of KV head g -------
     if (lane < 16) {
-        float* rec = part + (static_cast<size_t>(g) * chunks + chunk) * 4 * kRecord;
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
 #pragma unroll
-            for (uint32_t c = 0; c < 8; ++c) rec[j * kRecord + 2 + part16 * 8 + c] = o[j][c];
+            for (uint32_t c = 0; c < 8; ++c) rec[j * kRecord + 2 + r16 * 8 + c] = o[j][c];
             if (lane == 0) {
                 rec[j * kRecord + 0] = m[j];
                 rec[j * kRecord + 1] = l[j];
