@@ -113,18 +113,26 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
     const uint32_t words = (n + 31) / 32;
     const uint32_t base = chunk * kChunk;
 
+    const uint32_t r16 = lane & 15u, q16 = lane >> 4;
     // ---- union of the 4 query heads' selections, compacted in id order ----
+    // (every membership word is requested before any is used: straight-line
+    // loads, the index clamped to the last id)
+    constexpr uint32_t kSteps = kChunk / 64;
+    uint32_t mw[kSteps][4];
+#pragma unroll
+    for (uint32_t c = 0; c < kSteps; ++c) {
+        const uint32_t at = min(base + 64 * c + lane, n - 1) >> 5;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) mw[c][j] = member[static_cast<size_t>(4 * g + j) * words + at];
+    }
     uint32_t total = 0;
 #pragma unroll
-    for (uint32_t c = 0; c < kChunk; c += 64) {
-        const uint32_t id = base + c + lane;
+    for (uint32_t c = 0; c < kSteps; ++c) {
+        const uint32_t id = base + 64 * c + lane;
         uint32_t mk = 0, r = id;
         if (id < n) {
 #pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) {
-                const uint32_t w = member[static_cast<size_t>(4 * g + j) * words + (id >> 5)];
-                mk |= ((w >> (id & 31u)) & 1u) << j;
-            }
+            for (uint32_t j = 0; j < 4; ++j) mk |= ((mw[c][j] >> (id & 31u)) & 1u) << j;
             if (kRows && mk) {
                 r = static_cast<uint32_t>(rows[id]);
                 if (r >= pool_rows) mk = 0;  // rows outside the pool contribute nothing
@@ -140,7 +148,6 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
     }
     __builtin_amdgcn_wave_barrier();
     float* rec = part + (static_cast<size_t>(g) * chunks + chunk) * 4 * kRecord;
-    const uint32_t r16 = lane & 15u, q16 = lane >> 4;
     if (total == 0) {  // no selected row: an empty record, and no row is read
         if (lane < 16) {
 #pragma unroll
@@ -156,20 +163,7 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
         return;
     }
 
-    // A operands: this wave's query rows, hi and lo parts (lanes with
-    // l%16 >= 4 hold the zero rows)
-    half8 ahi[4], alo[4];
-#pragma unroll
-    for (uint32_t s = 0; s < 4; ++s) {
-#pragma unroll
-        for (uint32_t e = 0; e < 8; ++e) {
-            const float qv = q[(4 * g + (r16 & 3u)) * 128 + 32 * s + 8 * q16 + e];  // in range
-            const float x = r16 < 4 ? qv : 0.0f;
-            const _Float16 hi = static_cast<_Float16>(x);
-            ahi[s][e] = hi;
-            alo[s][e] = static_cast<_Float16>(x - static_cast<float>(hi));
-        }
-    }
+    half8 ahi[4], alo[4];  // the MFMA A operands (filled below)
     const uint32_t head_off = g * 256;  // the wave's KV head within a row
     // tile t: K rows 16t + l%16 (MFMA B layout) and V rows 16t + l/16 + 4i
     // (16 B per lane at channel group l%16); rows past the union re-read its
@@ -258,6 +252,20 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
     const uint32_t tiles = (total + 15) / 16;
     const uint32_t pairs = (tiles + 1) / 2;
     load_tile(0, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+    // A operands: this wave's query rows, hi and lo parts (lanes with
+    // l%16 >= 4 hold the zero rows), read while the first tile is in flight
+#pragma unroll
+    for (uint32_t s = 0; s < 4; ++s) {
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e) {
+            const float qv = q[(4 * g + (r16 & 3u)) * 128 + 32 * s + 8 * q16 + e];  // in range
+            const float x = r16 < 4 ? qv : 0.0f;
+            const _Float16 hi = static_cast<_Float16>(x);
+            ahi[s][e] = hi;
+            alo[s][e] = static_cast<_Float16>(x - static_cast<float>(hi));
+        }
+    }
     for (uint32_t pi = 0; pi < pairs; ++pi) {
         load_tile(2 * pi + 1, kb, vb);
         __builtin_amdgcn_sched_barrier(0);

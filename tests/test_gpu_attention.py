@@ -85,3 +85,23 @@ def test_split_kv_arrays_equal_records(hs, port, mapped):
     ref = port.attention(q, records.view(np.uint8).reshape(-1), ids,
                          rows=None if rows is None else perm)
     assert rel_err(b.cpu().numpy().astype(np.float64), ref) <= TOL
+
+
+def test_chunks_with_empty_unions(hs, port):
+    # Every query head selects only ids below 1000 of 4096, so most 128-id
+    # chunks have an empty union for every KV head: those chunks read no row
+    # and contribute nothing (and a head whose ids are all in one chunk still
+    # gets its output from that chunk alone).
+    n = 4096
+    g = rng(31)
+    k = rope_keys(n, 32)
+    v = f16_bits(g.standard_normal((n, 8, 128)))
+    pool = pool_rows(k, v)
+    q = g.standard_normal((32, 128)).astype(np.float32)
+    ids = [np.sort(g.choice(1000, size=50, replace=False)) for _ in range(32)]
+    ids[5] = np.array([3000])  # a single row far from the others
+    member = member_words(ids, n)
+    out = hs.ops.sparse_attention(torch.from_numpy(q).cuda(), to_dev(pool.reshape(-1)), n,
+                                  to_dev(member.reshape(-1)))
+    ref = port.attention(q, pool.view(np.uint8), ids)
+    assert rel_err(out.cpu().numpy().astype(np.float64), ref) <= TOL
