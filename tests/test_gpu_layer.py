@@ -1,9 +1,9 @@
 """End-to-end sparse decode layer on the GPU against the oracle.
 
-config 1 against the golden fixture written by the
-compiled reference; config 3 (score N=32768 over the hot pool, select at the
-cap, sparse attention) against the oracle: scores and ids bit-exact,
-attention within 2e-3."""
+BASELINE.json configs[0] against the golden fixture written by the compiled
+reference; configs[2] (score N=32768 over the hot pool, select at the cap,
+sparse attention) against the oracle: scores and ids bit-exact, attention
+within 2e-3."""
 from pathlib import Path
 
 import numpy as np
