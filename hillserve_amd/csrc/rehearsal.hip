@@ -16,7 +16,10 @@
 // K = 4096 and HBM-bound (Wq is 32 MiB, read once); each workgroup owns 16
 // output features and its 8 waves split K eight ways, each issuing
 // v_mfma_f32_16x16x32_bf16 over a 512-wide K slice (A = the batch's hidden
-// rows, B = 16 rows of Wq).  The 8 partial tiles are added in LDS in a fixed
+// rows, B = 16 rows of Wq).  A wave reads its Wq slice one row per
+// instruction (64 lanes x 16 B = 1 KiB contiguous) into a padded LDS tile
+// and takes the MFMA B operands from there: read straight into the MFMA
+// layout, an instruction would cover only 64 B of each of 16 rows.  The 8 partial tiles are added in LDS in a fixed
 // order (deterministic), the RMS scale (sums of squares taken from the same
 // A fragments, so hidden is never rounded again) and RoPE (FP64 angle and
 // rotation) run in the epilogue, and each workgroup records per-sequence
@@ -58,7 +61,12 @@ struct RehearsalArgs {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// A wave's Wq slice in LDS: 16 rows of 1 KiB (64 x 16 B), padded by 16 B so
+// the 16 rows of an MFMA operand read fall in different banks.
+constexpr uint32_t kRowChunks = kSliceK * 2 / 16;  // 64
+
 __global__ void __launch_bounds__(kSplits * 64) rehearsal_kernel(const RehearsalArgs a) {
+    __shared__ uint4 wtile[kSplits][kTileN][kRowChunks + 1];
     __shared__ float part[kSplits][16][kTileN + 1];
     __shared__ float sq[kSplits][16];
     __shared__ float yv[16][kTileN];
@@ -69,25 +77,35 @@ __global__ void __launch_bounds__(kSplits * 64) rehearsal_kernel(const Rehearsal
     const uint32_t r = lane & 15u, grp = lane >> 4;  // A row (sequence) / B column (feature)
     const bool live = r < a.batch;
     const uint32_t k0 = w * kSliceK + 8 * grp;
-    const uint16_t* wrow = a.wq + static_cast<size_t>(o0 + r) * kModel + k0;
     const uint16_t* hrow = a.hidden + static_cast<size_t>(live ? r : 0u) * kModel + k0;
     if (tid < 16) bad[tid] = 0;
 
     // every load of the K slice is issued before the first product: with 8
-    // waves per CU the whole of Wq is in flight at once
-    uint4 wb[kSteps], hb[kSteps];
+    // waves per CU the whole of Wq is in flight at once.  Wq: row i of the
+    // tile per instruction; hidden (small, cached): straight into the MFMA
+    // layout.
+    const uint16_t* wslice = a.wq + static_cast<size_t>(o0) * kModel + w * kSliceK + lane * 8;
+    uint4 wv[kTileN], hb[kSteps];
 #pragma unroll
-    for (uint32_t s = 0; s < kSteps; ++s) {
-        wb[s] = *reinterpret_cast<const uint4*>(wrow + s * kMfmaK);
+    for (uint32_t i = 0; i < kTileN; ++i)
+        wv[i] = *reinterpret_cast<const uint4*>(wslice + static_cast<size_t>(i) * kModel);
+#pragma unroll
+    for (uint32_t s = 0; s < kSteps; ++s)
         hb[s] = live ? *reinterpret_cast<const uint4*>(hrow + s * kMfmaK)
                      : make_uint4(0u, 0u, 0u, 0u);
-    }
+#pragma unroll
+    for (uint32_t i = 0; i < kTileN; ++i) wtile[w][i][lane] = wv[i];
+    // the tile is this wave's alone: its LDS writes precede its reads in
+    // issue order, and the barrier keeps the compiler from moving them
+    __builtin_amdgcn_wave_barrier();
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     float ss = 0.0f;
 #pragma unroll
     for (uint32_t s = 0; s < kSteps; ++s) {
+        // B: Wq[o0 + r][w * kSliceK + 32 s + 8 grp .. +7] = 16 B chunk 4 s + grp of row r
+        const uint4 wb = wtile[w][r][4 * s + grp];
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hb[s]),
-                                                      __builtin_bit_cast(bf16x8, wb[s]), acc, 0,
+                                                      __builtin_bit_cast(bf16x8, wb), acc, 0,
                                                       0, 0);
         const uint32_t hw[4] = {hb[s].x, hb[s].y, hb[s].z, hb[s].w};
 #pragma unroll
