@@ -5,7 +5,11 @@ decode step of 30 sparse layers at N=32768 (32 query / 8 KV heads, D=128):
 per layer the ordered-FP32 scorer over that layer's own F16 K[32768,8,128]
 (RoPE-structured synthetic keys, theta 500000) and the head-0 alpha-margin
 selection at the 20 % cap.  30 distinct 64 MiB key buffers rotate, so the
-256 MB MALL cannot serve repeats.
+256 MB MALL cannot serve repeats.  The layers are pipelined as the
+reference prepares history one layer early: layer l's per-head selection
+and layer l+1's scoring share one launch (hs_gqa_select_then_score), the
+scoring on the CUs the selection leaves idle.  The same step one layer at a
+time is timed as well (serial_ms_per_step) and must select the same ids.
 
 Also reported on the same line:
   roofline      the scoring kernel (dominant): algorithmic bytes per launch
@@ -471,8 +475,9 @@ def main():
     for layer in range(LAYERS):
         ops.fill_rope_keys(keys[layer], N, 1024, 8, seed=1000 + layer, theta=500000.0)
         ops.fill_gaussian(qs[layer], seed=5000 + layer)
-    raw = torch.empty((32, N), dtype=torch.float16, device=dev)
-    partial = torch.empty((N + 63) // 64, dtype=torch.int32, device=dev)
+    raws = [torch.empty((32, N), dtype=torch.float16, device=dev) for _ in range(2)]
+    partials = [torch.empty((N + 63) // 64, dtype=torch.int32, device=dev) for _ in range(2)]
+    raw, partial = raws[0], partials[0]
     ids = torch.empty((32, kmax), dtype=torch.int32, device=dev)
     counts = torch.empty(32, dtype=torch.int32, device=dev)
     status = ops.new_status(dev)
@@ -482,11 +487,32 @@ def main():
     def new_event():
         return torch.cuda.Event(enable_timing=True)
 
-    def step():
+    def select_layer(b):
+        ops.select(raws[b], 32, N, N, ALPHA, RATIO, scale_raw=True, head0_partial=partials[b],
+                   ids=ids, ids_stride=kmax, counts=counts, status=status, ws=ws)
+
+    def serial_step():
+        # one layer at a time: score, then select
         for layer in range(LAYERS):
             ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
-            ops.select(raw, 32, N, N, ALPHA, RATIO, scale_raw=True, head0_partial=partial,
-                       ids=ids, ids_stride=kmax, counts=counts, status=status, ws=ws)
+            select_layer(0)
+
+    # Pipelined: layer l's selection shares a launch with layer l+1's scoring
+    # (hs_gqa_select_then_score); the score buffers alternate between layers.
+    pipe_calls = [
+        ops.prepare_select_then_score(
+            [dict(scores=raws[l % 2], n=N, head0_partial=partials[l % 2], ids=ids,
+                  ids_stride=kmax, counts=counts, status=status, ws=ws)],
+            [dict(q16=qs[l + 1], keys=keys[l + 1], tokens=N, out=raws[(l + 1) % 2],
+                  head0_partial=partials[(l + 1) % 2])],
+            32, ALPHA, RATIO, scale_raw=True)
+        for l in range(LAYERS - 1)]
+
+    def step():
+        ops.score(qs[0], keys[0], N, out=raws[0], head0_partial=partials[0])
+        for call in pipe_calls:
+            call()
+        select_layer((LAYERS - 1) % 2)
 
     if args.only == "batch":
         batch_leg(args, hs, ops, torch, stream, dev)
@@ -512,6 +538,18 @@ def main():
     ms_per_step = begin.elapsed_time(end) / args.steps
     st = ops.read_status(status)
     assert st["code"] == 0 and st["k"] == kmax, st
+    last_ids = ids.clone()
+    # the same step one layer at a time (no pipelining), for comparison
+    serial_step()
+    torch.cuda.synchronize()
+    assert torch.equal(ids, last_ids), "pipelined and serial selections differ"
+    sb, se = new_event(), new_event()
+    sb.record(stream)
+    for i in range(args.steps):
+        serial_step()
+    se.record(stream)
+    torch.cuda.synchronize()
+    serial_ms = sb.elapsed_time(se) / args.steps
     # scoring kernel alone: 30*K back-to-back launches over the rotating layers
     sb, se = new_event(), new_event()
     sb.record(stream)
@@ -525,7 +563,8 @@ def main():
     step_bytes = LAYERS * (SCORE_BYTES + 2 * 32 * N * 2 + 4 * 32 * kmax)
     avg_score_us = 1e3 * sum(score_ms) / len(score_ms)
     score_gbs = SCORE_BYTES / (avg_score_us * 1e-6) / 1e9
-    log(f"configs[1]: {ms_per_step:.3f} ms/step ({LAYERS} layers), {keys_per_s/1e9:.2f} G keys/s; "
+    log(f"configs[1]: {ms_per_step:.3f} ms/step pipelined ({serial_ms:.3f} one layer at a time), "
+        f"{LAYERS} layers, {keys_per_s/1e9:.2f} G keys/s; "
         f"score kernel {avg_score_us:.2f} us avg = {score_gbs:.0f} GB/s")
 
     # ---- full sparse layer over 30 hot pools ---------------------
@@ -623,7 +662,11 @@ def main():
             "workload": "configs[1]: score + select, 30 sparse layers per decode step, N=32768",
             "tokens": N, "layers": LAYERS, "query_heads": 32, "kv_heads": 8, "head_dim": 128,
             "alpha": ALPHA, "cap_ratio": RATIO, "k": kmax, "io_dtype": "f16",
+            "schedule": "layer l's selection co-launched with layer l+1's scoring "
+                        "(hs_gqa_select_then_score)",
         },
+        "serial_ms_per_step": serial_ms,
+        "serial_keys_per_s": LAYERS * N / (serial_ms / 1e3),
         "hbm_gbps": step_bytes / (ms_per_step * 1e-3) / 1e9,
         "roofline": {
             "bound": "hbm", "achieved": score_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -43,6 +43,11 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
 int launch_select_batched(const hs_select_job_t* jobs, uint32_t count, uint32_t heads,
                           float alpha, float ratio, uint32_t flags, hipStream_t stream);
 
+int launch_select_then_score(const hs_select_job_t* select_jobs, uint32_t select_count,
+                             uint32_t heads, float alpha, float ratio, uint32_t flags,
+                             const hs_score_job_t* score_jobs, uint32_t score_count,
+                             hipStream_t stream);
+
 size_t attention_workspace_bytes(uint32_t n);
 int launch_attention(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
                      size_t row_bytes, const int32_t* rows, uint32_t pool_rows,

@@ -1,0 +1,182 @@
+// The scoring waves shared by the scoring launch (score.hip) and by the
+// selection launch that scores the next layer alongside (select.hip).  The
+// algorithm, work split and pipeline are described in score.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "hs_device.hpp"
+#include "hs_gpu.h"
+
+namespace hs {
+
+constexpr uint32_t kTileTokens = 64;
+constexpr uint32_t kChunks = 16;  // 16-byte chunks per 128-channel F16 head row
+constexpr uint32_t kHalfTileChunks = kTileTokens * kChunks / 2;  // one wave's LDS region (8 KiB)
+
+__device__ __forceinline__ float lo_half(uint32_t w) { return h2f(w & 0xffffu); }
+__device__ __forceinline__ float hi_half(uint32_t w) { return h2f(w >> 16); }
+
+// One scoring job: a query, its keys and where the scores go.  A launch
+// covers one job or, batched, up to kMaxScoreJobs of them; job j owns the
+// (token tile, KV head) ids [first_id, first_id + tiles_j * 8) of the launch.
+struct ScoreJob {
+    const uint32_t* q32;  // F16 pairs: head h channel c at q32[(h*128 + c)/2]
+    const uint16_t* keys;
+    uint16_t* out;
+    uint32_t* head0_partial;
+    uint32_t stride_words, n, out_stride, first_id;
+};
+constexpr uint32_t kMaxScoreJobs = 16;
+struct ScoreJobs {
+    ScoreJob job[kMaxScoreJobs];
+    uint32_t count, total_ids;
+};
+
+// Checks a batch of score jobs and fills the launch table (score.hip).
+int build_score_jobs(const hs_score_job_t* jobs, uint32_t count, ScoreJobs& out);
+
+// Wave `wave` of `waves` scoring waves takes the (token tile, KV head) ids
+// wave, wave + waves, ... of `jobs`; `region` is its own kHalfTileChunks
+// of LDS.  Waves never wait on one another.
+template <bool kRows, bool kBatch>
+__device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t* __restrict__ rows,
+                                            uint32_t pool_rows, uint32_t wave, uint32_t waves,
+                                            uint4* region) {
+    constexpr uint32_t kHalf = kChunks / 2;  // 16 B chunks of one half row (64 channels)
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t tiles = jobs.total_ids;  // (token tile, KV head) pairs of all jobs
+
+    auto job_of = [&](uint32_t id) -> uint32_t {
+        if (!kBatch) return 0;
+        uint32_t j = 0;
+        for (uint32_t i = 1; i < jobs.count; ++i) j = id >= jobs.job[i].first_id ? i : j;
+        return __builtin_amdgcn_readfirstlane(j);
+    };
+    auto row_of = [&](const ScoreJob& jb, uint32_t id) -> uint32_t {
+        const uint32_t token = ((id - jb.first_id) >> 3) * kTileTokens + lane;
+        if (token >= jb.n) return 0xffffffffu;
+        if (!kRows) return token;
+        const uint32_t r = static_cast<uint32_t>(rows[token]);
+        return r < pool_rows ? r : 0xffffffffu;
+    };
+    // Half h of the tile: instruction j reads chunk 8h + (lane & 7) of token
+    // 8j + (lane >> 3), i.e. 8 whole 128 B lines per instruction.
+    auto load = [&](const ScoreJob& jb, uint32_t id, uint32_t h, uint32_t my_row, uint4 (&v)[kHalf]) {
+        const uint32_t local = id - jb.first_id;
+        const uint16_t* base = jb.keys + (local & 7u) * 128u + h * 64u + (lane & 7u) * 8u;
+        uint32_t r[kHalf];
+#pragma unroll
+        for (uint32_t j = 0; j < kHalf; ++j) {
+            if (kRows) {
+                r[j] = __shfl(my_row, 8 * j + (lane >> 3), 64);
+            } else {
+                const uint32_t t = (local >> 3) * kTileTokens + 8 * j + (lane >> 3);
+                r[j] = t < jb.n ? t : 0xffffffffu;
+            }
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kHalf; ++j) {
+            const bool ok = r[j] != 0xffffffffu;
+            const uint4 x = *reinterpret_cast<const uint4*>(
+                base + static_cast<size_t>(ok ? r[j] : 0u) * jb.stride_words);
+            v[j] = ok ? x : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto hslot = [](uint32_t t, uint32_t c) { return t * kHalf + (c ^ (t & 7u)); };
+    auto stash = [&](const uint4 (&v)[kHalf]) {
+#pragma unroll
+        for (uint32_t j = 0; j < kHalf; ++j) region[hslot(8 * j + (lane >> 3), lane & 7u)] = v[j];
+    };
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    // channels 64h .. 64h+63 of the 4 ordered chains
+    auto compute = [&](const ScoreJob& jb, uint32_t id, uint32_t h) {
+        const uint32_t local = id - jb.first_id;
+        const uint32_t head_kv = local & 7u;  // wave-uniform
+        using ConstU32 = const __attribute__((address_space(4))) uint32_t;
+        // a wave-uniform pointer: the job's query is read with scalar loads
+        const uint64_t qa = reinterpret_cast<uint64_t>(jb.q32);
+        // (readfirstlane returns int: widen each half through uint32_t, or a
+        // low word with bit 31 set would sign-extend over the high word)
+        const uint32_t q_hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(uint32_t(qa >> 32)));
+        const uint32_t q_lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(uint32_t(qa)));
+        const uint64_t qu = (static_cast<uint64_t>(q_hi) << 32) | static_cast<uint64_t>(q_lo);
+        ConstU32* qh = (ConstU32*)(reinterpret_cast<const uint32_t*>(qu)) + head_kv * 4 * 64 + h * 32;
+#pragma unroll
+        for (uint32_t j = 0; j < kHalf; ++j) {
+            const uint4 k4 = region[hslot(lane, j)];
+            const uint32_t kw[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+            for (uint32_t p = 0; p < 4; ++p) {
+                const uint32_t c2 = j * 4 + p;
+                const float klo = lo_half(kw[p]), khi = hi_half(kw[p]);
+                const uint32_t q0 = qh[c2], q1 = qh[64 + c2], q2 = qh[128 + c2], q3 = qh[192 + c2];
+                a0 = __builtin_fmaf(lo_half(q0), klo, a0);
+                a1 = __builtin_fmaf(lo_half(q1), klo, a1);
+                a2 = __builtin_fmaf(lo_half(q2), klo, a2);
+                a3 = __builtin_fmaf(lo_half(q3), klo, a3);
+                a0 = __builtin_fmaf(hi_half(q0), khi, a0);
+                a1 = __builtin_fmaf(hi_half(q1), khi, a1);
+                a2 = __builtin_fmaf(hi_half(q2), khi, a2);
+                a3 = __builtin_fmaf(hi_half(q3), khi, a3);
+            }
+        }
+    };
+    auto finish = [&](const ScoreJob& jb, uint32_t id) {
+        const uint32_t local = id - jb.first_id;
+        const uint32_t head_kv = local & 7u;
+        const uint32_t token = (local >> 3) * kTileTokens + lane;
+        const uint32_t s0 = f2h(a0), s1 = f2h(a1), s2 = f2h(a2), s3 = f2h(a3);
+        if (token < jb.n) {
+            uint16_t* o = jb.out + static_cast<size_t>(head_kv * 4) * jb.out_stride + token;
+            o[0] = static_cast<uint16_t>(s0);
+            o[jb.out_stride] = static_cast<uint16_t>(s1);
+            o[2 * static_cast<size_t>(jb.out_stride)] = static_cast<uint16_t>(s2);
+            o[3 * static_cast<size_t>(jb.out_stride)] = static_cast<uint16_t>(s3);
+        }
+        if (jb.head0_partial != nullptr && head_kv == 0) {
+            const uint32_t best =
+                wave_max_u32(token < jb.n && !is_nan_half(s0) ? order_key(s0) : 0u);
+            if (lane == 0) jb.head0_partial[local >> 3] = best;
+        }
+        a0 = a1 = a2 = a3 = 0.0f;
+    };
+
+    // Pipeline unit: half a tile.  While one half is computed, the next is
+    // in flight; the tile's 4 chains run on across its two halves.
+    uint4 v[kHalf];
+    uint32_t id = wave;
+    if (id >= tiles) return;
+    ScoreJob cur = jobs.job[job_of(id)];
+    uint32_t row = row_of(cur, id);
+    load(cur, id, 0, row, v);
+    while (true) {
+        stash(v);
+        __builtin_amdgcn_wave_barrier();
+        load(cur, id, 1, row, v);
+        compute(cur, id, 0);
+        __builtin_amdgcn_wave_barrier();
+        stash(v);
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t next = id + waves;
+        ScoreJob nxt = cur;
+        uint32_t nrow = 0;
+        if (next < tiles) {
+            nxt = jobs.job[job_of(next)];
+            nrow = row_of(nxt, next);
+            load(nxt, next, 0, nrow, v);
+        }
+        compute(cur, id, 1);
+        finish(cur, id);
+        __builtin_amdgcn_wave_barrier();
+        if (next >= tiles) break;
+        id = next;
+        cur = nxt;
+        row = nrow;
+    }
+}
+
+
+}  // namespace hs

@@ -46,6 +46,7 @@
 
 #include "hs_device.hpp"
 #include "hs_internal.hpp"
+#include "score_tile.hpp"
 
 namespace hs {
 namespace {
@@ -967,19 +968,34 @@ static_assert(kHeadMaxN / 64 <= kHThreads, "one head-0 tile maximum per thread")
 static_assert(kMaxHeads * (kHeadMaxN / kSlice) <= kHThreads, "one slice count per thread");
 static_assert(kSortRange % kHThreads == 0, "whole key bins per thread");
 
+// LDS of one per-head workgroup.
 template <bool kRankOrder>
-__global__ void __launch_bounds__(kHThreads) head_select_kernel(const SelectJobs js) {
-    __shared__ uint32_t hist[2][256];
-    __shared__ uint32_t head_count[kMaxHeads], head_bad[kMaxHeads];
-    __shared__ uint32_t tmp[kHWaves];
-    __shared__ uint32_t sh[8];
-    __shared__ uint32_t sort_lds[kRankOrder ? 2 * kHeadMaxK : 1];
-    __shared__ uint32_t tables[kRankOrder ? 2 * kSortRange : 1];
-    __shared__ uint32_t whist[kRankOrder ? kHWaves : 1][256];
+struct HeadSelectLds {
+    uint32_t hist[2][256];
+    uint32_t head_count[kMaxHeads], head_bad[kMaxHeads];
+    uint32_t tmp[kHWaves];
+    uint32_t sh[8];
+    uint32_t sort_lds[kRankOrder ? 2 * kHeadMaxK : 1];
+    uint32_t tables[kRankOrder ? 2 * kSortRange : 1];
+    uint32_t whist[kRankOrder ? kHWaves : 1][256];
+};
+
+// The selection of head h of job `job` by one kHThreads workgroup.
+template <bool kRankOrder>
+__device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, uint32_t job,
+                                            HeadSelectLds<kRankOrder>& lds) {
+    auto& hist = lds.hist;
+    auto& head_count = lds.head_count;
+    auto& head_bad = lds.head_bad;
+    auto& tmp = lds.tmp;
+    auto& sh = lds.sh;
+    auto& sort_lds = lds.sort_lds;
+    auto& tables = lds.tables;
+    auto& whist = lds.whist;
     enum { kCode, kK, kBucket, kAbove, kBucket2, kAbove2, kFlag };
-    const SelectArgs a = job_args(js, blockIdx.y);
+    const SelectArgs a = job_args(js, job);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t h = blockIdx.x, S = a.S, n = a.n, groups = a.heads * S;
+    const uint32_t S = a.S, n = a.n, groups = a.heads * S;
     const uint32_t begin = tid * kHRun, words = (n + 31) / 32;
 
     // every global read is issued up front: head-0 tile maxima, all slice
@@ -1216,6 +1232,38 @@ __global__ void __launch_bounds__(kHThreads) head_select_kernel(const SelectJobs
     }
 }
 
+template <bool kRankOrder>
+__global__ void __launch_bounds__(kHThreads) head_select_kernel(const SelectJobs js) {
+    __shared__ HeadSelectLds<kRankOrder> lds;
+    head_select<kRankOrder>(js, blockIdx.x, blockIdx.y, lds);
+}
+
+// One layer's per-head selection and the next layer's scoring in one launch
+// (the early history preparation of runtime/gqa_executor.cpp:291-295 and
+// policy/full_gqa_runtime.cpp:493-496, where the next layer's history is
+// scored while the current layer goes on).  The first heads x jobs
+// workgroups each select one head; the others run scoring waves, 16 per
+// workgroup with 8 KiB of LDS each, on the CUs the selection leaves idle.
+// Every workgroup takes one CU (its LDS), so the selecting workgroups are
+// placed first and the scoring cannot crowd them out.
+template <bool kRankOrder, bool kBatch>
+__global__ void __launch_bounds__(kHThreads)
+select_score_kernel(const SelectJobs js, const ScoreJobs sj) {
+    __shared__ union {
+        HeadSelectLds<kRankOrder> select;
+        uint4 score[kHWaves][kHalfTileChunks];
+    } lds;
+    const uint32_t selectors = js.heads * js.count;
+    if (blockIdx.x < selectors) {
+        head_select<kRankOrder>(js, blockIdx.x % js.heads, blockIdx.x / js.heads, lds.select);
+        return;
+    }
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    score_waves<false, kBatch>(sj, nullptr, 0u,
+                               __builtin_amdgcn_readfirstlane((blockIdx.x - selectors) * kHWaves + w),
+                               (gridDim.x - selectors) * kHWaves, lds.score[w]);
+}
+
 // ---- 4. rank ----------------------------------------------------------------
 // Number of keys >= v (strict: > v) in each of four lists sorted by
 // descending key, searched in lockstep: fixed steps, and every probe reads
@@ -1445,19 +1493,36 @@ bool per_head_path(uint32_t n, float ratio, uint32_t flags) {
            ((flags & HS_SELECT_ID_ORDER) || kmax_of(n, ratio, flags) <= kHeadMaxK);
 }
 
+// What the launches of a batch need to know about its jobs.
+struct BatchShape {
+    uint32_t max_partials = 0, max_groups = 0;
+    bool any_own_partial = false, all_per_head = true;
+};
+BatchShape batch_shape(const SelectJobs& js) {
+    BatchShape b;
+    for (uint32_t j = 0; j < js.count; ++j) {
+        const SelectPlan p = plan_select(js.heads, js.job[j].n, kmax_of(js.job[j].n, js.ratio, js.flags));
+        b.max_partials = std::max(b.max_partials, p.partials);
+        b.max_groups = std::max(b.max_groups, p.groups);
+        b.any_own_partial |= js.job[j].partial == nullptr;
+        b.all_per_head &= per_head_path(js.job[j].n, js.ratio, js.flags);
+    }
+    return b;
+}
+
+// The head-0 maxima (jobs without the scorer's) and the count launch.
+void launch_counts(const SelectJobs& js, const BatchShape& b, hipStream_t stream) {
+    if (b.any_own_partial)
+        hipLaunchKernelGGL(head0_max_kernel, dim3((b.max_partials + 3) / 4, js.count), dim3(256), 0,
+                           stream, js);
+    hipLaunchKernelGGL(count_kernel, dim3(b.max_groups, js.count), dim3(kThreads), 0, stream, js);
+}
+
 // Launches for the checked jobs of `js`.  Batches whose jobs all take the
 // per-head path run as one launch per phase; otherwise each job runs alone.
 int launch_jobs(const SelectJobs& js, hipStream_t stream) {
-    uint32_t max_partials = 0, max_groups = 0;
-    bool any_own_partial = false, all_per_head = true;
-    for (uint32_t j = 0; j < js.count; ++j) {
-        const SelectPlan p = plan_select(js.heads, js.job[j].n, kmax_of(js.job[j].n, js.ratio, js.flags));
-        max_partials = std::max(max_partials, p.partials);
-        max_groups = std::max(max_groups, p.groups);
-        any_own_partial |= js.job[j].partial == nullptr;
-        all_per_head &= per_head_path(js.job[j].n, js.ratio, js.flags);
-    }
-    if (!all_per_head && js.count > 1) {
+    const BatchShape b = batch_shape(js);
+    if (!b.all_per_head && js.count > 1) {
         for (uint32_t j = 0; j < js.count; ++j) {
             SelectJobs one = js;
             one.count = 1;
@@ -1467,12 +1532,9 @@ int launch_jobs(const SelectJobs& js, hipStream_t stream) {
         }
         return HS_OK;
     }
-    if (any_own_partial)
-        hipLaunchKernelGGL(head0_max_kernel, dim3((max_partials + 3) / 4, js.count), dim3(256), 0,
-                           stream, js);
-    hipLaunchKernelGGL(count_kernel, dim3(max_groups, js.count), dim3(kThreads), 0, stream, js);
+    launch_counts(js, b, stream);
     const bool id_order = (js.flags & HS_SELECT_ID_ORDER) != 0;
-    if (all_per_head) {
+    if (b.all_per_head) {
         // one workgroup per (head, job) finishes the selection
         if (id_order)
             hipLaunchKernelGGL(head_select_kernel<false>, dim3(js.heads, js.count), dim3(kHThreads),
@@ -1483,7 +1545,7 @@ int launch_jobs(const SelectJobs& js, hipStream_t stream) {
     } else {
         // one large job: the slice launch chain
         const SelectArgs args = job_args(js, 0);
-        const dim3 grid(max_groups), block(kThreads);
+        const dim3 grid(b.max_groups), block(kThreads);
         hipLaunchKernelGGL(plan_kernel, grid, block, 0, stream, args);
         if (id_order) {
             hipLaunchKernelGGL(slice_select_kernel<false>, grid, block, 0, stream, args);
@@ -1498,6 +1560,79 @@ int launch_jobs(const SelectJobs& js, hipStream_t stream) {
     }
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "select launch");
+}
+
+// Checked selection jobs of a batch call.
+int build_select_jobs(const hs_select_job_t* jobs, uint32_t count, uint32_t heads, float alpha,
+                      float ratio, uint32_t flags, SelectJobs& js) {
+    if (!jobs || count == 0 || count > kMaxBatch) return reject("select batch: 1..16 jobs");
+    int rc = check_common(heads, alpha, ratio, flags);
+    if (rc != HS_OK) return rc;
+    js = SelectJobs{};
+    js.count = count;
+    js.heads = heads;
+    js.flags = flags;
+    js.alpha = alpha;
+    js.ratio = ratio;
+    for (uint32_t j = 0; j < count; ++j) {
+        const hs_select_job_t& q = jobs[j];
+        rc = check_job(q.scores, q.stride, q.n, q.head0_partial, q.ids, q.ids_stride, q.counts,
+                       q.member, q.status, q.workspace, ratio, flags, js.job[j]);
+        if (rc != HS_OK) return rc;
+    }
+    return HS_OK;
+}
+
+// Byte ranges [begin, end) of device buffers; empty for null pointers.
+struct Span {
+    uintptr_t begin, end;
+};
+Span span(const void* p, size_t bytes) {
+    const uintptr_t b = reinterpret_cast<uintptr_t>(p);
+    return p ? Span{b, b + bytes} : Span{0, 0};
+}
+bool overlap(const Span& x, const Span& y) {
+    return x.begin < x.end && y.begin < y.end && x.begin < y.end && y.begin < x.end;
+}
+
+// The scoring of a combined launch runs while the selection runs: nothing it
+// writes may be read or written by the selection, and nothing it reads
+// written by the selection.
+int check_disjoint(const hs_select_job_t* sel, uint32_t scount, uint32_t heads, float ratio,
+                   uint32_t flags, const hs_score_job_t* sco, uint32_t tcount) {
+    for (uint32_t i = 0; i < scount; ++i) {
+        const hs_select_job_t& s = sel[i];
+        const size_t words = (size_t(s.n) + 31) / 32;
+        const Span reads[] = {
+            span(s.scores, size_t(heads) * s.stride * sizeof(uint16_t)),
+            span(s.head0_partial, (size_t(s.n) + 63) / 64 * sizeof(uint32_t))};
+        const Span writes[] = {
+            span(s.ids, size_t(heads) * s.ids_stride * sizeof(uint32_t)),
+            span(s.counts, size_t(heads) * sizeof(uint32_t)),
+            span(s.member, size_t(heads) * words * sizeof(uint32_t)),
+            span(s.status, sizeof(hs_status_t)),
+            span(s.workspace, plan_select(heads, s.n, kmax_of(s.n, ratio, flags)).total)};
+        for (uint32_t j = 0; j < tcount; ++j) {
+            const hs_score_job_t& t = sco[j];
+            const Span out[] = {
+                span(t.scores, size_t(32) * t.score_stride * sizeof(uint16_t)),
+                span(t.head0_partial, (size_t(t.tokens) + 63) / 64 * sizeof(uint32_t))};
+            const Span in[] = {
+                span(t.q, size_t(32) * 128 * sizeof(uint16_t)),
+                span(t.keys, (size_t(t.tokens) - 1) * t.key_stride_words * sizeof(uint16_t) +
+                                 8 * 128 * sizeof(uint16_t))};
+            for (const Span& o : out) {
+                for (const Span& r : reads)
+                    if (overlap(o, r)) return reject("select-then-score: scores written over a selection input");
+                for (const Span& w : writes)
+                    if (overlap(o, w)) return reject("select-then-score: scores written over a selection output");
+            }
+            for (const Span& r : in)
+                for (const Span& w : writes)
+                    if (overlap(r, w)) return reject("select-then-score: scoring input overlaps a selection output");
+        }
+    }
+    return HS_OK;
 }
 
 }  // namespace
@@ -1522,22 +1657,52 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
 
 int launch_select_batched(const hs_select_job_t* jobs, uint32_t count, uint32_t heads,
                           float alpha, float ratio, uint32_t flags, hipStream_t stream) {
-    if (!jobs || count == 0 || count > kMaxBatch) return reject("select batch: 1..16 jobs");
-    int rc = check_common(heads, alpha, ratio, flags);
+    SelectJobs js;
+    const int rc = build_select_jobs(jobs, count, heads, alpha, ratio, flags, js);
     if (rc != HS_OK) return rc;
-    SelectJobs js{};
-    js.count = count;
-    js.heads = heads;
-    js.flags = flags;
-    js.alpha = alpha;
-    js.ratio = ratio;
-    for (uint32_t j = 0; j < count; ++j) {
-        const hs_select_job_t& q = jobs[j];
-        rc = check_job(q.scores, q.stride, q.n, q.head0_partial, q.ids, q.ids_stride, q.counts,
-                       q.member, q.status, q.workspace, ratio, flags, js.job[j]);
-        if (rc != HS_OK) return rc;
-    }
     return launch_jobs(js, stream);
+}
+
+int launch_select_then_score(const hs_select_job_t* select_jobs, uint32_t select_count,
+                             uint32_t heads, float alpha, float ratio, uint32_t flags,
+                             const hs_score_job_t* score_jobs, uint32_t score_count,
+                             hipStream_t stream) {
+    SelectJobs js;
+    int rc = build_select_jobs(select_jobs, select_count, heads, alpha, ratio, flags, js);
+    if (rc != HS_OK) return rc;
+    ScoreJobs sj;
+    rc = build_score_jobs(score_jobs, score_count, sj);
+    if (rc != HS_OK) return rc;
+    rc = check_disjoint(select_jobs, select_count, heads, ratio, flags, score_jobs, score_count);
+    if (rc != HS_OK) return rc;
+    const BatchShape b = batch_shape(js);
+    if (!b.all_per_head) {  // the slice chain: the two calls in turn
+        rc = launch_jobs(js, stream);
+        return rc != HS_OK ? rc : launch_score_batched(score_jobs, score_count, stream);
+    }
+    launch_counts(js, b, stream);
+    // Scoring workgroups: as few rounds of tiles per wave as the CUs left
+    // free allow, and the tiles spread evenly over the waves, so no wave
+    // holds a round more than the others (at N = 32768 beside 32 selecting
+    // heads: 128 workgroups, 2 tiles per wave).  Fewer scoring waves also
+    // leave the latency-bound selection more of the memory system.
+    const uint32_t selectors = js.heads * js.count;
+    const uint32_t cus = static_cast<uint32_t>(device_cu_count());
+    const uint32_t free_cus = selectors < cus ? cus - selectors : cus;
+    const uint32_t rounds = (sj.total_ids + free_cus * kHWaves - 1) / (free_cus * kHWaves);
+    const uint32_t scorers = std::max(1u, (sj.total_ids + rounds * kHWaves - 1) / (rounds * kHWaves));
+    const dim3 grid(selectors + scorers), block(kHThreads);
+    const bool id_order = (js.flags & HS_SELECT_ID_ORDER) != 0, batch = sj.count > 1;
+    if (id_order && batch)
+        hipLaunchKernelGGL((select_score_kernel<false, true>), grid, block, 0, stream, js, sj);
+    else if (id_order)
+        hipLaunchKernelGGL((select_score_kernel<false, false>), grid, block, 0, stream, js, sj);
+    else if (batch)
+        hipLaunchKernelGGL((select_score_kernel<true, true>), grid, block, 0, stream, js, sj);
+    else
+        hipLaunchKernelGGL((select_score_kernel<true, false>), grid, block, 0, stream, js, sj);
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hip_fail(st, "select-then-score launch");
 }
 
 }  // namespace hs
@@ -1564,6 +1729,15 @@ int hs_gqa_select_batched(const hs_select_job_t* jobs, uint32_t count, uint32_t 
     hs::clear_error();
     return hs::launch_select_batched(jobs, count, heads, alpha, ratio, flags,
                                      hs::as_stream(stream));
+}
+
+int hs_gqa_select_then_score(const hs_select_job_t* select_jobs, uint32_t select_count,
+                             uint32_t heads, float alpha, float ratio, uint32_t flags,
+                             const hs_score_job_t* score_jobs, uint32_t score_count,
+                             void* stream) {
+    hs::clear_error();
+    return hs::launch_select_then_score(select_jobs, select_count, heads, alpha, ratio, flags,
+                                        score_jobs, score_count, hs::as_stream(stream));
 }
 
 }  // extern "C"

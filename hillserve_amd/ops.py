@@ -171,6 +171,59 @@ def select_batched(jobs, heads, alpha, ratio, *, scale_raw=False, fp32_counts=Fa
     return [r[:4] for r in results]
 
 
+def prepare_select_then_score(select_jobs, score_jobs, heads, alpha, ratio, *, scale_raw=False,
+                              fp32_counts=False, require_k=False, id_order=False, cover=False,
+                              stream=None):
+    """Bind hs_gqa_select_then_score to fixed buffers: returns a callable
+    that enqueues the call (on `stream`, default the current stream at bind
+    time) with job tables built once.  For a decode loop that reuses its
+    buffers every step.
+
+    select_jobs: dicts with scores, n and the caller's ids, status and ws
+    (optional stride, head0_partial, counts, member, ids_stride);
+    score_jobs: as score_batched, each with its own out (which must not
+    overlap any selection buffer)."""
+    from . import ScoreJob, SelectJob
+    stable = (SelectJob * max(1, len(select_jobs)))()
+    for i, j in enumerate(select_jobs):
+        _need_cuda(j["scores"], j["ids"], j["status"], j["ws"])
+        n = int(j["n"])
+        stride = int(j.get("stride") or j["scores"].shape[-1])
+        ids_stride = int(j.get("ids_stride") or j["ids"].shape[-1])
+        stable[i] = SelectJob(_p(j["scores"]), _p(j.get("head0_partial")), _p(j["ids"]),
+                              _p(j.get("counts")), _p(j.get("member")), _p(j["status"]),
+                              _p(j["ws"]), stride, n, ids_stride, 0)
+    ttable = (ScoreJob * max(1, len(score_jobs)))()
+    for i, j in enumerate(score_jobs):
+        _need_cuda(j["q16"], j["keys"], j["out"])
+        tokens = int(j["tokens"])
+        ttable[i] = ScoreJob(_p(j["q16"]), _p(j["keys"]), _p(j["out"]), _p(j.get("head0_partial")),
+                             int(j.get("key_stride_words", 1024)), tokens,
+                             int(j.get("score_stride") or tokens), 0)
+    flags = ((HS_SELECT_SCALE_RAW if scale_raw else 0) | (HS_SELECT_FP32_COUNTS if fp32_counts else 0)
+             | (HS_SELECT_REQUIRE_K if require_k else 0) | (HS_SELECT_ID_ORDER if id_order else 0)
+             | (HS_SELECT_COVER if cover else 0))
+    fn = lib().hs_gqa_select_then_score
+    sp, tp, st = ctypes.cast(stable, ctypes.c_void_p), ctypes.cast(ttable, ctypes.c_void_p), _s(stream)
+    ns, nt = len(select_jobs), len(score_jobs)
+    keep = (select_jobs, score_jobs, stable, ttable)  # the tensors and tables outlive the callable
+
+    def call():
+        check(fn(sp, ns, heads, alpha, ratio, flags, tp, nt, st))
+        return keep
+
+    return call
+
+
+def select_then_score(select_jobs, score_jobs, heads, alpha, ratio, stream=None, **flags):
+    """One layer's selections and the next layer's scoring in one call
+    (hs_gqa_select_then_score): the scoring runs on the CUs the per-head
+    selection leaves idle.  Outputs equal select_batched then score_batched;
+    arguments as prepare_select_then_score."""
+    prepare_select_then_score(select_jobs, score_jobs, heads, alpha, ratio, stream=stream,
+                              **flags)()
+
+
 def rehearsal_query(hidden, wq, positions, eps=1e-5, theta=500000.0, out=None, status=True,
                     stream=None):
     """Rehearsal query of a batch (<= 16 sequences) on MFMA.

@@ -161,6 +161,23 @@ typedef struct {
 int hs_gqa_select_batched(const hs_select_job_t *jobs, uint32_t count, uint32_t heads,
                           float alpha, float ratio, uint32_t flags, void *stream);
 
+/* Layer pipelining: the selection of one layer (select_jobs, as
+ * hs_gqa_select_batched) and the scoring of the next layer (score_jobs, as
+ * hs_gqa_score_batched) in one call, the next layer's history scored while
+ * this layer's selection finishes (the early history preparation of
+ * runtime/gqa_executor.cpp:291-295 and policy/full_gqa_runtime.cpp:493-496,
+ * whose next-layer query comes from the rehearsal query).  After the
+ * selection's count launch, its per-head workgroups and the scoring waves
+ * share one launch, so the scoring runs on the CUs the selection leaves
+ * idle.  The score jobs' scores and tile maxima must not overlap any buffer
+ * of the selection jobs, nor their queries and keys a selection output
+ * (HS_ERR_ARGUMENT otherwise).  Every output equals that of the two calls
+ * made in turn; jobs off the per-head path run as those two calls. */
+int hs_gqa_select_then_score(const hs_select_job_t *select_jobs, uint32_t select_count,
+                             uint32_t heads, float alpha, float ratio, uint32_t flags,
+                             const hs_score_job_t *score_jobs, uint32_t score_count,
+                             void *stream);
+
 /* Rehearsal query (patches/llama-b6000-early-rehearsal.patch:17-27, then
  * query_f16 of policy/full_gqa_runtime.cpp:61-64) for up to 16 sequences:
  *   q_b = F16_RNE(RoPE(Wq . (hidden_b / sqrt(mean(hidden_b^2) + eps)), pos_b))

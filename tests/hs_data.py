@@ -119,3 +119,25 @@ def markers_v3(n: int, g: np.random.Generator):
     k[last + 2] = 0x6C00
     k[last + 3] = (0x8000 | (t + 1)).astype(np.uint16)
     return q, k
+
+
+def make_jobs(hs, ns, seed):
+    """Device scoring jobs: a Gaussian query and RoPE-structured keys of n
+    tokens each, with a head-0 tile-maximum buffer."""
+    import torch
+    jobs = []
+    for i, n in enumerate(ns):
+        q = torch.empty(4096, dtype=torch.float16, device="cuda")
+        k = torch.empty(n * 1024, dtype=torch.float16, device="cuda")
+        hs.ops.fill_gaussian(q, seed=seed + 2 * i)
+        hs.ops.fill_rope_keys(k, n, 1024, 8, seed=seed + 2 * i + 1, theta=500000.0)
+        jobs.append(dict(q16=q, keys=k, tokens=n,
+                         head0_partial=torch.empty((n + 63) // 64, dtype=torch.int32,
+                                                   device="cuda")))
+    return jobs
+
+
+def batch_ns(seed, count=16):
+    """Sequence lengths of a batch: multiples of 64 in 8192..32768."""
+    g = rng(seed)
+    return [int(x) * 64 for x in g.integers(8192 // 64, 32768 // 64 + 1, size=count)]

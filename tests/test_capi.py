@@ -120,3 +120,39 @@ def test_cpp_contracts_binary_links():
         pytest.skip("GPU visible: the contract run itself is a gpu test")
     proc = subprocess.run([str(CONTRACTS)], capture_output=True, text=True, timeout=60)
     assert proc.returncode == 77 and "skipped" in proc.stdout, proc.stdout + proc.stderr
+
+
+def test_select_then_score_rejects_overlap(hs):
+    # The scoring of the next layer runs beside the selection: its scores may
+    # not land on the selection's scores, and nothing may alias a selection
+    # output.  Every check is on the host, before any launch.
+    L = hs.lib()
+    MB = 1 << 20
+    base = 0x10000000
+
+    def sel(scores, ids, status, ws):
+        return hs.SelectJob(scores, None, ids, None, None, status, ws, 4096, 4096, 819, 0)
+
+    def sco(q, keys, out):
+        return hs.ScoreJob(q, keys, out, None, 1024, 4096, 4096, 0)
+
+    scores, ids, status, ws = base, base + MB, base + 2 * MB, base + 3 * MB
+    q, keys, out = base + 8 * MB, base + 16 * MB, base + 32 * MB
+
+    def call(s, t):
+        st = (hs.SelectJob * 1)(s)
+        tt = (hs.ScoreJob * 1)(t)
+        return L.hs_gqa_select_then_score(ctypes.cast(st, ctypes.c_void_p), 1, 32, 5.0, 0.2, 0,
+                                          ctypes.cast(tt, ctypes.c_void_p), 1, None)
+
+    assert call(sel(scores, ids, status, ws), sco(q, keys, scores + 4096)) == hs.HS_ERR_ARGUMENT
+    assert "selection input" in hs.last_error()
+    assert call(sel(scores, ids, status, ws), sco(q, keys, ws)) == hs.HS_ERR_ARGUMENT
+    assert "selection output" in hs.last_error()
+    assert call(sel(scores, ids, status, ws), sco(ids, keys, out)) == hs.HS_ERR_ARGUMENT
+    assert "scoring input" in hs.last_error()
+    # the usual shape checks of both halves still apply
+    assert call(sel(scores, ids, status, ws), sco(q, keys + 8, out)) == hs.HS_ERR_ARGUMENT
+    bad = sel(scores, ids, status, ws)
+    bad.ids_stride = 10
+    assert call(bad, sco(q, keys, out)) == hs.HS_ERR_ARGUMENT

@@ -6,27 +6,9 @@ import numpy as np
 import pytest
 import torch
 
-from hs_data import from_dev, rng, v3_sample
+from hs_data import batch_ns, from_dev, make_jobs, rng, v3_sample
 
 pytestmark = pytest.mark.gpu
-
-
-def make_jobs(hs, ns, seed):
-    jobs = []
-    for i, n in enumerate(ns):
-        q = torch.empty(4096, dtype=torch.float16, device="cuda")
-        k = torch.empty(n * 1024, dtype=torch.float16, device="cuda")
-        hs.ops.fill_gaussian(q, seed=seed + 2 * i)
-        hs.ops.fill_rope_keys(k, n, 1024, 8, seed=seed + 2 * i + 1, theta=500000.0)
-        jobs.append(dict(q16=q, keys=k, tokens=n,
-                         head0_partial=torch.empty((n + 63) // 64, dtype=torch.int32,
-                                                   device="cuda")))
-    return jobs
-
-
-def batch_ns(seed, count=16):
-    g = rng(seed)
-    return [int(x) * 64 for x in g.integers(8192 // 64, 32768 // 64 + 1, size=count)]
 
 
 def test_batched_scores_match_single_calls(hs):
