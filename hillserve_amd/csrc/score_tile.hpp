@@ -40,8 +40,11 @@ int build_score_jobs(const hs_score_job_t* jobs, uint32_t count, ScoreJobs& out)
 
 // Wave `wave` of `waves` scoring waves takes the (token tile, KV head) ids
 // wave, wave + waves, ... of `jobs`; `region` is its own kHalfTileChunks
-// of LDS.  Waves never wait on one another.
-template <bool kRows, bool kBatch>
+// of LDS.  Waves never wait on one another.  kAhead: both halves of a tile
+// are requested before the first is used (32 more VGPRs), so a tile costs
+// one memory round trip instead of two; otherwise the second half is
+// requested once the first is parked in LDS.
+template <bool kRows, bool kBatch, bool kAhead>
 __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t* __restrict__ rows,
                                             uint32_t pool_rows, uint32_t wave, uint32_t waves,
                                             uint4* region) {
@@ -146,19 +149,21 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
 
     // Pipeline unit: half a tile.  While one half is computed, the next is
     // in flight; the tile's 4 chains run on across its two halves.
-    uint4 v[kHalf];
+    uint4 v[kHalf], v2[kAhead ? kHalf : 1];
+    uint4 (&second)[kHalf] = *reinterpret_cast<uint4 (*)[kHalf]>(kAhead ? v2 : v);
     uint32_t id = wave;
     if (id >= tiles) return;
     ScoreJob cur = jobs.job[job_of(id)];
     uint32_t row = row_of(cur, id);
     load(cur, id, 0, row, v);
+    if (kAhead) load(cur, id, 1, row, second);
     while (true) {
         stash(v);
         __builtin_amdgcn_wave_barrier();
-        load(cur, id, 1, row, v);
+        if (!kAhead) load(cur, id, 1, row, second);
         compute(cur, id, 0);
         __builtin_amdgcn_wave_barrier();
-        stash(v);
+        stash(second);
         __builtin_amdgcn_wave_barrier();
         const uint32_t next = id + waves;
         ScoreJob nxt = cur;
@@ -167,6 +172,7 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
             nxt = jobs.job[job_of(next)];
             nrow = row_of(nxt, next);
             load(nxt, next, 0, nrow, v);
+            if (kAhead) load(nxt, next, 1, nrow, second);
         }
         compute(cur, id, 1);
         finish(cur, id);

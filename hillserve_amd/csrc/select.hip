@@ -1259,7 +1259,9 @@ select_score_kernel(const SelectJobs js, const ScoreJobs sj) {
         return;
     }
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    score_waves<false, kBatch>(sj, nullptr, 0u,
+    // one half ahead: both halves ahead took more of the memory system from
+    // the selection and lengthened the launch
+    score_waves<false, kBatch, false>(sj, nullptr, 0u,
                                __builtin_amdgcn_readfirstlane((blockIdx.x - selectors) * kHWaves + w),
                                (gridDim.x - selectors) * kHWaves, lds.score[w]);
 }
