@@ -16,6 +16,11 @@ Also reported on the same line:
                 (N*2112 + 8192) / its average duration, from HIP events
                 bracketing 30*K back-to-back scoring launches (one per layer
                 buffer) right after the timed steps, on the same stream.
+  roofline_pipelined_call
+                the timed step's dominant launches (count + combined
+                select-then-score launch): the next layer's scoring bytes
+                plus this layer's selection bytes / the call's average
+                duration over 29*K back-to-back calls.
   layer_step    configs[2]: one full sparse layer (score over the hot pool ->
                 select at the cap -> sparse attention), microseconds per layer
                 over 30 distinct hot pools held as K and V arrays (and, for
@@ -561,13 +566,32 @@ def main():
     se.record(stream)
     torch.cuda.synchronize()
     score_ms = [sb.elapsed_time(se) / (args.steps * LAYERS)]
+    # the pipelined step's own launches alone: 29*K back-to-back
+    # select-then-score calls (count launch + combined launch), each layer's
+    # selection beside the next layer's scoring
+    torch.cuda.synchronize()
+    ops.score(qs[0], keys[0], N, out=raws[0], head0_partial=partials[0])
+    pb, pe = new_event(), new_event()
+    pb.record(stream)
+    for _ in range(args.steps):
+        for call in pipe_calls:
+            call()
+    pe.record(stream)
+    torch.cuda.synchronize()
+    pipe_call_us = 1e3 * pb.elapsed_time(pe) / (args.steps * len(pipe_calls))
+    st = ops.read_status(status)
+    assert st["code"] == 0 and st["k"] == kmax, st
+    # per call: the next layer's scoring plus this layer's selection
+    pipe_bytes = SCORE_BYTES + 2 * 32 * N * 2 + 4 * 32 * kmax
+    pipe_gbs = pipe_bytes / (pipe_call_us * 1e-6) / 1e9
     keys_per_s = LAYERS * N / (ms_per_step / 1e3)
     step_bytes = LAYERS * (SCORE_BYTES + 2 * 32 * N * 2 + 4 * 32 * kmax)
     avg_score_us = 1e3 * sum(score_ms) / len(score_ms)
     score_gbs = SCORE_BYTES / (avg_score_us * 1e-6) / 1e9
     log(f"configs[1]: {ms_per_step:.3f} ms/step pipelined ({serial_ms:.3f} one layer at a time), "
         f"{LAYERS} layers, {keys_per_s/1e9:.2f} G keys/s; "
-        f"score kernel {avg_score_us:.2f} us avg = {score_gbs:.0f} GB/s")
+        f"score kernel {avg_score_us:.2f} us avg = {score_gbs:.0f} GB/s; "
+        f"select-then-score call {pipe_call_us:.2f} us = {pipe_gbs:.0f} GB/s")
 
     # ---- full sparse layer over 30 hot pools ---------------------
     # The hot pool as a K array and a V array (2048 B rows each, the layout
@@ -715,6 +739,14 @@ def main():
             "traffic_source": TRAFFIC_PROFILE,
             "kernel": "score_kernel", "avg_launch_us": avg_score_us,
             "algorithmic_bytes_per_launch": SCORE_BYTES,
+        },
+        "roofline_pipelined_call": {
+            "bound": "hbm", "achieved": pipe_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": pipe_gbs / HBM_PEAK_GBS, "traffic": None,
+            "kernel": "count_kernel + select_score_kernel (hs_gqa_select_then_score)",
+            "avg_call_us": pipe_call_us, "algorithmic_bytes_per_call": pipe_bytes,
+            "note": "the timed step's dominant launches: one layer's selection (scores read, "
+                    "order keys written and read, ids written) beside the next layer's scoring",
         },
         "layer_step": {
             "workload": "configs[2]: score over hot pool + select at cap + sparse attention",
