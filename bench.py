@@ -27,7 +27,8 @@ Also reported on the same line:
                 comparison, as 4096 B KV records), and its algorithmic HBM
                 rate; us_per_layer_pipelined: the same 30 layers with each
                 layer's selection co-launched with the next layer's scoring
-                (amortized per layer; the outputs must match).
+                and its attention merge with the next layer's selection
+                count (amortized per layer; the outputs must match).
   cpu_baseline  the reference's own CPU path (FullGqaCpuScorer + scaling +
                 select_gqa_scores, compiled from the reference sources into
                 oracle/_ref) on a bounded sample, timed on this host.
@@ -651,32 +652,41 @@ def main():
         pipe_us = None
         if split:
             # The same 30 layers pipelined: layer l's selection shares a launch
-            # with layer l+1's scoring, then layer l's attention.
+            # with layer l+1's scoring, layer l's attention merge one with
+            # layer l+1's selection count.
             last_out = out.clone()
             member_p = torch.empty((32, (N + 31) // 32), dtype=torch.int32, device=dev)
             aws = ops.workspace(ops.attention_workspace_bytes(N), dev)
+            flags = dict(scale_raw=True, require_k=True, id_order=True)
+            jobs = [dict(scores=raws[l % 2], n=N, head0_partial=partials[l % 2], ids=ids,
+                         ids_stride=kmax, counts=counts, member=member_p, status=status, ws=ws)
+                    for l in range(2)]
+            # layer l: its selection (counted after layer 0) beside layer l+1's
+            # scoring, then its attention beside layer l+1's count launch
             calls = [
                 ops.prepare_select_then_score(
-                    [dict(scores=raws[l % 2], n=N, head0_partial=partials[l % 2], ids=ids,
-                          ids_stride=kmax, counts=counts, member=member_p, status=status, ws=ws)],
+                    [jobs[l % 2]],
                     [dict(q16=qs[l + 1], keys=k_pools[l + 1], tokens=N, out=raws[(l + 1) % 2],
                           head0_partial=partials[(l + 1) % 2])],
-                    32, ALPHA, RATIO, scale_raw=True, require_k=True, id_order=True)
+                    32, ALPHA, RATIO, counted=l > 0, **flags)
+                for l in range(LAYERS - 1)]
+            attends = [
+                ops.prepare_attention_then_count(
+                    q32s[l], k_pools[l], N, member_p, [jobs[(l + 1) % 2]], 32, ALPHA, RATIO,
+                    out=out, ws=aws, v_pool=v_pools[l], row_bytes=row_bytes, **flags)
                 for l in range(LAYERS - 1)]
 
             def pipelined_pass():
                 ops.score(qs[0], k_pools[0], N, out=raws[0], head0_partial=partials[0])
-                for layer in range(LAYERS):
-                    if layer + 1 < LAYERS:
-                        calls[layer]()
-                    else:
-                        b = layer % 2
-                        ops.select(raws[b], 32, N, N, ALPHA, RATIO, scale_raw=True, require_k=True,
-                                   id_order=True, head0_partial=partials[b], ids=ids,
-                                   ids_stride=kmax, counts=counts, member=member_p,
-                                   status=status, ws=ws)
-                    ops.sparse_attention(q32s[layer], k_pools[layer], N, member_p, out=out,
-                                         ws=aws, v_pool=v_pools[layer], row_bytes=row_bytes)
+                for layer in range(LAYERS - 1):
+                    calls[layer]()
+                    attends[layer]()
+                last = jobs[(LAYERS - 1) % 2]
+                ops.select(last["scores"], 32, N, N, ALPHA, RATIO, counted=True,
+                           head0_partial=last["head0_partial"], ids=ids, ids_stride=kmax,
+                           counts=counts, member=member_p, status=status, ws=ws, **flags)
+                ops.sparse_attention(q32s[LAYERS - 1], k_pools[LAYERS - 1], N, member_p, out=out,
+                                     ws=aws, v_pool=v_pools[LAYERS - 1], row_bytes=row_bytes)
 
             pipelined_pass()
             torch.cuda.synchronize()

@@ -38,6 +38,7 @@ HS_SELECT_FP32_COUNTS = 2
 HS_SELECT_REQUIRE_K = 4
 HS_SELECT_ID_ORDER = 8
 HS_SELECT_COVER = 16
+HS_SELECT_COUNTED = 32
 
 ERROR_NAMES = {
     HS_ERR_ARGUMENT: "argument",
@@ -120,6 +121,8 @@ SIGNATURES = {
     "hs_gqa_select": (_I, [_P, _U32, _SZ, _U32, _F, _F, _U32, _P, _P, _SZ, _P, _P, _P, _P, _P]),
     "hs_gqa_select_batched": (_I, [_P, _U32, _U32, _F, _F, _U32, _P]),
     "hs_gqa_select_then_score": (_I, [_P, _U32, _U32, _F, _F, _U32, _P, _U32, _P]),
+    "hs_gqa_attention_then_count": (_I, [_P, _P, _P, _SZ, _P, _U32, _P, _U32, _P, _P, _P, _U32,
+                                         _U32, _F, _F, _U32, _P]),
     "hs_rehearsal_workspace_bytes": (_SZ, [_U32]),
     "hs_rehearsal_query": (_I, [_P, _P, _P, _U32, _F, _F, _P, _P, _P, _P]),
     "hs_kv_store_bytes": (_U64, [_U32, _U32]),

@@ -32,14 +32,15 @@
 #include <cmath>
 
 #include "hs_device.hpp"
+#include "attention_combine.hpp"
 #include "hs_internal.hpp"
 
 namespace hs {
 namespace {
 
-constexpr uint32_t kChunk = 128;   // token ids per workgroup
+constexpr uint32_t kChunk = kAttnChunk;  // token ids per workgroup
 constexpr uint32_t kThreads = 512; // 8 waves: one per KV head
-constexpr uint32_t kRecord = 2 + 128;
+constexpr uint32_t kRecord = kAttnRecord;
 constexpr float kScale = 0.088388347648318440550f;  // 1/sqrt(128)
 
 // Sum over the 16 lanes of a DPP row (one 16-lane group), returned to every
@@ -299,70 +300,10 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
     }
 }
 
-// Merge the per-chunk (m, l, o) records of each query head.  Grid (32 query
-// heads, 4 groups of 32 channels).  Every record value a workgroup needs is
-// requested up front, since none depends on another: the o values of this
-// thread's channel over every 16th chunk, and one chunk's (m, l) per thread.
-// Then the chunk weights exp(m_i - max m) and their l sum, 16 rows of 32
-// threads each summing the weighted o of their chunks, and the 16 partial
-// sums added in LDS.
-constexpr uint32_t kMaxChunks = 65536 / kChunk;
-constexpr uint32_t kCombineThreads = 512;
-constexpr uint32_t kCombineRows = 16;  // chunks r, r + 16, ... per row of 32 threads
-static_assert(kMaxChunks <= kCombineThreads, "one chunk weight per thread");
 __global__ void __launch_bounds__(kCombineThreads)
 attn_combine_kernel(const float* __restrict__ part, uint32_t chunks, float* __restrict__ out) {
-    __shared__ float weight[kMaxChunks];
-    __shared__ float red[8];
-    __shared__ float acc16[kCombineRows][33];
-    const uint32_t h = blockIdx.x, g = h >> 2, j = h & 3u, tid = threadIdx.x;
-    const uint32_t lane = tid & 63u, wave = tid >> 6;
-    const float* recs = part + static_cast<size_t>(g) * chunks * 4 * kRecord + j * kRecord;
-    const uint32_t c = tid & 31u, r = tid >> 5, ch = blockIdx.y * 32 + c;
-    const uint32_t last = chunks - 1;  // reads past the last chunk are clamped to it
-    constexpr uint32_t kFirst = 16;    // o values per thread in the first batch
-    float v[kFirst];
-#pragma unroll
-    for (uint32_t u = 0; u < kFirst; ++u)
-        v[u] = recs[min(r + kCombineRows * u, last) * 4 * kRecord + 2 + ch];
-    const float* mine = recs + min(tid, last) * 4 * kRecord;
-    const float m_rec = mine[0], l_rec = mine[1];
-    const float m = tid < chunks ? m_rec : -INFINITY;
-    const float l = tid < chunks ? l_rec : 0.0f;
-    float top = wave_max_f32(m);
-    if (lane == 0) red[wave] = top;
-    __syncthreads();
-    top = red[0];
-#pragma unroll
-    for (uint32_t w = 1; w < 8; ++w) top = fmaxf(top, red[w]);
-    const float w_self = (m == -INFINITY || top == -INFINITY) ? 0.0f : __expf(m - top);
-    weight[tid] = w_self;
-    __syncthreads();
-    const float lsum = wave_sum_f32(l * w_self);
-    __syncthreads();  // every wave has read red[] before it is reused
-    if (lane == 0) red[wave] = lsum;
-    __syncthreads();
-    float L = 0.0f;
-#pragma unroll
-    for (uint32_t w = 0; w < 8; ++w) L += red[w];
-    float a = 0.0f;
-#pragma unroll
-    for (uint32_t u = 0; u < kFirst; ++u) {
-        const uint32_t i = r + kCombineRows * u;
-        if (i < chunks && weight[i] != 0.0f) a = __builtin_fmaf(v[u], weight[i], a);
-    }
-    for (uint32_t i = r + kCombineRows * kFirst; i < chunks; i += kCombineRows) {  // n > 32768
-        const float x = recs[i * 4 * kRecord + 2 + ch];
-        if (weight[i] != 0.0f) a = __builtin_fmaf(x, weight[i], a);
-    }
-    acc16[r][c] = a;
-    __syncthreads();
-    if (tid < 32) {
-        float sum = 0.0f;
-#pragma unroll
-        for (uint32_t k = 0; k < kCombineRows; ++k) sum += acc16[k][tid];
-        out[h * 128 + ch] = L > 0.0f ? sum / L : 0.0f;
-    }
+    __shared__ CombineLds lds;
+    combine_records(part, chunks, out, blockIdx.x, blockIdx.y, lds);
 }
 
 }  // namespace
@@ -372,10 +313,10 @@ size_t attention_workspace_bytes(uint32_t n) {
     return align256(sizeof(float) * 8 * chunks * 4 * kRecord);
 }
 
-int launch_attention(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
-                     size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
-                     const uint32_t* member, uint32_t n, float* out, void* workspace,
-                     hipStream_t stream) {
+int launch_attention_partial(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
+                             size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
+                             const uint32_t* member, uint32_t n, float* out, void* workspace,
+                             hipStream_t stream) {
     if (!q || !k_pool || !v_pool || !member || !out || !workspace)
         return reject("attention: null pointer");
     if (n == 0 || n > 65536) return reject("attention: n must be 1..65536");
@@ -394,8 +335,20 @@ int launch_attention(const float* q, const uint8_t* k_pool, const uint8_t* v_poo
         hipLaunchKernelGGL(attn_partial_kernel<false>, dim3(chunks), dim3(kThreads), 0, stream,
                            q, k_pool, static_cast<uint32_t>(row_bytes), v_delta, rows, 0u, member,
                            n, chunks, part);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(32, 4), dim3(kCombineThreads), 0, stream, part, chunks,
-                       out);
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hip_fail(st, "attention launch");
+}
+
+int launch_attention(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
+                     size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
+                     const uint32_t* member, uint32_t n, float* out, void* workspace,
+                     hipStream_t stream) {
+    const int rc = launch_attention_partial(q, k_pool, v_pool, row_bytes, rows, pool_rows, member,
+                                            n, out, workspace, stream);
+    if (rc != HS_OK) return rc;
+    const uint32_t chunks = (n + kChunk - 1) / kChunk;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(32, 4), dim3(kCombineThreads), 0, stream,
+                       static_cast<const float*>(workspace), chunks, out);
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "attention launch");
 }

@@ -43,12 +43,25 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
 int launch_select_batched(const hs_select_job_t* jobs, uint32_t count, uint32_t heads,
                           float alpha, float ratio, uint32_t flags, hipStream_t stream);
 
+int launch_attention_then_count(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
+                                size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
+                                const uint32_t* member, uint32_t n, float* out, void* workspace,
+                                const hs_select_job_t* next_jobs, uint32_t next_count,
+                                uint32_t heads, float alpha, float ratio, uint32_t flags,
+                                hipStream_t stream);
+
 int launch_select_then_score(const hs_select_job_t* select_jobs, uint32_t select_count,
                              uint32_t heads, float alpha, float ratio, uint32_t flags,
                              const hs_score_job_t* score_jobs, uint32_t score_count,
                              hipStream_t stream);
 
 size_t attention_workspace_bytes(uint32_t n);
+// The partial (per-chunk record) launch of the attention alone; its records
+// are merged by combine_records (attention_combine.hpp).
+int launch_attention_partial(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
+                             size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
+                             const uint32_t* member, uint32_t n, float* out, void* workspace,
+                             hipStream_t stream);
 int launch_attention(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
                      size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
                      const uint32_t* member, uint32_t n, float* out, void* workspace,

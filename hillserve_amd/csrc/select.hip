@@ -45,6 +45,7 @@
 #include <cmath>
 
 #include "hs_device.hpp"
+#include "attention_combine.hpp"
 #include "hs_internal.hpp"
 #include "score_tile.hpp"
 
@@ -413,12 +414,18 @@ __device__ __forceinline__ uint32_t partial_max(const SelectArgs& a) {
 }
 
 // ---- 1. count ---------------------------------------------------------------
-__global__ void __launch_bounds__(kThreads) count_kernel(const SelectJobs js) {
-    __shared__ uint32_t whist[kHistWords];
-    __shared__ uint32_t tmp[kWaves];
-    const SelectArgs a = job_args(js, blockIdx.y);
+struct CountLds {
+    uint32_t whist[kHistWords];
+    uint32_t tmp[kWaves];
+};
+
+// Group g (head, slice) of job `job` by one kThreads workgroup.
+__device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, uint32_t job,
+                                            CountLds& lds) {
+    auto& whist = lds.whist;
+    auto& tmp = lds.tmp;
+    const SelectArgs a = job_args(js, job);
     const uint32_t tid = threadIdx.x;
-    const uint32_t g = blockIdx.x;
     if (g >= a.heads * a.S) return;  // a shorter job of the batch
     const uint32_t h = g / a.S, s = g - h * a.S;
     const uint32_t begin = s * kSlice + tid * kRun;
@@ -463,6 +470,11 @@ __global__ void __launch_bounds__(kThreads) count_kernel(const SelectJobs js) {
         if (tid == 0) a.status->boundary_tied_heads = 0;
         if (tid < a.heads) a.g_tie[tid] = 0ull;
     }
+}
+
+__global__ void __launch_bounds__(kThreads) count_kernel(const SelectJobs js) {
+    __shared__ CountLds lds;
+    count_group(js, blockIdx.x, blockIdx.y, lds);
 }
 
 // k from every head's count and nonfinite flag (policy/gqa_policy.cpp:51-63),
@@ -1452,6 +1464,27 @@ __global__ void __launch_bounds__(kThreads) rank_kernel(SelectArgs a) {
     }
 }
 
+// One layer's attention record merge (the first 128 workgroups: 32 query
+// heads x 4 channel groups) and the next layer's selection count (the
+// others: (head, slice) groups x jobs) in one launch; both are short and
+// latency-bound, and neither reads what the other writes.
+__global__ void __launch_bounds__(kThreads)
+combine_count_kernel(const float* __restrict__ part, uint32_t chunks, float* __restrict__ out,
+                     const SelectJobs js, uint32_t groups) {
+    static_assert(kThreads == kCombineThreads, "one workgroup shape for both");
+    __shared__ union {
+        CombineLds combine;
+        CountLds count;
+    } lds;
+    constexpr uint32_t kMergers = 32 * 4;
+    if (blockIdx.x < kMergers) {
+        combine_records(part, chunks, out, blockIdx.x >> 2, blockIdx.x & 3u, lds.combine);
+        return;
+    }
+    const uint32_t b = blockIdx.x - kMergers;
+    count_group(js, b % groups, b / groups, lds.count);
+}
+
 }  // namespace
 
 size_t select_workspace_bytes(uint32_t heads, uint32_t n) { return plan_select(heads, n, n).total; }
@@ -1459,7 +1492,7 @@ size_t select_workspace_bytes(uint32_t heads, uint32_t n) { return plan_select(h
 namespace {
 
 constexpr uint32_t kAllFlags = HS_SELECT_SCALE_RAW | HS_SELECT_FP32_COUNTS | HS_SELECT_REQUIRE_K |
-                               HS_SELECT_ID_ORDER | HS_SELECT_COVER;
+                               HS_SELECT_ID_ORDER | HS_SELECT_COVER | HS_SELECT_COUNTED;
 
 int check_common(uint32_t heads, float alpha, float ratio, uint32_t flags) {
     if (heads == 0 || heads > kMaxHeads) return reject("GQA selector shape: heads must be 1..128");
@@ -1512,8 +1545,10 @@ BatchShape batch_shape(const SelectJobs& js) {
     return b;
 }
 
-// The head-0 maxima (jobs without the scorer's) and the count launch.
+// The head-0 maxima (jobs without the scorer's) and the count launch, unless
+// hs_gqa_attention_then_count ran them (HS_SELECT_COUNTED).
 void launch_counts(const SelectJobs& js, const BatchShape& b, hipStream_t stream) {
+    if (js.flags & HS_SELECT_COUNTED) return;
     if (b.any_own_partial)
         hipLaunchKernelGGL(head0_max_kernel, dim3((b.max_partials + 3) / 4, js.count), dim3(256), 0,
                            stream, js);
@@ -1707,6 +1742,46 @@ int launch_select_then_score(const hs_select_job_t* select_jobs, uint32_t select
     return st == hipSuccess ? HS_OK : hip_fail(st, "select-then-score launch");
 }
 
+int launch_attention_then_count(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
+                                size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
+                                const uint32_t* member, uint32_t n, float* out, void* workspace,
+                                const hs_select_job_t* next_jobs, uint32_t next_count,
+                                uint32_t heads, float alpha, float ratio, uint32_t flags,
+                                hipStream_t stream) {
+    if (flags & HS_SELECT_COUNTED) return reject("attention-then-count: the count is this call's");
+    SelectJobs js;
+    int rc = build_select_jobs(next_jobs, next_count, heads, alpha, ratio, flags, js);
+    if (rc != HS_OK) return rc;
+    // the merge reads the attention records and writes out while the count
+    // reads the next scores and writes its workspace and status
+    const uint32_t chunks = (n + kAttnChunk - 1) / kAttnChunk;
+    const Span merge_in = span(workspace, sizeof(float) * 8 * size_t(chunks) * 4 * kAttnRecord);
+    const Span merge_out = span(out, sizeof(float) * 32 * 128);
+    for (uint32_t j = 0; j < next_count; ++j) {
+        const hs_select_job_t& x = next_jobs[j];
+        const Span count_in[] = {span(x.scores, size_t(heads) * x.stride * sizeof(uint16_t)),
+                                 span(x.head0_partial, (size_t(x.n) + 63) / 64 * sizeof(uint32_t))};
+        const Span count_out[] = {span(x.workspace, plan_select(heads, x.n, kmax_of(x.n, ratio, flags)).total),
+                                  span(x.status, sizeof(hs_status_t))};
+        for (const Span& w : count_out)
+            if (overlap(w, merge_in) || overlap(w, merge_out))
+                return reject("attention-then-count: selection workspace or status overlaps the attention's");
+        for (const Span& r : count_in)
+            if (overlap(r, merge_out)) return reject("attention-then-count: attention output overlaps the next scores");
+    }
+    rc = launch_attention_partial(q, k_pool, v_pool, row_bytes, rows, pool_rows, member, n, out,
+                                  workspace, stream);
+    if (rc != HS_OK) return rc;
+    const BatchShape b = batch_shape(js);
+    if (b.any_own_partial)
+        hipLaunchKernelGGL(head0_max_kernel, dim3((b.max_partials + 3) / 4, js.count), dim3(256), 0,
+                           stream, js);
+    hipLaunchKernelGGL(combine_count_kernel, dim3(32 * 4 + b.max_groups * js.count), dim3(kThreads),
+                       0, stream, static_cast<const float*>(workspace), chunks, out, js, b.max_groups);
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hip_fail(st, "attention-then-count launch");
+}
+
 }  // namespace hs
 
 extern "C" {
@@ -1731,6 +1806,20 @@ int hs_gqa_select_batched(const hs_select_job_t* jobs, uint32_t count, uint32_t 
     hs::clear_error();
     return hs::launch_select_batched(jobs, count, heads, alpha, ratio, flags,
                                      hs::as_stream(stream));
+}
+
+int hs_gqa_attention_then_count(const float* q_dev, const uint8_t* k_pool_dev,
+                                const uint8_t* v_pool_dev, size_t row_bytes,
+                                const int32_t* row_of_id_dev, uint32_t pool_rows,
+                                const uint32_t* member_dev, uint32_t n, float* out_dev,
+                                void* workspace_dev, const hs_select_job_t* next_jobs,
+                                uint32_t next_count, uint32_t heads, float alpha, float ratio,
+                                uint32_t flags, void* stream) {
+    hs::clear_error();
+    return hs::launch_attention_then_count(q_dev, k_pool_dev, v_pool_dev, row_bytes, row_of_id_dev,
+                                           pool_rows, member_dev, n, out_dev, workspace_dev,
+                                           next_jobs, next_count, heads, alpha, ratio, flags,
+                                           hs::as_stream(stream));
 }
 
 int hs_gqa_select_then_score(const hs_select_job_t* select_jobs, uint32_t select_count,

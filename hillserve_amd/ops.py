@@ -12,7 +12,7 @@ import math
 
 import torch
 
-from . import (HS_SELECT_COVER, HS_SELECT_FP32_COUNTS, HS_SELECT_ID_ORDER, HS_SELECT_REQUIRE_K, HS_SELECT_SCALE_RAW, HsError, check,
+from . import (HS_SELECT_COUNTED, HS_SELECT_COVER, HS_SELECT_FP32_COUNTS, HS_SELECT_ID_ORDER, HS_SELECT_REQUIRE_K, HS_SELECT_SCALE_RAW, HsError, check,
                lib)
 
 H, KH, D = 32, 8, 128
@@ -101,19 +101,27 @@ def score_batched(jobs, stream=None):
     return outs
 
 
+def _select_flags(scale_raw, fp32_counts, require_k, id_order, cover, counted=False):
+    return ((HS_SELECT_SCALE_RAW if scale_raw else 0) | (HS_SELECT_FP32_COUNTS if fp32_counts else 0)
+            | (HS_SELECT_REQUIRE_K if require_k else 0) | (HS_SELECT_ID_ORDER if id_order else 0)
+            | (HS_SELECT_COVER if cover else 0) | (HS_SELECT_COUNTED if counted else 0))
+
+
 def select_workspace_bytes(heads, n):
     return lib().hs_gqa_select_workspace_bytes(heads, n)
 
 
 def select(scores, heads, stride, n, alpha, ratio, *, scale_raw=False, fp32_counts=False,
-           require_k=False, id_order=False, cover=False, head0_partial=None, ids=None,
+           require_k=False, id_order=False, cover=False, counted=False, head0_partial=None, ids=None,
            ids_stride=None, counts=None, member=None, status=None, ws=None, stream=None):
     """select_gqa_scores on device.  Returns (ids, counts, member, status).
 
     ids per head are in rank order (key desc, id asc), or ascending id order
     with id_order=True (same set, no rank sort).  cover=True selects the
     history cover of prefetch_payload (policy/full_gqa_runtime.cpp:299-344)
-    over the n historical columns; status["k"] is then the cover bound."""
+    over the n historical columns; status["k"] is then the cover bound.
+    counted=True: the count launch already ran on this ws
+    (attention_then_count)."""
     _need_cuda(scores)
     dev = scores.device
     cols = n + 1 if cover else n
@@ -128,9 +136,7 @@ def select(scores, heads, stride, n, alpha, ratio, *, scale_raw=False, fp32_coun
         status = new_status(dev)
     if ws is None:
         ws = workspace(select_workspace_bytes(heads, n), dev)
-    flags = ((HS_SELECT_SCALE_RAW if scale_raw else 0) | (HS_SELECT_FP32_COUNTS if fp32_counts else 0)
-             | (HS_SELECT_REQUIRE_K if require_k else 0) | (HS_SELECT_ID_ORDER if id_order else 0)
-             | (HS_SELECT_COVER if cover else 0))
+    flags = _select_flags(scale_raw, fp32_counts, require_k, id_order, cover, counted)
     check(lib().hs_gqa_select(_p(scores), heads, stride, n, alpha, ratio, flags,
                               _p(head0_partial), _p(ids), ids_stride, _p(counts), _p(member),
                               _p(status), _p(ws), _s(stream)))
@@ -163,9 +169,7 @@ def select_batched(jobs, heads, alpha, ratio, *, scale_raw=False, fp32_counts=Fa
         results.append((ids, counts, member, status, ws))
         table[i] = SelectJob(_p(scores), _p(j.get("head0_partial")), _p(ids), _p(counts),
                              _p(member), _p(status), _p(ws), stride, n, ids_stride, 0)
-    flags = ((HS_SELECT_SCALE_RAW if scale_raw else 0) | (HS_SELECT_FP32_COUNTS if fp32_counts else 0)
-             | (HS_SELECT_REQUIRE_K if require_k else 0) | (HS_SELECT_ID_ORDER if id_order else 0)
-             | (HS_SELECT_COVER if cover else 0))
+    flags = _select_flags(scale_raw, fp32_counts, require_k, id_order, cover)
     check(lib().hs_gqa_select_batched(ctypes.cast(table, ctypes.c_void_p), len(jobs), heads,
                                       alpha, ratio, flags, _s(stream)))
     return [r[:4] for r in results]
@@ -173,7 +177,7 @@ def select_batched(jobs, heads, alpha, ratio, *, scale_raw=False, fp32_counts=Fa
 
 def prepare_select_then_score(select_jobs, score_jobs, heads, alpha, ratio, *, scale_raw=False,
                               fp32_counts=False, require_k=False, id_order=False, cover=False,
-                              stream=None):
+                              counted=False, stream=None):
     """Bind hs_gqa_select_then_score to fixed buffers: returns a callable
     that enqueues the call (on `stream`, default the current stream at bind
     time) with job tables built once.  For a decode loop that reuses its
@@ -200,9 +204,7 @@ def prepare_select_then_score(select_jobs, score_jobs, heads, alpha, ratio, *, s
         ttable[i] = ScoreJob(_p(j["q16"]), _p(j["keys"]), _p(j["out"]), _p(j.get("head0_partial")),
                              int(j.get("key_stride_words", 1024)), tokens,
                              int(j.get("score_stride") or tokens), 0)
-    flags = ((HS_SELECT_SCALE_RAW if scale_raw else 0) | (HS_SELECT_FP32_COUNTS if fp32_counts else 0)
-             | (HS_SELECT_REQUIRE_K if require_k else 0) | (HS_SELECT_ID_ORDER if id_order else 0)
-             | (HS_SELECT_COVER if cover else 0))
+    flags = _select_flags(scale_raw, fp32_counts, require_k, id_order, cover, counted)
     fn = lib().hs_gqa_select_then_score
     sp, tp, st = ctypes.cast(stable, ctypes.c_void_p), ctypes.cast(ttable, ctypes.c_void_p), _s(stream)
     ns, nt = len(select_jobs), len(score_jobs)
@@ -222,6 +224,39 @@ def select_then_score(select_jobs, score_jobs, heads, alpha, ratio, stream=None,
     arguments as prepare_select_then_score."""
     prepare_select_then_score(select_jobs, score_jobs, heads, alpha, ratio, stream=stream,
                               **flags)()
+
+
+def prepare_attention_then_count(q32, pool, n, member, next_jobs, heads, alpha, ratio, *,
+                                 out, ws, v_pool=None, row_bytes=4096, scale_raw=False,
+                                 fp32_counts=False, require_k=False, id_order=False, cover=False,
+                                 stream=None):
+    """Bind hs_gqa_attention_then_count to fixed buffers (as
+    prepare_select_then_score): this layer's sparse attention, and the count
+    launch of the next layer's selections (next_jobs as in
+    prepare_select_then_score; run them afterwards with counted=True)."""
+    from . import SelectJob
+    _need_cuda(q32, pool, member, out, ws, v_pool)
+    kp, vp, row_bytes, pool_rows = _kv_pool(pool, v_pool, row_bytes)
+    table = (SelectJob * max(1, len(next_jobs)))()
+    for i, j in enumerate(next_jobs):
+        _need_cuda(j["scores"], j["ids"], j["status"], j["ws"])
+        stride = int(j.get("stride") or j["scores"].shape[-1])
+        ids_stride = int(j.get("ids_stride") or j["ids"].shape[-1])
+        table[i] = SelectJob(_p(j["scores"]), _p(j.get("head0_partial")), _p(j["ids"]),
+                             _p(j.get("counts")), _p(j.get("member")), _p(j["status"]),
+                             _p(j["ws"]), stride, int(j["n"]), ids_stride, 0)
+    flags = _select_flags(scale_raw, fp32_counts, require_k, id_order, cover)
+    fn = lib().hs_gqa_attention_then_count
+    args = (_p(q32), kp, vp, row_bytes, None, pool_rows, _p(member), n, _p(out), _p(ws),
+            ctypes.cast(table, ctypes.c_void_p), len(next_jobs), heads, alpha, ratio, flags,
+            _s(stream))
+    keep = (q32, pool, v_pool, member, out, ws, next_jobs, table)
+
+    def call():
+        check(fn(*args))
+        return keep
+
+    return call
 
 
 def rehearsal_query(hidden, wq, positions, eps=1e-5, theta=500000.0, out=None, status=True,

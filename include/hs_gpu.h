@@ -127,13 +127,17 @@ int hs_gqa_score_batched(const hs_score_job_t *jobs, uint32_t count, void *strea
  * One call is 2 launches on `stream` when n <= 32768 (and, in rank
  * order, floor(n*ratio) <= 8192), otherwise 3 (4 in rank order); +1
  * without head0_partial_dev.  Calls sharing a workspace must be ordered on
- * one stream. */
+ * one stream.
+ * HS_SELECT_COUNTED: the first (count) launch of this selection already ran
+ * in hs_gqa_attention_then_count with the same jobs, workspace and flags;
+ * the call runs the rest only. */
 enum {
     HS_SELECT_SCALE_RAW = 1u,
     HS_SELECT_FP32_COUNTS = 2u,
     HS_SELECT_REQUIRE_K = 4u,
     HS_SELECT_ID_ORDER = 8u,
-    HS_SELECT_COVER = 16u
+    HS_SELECT_COVER = 16u,
+    HS_SELECT_COUNTED = 32u
 };
 size_t hs_gqa_select_workspace_bytes(uint32_t heads, uint32_t n);
 int hs_gqa_select(const uint16_t *scores_dev, uint32_t heads, size_t stride,
@@ -304,6 +308,24 @@ int hs_gqa_sparse_attention(const float *q_dev, const uint8_t *k_pool_dev,
                             uint32_t pool_rows, const uint32_t *member_dev,
                             uint32_t n,
                             float *out_dev, void *workspace_dev, void *stream);
+
+/* Layer pipelining, second half: the sparse attention of one layer (as
+ * hs_gqa_sparse_attention, same arguments) and the count launch of the next
+ * layer's selection (next_jobs, heads, alpha, ratio, flags as
+ * hs_gqa_select_batched, whose scores the next layer's scoring has
+ * written).  The attention's record merge and that count share one launch;
+ * the next layer's selection then runs with HS_SELECT_COUNTED (in
+ * hs_gqa_select_then_score or hs_gqa_select).  The attention's output and
+ * workspace must not overlap the selection jobs' scores, tile maxima,
+ * workspace or status (HS_ERR_ARGUMENT).  Outputs equal
+ * hs_gqa_sparse_attention followed by the selection's own count launch. */
+int hs_gqa_attention_then_count(const float *q_dev, const uint8_t *k_pool_dev,
+                                const uint8_t *v_pool_dev, size_t row_bytes,
+                                const int32_t *row_of_id_dev, uint32_t pool_rows,
+                                const uint32_t *member_dev, uint32_t n, float *out_dev,
+                                void *workspace_dev, const hs_select_job_t *next_jobs,
+                                uint32_t next_count, uint32_t heads, float alpha,
+                                float ratio, uint32_t flags, void *stream);
 
 /* ---- fused layer step ----------------------------------------------------
  * One sparse decode layer: score (rehearsal q16 over the hot pool's K rows)

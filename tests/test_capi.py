@@ -58,7 +58,7 @@ def test_select_rejects_bad_parameters(hs):
     assert call(ratio=0.0) == hs.HS_ERR_ARGUMENT
     assert call(ratio=1.5) == hs.HS_ERR_ARGUMENT
     assert call(ids_stride=11) == hs.HS_ERR_ARGUMENT  # floor(64*0.2f) = 12
-    assert call(flags=32) == hs.HS_ERR_ARGUMENT
+    assert call(flags=64) == hs.HS_ERR_ARGUMENT
     assert call(scores=None) == hs.HS_ERR_ARGUMENT
 
 
@@ -156,3 +156,26 @@ def test_select_then_score_rejects_overlap(hs):
     bad = sel(scores, ids, status, ws)
     bad.ids_stride = 10
     assert call(bad, sco(q, keys, out)) == hs.HS_ERR_ARGUMENT
+
+
+def test_attention_then_count_rejects_overlap(hs):
+    L = hs.lib()
+    MB = 1 << 20
+    base = 0x20000000
+    q, kp, vp, member, out, aws = (base + i * 4 * MB for i in range(6))
+    scores, ws, status, ids = (base + 64 * MB + i * 8 * MB for i in range(4))
+
+    def call(job, out_ptr=out, ws_ptr=aws, flags=hs.HS_SELECT_SCALE_RAW):
+        t = (hs.SelectJob * 1)(job)
+        return L.hs_gqa_attention_then_count(q, kp, vp, 2048, None, 0, member, 4096, out_ptr,
+                                             ws_ptr, ctypes.cast(t, ctypes.c_void_p), 1, 32, 5.0,
+                                             0.2, flags, None)
+
+    def job(scores=scores, ws=ws, status=status):
+        return hs.SelectJob(scores, None, ids, None, None, status, ws, 4096, 4096, 819, 0)
+
+    assert call(job(ws=aws)) == hs.HS_ERR_ARGUMENT          # count workspace = attention records
+    assert call(job(status=out)) == hs.HS_ERR_ARGUMENT      # status over the attention output
+    assert call(job(scores=out)) == hs.HS_ERR_ARGUMENT      # next scores under the output
+    assert call(job(), flags=hs.HS_SELECT_SCALE_RAW | hs.HS_SELECT_COUNTED) == hs.HS_ERR_ARGUMENT
+    assert call(job(), out_ptr=0) == hs.HS_ERR_ARGUMENT     # attention shape checks still apply

@@ -138,3 +138,66 @@ def test_select_then_score_small_layers(hs):
     assert torch.equal(out_b.view(torch.int16), want_b.view(torch.int16))
     assert torch.equal(part_b, want_part_b)
     assert_select_equal(hs, job, want)
+
+
+def kv_layers(hs, n, count, seed):
+    """Hot pools as K and V arrays (2048 B rows) with their rehearsal queries."""
+    layers = []
+    for i in range(count):
+        kp = torch.empty(n * 1024, dtype=torch.float16, device="cuda")
+        vp = torch.empty(n * 1024, dtype=torch.float16, device="cuda")
+        q16 = torch.empty(4096, dtype=torch.float16, device="cuda")
+        hs.ops.fill_rope_keys(kp, n, 1024, 8, seed=seed + 3 * i, theta=500000.0)
+        hs.ops.fill_gaussian(vp, seed=seed + 3 * i + 1)
+        hs.ops.fill_gaussian(q16, seed=seed + 3 * i + 2)
+        q32 = torch.randn((32, 128), generator=torch.Generator(device="cuda").manual_seed(seed + i),
+                          device="cuda")
+        layers.append(dict(k=kp, v=vp, q16=q16, q32=q32))
+    return layers
+
+
+@pytest.mark.parametrize("n", [32768, 3000])
+def test_pipelined_layers_equal_one_layer_at_a_time(hs, n):
+    # score 0; per layer: select l (counted after the first) beside score l+1,
+    # then attention l beside the count of l+1; the last layer alone
+    layers = kv_layers(hs, n, 3, 7500 + n)
+    want = []
+    for L in layers:
+        raw = torch.empty((32, n), dtype=torch.float16, device="cuda")
+        part = torch.empty((n + 63) // 64, dtype=torch.int32, device="cuda")
+        hs.ops.score(L["q16"], L["k"], n, out=raw, head0_partial=part)
+        ids, counts, member, st = hs.ops.select(
+            raw, 32, n, n, ALPHA, RATIO, scale_raw=True, require_k=True, id_order=True,
+            head0_partial=part, member=torch.zeros((32, (n + 31) // 32), dtype=torch.int32,
+                                                   device="cuda"))
+        out = hs.ops.sparse_attention(L["q32"], L["k"], n, member, v_pool=L["v"], row_bytes=2048)
+        want.append((ids.clone(), counts.clone(), member.clone(), hs.ops.read_status(st), out.clone()))
+
+    raws = [torch.empty((32, n), dtype=torch.float16, device="cuda") for _ in range(2)]
+    parts = [torch.empty((n + 63) // 64, dtype=torch.int32, device="cuda") for _ in range(2)]
+    aws = hs.ops.workspace(hs.ops.attention_workspace_bytes(n), "cuda")
+    jobs = [select_job(hs, raws[i % 2], n, parts[i % 2]) for i in range(len(layers))]
+    outs = [torch.full((32, 128), float("nan"), device="cuda") for _ in layers]
+    flags = dict(scale_raw=True, require_k=True, id_order=True)
+    hs.ops.score(layers[0]["q16"], layers[0]["k"], n, out=raws[0], head0_partial=parts[0])
+    for i, L in enumerate(layers):
+        if i + 1 < len(layers):
+            nxt = layers[i + 1]
+            hs.ops.select_then_score(
+                [jobs[i]], [dict(q16=nxt["q16"], keys=nxt["k"], tokens=n, out=raws[(i + 1) % 2],
+                                 head0_partial=parts[(i + 1) % 2])],
+                32, ALPHA, RATIO, counted=i > 0, **flags)
+            hs.ops.prepare_attention_then_count(
+                L["q32"], L["k"], n, jobs[i]["member"], [jobs[i + 1]], 32, ALPHA, RATIO,
+                out=outs[i], ws=aws, v_pool=L["v"], row_bytes=2048, **flags)()
+        else:
+            j = jobs[i]
+            hs.ops.select(j["scores"], 32, n, n, ALPHA, RATIO, counted=True,
+                          head0_partial=j["head0_partial"], ids=j["ids"], counts=j["counts"],
+                          member=j["member"], status=j["status"], ws=j["ws"], **flags)
+            hs.ops.sparse_attention(L["q32"], L["k"], n, j["member"], out=outs[i], ws=aws,
+                                    v_pool=L["v"], row_bytes=2048)
+        torch.cuda.synchronize()
+        w_ids, w_counts, w_member, w_status, w_out = want[i]
+        assert_select_equal(hs, jobs[i], (w_ids, w_counts, w_member, w_status))
+        assert torch.equal(outs[i], w_out), i
