@@ -156,8 +156,10 @@ def kv_layers(hs, n, count, seed):
     return layers
 
 
-@pytest.mark.parametrize("n", [32768, 3000])
+@pytest.mark.parametrize("n", [32768, 3000, 40000])
 def test_pipelined_layers_equal_one_layer_at_a_time(hs, n):
+    # (n = 40000 takes the slice launch chain: the counted selection skips
+    # only the count launch there too)
     # score 0; per layer: select l (counted after the first) beside score l+1,
     # then attention l beside the count of l+1; the last layer alone
     layers = kv_layers(hs, n, 3, 7500 + n)
@@ -201,3 +203,38 @@ def test_pipelined_layers_equal_one_layer_at_a_time(hs, n):
         w_ids, w_counts, w_member, w_status, w_out = want[i]
         assert_select_equal(hs, jobs[i], (w_ids, w_counts, w_member, w_status))
         assert torch.equal(outs[i], w_out), i
+
+
+@pytest.mark.parametrize("id_order", [False, True])
+def test_counted_selection_equals_plain(hs, id_order):
+    # the count launch of hs_gqa_attention_then_count feeds a selection run
+    # with HS_SELECT_COUNTED (rank and id order), batched over two next jobs
+    n = 32768
+    layers = kv_layers(hs, n, 1, 7700)
+    nxt = make_jobs(hs, [n, 8192], 7800 + id_order)
+    raws = [scored_layer(hs, j) for j in nxt]
+    wants = [expected_select(hs, select_job(hs, r, j["tokens"], j["head0_partial"]), id_order)
+             for r, j in zip(raws, nxt)]
+    L = layers[0]
+    raw = torch.empty((32, n), dtype=torch.float16, device="cuda")
+    part = torch.empty((n + 63) // 64, dtype=torch.int32, device="cuda")
+    hs.ops.score(L["q16"], L["k"], n, out=raw, head0_partial=part)
+    _, _, member, _ = hs.ops.select(raw, 32, n, n, ALPHA, RATIO, scale_raw=True, id_order=True,
+                                    head0_partial=part,
+                                    member=torch.zeros((32, n // 32), dtype=torch.int32, device="cuda"))
+    want_out = hs.ops.sparse_attention(L["q32"], L["k"], n, member, v_pool=L["v"], row_bytes=2048)
+    jobs = [select_job(hs, r, j["tokens"], j["head0_partial"]) for r, j in zip(raws, nxt)]
+    out = torch.empty((32, 128), device="cuda")
+    aws = hs.ops.workspace(hs.ops.attention_workspace_bytes(n), "cuda")
+    hs.ops.prepare_attention_then_count(L["q32"], L["k"], n, member, jobs, 32, ALPHA, RATIO,
+                                        out=out, ws=aws, v_pool=L["v"], row_bytes=2048,
+                                        scale_raw=True, id_order=id_order)()
+    for j in jobs:
+        hs.ops.select(j["scores"], 32, j["n"], j["n"], ALPHA, RATIO, scale_raw=True,
+                      id_order=id_order, counted=True, head0_partial=j["head0_partial"],
+                      ids=j["ids"], counts=j["counts"], member=j["member"], status=j["status"],
+                      ws=j["ws"])
+    torch.cuda.synchronize()
+    assert torch.equal(out, want_out)
+    for j, w in zip(jobs, wants):
+        assert_select_equal(hs, j, w)
