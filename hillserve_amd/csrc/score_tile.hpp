@@ -38,6 +38,17 @@ struct ScoreJobs {
 // Checks a batch of score jobs and fills the launch table (score.hip).
 int build_score_jobs(const hs_score_job_t* jobs, uint32_t count, ScoreJobs& out);
 
+// The buffer of a tile's second half: its own with kAhead, else the first's.
+template <bool kAhead, size_t kN, size_t kM>
+__device__ __forceinline__ uint4 (&second_half_buffer(uint4 (&first)[kN], uint4 (&own)[kM]))[kN] {
+    if constexpr (kAhead) {
+        static_assert(kM == kN, "a second buffer of the same size");
+        return own;
+    } else {
+        return first;
+    }
+}
+
 // Wave `wave` of `waves` scoring waves takes the (token tile, KV head) ids
 // wave, wave + waves, ... of `jobs`; `region` is its own kHalfTileChunks
 // of LDS.  Waves never wait on one another.  kAhead: both halves of a tile
@@ -150,7 +161,7 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
     // Pipeline unit: half a tile.  While one half is computed, the next is
     // in flight; the tile's 4 chains run on across its two halves.
     uint4 v[kHalf], v2[kAhead ? kHalf : 1];
-    uint4 (&second)[kHalf] = *reinterpret_cast<uint4 (*)[kHalf]>(kAhead ? v2 : v);
+    uint4 (&second)[kHalf] = second_half_buffer<kAhead>(v, v2);  // v2, or v itself
     uint32_t id = wave;
     if (id >= tiles) return;
     ScoreJob cur = jobs.job[job_of(id)];
