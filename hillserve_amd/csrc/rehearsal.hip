@@ -19,12 +19,12 @@
 // rows, B = 16 rows of Wq).  A wave reads its Wq slice one row per
 // instruction (64 lanes x 16 B = 1 KiB contiguous) into a padded LDS tile
 // and takes the MFMA B operands from there: read straight into the MFMA
-// layout, an instruction would cover only 64 B of each of 16 rows.  The 8 partial tiles are added in LDS in a fixed
-// order (deterministic), the RMS scale (sums of squares taken from the same
-// A fragments, so hidden is never rounded again) and RoPE (FP64 angle and
-// rotation) run in the epilogue, and each workgroup records per-sequence
-// nonfinite / overflow flags that rehearsal_status_kernel folds into the
-// status words.
+// layout, an instruction would cover only 64 B of each of 16 rows.  The 8
+// partial tiles are added in LDS in a fixed order (deterministic), the RMS
+// scale (sums of squares taken from the same A fragments, so hidden is never
+// rounded again) and RoPE (FP64 angle and rotation) run in the epilogue, and
+// each workgroup records per-sequence nonfinite / overflow flags that
+// rehearsal_status_kernel folds into the status words.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
