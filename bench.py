@@ -69,7 +69,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bounded CPU-baseline sample duration")
     p.add_argument("--layer-steps", type=int, default=20)
-    p.add_argument("--only", choices=["score", "select", "select_id", "layer", "batch", "tier"],
+    p.add_argument("--only", choices=["score", "select", "select_id", "pipe", "layer", "batch",
+                                      "tier"],
                    default=None,
                    help="profiling aid: run just one kernel family over the 30 layers "
                         "(prints its own timing line, not the benchmark JSON)")
@@ -132,14 +133,17 @@ TRAFFIC_PROFILE = "profiles/score_kernel_hbm_counters.md"
 
 
 
-def pmc_traffic():
-    """HBM bytes per score_kernel launch from the committed rocprofv3
+PIPE_TRAFFIC_PROFILE = "profiles/select_then_score_hbm_counters.md"
+
+
+def pmc_traffic(profile=TRAFFIC_PROFILE, key="traffic_bytes_per_launch"):
+    """HBM bytes per launch (or call) from a committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (copy-calibrated); None if absent."""
     import re
-    path = Path(__file__).resolve().parent / TRAFFIC_PROFILE
+    path = Path(__file__).resolve().parent / profile
     if not path.exists():
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", path.read_text())
+    m = re.search(key + r":\s*(\d+)", path.read_text())
     return int(m.group(1)) if m else None
 
 
@@ -440,9 +444,15 @@ def tier_leg(args, hs, ops, torch, stream, dev):
     return out
 
 
-def profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status, ws, kmax):
-    """Back-to-back launches of one kernel family over the 30 layers."""
+def profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status, ws, kmax,
+                 pipe_calls):
+    """Back-to-back launches of one kernel family over the 30 layers
+    (pipe: the 29 select-then-score calls of the pipelined step)."""
     def run():
+        if args.only == "pipe":
+            for call in pipe_calls:
+                call()
+            return
         for layer in range(LAYERS):
             if args.only == "score":
                 ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
@@ -464,7 +474,7 @@ def profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, 
         run()
     e.record(stream)
     torch.cuda.synchronize()
-    us = 1e3 * b.elapsed_time(e) / (args.steps * LAYERS)
+    us = 1e3 * b.elapsed_time(e) / (args.steps * (len(pipe_calls) if args.only == "pipe" else LAYERS))
     extra = f", {SCORE_BYTES / (us * 1e-6) / 1e9:.0f} GB/s" if args.only == "score" else ""
     print(f"only {args.only}: {us:.2f} us per launch (back to back, {LAYERS} layers x "
           f"{args.steps} steps){extra}", flush=True)
@@ -541,9 +551,9 @@ def main():
     if args.only == "tier":
         tier_leg(args, hs, ops, torch, stream, dev)
         return 0
-    if args.only in ("score", "select", "select_id"):
+    if args.only in ("score", "select", "select_id", "pipe"):
         return profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status,
-                            ws, kmax)
+                            ws, kmax, pipe_calls)
 
     for _ in range(args.warmup):
         step()
@@ -765,7 +775,9 @@ def main():
         },
         "roofline_pipelined_call": {
             "bound": "hbm", "achieved": pipe_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": pipe_gbs / HBM_PEAK_GBS, "traffic": None,
+            "frac": pipe_gbs / HBM_PEAK_GBS,
+            "traffic": pmc_traffic(PIPE_TRAFFIC_PROFILE, "traffic_bytes_per_call"),
+            "traffic_source": PIPE_TRAFFIC_PROFILE,
             "kernel": "count_kernel + select_score_kernel (hs_gqa_select_then_score)",
             "avg_call_us": pipe_call_us, "algorithmic_bytes_per_call": pipe_bytes,
             "note": "the timed step's dominant launches: one layer's selection (scores read, "
