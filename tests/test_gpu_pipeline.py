@@ -238,3 +238,35 @@ def test_counted_selection_equals_plain(hs, id_order):
     assert torch.equal(out, want_out)
     for j, w in zip(jobs, wants):
         assert_select_equal(hs, j, w)
+
+
+def test_select_then_score_history_cover(hs):
+    # the history cover (HS_SELECT_COVER) through the combined launch
+    n = 32767
+    layer_a, layer_b = make_jobs(hs, [n, 4096], 7900)
+    raw_a = scored_layer(hs, layer_a)
+    want_b = scored_layer(hs, dict(layer_b))
+    cover_k = min(n, math.floor((n + 1) * float(np.float32(RATIO))))
+    ids, counts, member, st = hs.ops.select(raw_a, 32, n, n, ALPHA, RATIO, scale_raw=True,
+                                            cover=True, id_order=True,
+                                            head0_partial=layer_a["head0_partial"],
+                                            member=torch.zeros((32, (n + 31) // 32),
+                                                               dtype=torch.int32, device="cuda"))
+    want = hs.ops.read_status(st)
+    job = dict(scores=raw_a, n=n, head0_partial=layer_a["head0_partial"],
+               ids=torch.full((32, cover_k), -1, dtype=torch.int32, device="cuda"),
+               counts=torch.full((32,), -1, dtype=torch.int32, device="cuda"),
+               member=torch.full((32, (n + 31) // 32), -1, dtype=torch.int32, device="cuda"),
+               status=hs.ops.new_status("cuda"),
+               ws=hs.ops.workspace(hs.ops.select_workspace_bytes(32, n), "cuda"))
+    out_b = torch.empty((32, 4096), dtype=torch.float16, device="cuda")
+    hs.ops.select_then_score([job], [dict(q16=layer_b["q16"], keys=layer_b["keys"], tokens=4096,
+                                          out=out_b)],
+                             32, ALPHA, RATIO, scale_raw=True, cover=True, id_order=True)
+    torch.cuda.synchronize()
+    assert hs.ops.read_status(job["status"]) == want
+    k = want["k"]
+    assert torch.equal(job["ids"][:, :k], ids[:, :k])
+    assert torch.equal(job["counts"], counts)
+    assert torch.equal(job["member"], member)
+    assert torch.equal(out_b.view(torch.int16), want_b.view(torch.int16))
