@@ -627,6 +627,119 @@ void cover_contracts() {
     rejects([&] { history_cover_gqa(inf, H, capacity, position, 1.f); }, "nonfinite historical threshold");
 }
 
+// ---- layer pipelining: the combined calls equal the single calls --------------
+template <class T>
+std::vector<T> from_dev(const Dev& d, std::size_t count) {
+    std::vector<T> h(count);
+    if (hipMemcpy(h.data(), d.p, count * sizeof(T), hipMemcpyDeviceToHost) != hipSuccess)
+        throw std::runtime_error("hipMemcpy D2H");
+    return h;
+}
+
+void pipeline_contracts() {
+    constexpr std::uint32_t H = 32, n = 4096;
+    const float alpha = 5.f, ratio = .2f;
+    const std::uint32_t cap = static_cast<std::uint32_t>(std::floor(double(n) * double(ratio)));
+    std::uint64_t state = 0x9e3779b97f4a7c15ull;
+    auto next_half = [&] {  // N(0,1)-ish F16 values from a 64-bit LCG
+        state = state * 6364136223846793005ull + 1442695040888963407ull;
+        const float u = float((state >> 40) & 0xffffff) / 16777216.f;
+        return half_bits((u - 0.5f) * 4.f);
+    };
+    std::vector<std::uint16_t> qa(H * 128), qb(H * 128), ka(std::size_t(n) * 1024), kb(ka.size()),
+        vb(ka.size());
+    for (auto* v : {&qa, &qb, &ka, &kb, &vb})
+        for (auto& x : *v) x = next_half();
+    std::vector<float> q32(H * 128);
+    for (auto& x : q32) x = half_value(next_half());
+    Dev dqa(qa.size() * 2), dqb(qb.size() * 2), dka(ka.size() * 2), dkb(kb.size() * 2),
+        dvb(vb.size() * 2), dq32(q32.size() * 4);
+    to_dev(dqa, qa); to_dev(dqb, qb); to_dev(dka, ka); to_dev(dkb, kb); to_dev(dvb, vb);
+    to_dev(dq32, q32);
+    const std::size_t words = (n + 31) / 32, parts = (n + 63) / 64;
+    Dev raw_a(H * n * 2), part_a(parts * 4), raw_b1(H * n * 2), part_b1(parts * 4), raw_b2(H * n * 2),
+        part_b2(parts * 4);
+    Dev ids1(H * cap * 4), ids2(H * cap * 4), counts1(H * 4), counts2(H * 4), member1(H * words * 4),
+        member2(H * words * 4), st1(sizeof(hs_status_t)), st2(sizeof(hs_status_t)),
+        ws1(hs_gqa_select_workspace_bytes(H, n)), ws2(hs_gqa_select_workspace_bytes(H, n));
+    check(hs_gqa_score(dqa.as<std::uint16_t>(), dka.as<std::uint16_t>(), 1024, nullptr, 0, n,
+                       raw_a.as<std::uint16_t>(), n, part_a.as<std::uint32_t>(), nullptr) == HS_OK,
+          "score layer a");
+    for (std::uint32_t flags : {std::uint32_t(HS_SELECT_SCALE_RAW),
+                                std::uint32_t(HS_SELECT_SCALE_RAW | HS_SELECT_ID_ORDER)}) {
+        // single calls
+        check(hs_gqa_select(raw_a.as<std::uint16_t>(), H, n, n, alpha, ratio, flags,
+                            part_a.as<std::uint32_t>(), ids1.as<std::uint32_t>(), cap,
+                            counts1.as<std::uint32_t>(), member1.as<std::uint32_t>(),
+                            st1.as<hs_status_t>(), ws1.p, nullptr) == HS_OK, "select a");
+        check(hs_gqa_score(dqb.as<std::uint16_t>(), dkb.as<std::uint16_t>(), 1024, nullptr, 0, n,
+                           raw_b1.as<std::uint16_t>(), n, part_b1.as<std::uint32_t>(), nullptr) == HS_OK,
+              "score layer b");
+        // one call
+        hs_select_job_t sel = {raw_a.as<std::uint16_t>(), part_a.as<std::uint32_t>(),
+                               ids2.as<std::uint32_t>(), counts2.as<std::uint32_t>(),
+                               member2.as<std::uint32_t>(), st2.as<hs_status_t>(), ws2.p, n, n, cap, 0};
+        hs_score_job_t sco = {dqb.as<std::uint16_t>(), dkb.as<std::uint16_t>(),
+                              raw_b2.as<std::uint16_t>(), part_b2.as<std::uint32_t>(), 1024, n, n, 0};
+        check(hs_gqa_select_then_score(&sel, 1, H, alpha, ratio, flags, &sco, 1, nullptr) == HS_OK,
+              "select-then-score");
+        hs_score_job_t bad = sco;
+        bad.scores = raw_a.as<std::uint16_t>();
+        rejects([&] {
+            if (hs_gqa_select_then_score(&sel, 1, H, alpha, ratio, flags, &bad, 1, nullptr) != HS_OK)
+                throw std::invalid_argument(hs_last_error());
+        }, "scores written over the selection's input rejected");
+        check(hipDeviceSynchronize() == hipSuccess, "sync");
+        ++cases;
+        const auto s1 = from_dev<hs_status_t>(st1, 1)[0], s2 = from_dev<hs_status_t>(st2, 1)[0];
+        check(s1.code == HS_OK && s2.code == s1.code && s2.k == s1.k &&
+                  s2.boundary_tied_heads == s1.boundary_tied_heads, "status equal");
+        check(from_dev<std::uint32_t>(ids1, H * cap) == from_dev<std::uint32_t>(ids2, H * cap),
+              "ids equal");
+        check(from_dev<std::uint32_t>(counts1, H) == from_dev<std::uint32_t>(counts2, H), "counts equal");
+        check(from_dev<std::uint32_t>(member1, H * words) == from_dev<std::uint32_t>(member2, H * words),
+              "membership equal");
+        const auto b1 = from_dev<std::uint16_t>(raw_b1, H * n), b2 = from_dev<std::uint16_t>(raw_b2, H * n);
+        check(b1 == b2, "next layer's scores equal");
+        comparisons += b1.size();
+        check(from_dev<std::uint32_t>(part_b1, parts) == from_dev<std::uint32_t>(part_b2, parts),
+              "next layer's tile maxima equal");
+    }
+    // attention of layer b beside the count of layer a's selection, then the
+    // counted selection, against the two plain calls
+    const std::uint32_t flags = HS_SELECT_SCALE_RAW | HS_SELECT_ID_ORDER;
+    Dev aws(hs_gqa_attention_workspace_bytes(n)), out1(H * 128 * 4), out2(H * 128 * 4);
+    check(hs_gqa_select(raw_b1.as<std::uint16_t>(), H, n, n, alpha, ratio, flags,
+                        part_b1.as<std::uint32_t>(), ids1.as<std::uint32_t>(), cap,
+                        counts1.as<std::uint32_t>(), member1.as<std::uint32_t>(),
+                        st1.as<hs_status_t>(), ws1.p, nullptr) == HS_OK, "select b");
+    const std::uint32_t* member_b = member1.as<std::uint32_t>();
+    check(hs_gqa_sparse_attention(dq32.as<float>(), reinterpret_cast<const std::uint8_t*>(dkb.p),
+                                  reinterpret_cast<const std::uint8_t*>(dvb.p), 2048, nullptr, 0,
+                                  member_b, n, out1.as<float>(), aws.p, nullptr) == HS_OK, "attention b");
+    check(hs_gqa_select(raw_a.as<std::uint16_t>(), H, n, n, alpha, ratio, flags,
+                        part_a.as<std::uint32_t>(), ids1.as<std::uint32_t>(), cap,
+                        counts1.as<std::uint32_t>(), nullptr, st1.as<hs_status_t>(), ws1.p,
+                        nullptr) == HS_OK, "plain select a");
+    hs_select_job_t sel = {raw_a.as<std::uint16_t>(), part_a.as<std::uint32_t>(),
+                           ids2.as<std::uint32_t>(), counts2.as<std::uint32_t>(), nullptr,
+                           st2.as<hs_status_t>(), ws2.p, n, n, cap, 0};
+    check(hs_gqa_attention_then_count(dq32.as<float>(), reinterpret_cast<const std::uint8_t*>(dkb.p),
+                                      reinterpret_cast<const std::uint8_t*>(dvb.p), 2048, nullptr, 0,
+                                      member_b, n, out2.as<float>(), aws.p, &sel, 1, H, alpha, ratio,
+                                      flags, nullptr) == HS_OK, "attention-then-count");
+    check(hs_gqa_select(raw_a.as<std::uint16_t>(), H, n, n, alpha, ratio, flags | HS_SELECT_COUNTED,
+                        part_a.as<std::uint32_t>(), ids2.as<std::uint32_t>(), cap,
+                        counts2.as<std::uint32_t>(), nullptr, st2.as<hs_status_t>(), ws2.p,
+                        nullptr) == HS_OK, "counted select a");
+    check(hipDeviceSynchronize() == hipSuccess, "sync");
+    ++cases;
+    check(from_dev<float>(out1, H * 128) == from_dev<float>(out2, H * 128), "attention outputs equal");
+    check(from_dev<std::uint32_t>(ids1, H * cap) == from_dev<std::uint32_t>(ids2, H * cap),
+          "counted selection equals the plain one");
+    check(from_dev<std::uint32_t>(counts1, H) == from_dev<std::uint32_t>(counts2, H), "counts equal");
+}
+
 int main() {
     try {
         stream_layout_contracts();  // host-only contracts run with or without a GPU
@@ -646,6 +759,7 @@ int main() {
         pack_contracts();
         cover_contracts();
         stream_score_contracts();
+        pipeline_contracts();
         std::cout << "{\"status\":\"passed\",\"cases\":" << cases
                   << ",\"bitwise_scores_compared\":" << comparisons << "}" << std::endl;
         return 0;
