@@ -1,5 +1,6 @@
 """The reference's own C++ contract cases, run through the C++17 host
-adapters (include/hs_gqa.hpp) on the GPU: tests/cpp/gqa_gpu_contracts."""
+adapters (include/hs_gqa.hpp) on the GPU, and the layer-pipelining C calls
+against the single calls: tests/cpp/gqa_gpu_contracts."""
 import json
 import subprocess
 from pathlib import Path
