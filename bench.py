@@ -421,6 +421,24 @@ def tier_leg(args, hs, ops, torch, stream, dev):
             assert ops.read_status(d["status"])["code"] == 0
             assert ops.read_status(d["cstatus"])["code"] == 0, ops.read_status(d["cstatus"])
     counts = [int(d["count"].item()) for sq in seqs for d in sq["layers"]]
+    # the step's last layer, checked per sequence: its attention over hot +
+    # fetched-cold rows equals, bit for bit, the attention over every row of
+    # the layer fetched from the same image into an all-hot pool
+    last = (LAYERS - 1) % TIER_PHYS
+    every = torch.arange(TIER_N, dtype=torch.int32, device=dev)
+    full = torch.empty((TIER_N, 2048), dtype=torch.float16, device=dev)
+    fstatus = ops.new_status(dev)
+    fws = ops.workspace(L.hs_kv_cold_fetch_workspace_bytes(TIER_N), dev)
+    for sq in seqs:
+        d = sq["layers"][last]
+        hs.check(L.hs_kv_cold_fetch(vp(sq["image"]), last, vp(every), TIER_N, vp(full),
+                                    ctypes.c_void_p(full.data_ptr() + 2048), 4096, vp(fstatus),
+                                    vp(fws), sp))
+        ref = ops.sparse_attention(d["q32"], full.reshape(-1), TIER_N, d["member"], stream=stream)
+        assert ops.read_status(fstatus)["code"] == 0
+        assert torch.equal(ref.view(torch.int32), d["out"].view(torch.int32)), \
+            "configs[4]: hot + fetched-cold attention differs from the all-hot attention"
+    del full, fws
     reps = 2
     step_ms = timed(step, reps)
     main_ms = timed(lambda: step(False), reps)
@@ -512,7 +530,14 @@ def main():
     ids = torch.empty((32, kmax), dtype=torch.int32, device=dev)
     counts = torch.empty(32, dtype=torch.int32, device=dev)
     status = ops.new_status(dev)
+    # one status per layer in the pipelined step: a failed selection of any
+    # layer stays visible after the step (a shared status would keep only the
+    # last layer's)
+    statuses = [ops.new_status(dev) for _ in range(LAYERS)]
     ws = ops.workspace(ops.select_workspace_bytes(32, N), dev)
+    # the current token of each layer: column N - 1, whose K row is the last
+    # row of the layer's keys (appended at this step)
+    cur_keys = [keys[layer][(N - 1) * 1024:] for layer in range(LAYERS)]
     torch.cuda.synchronize()
 
     def new_event():
@@ -528,22 +553,40 @@ def main():
             ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
             select_layer(0)
 
-    # Pipelined: layer l's selection shares a launch with layer l+1's scoring
-    # (hs_gqa_select_then_score); the score buffers alternate between layers.
-    pipe_calls = [
-        ops.prepare_select_then_score(
-            [dict(scores=raws[l % 2], n=N, head0_partial=partials[l % 2], ids=ids,
-                  ids_stride=kmax, counts=counts, status=status, ws=ws)],
-            [dict(q16=qs[l + 1], keys=keys[l + 1], tokens=N, out=raws[(l + 1) % 2],
-                  head0_partial=partials[(l + 1) % 2])],
-            32, ALPHA, RATIO, scale_raw=True)
-        for l in range(LAYERS - 1)]
+    # Pipelined as a decode can run it (the early history preparation of
+    # runtime/gqa_executor.cpp:291-295 and policy/full_gqa_runtime.cpp:
+    # 493-569): layer l+1's history, the N - 1 tokens before the current one,
+    # is scored while layer l's selection runs (hs_gqa_select_then_score);
+    # layer l's selection first completes its own current token, column
+    # N - 1, from the rehearsal query and the token's K row (the count
+    # launch's current-token completion).  The score buffers alternate.
+    def sel_job(l):
+        return dict(scores=raws[l % 2], n=N, head0_partial=partials[l % 2], ids=ids,
+                    ids_stride=kmax, counts=counts, status=statuses[l], ws=ws,
+                    current_q=qs[l], current_key=cur_keys[l])
+
+    def history(l):
+        return dict(q16=qs[l], keys=keys[l], tokens=N - 1, out=raws[l % 2], score_stride=N,
+                    head0_partial=partials[l % 2])
+
+    pipe_calls = [ops.prepare_select_then_score([sel_job(l)], [history(l + 1)], 32, ALPHA, RATIO,
+                                                scale_raw=True)
+                  for l in range(LAYERS - 1)]
+    last_select = ops.prepare_select_batched([sel_job(LAYERS - 1)], 32, ALPHA, RATIO,
+                                             scale_raw=True)
 
     def step():
-        ops.score(qs[0], keys[0], N, out=raws[0], head0_partial=partials[0])
+        h0 = history(0)
+        ops.score(h0["q16"], h0["keys"], N - 1, out=h0["out"], score_stride=N,
+                  head0_partial=h0["head0_partial"])
         for call in pipe_calls:
             call()
-        select_layer((LAYERS - 1) % 2)
+        last_select()
+
+    def check_statuses():
+        for l, stt in enumerate(statuses):
+            st = ops.read_status(stt)
+            assert st["code"] == 0 and st["k"] == kmax, (l, st)
 
     if args.only == "batch":
         batch_leg(args, hs, ops, torch, stream, dev)
@@ -557,8 +600,7 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    st = ops.read_status(status)
-    assert st["code"] == 0 and st["k"] == kmax, st
+    check_statuses()
     begin, end = new_event(), new_event()
     torch.cuda.synchronize()
     begin.record(stream)
@@ -567,8 +609,7 @@ def main():
     end.record(stream)
     torch.cuda.synchronize()
     ms_per_step = begin.elapsed_time(end) / args.steps
-    st = ops.read_status(status)
-    assert st["code"] == 0 and st["k"] == kmax, st
+    check_statuses()
     last_ids = ids.clone()
     # the same step one layer at a time (no pipelining), for comparison
     serial_step()
@@ -594,7 +635,9 @@ def main():
     # select-then-score calls (count launch + combined launch), each layer's
     # selection beside the next layer's scoring
     torch.cuda.synchronize()
-    ops.score(qs[0], keys[0], N, out=raws[0], head0_partial=partials[0])
+    h0 = history(0)
+    ops.score(h0["q16"], h0["keys"], N - 1, out=h0["out"], score_stride=N,
+              head0_partial=h0["head0_partial"])
     pb, pe = new_event(), new_event()
     pb.record(stream)
     for _ in range(args.steps):
@@ -603,8 +646,7 @@ def main():
     pe.record(stream)
     torch.cuda.synchronize()
     pipe_call_us = 1e3 * pb.elapsed_time(pe) / (args.steps * len(pipe_calls))
-    st = ops.read_status(status)
-    assert st["code"] == 0 and st["k"] == kmax, st
+    check_statuses()
     # per call: the next layer's scoring plus this layer's selection
     pipe_bytes = SCORE_BYTES + 2 * 32 * N * 2 + 4 * 32 * kmax
     pipe_gbs = pipe_bytes / (pipe_call_us * 1e-6) / 1e9
@@ -674,45 +716,49 @@ def main():
         us = 1e3 * b3.elapsed_time(e3) / (args.layer_steps * LAYERS)
         pipe_us = None
         if split:
-            # The same 30 layers pipelined: layer l's selection shares a launch
-            # with layer l+1's scoring, layer l's attention merge one with
-            # layer l+1's selection count.
+            # The same 30 layers pipelined as a decode can run them: layer
+            # l+1's history (N - 1 tokens) is scored beside layer l's
+            # selection, which first completes layer l's current token (column
+            # N - 1, K row N - 1 of the pool); then layer l's attention.  The
+            # next layer's selection cannot start before its current token
+            # exists, i.e. after this layer's attention (and the rest of the
+            # model layer), so nothing is co-launched with the attention.
             last_out = out.clone()
             member_p = torch.empty((32, (N + 31) // 32), dtype=torch.int32, device=dev)
             aws = ops.workspace(ops.attention_workspace_bytes(N), dev)
             flags = dict(scale_raw=True, require_k=True, id_order=True)
-            jobs = [dict(scores=raws[l % 2], n=N, head0_partial=partials[l % 2], ids=ids,
-                         ids_stride=kmax, counts=counts, member=member_p, status=status, ws=ws)
-                    for l in range(2)]
-            # layer l: its selection (counted after layer 0) beside layer l+1's
-            # scoring, then its attention beside layer l+1's count launch
-            calls = [
-                ops.prepare_select_then_score(
-                    [jobs[l % 2]],
-                    [dict(q16=qs[l + 1], keys=k_pools[l + 1], tokens=N, out=raws[(l + 1) % 2],
-                          head0_partial=partials[(l + 1) % 2])],
-                    32, ALPHA, RATIO, counted=l > 0, **flags)
-                for l in range(LAYERS - 1)]
-            attends = [
-                ops.prepare_attention_then_count(
-                    q32s[l], k_pools[l], N, member_p, [jobs[(l + 1) % 2]], 32, ALPHA, RATIO,
-                    out=out, ws=aws, v_pool=v_pools[l], row_bytes=row_bytes, **flags)
-                for l in range(LAYERS - 1)]
+
+            def job(l):
+                return dict(scores=raws[l % 2], n=N, head0_partial=partials[l % 2], ids=ids,
+                            ids_stride=kmax, counts=counts, member=member_p, status=statuses[l],
+                            ws=ws, current_q=qs[l], current_key=k_pools[l][(N - 1) * 1024:])
+
+            def hist(l):
+                return dict(q16=qs[l], keys=k_pools[l], tokens=N - 1, out=raws[l % 2],
+                            score_stride=N, head0_partial=partials[l % 2])
+
+            calls = [ops.prepare_select_then_score([job(l)], [hist(l + 1)], 32, ALPHA, RATIO,
+                                                   **flags)
+                     for l in range(LAYERS - 1)]
+            last_call = ops.prepare_select_batched([job(LAYERS - 1)], 32, ALPHA, RATIO, **flags)
+
+            def attend(l):
+                ops.sparse_attention(q32s[l], k_pools[l], N, member_p, out=out, ws=aws,
+                                     v_pool=v_pools[l], row_bytes=row_bytes)
 
             def pipelined_pass():
-                ops.score(qs[0], k_pools[0], N, out=raws[0], head0_partial=partials[0])
+                h0 = hist(0)
+                ops.score(h0["q16"], h0["keys"], N - 1, out=h0["out"], score_stride=N,
+                          head0_partial=h0["head0_partial"])
                 for layer in range(LAYERS - 1):
                     calls[layer]()
-                    attends[layer]()
-                last = jobs[(LAYERS - 1) % 2]
-                ops.select(last["scores"], 32, N, N, ALPHA, RATIO, counted=True,
-                           head0_partial=last["head0_partial"], ids=ids, ids_stride=kmax,
-                           counts=counts, member=member_p, status=status, ws=ws, **flags)
-                ops.sparse_attention(q32s[LAYERS - 1], k_pools[LAYERS - 1], N, member_p, out=out,
-                                     ws=aws, v_pool=v_pools[LAYERS - 1], row_bytes=row_bytes)
+                    attend(layer)
+                last_call()
+                attend(LAYERS - 1)
 
             pipelined_pass()
             torch.cuda.synchronize()
+            check_statuses()
             assert torch.equal(out, last_out), "pipelined and one-layer-at-a-time outputs differ"
             b3.record(stream)
             for _ in range(args.layer_steps):

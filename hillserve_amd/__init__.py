@@ -101,6 +101,8 @@ class SelectJob(ctypes.Structure):
         ("n", ctypes.c_uint32),
         ("ids_stride", ctypes.c_uint32),
         ("reserved", ctypes.c_uint32),
+        ("current_q", ctypes.c_void_p),
+        ("current_key", ctypes.c_void_p),
     ]
 
 

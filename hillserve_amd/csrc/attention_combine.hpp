@@ -84,7 +84,9 @@ __device__ __forceinline__ void combine_records(const float* __restrict__ part, 
         float sum = 0.0f;
 #pragma unroll
         for (uint32_t k = 0; k < kCombineRows; ++k) sum += acc16[k][tid];
-        out[h * 128 + ch] = L > 0.0f ? sum / L : 0.0f;
+        // no selected row: NaN, as a fully masked softmax row gives, never a
+        // silent zero (the reference refuses an empty selection)
+        out[h * 128 + ch] = L > 0.0f ? sum / L : __builtin_nanf("");
     }
 }
 

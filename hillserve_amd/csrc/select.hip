@@ -67,10 +67,13 @@ constexpr uint32_t kHRun = 32;                     // ids per thread: one member
 constexpr uint32_t kHeadMaxN = kHThreads * kHRun;  // 32768
 constexpr uint32_t kHeadMaxK = 8192;               // rank order: selection sorted in LDS
 
-// Published by group 0 of the plan launch.
+// code and k: published by group 0 of the plan launch or head 0 of the
+// per-head launch; head_max: the head-0 maximum order key (the current
+// token's included), published by group 0 of the count launch.
 struct SelectPlanDev {
     int32_t code;
     uint32_t k;
+    uint32_t head_max;
 };
 
 struct SelectPlan {
@@ -127,7 +130,9 @@ struct SelectArgs {
     float alpha, ratio;
     uint32_t flags;
     const uint32_t* partial;
-    uint32_t partials;
+    uint32_t partials;    // tile maxima of the history columns (all n without a current token)
+    const uint16_t* cur_q;    // current-token completion: query and K row of column n - 1, or null
+    const uint16_t* cur_key;
     SelectPlanDev* plan;
     uint32_t* g_count;  // [groups] slice counts >= thr
     uint32_t* g_bad;    // [groups] slice has a nonfinite score
@@ -160,6 +165,8 @@ struct SelectJob {
     uint32_t* member;
     hs_status_t* status;
     char* ws;
+    const uint16_t* cur_q;    // current-token completion of column n - 1, or null
+    const uint16_t* cur_key;
     uint32_t stride, n, ids_stride;
 };
 struct SelectJobs {
@@ -173,6 +180,8 @@ __host__ __device__ inline SelectArgs job_args(const SelectJobs& js, uint32_t j)
     const SelectJob& jb = js.job[j];
     const uint32_t kmax = kmax_of(jb.n, js.ratio, js.flags);
     const SelectPlan p = plan_select(js.heads, jb.n, kmax);
+    // with a current token the tile maxima cover the n - 1 history columns
+    const uint32_t history = jb.cur_key ? jb.n - 1u : jb.n;
     char* ws = jb.ws;
     SelectArgs a;
     a.scores = jb.scores;
@@ -184,7 +193,9 @@ __host__ __device__ inline SelectArgs job_args(const SelectJobs& js, uint32_t j)
     a.ratio = js.ratio;
     a.flags = js.flags;
     a.partial = jb.partial ? jb.partial : reinterpret_cast<const uint32_t*>(ws + p.off_partial);
-    a.partials = p.partials;
+    a.partials = (history + 63) / 64;
+    a.cur_q = jb.cur_q;
+    a.cur_key = jb.cur_key;
     a.plan = reinterpret_cast<SelectPlanDev*>(ws + p.off_plan);
     a.g_count = reinterpret_cast<uint32_t*>(ws + p.off_count);
     a.g_bad = reinterpret_cast<uint32_t*>(ws + p.off_bad);
@@ -215,10 +226,11 @@ __global__ void __launch_bounds__(256) head0_max_kernel(const SelectJobs js) {
     uint32_t* own = const_cast<uint32_t*>(a.partial);
     const uint32_t tile = blockIdx.x * 4 + (threadIdx.x >> 6);
     const uint32_t i = tile * 64 + (threadIdx.x & 63u);
-    const uint32_t bits = i < a.n ? a.scores[i] : 0u;
-    const uint32_t key = i < a.n && !is_nan_half(bits) ? order_key(bits) : 0u;
+    const uint32_t cols = a.cur_key ? a.n - 1u : a.n;  // the current column is the count's
+    const uint32_t bits = i < cols ? a.scores[i] : 0u;
+    const uint32_t key = i < cols && !is_nan_half(bits) ? order_key(bits) : 0u;
     const uint32_t best = wave_max_u32(key);
-    if ((threadIdx.x & 63u) == 0 && tile * 64 < a.n) own[tile] = best;
+    if ((threadIdx.x & 63u) == 0 && tile < a.partials) own[tile] = best;
 }
 
 // Threshold from the head-0 maximum key: thr = f32(F16(f32(max) - alpha)).
@@ -397,8 +409,38 @@ __device__ __forceinline__ uint32_t hist_total(const uint32_t* whist, uint32_t b
 // loads of a phase are in flight together instead of each waiting for the
 // last at a branch join.
 __device__ __forceinline__ uint32_t load_or_zero(const uint32_t* p, uint32_t i, uint32_t n) {
+    if (n == 0) return 0u;  // (uniform) nothing to read
     const uint32_t x = p[i < n ? i : n - 1u];
     return i < n ? x : 0u;
+}
+
+// Raw F16 score of one K row for query head h, the reference's current-token
+// completion (policy/full_gqa_runtime.cpp:531-548): s = +0, then
+// s = fl(s + fl(q[c] * k[c])) over channels 0..127 in order, rounded to F16
+// once.  F16 x F16 products are exact in FP32, so each step is one FMA, as
+// in the scorer.  q F16 [32][128], key F16 [8][128] (query head h reads KV
+// head h / 4).  One lane computes it.
+__device__ __noinline__ uint32_t score_current(const uint16_t* q, const uint16_t* key, uint32_t h) {
+    const uint4* qv = reinterpret_cast<const uint4*>(q + h * 128);
+    const uint4* kv = reinterpret_cast<const uint4*>(key + (h >> 2) * 128);
+    uint4 qa[16], ka[16];
+#pragma unroll
+    for (uint32_t i = 0; i < 16; ++i) {
+        qa[i] = qv[i];
+        ka[i] = kv[i];
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < 16; ++i) {
+        const uint32_t qw[4] = {qa[i].x, qa[i].y, qa[i].z, qa[i].w};
+        const uint32_t kw[4] = {ka[i].x, ka[i].y, ka[i].z, ka[i].w};
+#pragma unroll
+        for (uint32_t p = 0; p < 4; ++p) {
+            s = __builtin_fmaf(h2f(qw[p] & 0xffffu), h2f(kw[p] & 0xffffu), s);
+            s = __builtin_fmaf(h2f(qw[p] >> 16), h2f(kw[p] >> 16), s);
+        }
+    }
+    return f2h(s);
 }
 
 // Maximum of the head-0 per-tile maxima (at most kMaxN / 64 of them).
@@ -417,6 +459,7 @@ __device__ __forceinline__ uint32_t partial_max(const SelectArgs& a) {
 struct CountLds {
     uint32_t whist[kHistWords];
     uint32_t tmp[kWaves];
+    uint32_t current;  // raw bits of this head's current-token score
 };
 
 // Group g (head, slice) of job `job` by one kThreads workgroup.
@@ -433,7 +476,37 @@ __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, ui
     uint32_t packed[kRun / 2];
     load_run<kRun>(a, h, begin, packed);
     hist_clear(whist);
+    // Current-token completion: column n - 1 is scored here from the query
+    // and the appended K row.  Every group folds its head-0 score into the
+    // threshold maximum (wave 0); the group holding the column scores it for
+    // its head (wave 1, on another SIMD), writes it into the scores and
+    // counts it in place of what the column held.
+    const uint32_t last = a.n - 1u;
+    const bool holds_last = a.cur_key && last >= s * kSlice && last < s * kSlice + kSlice;
+    if (a.cur_key) {
+        if (tid == 0) {
+            const uint32_t c0 = score_current(a.cur_q, a.cur_key, 0);
+            if (!is_nan_half(c0)) best = max(best, order_key(c0));
+        }
+        if (tid == 64 && holds_last) {
+            const uint32_t ch = score_current(a.cur_q, a.cur_key, h);
+            lds.current = ch;
+            const_cast<uint16_t*>(a.scores)[static_cast<size_t>(h) * a.stride + last] =
+                static_cast<uint16_t>(ch);
+        }
+    }
     best = block_max(best, tmp);  // its barrier also orders the histogram clear
+    if (holds_last && last >= begin && last < begin + kRun) {
+        uint32_t bits = lds.current;
+        if (a.flags & HS_SELECT_SCALE_RAW) bits = scale_raw(bits);
+#pragma unroll
+        for (uint32_t j = 0; j < kRun; ++j) {  // constant indices: packed stays in registers
+            constexpr uint32_t kLow = 0xffffu;
+            if (begin + j == last)
+                packed[j >> 1] = (packed[j >> 1] & ~(kLow << ((j & 1u) * 16u))) | (bits << ((j & 1u) * 16u));
+        }
+    }
+    if (g == 0 && tid == 0) a.plan->head_max = best;
     const float thr = threshold_from_key(best, (a.flags & HS_SELECT_SCALE_RAW) != 0, a.alpha);
     // the history cover does not reject nonfinite scores (NaN counts as below)
     const bool cover = (a.flags & HS_SELECT_COVER) != 0;
@@ -546,7 +619,6 @@ __device__ int derive_k(const SelectArgs& a, const uint32_t* head_count, const u
 __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
     __shared__ uint32_t whist[kHistWords];
     __shared__ uint32_t hist[256];
-    __shared__ uint32_t tmp[kWaves];
     __shared__ uint32_t head_count[kMaxHeads];
     __shared__ uint32_t head_bad[kMaxHeads];
     __shared__ uint32_t sh[4];
@@ -556,8 +628,9 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
     const uint32_t groups = a.heads * S;
     const bool scale = (a.flags & HS_SELECT_SCALE_RAW) != 0;
 
-    // every global read of this kernel is issued up front
-    uint32_t best = partial_max(a);
+    // every global read of this kernel is issued up front (the head-0
+    // maximum as the count launch published it, the current token's included)
+    const uint32_t best = a.plan->head_max;
     constexpr uint32_t kCountLoads = kMaxHeads * kMaxSlices / kThreads;  // 8
     constexpr uint32_t kBinLoads = kMaxSlices * 256 / kThreads;           // 16
     uint32_t cnt[kCountLoads], bad[kCountLoads], hi_part[kBinLoads];
@@ -591,7 +664,7 @@ __global__ void __launch_bounds__(kThreads) plan_kernel(SelectArgs a) {
 #pragma unroll
     for (uint32_t u = 0; u < kBinLoads; ++u)
         if (hi_part[u]) atomicAdd(&hist[(tid + u * kThreads) & 255u], hi_part[u]);
-    best = block_max(best, tmp);  // its barrier also publishes the sums above
+    __syncthreads();  // publishes the sums above
     const float thr = threshold_from_key(best, scale, a.alpha);
 
     // k from every head's count (wave 0)
@@ -798,9 +871,10 @@ __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
     const int code = a.plan->code;
     const uint32_t k = a.plan->k;
     const uint32_t words = (n + 31) / 32;
-    if (code != HS_OK) return;
-    if (k == 0) {
-        // empty selection: clear this run's membership bits
+    if (code != HS_OK || k == 0) {
+        // failed or empty selection: clear this run's membership bits, so an
+        // attention that follows on the stream sees no selection instead of
+        // the bitmaps an earlier call left
         if (a.member && (tid & 3u) == 0 && begin / 32 < words)
             a.member[static_cast<size_t>(h) * words + begin / 32] = 0u;
         return;
@@ -1012,7 +1086,7 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
 
     // every global read is issued up front: head-0 tile maxima, all slice
     // counts and flags, this head's slice histograms and this thread's keys
-    uint32_t best = load_or_zero(a.partial, tid, a.partials);
+    const uint32_t best = a.plan->head_max;  // published by the count launch
     const uint32_t cnt = load_or_zero(a.g_count, tid, groups);
     const uint32_t bad = load_or_zero(a.g_bad, tid, groups);
     constexpr uint32_t kBinLoads = (kHeadMaxN / kSlice) * 256 / kHThreads;  // 2
@@ -1048,7 +1122,7 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
 #pragma unroll
     for (uint32_t u = 0; u < kBinLoads; ++u)
         if (hv[u]) atomicAdd(&hist[0][(tid + u * kHThreads) & 255u], hv[u]);
-    best = block_max<kHThreads>(best, tmp);  // its barrier also publishes the sums above
+    __syncthreads();  // publishes the sums above
     const float thr = threshold_from_key(best, (a.flags & HS_SELECT_SCALE_RAW) != 0, a.alpha);
     if (wave == 0) {
         uint32_t k = 0;
@@ -1070,8 +1144,7 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
     __syncthreads();
     const int code = static_cast<int>(sh[kCode]);
     const uint32_t k = sh[kK];
-    if (code != HS_OK) return;
-    if (k == 0) {
+    if (code != HS_OK || k == 0) {  // no stale bitmaps after a failed selection
         if (a.member && tid < words) a.member[static_cast<size_t>(h) * words + tid] = 0u;
         return;
     }
@@ -1505,8 +1578,15 @@ int check_common(uint32_t heads, float alpha, float ratio, uint32_t flags) {
 // Host checks of one job; on success fills the job's kernel record.
 int check_job(const uint16_t* scores, size_t stride, uint32_t n, const uint32_t* head0_partial,
               uint32_t* ids, size_t ids_stride, uint32_t* counts, uint32_t* member,
-              hs_status_t* status, void* workspace, float ratio, uint32_t flags, SelectJob& out) {
+              hs_status_t* status, void* workspace, float ratio, uint32_t flags, SelectJob& out,
+              const uint16_t* cur_q = nullptr, const uint16_t* cur_key = nullptr) {
     if (!scores || !ids || !status || !workspace) return reject("select: null pointer");
+    if ((cur_q == nullptr) != (cur_key == nullptr))
+        return reject("current-token completion needs both the query and the K row");
+    if (cur_key && (flags & HS_SELECT_COVER))
+        return reject("current-token completion: the history cover scores history only");
+    if (cur_key && ((reinterpret_cast<uintptr_t>(cur_q) | reinterpret_cast<uintptr_t>(cur_key)) & 15u))
+        return reject("current-token completion: query and K row must be 16-byte aligned");
     if (n == 0 || n > kMaxN) return reject("GQA selector shape: n must be 1..131072");
     if (stride < n || stride > 0xffffffffu) return reject("GQA selector shape: stride < n");
     // the history cover caps at the selection over n + 1 columns
@@ -1516,7 +1596,7 @@ int check_job(const uint16_t* scores, size_t stride, uint32_t n, const uint32_t*
     if (ids_stride < kmax || ids_stride > 0xffffffffu)
         return reject("select: ids_stride below the largest possible k");
     out = SelectJob{scores, head0_partial, ids, counts, member, status,
-                    static_cast<char*>(workspace), static_cast<uint32_t>(stride), n,
+                    static_cast<char*>(workspace), cur_q, cur_key, static_cast<uint32_t>(stride), n,
                     static_cast<uint32_t>(ids_stride)};
     return HS_OK;
 }
@@ -1613,8 +1693,11 @@ int build_select_jobs(const hs_select_job_t* jobs, uint32_t count, uint32_t head
     js.ratio = ratio;
     for (uint32_t j = 0; j < count; ++j) {
         const hs_select_job_t& q = jobs[j];
+        if (q.current_key && heads != 32)
+            return reject("current-token completion: 32 query heads over 8 KV heads");
         rc = check_job(q.scores, q.stride, q.n, q.head0_partial, q.ids, q.ids_stride, q.counts,
-                       q.member, q.status, q.workspace, ratio, flags, js.job[j]);
+                       q.member, q.status, q.workspace, ratio, flags, js.job[j], q.current_q,
+                       q.current_key);
         if (rc != HS_OK) return rc;
     }
     return HS_OK;
@@ -1642,7 +1725,9 @@ int check_disjoint(const hs_select_job_t* sel, uint32_t scount, uint32_t heads, 
         const size_t words = (size_t(s.n) + 31) / 32;
         const Span reads[] = {
             span(s.scores, size_t(heads) * s.stride * sizeof(uint16_t)),
-            span(s.head0_partial, (size_t(s.n) + 63) / 64 * sizeof(uint32_t))};
+            span(s.head0_partial, (size_t(s.n) + 63) / 64 * sizeof(uint32_t)),
+            span(s.current_q, size_t(32) * 128 * sizeof(uint16_t)),
+            span(s.current_key, size_t(8) * 128 * sizeof(uint16_t))};
         const Span writes[] = {
             span(s.ids, size_t(heads) * s.ids_stride * sizeof(uint32_t)),
             span(s.counts, size_t(heads) * sizeof(uint32_t)),
@@ -1760,14 +1845,19 @@ int launch_attention_then_count(const float* q, const uint8_t* k_pool, const uin
     for (uint32_t j = 0; j < next_count; ++j) {
         const hs_select_job_t& x = next_jobs[j];
         const Span count_in[] = {span(x.scores, size_t(heads) * x.stride * sizeof(uint16_t)),
-                                 span(x.head0_partial, (size_t(x.n) + 63) / 64 * sizeof(uint32_t))};
+                                 span(x.head0_partial, (size_t(x.n) + 63) / 64 * sizeof(uint32_t)),
+                                 span(x.current_q, size_t(32) * 128 * sizeof(uint16_t)),
+                                 span(x.current_key, size_t(8) * 128 * sizeof(uint16_t))};
         const Span count_out[] = {span(x.workspace, plan_select(heads, x.n, kmax_of(x.n, ratio, flags)).total),
                                   span(x.status, sizeof(hs_status_t))};
         for (const Span& w : count_out)
             if (overlap(w, merge_in) || overlap(w, merge_out))
                 return reject("attention-then-count: selection workspace or status overlaps the attention's");
+        // the partial launch writes the records before the count reads the
+        // scores, so the scores may overlap neither the records nor the output
         for (const Span& r : count_in)
-            if (overlap(r, merge_out)) return reject("attention-then-count: attention output overlaps the next scores");
+            if (overlap(r, merge_in) || overlap(r, merge_out))
+                return reject("attention-then-count: attention workspace or output overlaps the next scores");
     }
     rc = launch_attention_partial(q, k_pool, v_pool, row_bytes, rows, pool_rows, member, n, out,
                                   workspace, stream);

@@ -38,8 +38,23 @@ def workspace(nbytes: int, device="cuda") -> torch.Tensor:
     return torch.empty(max(256, int(nbytes)), dtype=torch.uint8, device=device)
 
 
-def new_status(device="cuda") -> torch.Tensor:
-    return torch.zeros(4, dtype=torch.int32, device=device)
+def _scratch(nbytes: int, device, stream) -> torch.Tensor:
+    """A workspace the wrapper drops on return: recorded on the launch
+    stream, so the caching allocator does not hand it out again while that
+    stream's kernels still use it."""
+    ws = workspace(nbytes, device)
+    ws.record_stream(stream if stream is not None else torch.cuda.current_stream(ws.device))
+    return ws
+
+
+def new_status(device="cuda", stream=None) -> torch.Tensor:
+    """A zeroed hs_status_t; zeroed on `stream` (default: the current
+    stream), so the fill is ordered before the kernels that write it."""
+    st = torch.empty(4, dtype=torch.int32, device=device)
+    if stream is None:
+        return st.zero_()
+    with torch.cuda.stream(stream):
+        return st.zero_()
 
 
 def read_status(status: torch.Tensor) -> dict:
@@ -133,9 +148,9 @@ def select(scores, heads, stride, n, alpha, ratio, *, scale_raw=False, fp32_coun
     if counts is None:
         counts = torch.empty(heads, dtype=torch.int32, device=dev)
     if status is None:
-        status = new_status(dev)
+        status = new_status(dev, stream)
     if ws is None:
-        ws = workspace(select_workspace_bytes(heads, n), dev)
+        ws = _scratch(select_workspace_bytes(heads, n), dev, stream)
     flags = _select_flags(scale_raw, fp32_counts, require_k, id_order, cover, counted)
     check(lib().hs_gqa_select(_p(scores), heads, stride, n, alpha, ratio, flags,
                               _p(head0_partial), _p(ids), ids_stride, _p(counts), _p(member),
@@ -143,12 +158,23 @@ def select(scores, heads, stride, n, alpha, ratio, *, scale_raw=False, fp32_coun
     return ids, counts, member, status
 
 
+def _current(job):
+    """(current_q, current_key) of a selection job dict: the current-token
+    completion of column n - 1 (both or neither)."""
+    q, key = job.get("current_q"), job.get("current_key")
+    _need_cuda(q, key)
+    return _p(q), _p(key)
+
+
 def select_batched(jobs, heads, alpha, ratio, *, scale_raw=False, fp32_counts=False,
                    require_k=False, id_order=False, cover=False, stream=None):
     """Up to 16 selections sharing heads/alpha/ratio/flags in one batch.
 
     jobs: dicts with scores [heads, stride] and n, optional head0_partial,
-    member (int32 [heads, ceil(n/32)]).  Returns a list of
+    member (int32 [heads, ceil(n/32)]), current_q and current_key (the
+    current-token completion of column n - 1: F16 [32, 128] query and the
+    token's F16 [8, 128] K row; head0_partial then covers the n - 1 history
+    columns).  Returns a list of
     (ids, counts, member, status) per job."""
     from . import SelectJob
     table = (SelectJob * max(1, len(jobs)))()
@@ -163,16 +189,50 @@ def select_batched(jobs, heads, alpha, ratio, *, scale_raw=False, fp32_counts=Fa
         ids_stride = max(1, kmax)
         ids = torch.empty((heads, ids_stride), dtype=torch.int32, device=dev)
         counts = torch.empty(heads, dtype=torch.int32, device=dev)
-        status = new_status(dev)
-        ws = workspace(select_workspace_bytes(heads, n), dev)
+        status = new_status(dev, stream)
+        ws = _scratch(select_workspace_bytes(heads, n), dev, stream)
         member = j.get("member")
         results.append((ids, counts, member, status, ws))
         table[i] = SelectJob(_p(scores), _p(j.get("head0_partial")), _p(ids), _p(counts),
-                             _p(member), _p(status), _p(ws), stride, n, ids_stride, 0)
+                             _p(member), _p(status), _p(ws), stride, n, ids_stride, 0,
+                             *_current(j))
     flags = _select_flags(scale_raw, fp32_counts, require_k, id_order, cover)
     check(lib().hs_gqa_select_batched(ctypes.cast(table, ctypes.c_void_p), len(jobs), heads,
                                       alpha, ratio, flags, _s(stream)))
     return [r[:4] for r in results]
+
+
+def _select_table(jobs):
+    """hs_select_job_t table over caller-owned buffers (scores, n, ids,
+    status, ws; optional stride, head0_partial, counts, member, ids_stride,
+    current_q, current_key)."""
+    from . import SelectJob
+    table = (SelectJob * max(1, len(jobs)))()
+    for i, j in enumerate(jobs):
+        _need_cuda(j["scores"], j["ids"], j["status"], j["ws"])
+        stride = int(j.get("stride") or j["scores"].shape[-1])
+        ids_stride = int(j.get("ids_stride") or j["ids"].shape[-1])
+        table[i] = SelectJob(_p(j["scores"]), _p(j.get("head0_partial")), _p(j["ids"]),
+                             _p(j.get("counts")), _p(j.get("member")), _p(j["status"]),
+                             _p(j["ws"]), stride, int(j["n"]), ids_stride, 0, *_current(j))
+    return table
+
+
+def prepare_select_batched(jobs, heads, alpha, ratio, *, scale_raw=False, fp32_counts=False,
+                           require_k=False, id_order=False, cover=False, counted=False,
+                           stream=None):
+    """Bind hs_gqa_select_batched to caller-owned buffers (as
+    prepare_select_then_score): returns a callable that enqueues it."""
+    table = _select_table(jobs)
+    flags = _select_flags(scale_raw, fp32_counts, require_k, id_order, cover, counted)
+    fn, tp, st, nj = lib().hs_gqa_select_batched, ctypes.cast(table, ctypes.c_void_p), _s(stream), len(jobs)
+    keep = (jobs, table)
+
+    def call():
+        check(fn(tp, nj, heads, alpha, ratio, flags, st))
+        return keep
+
+    return call
 
 
 def prepare_select_then_score(select_jobs, score_jobs, heads, alpha, ratio, *, scale_raw=False,
@@ -196,7 +256,7 @@ def prepare_select_then_score(select_jobs, score_jobs, heads, alpha, ratio, *, s
         ids_stride = int(j.get("ids_stride") or j["ids"].shape[-1])
         stable[i] = SelectJob(_p(j["scores"]), _p(j.get("head0_partial")), _p(j["ids"]),
                               _p(j.get("counts")), _p(j.get("member")), _p(j["status"]),
-                              _p(j["ws"]), stride, n, ids_stride, 0)
+                              _p(j["ws"]), stride, n, ids_stride, 0, *_current(j))
     ttable = (ScoreJob * max(1, len(score_jobs)))()
     for i, j in enumerate(score_jobs):
         _need_cuda(j["q16"], j["keys"], j["out"])
@@ -244,7 +304,7 @@ def prepare_attention_then_count(q32, pool, n, member, next_jobs, heads, alpha, 
         ids_stride = int(j.get("ids_stride") or j["ids"].shape[-1])
         table[i] = SelectJob(_p(j["scores"]), _p(j.get("head0_partial")), _p(j["ids"]),
                              _p(j.get("counts")), _p(j.get("member")), _p(j["status"]),
-                             _p(j["ws"]), stride, int(j["n"]), ids_stride, 0)
+                             _p(j["ws"]), stride, int(j["n"]), ids_stride, 0, *_current(j))
     flags = _select_flags(scale_raw, fp32_counts, require_k, id_order, cover)
     fn = lib().hs_gqa_attention_then_count
     args = (_p(q32), kp, vp, row_bytes, None, pool_rows, _p(member), n, _p(out), _p(ws),
@@ -272,8 +332,10 @@ def rehearsal_query(hidden, wq, positions, eps=1e-5, theta=500000.0, out=None, s
         out = torch.empty((batch, 32, 128), dtype=torch.float16, device=hidden.device)
     st = ws = None
     if status:
-        st = torch.zeros((batch, 4), dtype=torch.int32, device=hidden.device)
-        ws = workspace(lib().hs_rehearsal_workspace_bytes(batch), hidden.device)
+        st = torch.empty((batch, 4), dtype=torch.int32, device=hidden.device)
+        with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
+            st.zero_()
+        ws = _scratch(lib().hs_rehearsal_workspace_bytes(batch), hidden.device, stream)
     check(lib().hs_rehearsal_query(_p(hidden), _p(wq), ctypes.cast(pos, ctypes.c_void_p), batch,
                                    eps, theta, _p(out), _p(st), _p(ws), _s(stream)))
     return out, st
@@ -284,9 +346,11 @@ def rehearsal_query(hidden, wq, positions, eps=1e-5, theta=500000.0, out=None, s
 def physical_union(ids, lens, ids_stride, visible, stream=None):
     dev = ids.device
     out = torch.empty(visible, dtype=torch.int32, device=dev)
-    out_n = torch.zeros(1, dtype=torch.int32, device=dev)
-    status = new_status(dev)
-    ws = workspace(lib().hs_gqa_union_workspace_bytes(visible), dev)
+    out_n = torch.empty(1, dtype=torch.int32, device=dev)
+    with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
+        out_n.zero_()
+    status = new_status(dev, stream)
+    ws = _scratch(lib().hs_gqa_union_workspace_bytes(visible), dev, stream)
     check(lib().hs_gqa_physical_union(_p(ids), _p(lens), ids_stride, visible, _p(out), _p(out_n),
                                       _p(status), _p(ws), _s(stream)))
     return out, out_n, status
@@ -314,7 +378,7 @@ def pack(pool, ids, lens, ids_stride, positions, count, row_of_id=None, max_id=N
     k = torch.empty(count * H * D, dtype=torch.float16, device=dev)
     v = torch.empty(count * H * D, dtype=torch.float16, device=dev)
     mask = torch.empty(H * qpad * count, dtype=torch.float32, device=dev)
-    status = new_status(dev)
+    status = new_status(dev, stream)
     kp, vp, row_bytes, pool_rows = _kv_pool(pool, v_pool, row_bytes)
     if max_id is None:
         max_id = row_of_id.numel() if row_of_id is not None else pool_rows
@@ -329,7 +393,7 @@ def gather_rows(prefetched, misses, row_map, count, stream=None):
     dev = row_map.device
     k = torch.empty(count * H * D, dtype=torch.float16, device=dev)
     v = torch.empty(count * H * D, dtype=torch.float16, device=dev)
-    status = new_status(dev)
+    status = new_status(dev, stream)
     rows_of = lambda t: 0 if t is None else t.numel() * t.element_size() // 4096
     check(lib().hs_gqa_gather_rows(_p(prefetched), rows_of(prefetched), _p(misses), rows_of(misses),
                                    _p(row_map), count, _p(k), _p(v), _p(status), _s(stream)))
@@ -350,7 +414,7 @@ def sparse_attention(q32, pool, n, member, rows=None, out=None, ws=None, pool_ro
     if out is None:
         out = torch.empty((H, D), dtype=torch.float32, device=dev)
     if ws is None:
-        ws = workspace(attention_workspace_bytes(n), dev)
+        ws = _scratch(attention_workspace_bytes(n), dev, stream)
     kp, vp, row_bytes, rows_in_pool = _kv_pool(pool, v_pool, row_bytes)
     if pool_rows is None:
         pool_rows = rows_in_pool
@@ -382,9 +446,9 @@ def decode_layer(q16, q32, pool, n, alpha, ratio, *, rows=None, fp32_counts=Fals
     if out is None:
         out = torch.empty((H, D), dtype=torch.float32, device=dev)
     if status is None:
-        status = new_status(dev)
+        status = new_status(dev, stream)
     if ws is None:
-        ws = workspace(decode_layer_workspace_bytes(n), dev)
+        ws = _scratch(decode_layer_workspace_bytes(n), dev, stream)
     kp, vp, row_bytes, rows_in_pool = _kv_pool(pool, v_pool, row_bytes)
     if pool_rows is None:
         pool_rows = rows_in_pool
@@ -411,9 +475,9 @@ def kv_cold_fetch(image, layer, positions, k_out, *, v_out=None, row_bytes=4096,
     else:
         kp, vp = _p(k_out), _p(v_out)
     if status is None:
-        status = new_status(k_out.device)
+        status = new_status(k_out.device, stream)
     if ws is None:
-        ws = workspace(lib().hs_kv_cold_fetch_workspace_bytes(count), k_out.device)
+        ws = _scratch(lib().hs_kv_cold_fetch_workspace_bytes(count), k_out.device, stream)
     check(lib().hs_kv_cold_fetch(ctypes.c_void_p(image.data_ptr()), layer, _p(positions), count,
                                  kp, vp, row_bytes, _p(status), _p(ws), _s(stream)))
     return status

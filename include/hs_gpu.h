@@ -161,6 +161,20 @@ typedef struct {
     hs_status_t *status;
     void *workspace;
     uint32_t stride, n, ids_stride, reserved;
+    /* Current-token completion (score_current + select of
+     * policy/full_gqa_runtime.cpp:531-572), nullable together: the history
+     * (columns < n - 1) was scored earlier, e.g. by hs_gqa_score with
+     * tokens = n - 1 one layer ahead, and column n - 1 is the token just
+     * appended.  The selection's first launch scores that column itself,
+     * ordered FP32 as the scorer, from current_q (F16 [32][128]) and
+     * current_key (its F16 K row [8][128]), writes the raw F16 scores into
+     * scores[h*stride + n - 1] (the input column is ignored), folds the
+     * head-0 score into the threshold maximum and selects over all n
+     * columns.  head0_partial then covers the n - 1 history columns (the
+     * scorer's tile maxima of that call).  heads must be 32; not with
+     * HS_SELECT_COVER (history only); 16-byte aligned. */
+    const uint16_t *current_q;
+    const uint16_t *current_key;
 } hs_select_job_t;
 int hs_gqa_select_batched(const hs_select_job_t *jobs, uint32_t count, uint32_t heads,
                           float alpha, float ratio, uint32_t flags, void *stream);

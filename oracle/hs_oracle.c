@@ -499,8 +499,9 @@ void hso_attention_f64(const float *q, const uint8_t *pool, size_t row_bytes,
     for (size_t h = 0; h < 32; ++h) {
         const size_t kv = h / 4, m = lens[h];
         double *o = out + h * 128;
+        /* an empty selection: NaN, the fully masked softmax row */
         for (size_t d = 0; d < 128; ++d)
-            o[d] = 0.0;
+            o[d] = m == 0 ? NAN : 0.0;
         if (m == 0)
             continue;
         double *s = (double *)malloc(sizeof(double) * m);

@@ -105,3 +105,24 @@ def test_chunks_with_empty_unions(hs, port):
                                   to_dev(member.reshape(-1)))
     ref = port.attention(q, pool.view(np.uint8), ids)
     assert rel_err(out.cpu().numpy().astype(np.float64), ref) <= TOL
+
+
+def test_empty_head_gives_nan(hs, port):
+    # A head with no selected row has no softmax: its output is NaN (a fully
+    # masked row), never a silent zero; the other heads are unaffected.
+    n = 2048
+    g = rng(33)
+    k = rope_keys(n, 34)
+    v = f16_bits(g.standard_normal((n, 8, 128)))
+    pool = pool_rows(k, v)
+    q = g.standard_normal((32, 128)).astype(np.float32)
+    ids = [np.sort(g.choice(n, size=300, replace=False)) for _ in range(32)]
+    ids[7] = np.array([], dtype=np.int64)
+    member = member_words(ids, n)
+    out = hs.ops.sparse_attention(torch.from_numpy(q).cuda(), to_dev(pool.reshape(-1)), n,
+                                  to_dev(member.reshape(-1))).cpu().numpy().astype(np.float64)
+    ref = port.attention(q, pool.view(np.uint8), ids)
+    assert np.isnan(out[7]).all() and np.isnan(ref[7]).all()
+    keep = [h for h in range(32) if h != 7]
+    assert np.isfinite(out[keep]).all()
+    assert rel_err(out[keep], ref[keep]) <= TOL

@@ -299,3 +299,21 @@ def test_repeated_calls_share_workspace(hs, port):
             got = from_dev(dev_ids)[:, :k]
             assert np.array_equal(got, np.sort(ids, axis=1) if id_order else ids)
             assert np.array_equal(from_dev(dev_counts), counts)
+
+
+@pytest.mark.parametrize("n", [1000, 40000])
+def test_failed_selection_clears_member(hs, n):
+    # A failed selection leaves no stale bitmaps behind for an attention that
+    # follows on the stream: the member words it was given are cleared
+    # (per-head path and slice path).
+    g = rng(22)
+    s = f16_bits(g.standard_normal((32, n)))
+    s[0, n // 2] = 0x7E00  # NaN in head 0: nonfinite head-0 score
+    words = (n + 31) // 32
+    member = torch.full((32 * words,), -1, dtype=torch.int32, device="cuda")
+    for id_order in (False, True):
+        member.fill_(-1)
+        _, _, _, status = hs.ops.select(to_dev(s.reshape(-1)), 32, n, n, 2.0, 0.2, member=member,
+                                        id_order=id_order)
+        assert hs.ops.read_status(status)["code"] == hs.HS_ERR_NONFINITE
+        assert not from_dev(member).any()
