@@ -119,6 +119,8 @@ SIGNATURES = {
     "hs_full_gqa_pipeline": (_I, [_P, _P, _P, _U32, _P]),
     "hs_gqa_score": (_I, [_P, _P, _SZ, _P, _U32, _U32, _P, _SZ, _P, _P]),
     "hs_gqa_score_batched": (_I, [_P, _U32, _P]),
+    "hs_gqa_score_logits": (_I, [_P, _P, _P, _SZ, _P, _U32, _U32, _P, _SZ, _P, _P, _SZ, _P]),
+    "hs_gqa_sparse_attention_logits": (_I, [_P, _SZ, _P, _SZ, _P, _U32, _P, _U32, _P, _P, _P]),
     "hs_gqa_select_workspace_bytes": (_SZ, [_U32, _U32]),
     "hs_gqa_select": (_I, [_P, _U32, _SZ, _U32, _F, _F, _U32, _P, _P, _SZ, _P, _P, _P, _P, _P]),
     "hs_gqa_select_batched": (_I, [_P, _U32, _U32, _F, _F, _U32, _P]),

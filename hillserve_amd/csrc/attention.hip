@@ -300,6 +300,177 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
     }
 }
 
+// ---- attention from the scoring pass's dots (V rows only) ------------------
+// One workgroup per kChunk ids, one wave per KV head g, as above, but the q.k
+// dots of the chunk come precomputed (hs_gqa_score_logits read every K row
+// once for them), so each selected (id, g) costs only its 256 B V segment:
+//  1. the 4 query heads' membership words and dots are requested together;
+//     the union is compacted in id order into LDS: pool row, and per head
+//     the scaled dot or -inf where that head did not select the row;
+//  2. every V segment of the union is requested at once (lane (row group
+//     l/16, channel group l%16) holds 16 B of rows 4i + l/16, i < 32);
+//  3. while those are in flight: the chunk's exact maximum per head, then
+//     p = exp(s - m) per row into LDS and l = sum p (no running maximum, no
+//     rescaling);
+//  4. o += p * V as the rows land; the 4 row groups' o are added and the
+//     wave writes the chunk's (m, l, o[128]) record per query head, merged by
+//     attn_combine_kernel as before.
+template <bool kRows>
+__global__ void __launch_bounds__(kThreads)
+attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* __restrict__ v_pool,
+              uint32_t row_bytes, const int32_t* __restrict__ rows, uint32_t pool_rows,
+              const uint32_t* __restrict__ member, uint32_t n, uint32_t chunks,
+              float* __restrict__ part) {
+    __shared__ uint32_t sel_row[8][kChunk];
+    __shared__ float4 sel_p[8][kChunk];  // scaled dots of the union rows, then their p
+    const uint32_t chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t g = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave = KV head
+    const uint32_t words = (n + 31) / 32, base = chunk * kChunk;
+    constexpr uint32_t kSteps = kChunk / 64;
+    uint32_t mw[kSteps][4];
+    float sd[kSteps][4];
+#pragma unroll
+    for (uint32_t c = 0; c < kSteps; ++c) {
+        const uint32_t id = min(base + 64 * c + lane, n - 1);
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            mw[c][j] = member[static_cast<size_t>(4 * g + j) * words + (id >> 5)];
+            sd[c][j] = dots[static_cast<size_t>(4 * g + j) * dstride + id];
+        }
+    }
+    uint32_t total = 0;
+#pragma unroll
+    for (uint32_t c = 0; c < kSteps; ++c) {
+        const uint32_t id = base + 64 * c + lane;
+        uint32_t mk = 0, r = id;
+        if (id < n) {
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) mk |= ((mw[c][j] >> (id & 31u)) & 1u) << j;
+            if (kRows && mk) {
+                r = static_cast<uint32_t>(rows[id]);
+                if (r >= pool_rows) mk = 0;  // rows outside the pool contribute nothing
+            }
+        }
+        const uint64_t any = __ballot(mk != 0);
+        if (mk) {
+            const uint32_t at = total + lanes_below(any);
+            sel_row[g][at] = r;
+            float sv[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) sv[j] = ((mk >> j) & 1u) ? sd[c][j] * kScale : -INFINITY;
+            sel_p[g][at] = make_float4(sv[0], sv[1], sv[2], sv[3]);
+        }
+        total += static_cast<uint32_t>(__popcll(any));
+    }
+    __builtin_amdgcn_wave_barrier();
+    float* rec = part + (static_cast<size_t>(g) * chunks + chunk) * 4 * kRecord;
+    const uint32_t r16 = lane & 15u, q16 = lane >> 4;
+    if (total == 0) {  // no selected row: an empty record, and no row is read
+        if (lane < 16) {
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+#pragma unroll
+                for (uint32_t c = 0; c < 8; ++c) rec[j * kRecord + 2 + r16 * 8 + c] = 0.0f;
+                if (lane == 0) {
+                    rec[j * kRecord + 0] = -INFINITY;
+                    rec[j * kRecord + 1] = 0.0f;
+                }
+            }
+        }
+        return;
+    }
+    // ---- every V segment of the union in flight (groups of 4 rows) ----
+    constexpr uint32_t kGroups = kChunk / 4;
+    const uint32_t groups = (total + 3) / 4;  // wave-uniform
+    uint4 vw[kGroups];
+    const uint8_t* vbase = v_pool + g * 256 + 16 * r16;
+#pragma unroll
+    for (uint32_t i = 0; i < kGroups; ++i) {
+        if (i < groups) {  // (the last group re-reads the union's last row)
+            const uint32_t e = min(4 * i + q16, total - 1);
+            vw[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(sel_row[g][e]) * row_bytes);
+        }
+    }
+    // ---- the chunk's exact maximum per head, then p and l ----
+    float m[4], lsum[4];
+    {
+        float4 a[kSteps];
+        float top[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+        for (uint32_t c = 0; c < kSteps; ++c) {
+            const uint32_t e = 64 * c + lane;
+            a[c] = e < total ? sel_p[g][e] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            top[0] = fmaxf(top[0], a[c].x);
+            top[1] = fmaxf(top[1], a[c].y);
+            top[2] = fmaxf(top[2], a[c].z);
+            top[3] = fmaxf(top[3], a[c].w);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) m[j] = first_lane(wave_max_f32(top[j]));
+        float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t c = 0; c < kSteps; ++c) {
+            const float sv[4] = {a[c].x, a[c].y, a[c].z, a[c].w};
+            float p[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                p[j] = sv[j] == -INFINITY ? 0.0f : __expf(sv[j] - m[j]);
+                ps[j] += p[j];
+            }
+            if (64 * c + lane < total) sel_p[g][64 * c + lane] = make_float4(p[0], p[1], p[2], p[3]);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) lsum[j] = first_lane(wave_sum_f32(ps[j]));
+    }
+    __builtin_amdgcn_wave_barrier();
+    // ---- o += p * V: lane (row group q16, channel group r16) ----
+    float o[4][8];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j)
+#pragma unroll
+        for (uint32_t c = 0; c < 8; ++c) o[j][c] = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < kGroups; ++i) {
+        if (i < groups) {
+            const uint32_t e = 4 * i + q16;
+            const float4 pp = sel_p[g][min(e, total - 1)];
+            const bool live = e < total;
+            const float p0 = live ? pp.x : 0.0f, p1 = live ? pp.y : 0.0f;
+            const float p2 = live ? pp.z : 0.0f, p3 = live ? pp.w : 0.0f;
+            const uint32_t vwords[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
+#pragma unroll
+            for (uint32_t c2 = 0; c2 < 4; ++c2) {
+                const float v0 = h2f(vwords[c2] & 0xffffu), v1 = h2f(vwords[c2] >> 16);
+                o[0][2 * c2] = __builtin_fmaf(p0, v0, o[0][2 * c2]);
+                o[1][2 * c2] = __builtin_fmaf(p1, v0, o[1][2 * c2]);
+                o[2][2 * c2] = __builtin_fmaf(p2, v0, o[2][2 * c2]);
+                o[3][2 * c2] = __builtin_fmaf(p3, v0, o[3][2 * c2]);
+                o[0][2 * c2 + 1] = __builtin_fmaf(p0, v1, o[0][2 * c2 + 1]);
+                o[1][2 * c2 + 1] = __builtin_fmaf(p1, v1, o[1][2 * c2 + 1]);
+                o[2][2 * c2 + 1] = __builtin_fmaf(p2, v1, o[2][2 * c2 + 1]);
+                o[3][2 * c2 + 1] = __builtin_fmaf(p3, v1, o[3][2 * c2 + 1]);
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t off = 16; off < 64; off <<= 1)
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j)
+#pragma unroll
+            for (uint32_t c = 0; c < 8; ++c) o[j][c] += __shfl_xor(o[j][c], off, 64);
+    if (lane < 16) {
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+#pragma unroll
+            for (uint32_t c = 0; c < 8; ++c) rec[j * kRecord + 2 + r16 * 8 + c] = o[j][c];
+            if (lane == 0) {
+                rec[j * kRecord + 0] = m[j];
+                rec[j * kRecord + 1] = lsum[j];
+            }
+        }
+    }
+}
+
 __global__ void __launch_bounds__(kCombineThreads)
 attn_combine_kernel(const float* __restrict__ part, uint32_t chunks, float* __restrict__ out) {
     __shared__ CombineLds lds;
@@ -339,6 +510,34 @@ int launch_attention_partial(const float* q, const uint8_t* k_pool, const uint8_
     return st == hipSuccess ? HS_OK : hip_fail(st, "attention launch");
 }
 
+int launch_attention_logits(const float* logits, size_t logit_stride, const uint8_t* v_pool,
+                            size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
+                            const uint32_t* member, uint32_t n, float* out, void* workspace,
+                            hipStream_t stream) {
+    if (!logits || !v_pool || !member || !out || !workspace)
+        return reject("attention: null pointer");
+    if (n == 0 || n > 65536) return reject("attention: n must be 1..65536");
+    if (logit_stride < n || logit_stride > 0xffffffffu)
+        return reject("attention: logit stride must be >= n");
+    if (row_bytes < 2048 || row_bytes % 16 != 0 || row_bytes > (1u << 20))
+        return reject("attention: row_bytes must be 2048..1 MiB and a multiple of 16");
+    if (reinterpret_cast<uintptr_t>(v_pool) & 15u) return reject("attention: V pool must be 16-byte aligned");
+    const uint32_t chunks = (n + kChunk - 1) / kChunk;
+    float* part = static_cast<float*>(workspace);
+    const auto ls = static_cast<uint32_t>(logit_stride);
+    const auto rb = static_cast<uint32_t>(row_bytes);
+    if (rows)
+        hipLaunchKernelGGL(attn_v_kernel<true>, dim3(chunks), dim3(kThreads), 0, stream, logits, ls,
+                           v_pool, rb, rows, pool_rows, member, n, chunks, part);
+    else
+        hipLaunchKernelGGL(attn_v_kernel<false>, dim3(chunks), dim3(kThreads), 0, stream, logits, ls,
+                           v_pool, rb, rows, 0u, member, n, chunks, part);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(32, 4), dim3(kCombineThreads), 0, stream,
+                       static_cast<const float*>(workspace), chunks, out);
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hip_fail(st, "attention launch");
+}
+
 int launch_attention(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
                      size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
                      const uint32_t* member, uint32_t n, float* out, void* workspace,
@@ -370,6 +569,17 @@ int hs_gqa_sparse_attention(const float* q_dev, const uint8_t* k_pool_dev,
     return hs::launch_attention(q_dev, k_pool_dev, v_pool_dev, row_bytes, row_of_id_dev,
                                 pool_rows, member_dev, n, out_dev, workspace_dev,
                                 hs::as_stream(stream));
+}
+
+int hs_gqa_sparse_attention_logits(const float* logits_dev, size_t logit_stride,
+                                   const uint8_t* v_pool_dev, size_t row_bytes,
+                                   const int32_t* row_of_id_dev, uint32_t pool_rows,
+                                   const uint32_t* member_dev, uint32_t n, float* out_dev,
+                                   void* workspace_dev, void* stream) {
+    hs::clear_error();
+    return hs::launch_attention_logits(logits_dev, logit_stride, v_pool_dev, row_bytes,
+                                       row_of_id_dev, pool_rows, member_dev, n, out_dev,
+                                       workspace_dev, hs::as_stream(stream));
 }
 
 }  // extern "C"

@@ -28,9 +28,11 @@ inline hipStream_t as_stream(void* stream) { return static_cast<hipStream_t>(str
 inline size_t align256(size_t bytes) { return (bytes + 255) & ~size_t(255); }
 
 // ---- launch wrappers implemented in the .hip translation units ----------
+// With qf and logits (both or neither): the attention logits in the same pass.
 int launch_score(const uint16_t* q, const uint16_t* keys, size_t stride_words,
                  const int32_t* rows, uint32_t pool_rows, uint32_t tokens, uint16_t* scores,
-                 size_t score_stride, uint32_t* head0_partial, hipStream_t stream);
+                 size_t score_stride, uint32_t* head0_partial, hipStream_t stream,
+                 const float* qf = nullptr, float* logits = nullptr, size_t logit_stride = 0);
 
 int launch_score_batched(const hs_score_job_t* jobs, uint32_t count, hipStream_t stream);
 
@@ -62,6 +64,11 @@ int launch_attention_partial(const float* q, const uint8_t* k_pool, const uint8_
                              size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
                              const uint32_t* member, uint32_t n, float* out, void* workspace,
                              hipStream_t stream);
+// Attention from the scoring pass's logits (V rows only).
+int launch_attention_logits(const float* logits, size_t logit_stride, const uint8_t* v_pool,
+                            size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
+                            const uint32_t* member, uint32_t n, float* out, void* workspace,
+                            hipStream_t stream);
 int launch_attention(const float* q, const uint8_t* k_pool, const uint8_t* v_pool,
                      size_t row_bytes, const int32_t* rows, uint32_t pool_rows,
                      const uint32_t* member, uint32_t n, float* out, void* workspace,

@@ -50,7 +50,7 @@ namespace {
 // ---- fused decode layer ------------------------------------------------------
 
 struct LayerPlan {
-    size_t off_partial, off_member, off_select, off_attn, total;
+    size_t off_partial, off_member, off_select, off_attn, off_logits, total;
 };
 
 LayerPlan plan_layer(uint32_t n) {
@@ -65,6 +65,7 @@ LayerPlan plan_layer(uint32_t n) {
     p.off_member = take(sizeof(uint32_t) * 32 * ((n + 31) / 32));
     p.off_select = take(select_workspace_bytes(32, n));
     p.off_attn = take(attention_workspace_bytes(n));
+    p.off_logits = take(sizeof(float) * 32 * size_t(n));  // attention q.k dots [32][n]
     p.total = at;
     return p;
 }
@@ -171,16 +172,23 @@ int hs_decode_layer(const uint16_t* q16_dev, const float* q32_dev, const uint8_t
     char* ws = static_cast<char*>(workspace_dev);
     uint32_t* partial = reinterpret_cast<uint32_t*>(ws + p.off_partial);
     uint32_t* member = reinterpret_cast<uint32_t*>(ws + p.off_member);
+    float* logits = reinterpret_cast<float*>(ws + p.off_logits);
+    if (reinterpret_cast<uintptr_t>(q32_dev) & 3u) return hs::reject("decode layer: q32 must be 4-byte aligned");
+    // One pass over the K rows: the ordered raw scores for the selection and,
+    // from the same registers, the attention's q32.k dots for every token
+    // (both queries are known when a layer is scored at its own step), so the
+    // attention reads only the selected V rows.
     int rc = hs::launch_score(q16_dev, reinterpret_cast<const uint16_t*>(k_pool_dev),
-                              row_bytes / 2, row_of_id_dev, pool_rows, n, scores_dev, n, partial, s);
+                              row_bytes / 2, row_of_id_dev, pool_rows, n, scores_dev, n, partial, s,
+                              q32_dev, logits, n);
     if (rc != HS_OK) return rc;
     rc = hs::launch_select(scores_dev, 32, n, n, alpha, ratio,
                            flags | HS_SELECT_SCALE_RAW | HS_SELECT_REQUIRE_K | HS_SELECT_ID_ORDER,
                            partial, ids_dev,
                            ids_stride, counts_dev, member, status_dev, ws + p.off_select, s);
     if (rc != HS_OK) return rc;
-    return hs::launch_attention(q32_dev, k_pool_dev, v_pool_dev, row_bytes, row_of_id_dev,
-                                pool_rows, member, n, out_dev, ws + p.off_attn, s);
+    return hs::launch_attention_logits(logits, n, v_pool_dev, row_bytes, row_of_id_dev, pool_rows,
+                                       member, n, out_dev, ws + p.off_attn, s);
 }
 
 int hs_selftest_f16_checksums(uint64_t* checksums_dev, void* stream) {

@@ -52,6 +52,20 @@ score_kernel(const ScoreJobs jobs, const int32_t* __restrict__ rows, uint32_t po
                                gridDim.x * kWavesPerBlock, lds[w]);
 }
 
+// The scorer with the attention dots in the same pass (one job): each wave
+// also holds its KV head's split query (2 KiB of LDS); one half ahead.
+template <bool kRows>
+__global__ void __launch_bounds__(kWavesPerBlock * 64) __attribute__((amdgpu_waves_per_eu(4)))
+score_logits_kernel(const ScoreJobs jobs, const int32_t* __restrict__ rows, uint32_t pool_rows,
+                    const LogitsOut lo) {
+    __shared__ uint4 lds[kWavesPerBlock][kHalfTileChunks];
+    __shared__ uint4 qstage[kWavesPerBlock][8 * 16];
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    score_waves<kRows, false, false, true>(
+        jobs, rows, pool_rows, __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + w),
+        gridDim.x * kWavesPerBlock, lds[w], lo, qstage[w]);
+}
+
 // 16 waves per CU (four per SIMD, 8 KiB of LDS each), each streaming its
 // share of the (token tile, KV head) pairs: at N = 32768 one pair per wave.
 uint32_t score_grid(uint32_t ids) {
@@ -63,8 +77,14 @@ uint32_t score_grid(uint32_t ids) {
 
 int launch_score(const uint16_t* q, const uint16_t* keys, size_t stride_words,
                  const int32_t* rows, uint32_t pool_rows, uint32_t tokens, uint16_t* scores,
-                 size_t score_stride, uint32_t* head0_partial, hipStream_t stream) {
+                 size_t score_stride, uint32_t* head0_partial, hipStream_t stream,
+                 const float* qf, float* logits, size_t logit_stride) {
     if (!q || !keys || !scores) return reject("score: null pointer");
+    if ((qf == nullptr) != (logits == nullptr)) return reject("score: logits need the F32 query");
+    if (logits && (logit_stride < tokens || logit_stride > 0xffffffffu))
+        return reject("score: logit stride must be >= tokens");
+    if (logits && (reinterpret_cast<uintptr_t>(qf) & 3u))
+        return reject("score: F32 query must be 4-byte aligned");
     if (stride_words != 1024 && stride_words != 2048)
         return reject("score: key stride must be 1024 or 2048 F16 words");
     if (tokens == 0 || tokens > 65536) return reject("score: tokens must be 1..65536");
@@ -79,9 +99,15 @@ int launch_score(const uint16_t* q, const uint16_t* keys, size_t stride_words,
     jobs.job[0] = ScoreJob{reinterpret_cast<const uint32_t*>(q), keys, scores, head0_partial,
                            static_cast<uint32_t>(stride_words), tokens,
                            static_cast<uint32_t>(score_stride), 0u};
+    const LogitsOut lo{qf, logits, static_cast<uint32_t>(logit_stride)};
     jobs.total_ids = ((tokens + kTileTokens - 1) / kTileTokens) * 8;  // (token tile, KV head)
     const dim3 grid(score_grid(jobs.total_ids)), block(kWavesPerBlock * 64);
-    if (rows)
+    if (logits && rows)
+        hipLaunchKernelGGL(score_logits_kernel<true>, grid, block, 0, stream, jobs, rows, pool_rows,
+                           lo);
+    else if (logits)
+        hipLaunchKernelGGL(score_logits_kernel<false>, grid, block, 0, stream, jobs, rows, 0u, lo);
+    else if (rows)
         hipLaunchKernelGGL((score_kernel<true, false>), grid, block, 0, stream, jobs, rows, pool_rows);
     else
         hipLaunchKernelGGL((score_kernel<false, false>), grid, block, 0, stream, jobs, rows, 0u);
@@ -140,6 +166,18 @@ int hs_gqa_score(const uint16_t* q_dev, const uint16_t* keys_dev, size_t key_str
     return hs::launch_score(q_dev, keys_dev, key_stride_words, rows_dev, pool_rows, tokens,
                             scores_dev,
                             score_stride, head0_partial_dev, hs::as_stream(stream));
+}
+
+int hs_gqa_score_logits(const uint16_t* q_dev, const float* q32_dev, const uint16_t* keys_dev,
+                        size_t key_stride_words, const int32_t* rows_dev, uint32_t pool_rows,
+                        uint32_t tokens, uint16_t* scores_dev, size_t score_stride,
+                        uint32_t* head0_partial_dev, float* logits_dev, size_t logit_stride,
+                        void* stream) {
+    hs::clear_error();
+    if (!q32_dev || !logits_dev) return hs::reject("score logits: null pointer");
+    return hs::launch_score(q_dev, keys_dev, key_stride_words, rows_dev, pool_rows, tokens,
+                            scores_dev, score_stride, head0_partial_dev, hs::as_stream(stream),
+                            q32_dev, logits_dev, logit_stride);
 }
 
 int hs_full_gqa_pipeline(const void* query_dev, const void* keys_dev, void* scores_dev,

@@ -29,6 +29,13 @@ struct ScoreJob {
     uint32_t* head0_partial;
     uint32_t stride_words, n, out_stride, first_id;
 };
+// Attention logits in the same pass (kLogits launches, one job): the F32
+// query qf [32][128] and the unscaled FP32 dots out[h*stride + t].
+struct LogitsOut {
+    const float* qf;
+    float* out;
+    uint32_t stride;
+};
 constexpr uint32_t kMaxScoreJobs = 16;
 struct ScoreJobs {
     ScoreJob job[kMaxScoreJobs];
@@ -55,10 +62,19 @@ __device__ __forceinline__ uint4 (&second_half_buffer(uint4 (&first)[kN], uint4 
 // are requested before the first is used (32 more VGPRs), so a tile costs
 // one memory round trip instead of two; otherwise the second half is
 // requested once the first is parked in LDS.
-template <bool kRows, bool kBatch, bool kAhead>
+// kLogits: the same pass also produces the attention's q.k dots of the
+// tile's 64 tokens for the 4 query heads (F32 queries lo.qf), on MFMA from
+// the half tile already parked in LDS: v_mfma_f32_16x16x32_f16 with A = the
+// 4 query rows (rows 4..15 zero), split into F16 hi = f16(q) and lo =
+// f16(q - hi) (two products per step, ~22 bits of q, FP32 products and
+// sums), and B = K^T of 16 tokens.  The split query of the wave's KV head
+// sits in `qstage` (2 KiB of LDS per wave), staged when the KV head changes.
+// The unscaled dots go to lo.out; the attention then reads V rows only.
+template <bool kRows, bool kBatch, bool kAhead, bool kLogits = false>
 __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t* __restrict__ rows,
                                             uint32_t pool_rows, uint32_t wave, uint32_t waves,
-                                            uint4* region) {
+                                            uint4* region, const LogitsOut& lo = LogitsOut{},
+                                            uint4* qstage = nullptr) {
     constexpr uint32_t kHalf = kChunks / 2;  // 16 B chunks of one half row (64 channels)
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t tiles = jobs.total_ids;  // (token tile, KV head) pairs of all jobs
@@ -105,6 +121,35 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
         for (uint32_t j = 0; j < kHalf; ++j) region[hslot(8 * j + (lane >> 3), lane & 7u)] = v[j];
     };
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    // ---- attention dots on MFMA (kLogits) ----
+    typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+    typedef float floatx4_t __attribute__((ext_vector_type(4)));
+    floatx4_t dots[kLogits ? 4 : 1];  // token group tg: lanes 0..15 hold heads 0..3 of token 16tg + l
+    uint32_t staged = 0xffffffffu;    // KV head whose split query sits in qstage
+    auto clear_dots = [&]() {
+        if constexpr (kLogits) {
+#pragma unroll
+            for (uint32_t tg = 0; tg < 4; ++tg) dots[tg] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    };
+    clear_dots();
+    // qstage[(part * 4 + j) * 16 + chunk]: 8 channels of query head 4kv + j,
+    // part 0 = hi, 1 = lo; lane (j = l/16, chunk = l%16) converts its 8
+    auto stage_query = [&](uint32_t kv) {
+        const float4* src = reinterpret_cast<const float4*>(lo.qf + (kv * 4 + (lane >> 4)) * 128 +
+                                                            8 * (lane & 15u));
+        const float4 x0 = src[0], x1 = src[1];
+        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        half8_t hi, lo8;
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e) {
+            hi[e] = static_cast<_Float16>(x[e]);
+            lo8[e] = static_cast<_Float16>(x[e] - static_cast<float>(hi[e]));
+        }
+        qstage[(lane >> 4) * 16 + (lane & 15u)] = __builtin_bit_cast(uint4, hi);
+        qstage[(4 + (lane >> 4)) * 16 + (lane & 15u)] = __builtin_bit_cast(uint4, lo8);
+        __builtin_amdgcn_wave_barrier();
+    };
     // channels 64h .. 64h+63 of the 4 ordered chains
     auto compute = [&](const ScoreJob& jb, uint32_t id, uint32_t h) {
         const uint32_t local = id - jb.first_id;
@@ -138,6 +183,29 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
             }
         }
     };
+    // The dots of half h: for each group of 16 tokens and each 32-channel
+    // step, B = K^T (lane l: token 16tg + l%16, channels 8(l/16)..+7 of the
+    // step, one 16 B read of the parked half) against the split query.
+    auto dots_half = [&](uint32_t h) {
+        if constexpr (kLogits) {
+            const uint32_t j = lane & 15u, kq = lane >> 4;
+#pragma unroll
+            for (uint32_t kb = 0; kb < 2; ++kb) {
+                const uint32_t chunk = 8 * h + 4 * kb + kq;  // of the query row
+                const uint4 qh = qstage[(j & 3u) * 16 + chunk];
+                const uint4 ql = qstage[(4 + (j & 3u)) * 16 + chunk];
+                const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
+                const half8_t a_hi = __builtin_bit_cast(half8_t, j < 4 ? qh : zero);
+                const half8_t a_lo = __builtin_bit_cast(half8_t, j < 4 ? ql : zero);
+#pragma unroll
+                for (uint32_t tg = 0; tg < 4; ++tg) {
+                    const half8_t b = __builtin_bit_cast(half8_t, region[hslot(16 * tg + j, 4 * kb + kq)]);
+                    dots[tg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, b, dots[tg], 0, 0, 0);
+                    dots[tg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo, b, dots[tg], 0, 0, 0);
+                }
+            }
+        }
+    };
     auto finish = [&](const ScoreJob& jb, uint32_t id) {
         const uint32_t local = id - jb.first_id;
         const uint32_t head_kv = local & 7u;
@@ -155,6 +223,22 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
                 wave_max_u32(token < jb.n && !is_nan_half(s0) ? order_key(s0) : 0u);
             if (lane == 0) jb.head0_partial[local >> 3] = best;
         }
+        if constexpr (kLogits) {
+            // lanes 0..15: token 16tg + l of the tile, heads 0..3 in dots[tg]
+            const uint32_t base = (local >> 3) * kTileTokens;
+            if (lane < 16) {
+#pragma unroll
+                for (uint32_t tg = 0; tg < 4; ++tg) {
+                    const uint32_t t = base + 16 * tg + lane;
+                    if (t < jb.n) {
+                        float* o = lo.out + static_cast<size_t>(head_kv * 4) * lo.stride + t;
+#pragma unroll
+                        for (uint32_t i = 0; i < 4; ++i) o[i * static_cast<size_t>(lo.stride)] = dots[tg][i];
+                    }
+                }
+            }
+            clear_dots();
+        }
         a0 = a1 = a2 = a3 = 0.0f;
     };
 
@@ -169,10 +253,18 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
     load(cur, id, 0, row, v);
     if (kAhead) load(cur, id, 1, row, second);
     while (true) {
+        if constexpr (kLogits) {
+            const uint32_t kv = (id - cur.first_id) & 7u;  // wave-uniform
+            if (kv != staged) {
+                stage_query(kv);
+                staged = kv;
+            }
+        }
         stash(v);
         __builtin_amdgcn_wave_barrier();
         if (!kAhead) load(cur, id, 1, row, second);
         compute(cur, id, 0);
+        dots_half(0);
         __builtin_amdgcn_wave_barrier();
         stash(second);
         __builtin_amdgcn_wave_barrier();
@@ -186,6 +278,7 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
             if (kAhead) load(nxt, next, 1, nrow, second);
         }
         compute(cur, id, 1);
+        dots_half(1);
         finish(cur, id);
         __builtin_amdgcn_wave_barrier();
         if (next >= tiles) break;

@@ -91,6 +91,29 @@ def score(q16, keys, tokens, key_stride_words=1024, rows=None, out=None, score_s
     return out
 
 
+def score_logits(q16, q32, keys, tokens, key_stride_words=1024, rows=None, out=None,
+                 score_stride=None, head0_partial=None, logits=None, logit_stride=None,
+                 pool_rows=None, stream=None):
+    """hs_gqa_score_logits: the raw scores (as score) and, in the same pass,
+    the attention dots logits F32 [32, logit_stride] of q32 F32 [32, 128].
+    Returns (scores, logits)."""
+    _need_cuda(q16, q32, keys, rows, out, head0_partial, logits)
+    if score_stride is None:
+        score_stride = tokens if out is None else out.shape[-1]
+    if out is None:
+        out = torch.empty((H, score_stride), dtype=torch.float16, device=keys.device)
+    if logit_stride is None:
+        logit_stride = tokens if logits is None else logits.shape[-1]
+    if logits is None:
+        logits = torch.empty((H, logit_stride), dtype=torch.float32, device=keys.device)
+    if pool_rows is None:
+        pool_rows = keys.numel() // key_stride_words
+    check(lib().hs_gqa_score_logits(_p(q16), _p(q32), _p(keys), key_stride_words, _p(rows),
+                                    pool_rows, tokens, _p(out), score_stride, _p(head0_partial),
+                                    _p(logits), logit_stride, _s(stream)))
+    return out, logits
+
+
 # ---- selection ---------------------------------------------------------------
 
 def score_batched(jobs, stream=None):
@@ -420,6 +443,25 @@ def sparse_attention(q32, pool, n, member, rows=None, out=None, ws=None, pool_ro
         pool_rows = rows_in_pool
     check(lib().hs_gqa_sparse_attention(_p(q32), kp, vp, row_bytes, _p(rows), pool_rows,
                                         _p(member), n, _p(out), _p(ws), _s(stream)))
+    return out
+
+
+def sparse_attention_logits(logits, v_pool, n, member, rows=None, out=None, ws=None,
+                            pool_rows=None, row_bytes=2048, stream=None):
+    """hs_gqa_sparse_attention_logits: attention from the scoring pass's dots
+    (logits F32 [32, stride]) over the selected V rows of v_pool (rows of
+    row_bytes)."""
+    _need_cuda(logits, v_pool, member, rows)
+    dev = v_pool.device
+    if out is None:
+        out = torch.empty((H, D), dtype=torch.float32, device=dev)
+    if ws is None:
+        ws = _scratch(attention_workspace_bytes(n), dev, stream)
+    if pool_rows is None:
+        pool_rows = v_pool.numel() * v_pool.element_size() // row_bytes
+    check(lib().hs_gqa_sparse_attention_logits(_p(logits), logits.shape[-1], _p(v_pool), row_bytes,
+                                               _p(rows), pool_rows, _p(member), n, _p(out), _p(ws),
+                                               _s(stream)))
     return out
 
 

@@ -77,6 +77,19 @@ int hs_gqa_score(const uint16_t *q_dev, const uint16_t *keys_dev,
                  size_t score_stride, uint32_t *head0_partial_dev,
                  void *stream);
 
+/* The scorer (as hs_gqa_score) and, in the same pass over the keys, the
+ * decode attention's q.k dots: logits_dev[h*logit_stride + t] = FP32 sum
+ * over channels c in order of q32_dev[h][c] * K[t][h/4][c] (q32 F32
+ * [32][128], the attention query; FMA per channel), unscaled, for
+ * t < tokens.  For a layer scored at its own decode step, when both the
+ * rehearsal query and the current query are known, this replaces the K
+ * reads of hs_gqa_sparse_attention (see hs_gqa_sparse_attention_logits). */
+int hs_gqa_score_logits(const uint16_t *q_dev, const float *q32_dev, const uint16_t *keys_dev,
+                        size_t key_stride_words, const int32_t *rows_dev, uint32_t pool_rows,
+                        uint32_t tokens, uint16_t *scores_dev, size_t score_stride,
+                        uint32_t *head0_partial_dev, float *logits_dev, size_t logit_stride,
+                        void *stream);
+
 /* Batched scorer: up to 16 independent scoring jobs (one query each, its own
  * keys, token count and outputs; the decode sequences of a batch) in one
  * launch, each with hs_gqa_score's semantics and limits (no row map).  The
@@ -323,6 +336,17 @@ int hs_gqa_sparse_attention(const float *q_dev, const uint8_t *k_pool_dev,
                             uint32_t n,
                             float *out_dev, void *workspace_dev, void *stream);
 
+/* The same attention from the dots hs_gqa_score_logits wrote (logits_dev
+ * [32][logit_stride], logit_stride >= n): s = logits * (1/sqrt(128)) for the
+ * selected ids, softmax and p.V as hs_gqa_sparse_attention, reading only
+ * the V rows of the selection (V at v_pool_dev + r*row_bytes).  Same
+ * workspace size as hs_gqa_sparse_attention. */
+int hs_gqa_sparse_attention_logits(const float *logits_dev, size_t logit_stride,
+                                   const uint8_t *v_pool_dev, size_t row_bytes,
+                                   const int32_t *row_of_id_dev, uint32_t pool_rows,
+                                   const uint32_t *member_dev, uint32_t n, float *out_dev,
+                                   void *workspace_dev, void *stream);
+
 /* Layer pipelining, second half: the sparse attention of one layer (as
  * hs_gqa_sparse_attention, same arguments) and the count launch of the next
  * layer's selection (next_jobs, heads, alpha, ratio, flags as
@@ -342,11 +366,13 @@ int hs_gqa_attention_then_count(const float *q_dev, const uint8_t *k_pool_dev,
                                 float ratio, uint32_t flags, void *stream);
 
 /* ---- fused layer step ----------------------------------------------------
- * One sparse decode layer: score (rehearsal q16 over the hot pool's K rows)
- * -> select (scaled, alpha, ratio; ids in ascending id order) -> sparse
- * attention (q32).  Hot pool as for hs_gqa_pack, with row_bytes 2048 (K and
- * V arrays: the scorer streams K contiguously) or 4096 (the reference's KV
- * records).  workspace: hs_decode_layer_workspace_bytes. */
+ * One sparse decode layer: score (rehearsal q16 over the hot pool's K rows,
+ * with the attention's q32.k dots in the same pass) -> select (scaled,
+ * alpha, ratio; ids in ascending id order) -> sparse attention (q32) over
+ * the selected V rows.  Hot pool as for hs_gqa_pack, with row_bytes 2048 (K
+ * and V arrays: the scorer streams K contiguously) or 4096 (the reference's
+ * KV records).  workspace: hs_decode_layer_workspace_bytes (it holds the
+ * [32][n] F32 dots). */
 size_t hs_decode_layer_workspace_bytes(uint32_t n);
 int hs_decode_layer(const uint16_t *q16_dev, const float *q32_dev,
                     const uint8_t *k_pool_dev, const uint8_t *v_pool_dev, size_t row_bytes,
