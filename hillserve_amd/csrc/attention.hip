@@ -321,7 +321,9 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
               uint32_t row_bytes, const int32_t* __restrict__ rows, uint32_t pool_rows,
               const uint32_t* __restrict__ member, uint32_t n, uint32_t chunks,
               float* __restrict__ part) {
-    __shared__ uint32_t sel_row[8][kChunk];
+    // union row e's pool row at sel_row[g][e % 4][e / 4]: the row group a
+    // lane reads (e % 4 = l / 16) is contiguous, so its rows come in 4 at a time
+    __shared__ uint4 sel_row[8][4][kChunk / 16];
     __shared__ float4 sel_p[8][kChunk];  // scaled dots of the union rows, then their p
     const uint32_t chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63u;
     const uint32_t g = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave = KV head
@@ -354,7 +356,7 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
         const uint64_t any = __ballot(mk != 0);
         if (mk) {
             const uint32_t at = total + lanes_below(any);
-            sel_row[g][at] = r;
+            reinterpret_cast<uint32_t*>(&sel_row[g][at & 3u][0])[at >> 2] = r;
             float sv[4];
 #pragma unroll
             for (uint32_t j = 0; j < 4; ++j) sv[j] = ((mk >> j) & 1u) ? sd[c][j] * kScale : -INFINITY;
@@ -380,15 +382,27 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
         return;
     }
     // ---- every V segment of the union in flight (groups of 4 rows) ----
+    // the lane's rows 4i + q16 first (4 per LDS read), then the loads back to
+    // back; a row past the union reads the union's last row again
     constexpr uint32_t kGroups = kChunk / 4;
     const uint32_t groups = (total + 3) / 4;  // wave-uniform
+    const uint32_t last_row = reinterpret_cast<const uint32_t*>(&sel_row[g][(total - 1) & 3u][0])[(total - 1) >> 2];
+    uint32_t my_row[kGroups];
+#pragma unroll
+    for (uint32_t i4 = 0; i4 < kGroups / 4; ++i4) {
+        const uint4 r4 = sel_row[g][q16][i4];
+        my_row[4 * i4] = r4.x;
+        my_row[4 * i4 + 1] = r4.y;
+        my_row[4 * i4 + 2] = r4.z;
+        my_row[4 * i4 + 3] = r4.w;
+    }
     uint4 vw[kGroups];
     const uint8_t* vbase = v_pool + g * 256 + 16 * r16;
 #pragma unroll
     for (uint32_t i = 0; i < kGroups; ++i) {
-        if (i < groups) {  // (the last group re-reads the union's last row)
-            const uint32_t e = min(4 * i + q16, total - 1);
-            vw[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(sel_row[g][e]) * row_bytes);
+        if (i < groups) {
+            const uint32_t r = 4 * i + q16 < total ? my_row[i] : last_row;
+            vw[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(r) * row_bytes);
         }
     }
     // ---- the chunk's exact maximum per head, then p and l ----

@@ -64,12 +64,15 @@ __device__ __forceinline__ uint4 (&second_half_buffer(uint4 (&first)[kN], uint4 
 // requested once the first is parked in LDS.
 // kLogits: the same pass also produces the attention's q.k dots of the
 // tile's 64 tokens for the 4 query heads (F32 queries lo.qf), on MFMA from
-// the half tile already parked in LDS: v_mfma_f32_16x16x32_f16 with A = the
-// 4 query rows (rows 4..15 zero), split into F16 hi = f16(q) and lo =
-// f16(q - hi) (two products per step, ~22 bits of q, FP32 products and
-// sums), and B = K^T of 16 tokens.  The split query of the wave's KV head
-// sits in `qstage` (2 KiB of LDS per wave), staged when the KV head changes.
-// The unscaled dots go to lo.out; the attention then reads V rows only.
+// the K values the ordered chains already hold: v_mfma_f32_4x4x4_16b_f16
+// runs 16 blocks of 4 tokens, and lane 4b + i supplies 4 channels of its own
+// token (row i of block b's A), lane 4b + j 4 channels of query head j (column
+// j of B), so no K value is read twice.  The query is split into F16 hi =
+// f16(q) and lo = f16(q - hi) (two products per step, ~22 bits of q, FP32
+// products and sums); the wave's KV head's split query sits in `qstage` (2 KiB
+// of LDS per wave), staged when the KV head changes.  Lane 4b + j ends with
+// head j's dots of tokens 4b .. 4b+3, written to lo.out unscaled; the
+// attention then reads V rows only.
 template <bool kRows, bool kBatch, bool kAhead, bool kLogits = false>
 __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t* __restrict__ rows,
                                             uint32_t pool_rows, uint32_t wave, uint32_t waves,
@@ -123,16 +126,13 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
     float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     // ---- attention dots on MFMA (kLogits) ----
     typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
     typedef float floatx4_t __attribute__((ext_vector_type(4)));
-    floatx4_t dots[kLogits ? 4 : 1];  // token group tg: lanes 0..15 hold heads 0..3 of token 16tg + l
+    // lane 4b + j: head j, tokens 4b .. 4b+3; four accumulators (hi / lo parts
+    // of the query x the two 4-channel steps of a chunk) keep four MFMA chains
+    // in flight instead of one
+    floatx4_t dots[kLogits ? 4 : 1] = {};
     uint32_t staged = 0xffffffffu;    // KV head whose split query sits in qstage
-    auto clear_dots = [&]() {
-        if constexpr (kLogits) {
-#pragma unroll
-            for (uint32_t tg = 0; tg < 4; ++tg) dots[tg] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-    };
-    clear_dots();
     // qstage[(part * 4 + j) * 16 + chunk]: 8 channels of query head 4kv + j,
     // part 0 = hi, 1 = lo; lane (j = l/16, chunk = l%16) converts its 8
     auto stage_query = [&](uint32_t kv) {
@@ -167,6 +167,20 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
         for (uint32_t j = 0; j < kHalf; ++j) {
             const uint4 k4 = region[hslot(lane, j)];
             const uint32_t kw[4] = {k4.x, k4.y, k4.z, k4.w};
+            if constexpr (kLogits) {
+                // channels 8j .. 8j+7 of the half: two 4-channel steps, hi and lo
+                const uint32_t qi = (lane & 3u) * 16 + 8 * h + j;  // this lane's head, chunk 8h + j
+                const uint4 qh = qstage[qi], ql = qstage[64 + qi];
+                const uint2 ka = make_uint2(k4.x, k4.y), kb = make_uint2(k4.z, k4.w);
+                dots[0] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, ka),
+                                                             __builtin_bit_cast(half4_t, make_uint2(qh.x, qh.y)), dots[0], 0, 0, 0);
+                dots[1] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, ka),
+                                                             __builtin_bit_cast(half4_t, make_uint2(ql.x, ql.y)), dots[1], 0, 0, 0);
+                dots[2] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, kb),
+                                                             __builtin_bit_cast(half4_t, make_uint2(qh.z, qh.w)), dots[2], 0, 0, 0);
+                dots[3] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, kb),
+                                                             __builtin_bit_cast(half4_t, make_uint2(ql.z, ql.w)), dots[3], 0, 0, 0);
+            }
 #pragma unroll
             for (uint32_t p = 0; p < 4; ++p) {
                 const uint32_t c2 = j * 4 + p;
@@ -180,29 +194,6 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
                 a1 = __builtin_fmaf(hi_half(q1), khi, a1);
                 a2 = __builtin_fmaf(hi_half(q2), khi, a2);
                 a3 = __builtin_fmaf(hi_half(q3), khi, a3);
-            }
-        }
-    };
-    // The dots of half h: for each group of 16 tokens and each 32-channel
-    // step, B = K^T (lane l: token 16tg + l%16, channels 8(l/16)..+7 of the
-    // step, one 16 B read of the parked half) against the split query.
-    auto dots_half = [&](uint32_t h) {
-        if constexpr (kLogits) {
-            const uint32_t j = lane & 15u, kq = lane >> 4;
-#pragma unroll
-            for (uint32_t kb = 0; kb < 2; ++kb) {
-                const uint32_t chunk = 8 * h + 4 * kb + kq;  // of the query row
-                const uint4 qh = qstage[(j & 3u) * 16 + chunk];
-                const uint4 ql = qstage[(4 + (j & 3u)) * 16 + chunk];
-                const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
-                const half8_t a_hi = __builtin_bit_cast(half8_t, j < 4 ? qh : zero);
-                const half8_t a_lo = __builtin_bit_cast(half8_t, j < 4 ? ql : zero);
-#pragma unroll
-                for (uint32_t tg = 0; tg < 4; ++tg) {
-                    const half8_t b = __builtin_bit_cast(half8_t, region[hslot(16 * tg + j, 4 * kb + kq)]);
-                    dots[tg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, b, dots[tg], 0, 0, 0);
-                    dots[tg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo, b, dots[tg], 0, 0, 0);
-                }
             }
         }
     };
@@ -224,20 +215,19 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
             if (lane == 0) jb.head0_partial[local >> 3] = best;
         }
         if constexpr (kLogits) {
-            // lanes 0..15: token 16tg + l of the tile, heads 0..3 in dots[tg]
-            const uint32_t base = (local >> 3) * kTileTokens;
-            if (lane < 16) {
+            // lane 4b + j: head 4kv + j, tokens 4b .. 4b+3 of the tile
+            const uint32_t t0 = (local >> 3) * kTileTokens + 4 * (lane >> 2);
+            float* o = lo.out + static_cast<size_t>(head_kv * 4 + (lane & 3u)) * lo.stride + t0;
+            const floatx4_t d = (dots[0] + dots[2]) + (dots[1] + dots[3]);
+            if (t0 + 4 <= jb.n && (lo.stride & 3u) == 0) {
+                *reinterpret_cast<float4*>(o) = make_float4(d[0], d[1], d[2], d[3]);
+            } else {
 #pragma unroll
-                for (uint32_t tg = 0; tg < 4; ++tg) {
-                    const uint32_t t = base + 16 * tg + lane;
-                    if (t < jb.n) {
-                        float* o = lo.out + static_cast<size_t>(head_kv * 4) * lo.stride + t;
-#pragma unroll
-                        for (uint32_t i = 0; i < 4; ++i) o[i * static_cast<size_t>(lo.stride)] = dots[tg][i];
-                    }
-                }
+                for (uint32_t i = 0; i < 4; ++i)
+                    if (t0 + i < jb.n) o[i] = d[i];
             }
-            clear_dots();
+#pragma unroll
+            for (uint32_t a = 0; a < 4; ++a) dots[a] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
         }
         a0 = a1 = a2 = a3 = 0.0f;
     };
@@ -264,7 +254,6 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
         __builtin_amdgcn_wave_barrier();
         if (!kAhead) load(cur, id, 1, row, second);
         compute(cur, id, 0);
-        dots_half(0);
         __builtin_amdgcn_wave_barrier();
         stash(second);
         __builtin_amdgcn_wave_barrier();
@@ -278,7 +267,6 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
             if (kAhead) load(nxt, next, 1, nrow, second);
         }
         compute(cur, id, 1);
-        dots_half(1);
         finish(cur, id);
         __builtin_amdgcn_wave_barrier();
         if (next >= tiles) break;

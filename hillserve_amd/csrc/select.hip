@@ -414,6 +414,11 @@ __device__ __forceinline__ uint32_t load_or_zero(const uint32_t* p, uint32_t i, 
     return i < n ? x : 0u;
 }
 
+// max(a - b, 0) without a guarded subtraction: a guarded `b >= a ? 0 : a - b`
+// has been speculated by the compiler into an unguarded wrapping subtract
+// (the guard dropped), which the tie counts below cannot afford.
+__device__ __forceinline__ uint32_t sat_sub(uint32_t a, uint32_t b) { return a - min(a, b); }
+
 // Raw F16 score of one K row for query head h, the reference's current-token
 // completion (policy/full_gqa_runtime.cpp:531-548): s = +0, then
 // s = fl(s + fl(q[c] * k[c])) over channels 0..127 in order, rounded to F16
@@ -941,7 +946,7 @@ __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
             if (lane >= off) ties_before += y;
         }
         ties_before -= ties;
-        const uint32_t left = t_need > ties_before ? t_need - ties_before : 0u;
+        const uint32_t left = sat_sub(t_need, ties_before);
         const uint32_t taken = std::min(ties, left);
         const uint32_t sel = (lane < S ? s_above[lane] : 0u) + taken;
         uint32_t sel_before = sel;
@@ -977,7 +982,7 @@ __global__ void __launch_bounds__(kThreads) slice_select_kernel(SelectArgs a) {
         }
     }
     const uint32_t tie_start = block_exclusive_scan(my_ties, tmp);
-    const uint32_t my_taken = tie_start >= taken ? 0u : std::min(my_ties, taken - tie_start);
+    const uint32_t my_taken = std::min(my_ties, sat_sub(taken, tie_start));
     uint32_t pos = block_exclusive_scan(my_above + my_taken, tmp);
     uint32_t tie_rank = tie_start;
     uint32_t bits8 = 0;
@@ -1210,7 +1215,7 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
     const uint32_t both = block_exclusive_scan<kHThreads>(
         (static_cast<uint32_t>(__popc(above_mask)) << 16) | my_ties, tmp);
     const uint32_t tie_start = both & 0xffffu;
-    const uint32_t my_taken = tie_start >= t_need ? 0u : std::min(my_ties, t_need - tie_start);
+    const uint32_t my_taken = std::min(my_ties, sat_sub(t_need, tie_start));
     uint32_t pos = (both >> 16) + std::min(tie_start, t_need);
     uint32_t bits32 = above_mask, rest = tie_mask;
     for (uint32_t t = 0; t < my_taken; ++t) {  // the lowest-id ties first
