@@ -143,6 +143,7 @@ SIGNATURES = {
     "hs_gqa_sparse_attention": (_I, [_P, _P, _P, _SZ, _P, _U32, _P, _U32, _P, _P, _P]),
     "hs_decode_layer_workspace_bytes": (_SZ, [_U32]),
     "hs_decode_layer": (_I, [_P, _P, _P, _P, _SZ, _P, _U32, _U32, _F, _F, _U32, _P, _P, _SZ, _P, _P, _P, _P, _P]),
+    "hs_decode_layer_noalloc": (_I, [_P, _P, _P, _P, _SZ, _P, _U32, _U32, _F, _F, _U32, _P, _P, _SZ, _P, _P, _P, _P]),
     "hs_selftest_f16_checksums": (_I, [_P, _P]),
     "hs_selftest_scale_table": (_I, [_P, _P]),
     "hs_fill_gaussian_f16": (_I, [_P, _SZ, _U64, _F, _P]),

@@ -7,6 +7,7 @@
 #include <array>
 #include <atomic>
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "hs_device.hpp"
@@ -143,6 +144,77 @@ __global__ void rope_keys_kernel(uint16_t* __restrict__ dst, uint32_t tokens, si
 }
 
 }  // namespace
+
+// ---- the no-allocation entry point's scratch ---------------------------------
+// One device array per GPU holds the layer workspace of hs_decode_layer_noalloc
+// (HS_NOALLOC_MAX_TOKENS tokens: 17.5 MB of the 18 MiB).  Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in):
+// its device address is looked up once per device with that device current.
+constexpr size_t kScratchBytes = size_t(18) << 20;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::array<void*, kMaxDevices> g_scratch_ptr{};
+std::array<int, kMaxDevices> g_scratch_rc{};
+std::array<std::once_flag, kMaxDevices> g_scratch_once;
+}  // namespace
+
+// The device address of `scratch` on the current device (HS_ERR_HIP if it
+// cannot be found); the lookup allocates nothing.
+int scratch_address(void** out) {
+    int device = 0;
+    hipError_t st = hipGetDevice(&device);
+    if (st != hipSuccess) return hip_fail(st, "no-allocation layer: current device");
+    if (device < 0 || device >= kMaxDevices) return reject("no-allocation layer: device ordinal beyond 63");
+    std::call_once(g_scratch_once[device], [device]() {
+        void* p = nullptr;
+        const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_ptr[device] = rc == hipSuccess ? p : nullptr;
+        g_scratch_rc[device] = static_cast<int>(rc);
+    });
+    if (g_scratch_ptr[device] == nullptr)
+        return hip_fail(static_cast<hipError_t>(g_scratch_rc[device]), "no-allocation layer: scratch address");
+    *out = g_scratch_ptr[device];
+    return HS_OK;
+}
+
+// One sparse decode layer into the workspace `workspace_dev` (a caller's
+// buffer, or the device scratch array of the no-allocation entry point).
+int decode_layer(const uint16_t* q16_dev, const float* q32_dev, const uint8_t* k_pool_dev,
+                 const uint8_t* v_pool_dev, size_t row_bytes, const int32_t* row_of_id_dev,
+                 uint32_t pool_rows, uint32_t n, float alpha, float ratio, uint32_t flags,
+                 uint16_t* scores_dev, uint32_t* ids_dev, size_t ids_stride, uint32_t* counts_dev,
+                 float* out_dev, hs_status_t* status_dev, void* workspace_dev, hipStream_t s) {
+    if (!q16_dev || !q32_dev || !k_pool_dev || !v_pool_dev || !scores_dev || !ids_dev ||
+        !out_dev || !status_dev || !workspace_dev)
+        return reject("decode layer: null pointer");
+    if (n == 0 || n > 65536) return reject("decode layer: n must be 1..65536");
+    if (flags & ~uint32_t(HS_SELECT_FP32_COUNTS)) return reject("decode layer: unknown flags");
+    // the scorer streams K rows of 1024 or 2048 words
+    if (row_bytes != 2048 && row_bytes != 4096)
+        return reject("decode layer: row_bytes must be 2048 (K and V arrays) or 4096 (KV records)");
+    const LayerPlan p = plan_layer(n);
+    char* ws = static_cast<char*>(workspace_dev);
+    uint32_t* partial = reinterpret_cast<uint32_t*>(ws + p.off_partial);
+    uint32_t* member = reinterpret_cast<uint32_t*>(ws + p.off_member);
+    float* logits = reinterpret_cast<float*>(ws + p.off_logits);
+    if (reinterpret_cast<uintptr_t>(q32_dev) & 3u) return reject("decode layer: q32 must be 4-byte aligned");
+    // One pass over the K rows: the ordered raw scores for the selection and,
+    // from the same registers, the attention's q32.k dots for every token
+    // (both queries are known when a layer is scored at its own step), so the
+    // attention reads only the selected V rows.
+    int rc = launch_score(q16_dev, reinterpret_cast<const uint16_t*>(k_pool_dev), row_bytes / 2,
+                          row_of_id_dev, pool_rows, n, scores_dev, n, partial, s, q32_dev, logits, n);
+    if (rc != HS_OK) return rc;
+    rc = launch_select(scores_dev, 32, n, n, alpha, ratio,
+                       flags | HS_SELECT_SCALE_RAW | HS_SELECT_REQUIRE_K | HS_SELECT_ID_ORDER, partial,
+                       ids_dev, ids_stride, counts_dev, member, status_dev, ws + p.off_select, s);
+    if (rc != HS_OK) return rc;
+    return launch_attention_logits(logits, n, v_pool_dev, row_bytes, row_of_id_dev, pool_rows, member,
+                                   n, out_dev, ws + p.off_attn, s);
+}
+
 }  // namespace hs
 
 extern "C" {
@@ -159,36 +231,30 @@ int hs_decode_layer(const uint16_t* q16_dev, const float* q32_dev, const uint8_t
                     uint32_t* counts_dev, float* out_dev, hs_status_t* status_dev,
                     void* workspace_dev, void* stream) {
     hs::clear_error();
-    if (!q16_dev || !q32_dev || !k_pool_dev || !v_pool_dev || !scores_dev || !ids_dev ||
-        !out_dev || !status_dev || !workspace_dev)
-        return hs::reject("decode layer: null pointer");
-    if (n == 0 || n > 65536) return hs::reject("decode layer: n must be 1..65536");
-    if (flags & ~uint32_t(HS_SELECT_FP32_COUNTS)) return hs::reject("decode layer: unknown flags");
-    // the scorer streams K rows of 1024 or 2048 words
-    if (row_bytes != 2048 && row_bytes != 4096)
-        return hs::reject("decode layer: row_bytes must be 2048 (K and V arrays) or 4096 (KV records)");
-    hipStream_t s = hs::as_stream(stream);
-    const hs::LayerPlan p = hs::plan_layer(n);
-    char* ws = static_cast<char*>(workspace_dev);
-    uint32_t* partial = reinterpret_cast<uint32_t*>(ws + p.off_partial);
-    uint32_t* member = reinterpret_cast<uint32_t*>(ws + p.off_member);
-    float* logits = reinterpret_cast<float*>(ws + p.off_logits);
-    if (reinterpret_cast<uintptr_t>(q32_dev) & 3u) return hs::reject("decode layer: q32 must be 4-byte aligned");
-    // One pass over the K rows: the ordered raw scores for the selection and,
-    // from the same registers, the attention's q32.k dots for every token
-    // (both queries are known when a layer is scored at its own step), so the
-    // attention reads only the selected V rows.
-    int rc = hs::launch_score(q16_dev, reinterpret_cast<const uint16_t*>(k_pool_dev),
-                              row_bytes / 2, row_of_id_dev, pool_rows, n, scores_dev, n, partial, s,
-                              q32_dev, logits, n);
+    if (!workspace_dev) return hs::reject("decode layer: null pointer");
+    return hs::decode_layer(q16_dev, q32_dev, k_pool_dev, v_pool_dev, row_bytes, row_of_id_dev,
+                            pool_rows, n, alpha, ratio, flags, scores_dev, ids_dev, ids_stride,
+                            counts_dev, out_dev, status_dev, workspace_dev, hs::as_stream(stream));
+}
+
+int hs_decode_layer_noalloc(const uint16_t* q16_dev, const float* q32_dev,
+                            const uint8_t* k_pool_dev, const uint8_t* v_pool_dev,
+                            size_t row_bytes, const int32_t* row_of_id_dev, uint32_t pool_rows,
+                            uint32_t n, float alpha, float ratio, uint32_t flags,
+                            uint16_t* scores_dev, uint32_t* ids_dev, size_t ids_stride,
+                            uint32_t* counts_dev, float* out_dev, hs_status_t* status_dev,
+                            void* stream) {
+    hs::clear_error();
+    if (n == 0 || n > HS_NOALLOC_MAX_TOKENS)
+        return hs::reject("decode layer (no allocation): n must be 1..HS_NOALLOC_MAX_TOKENS");
+    if (hs::plan_layer(n).total > sizeof(hs::scratch))
+        return hs::reject("decode layer (no allocation): the layer's scratch exceeds the device array");
+    void* ws = nullptr;
+    const int rc = hs::scratch_address(&ws);
     if (rc != HS_OK) return rc;
-    rc = hs::launch_select(scores_dev, 32, n, n, alpha, ratio,
-                           flags | HS_SELECT_SCALE_RAW | HS_SELECT_REQUIRE_K | HS_SELECT_ID_ORDER,
-                           partial, ids_dev,
-                           ids_stride, counts_dev, member, status_dev, ws + p.off_select, s);
-    if (rc != HS_OK) return rc;
-    return hs::launch_attention_logits(logits, n, v_pool_dev, row_bytes, row_of_id_dev, pool_rows,
-                                       member, n, out_dev, ws + p.off_attn, s);
+    return hs::decode_layer(q16_dev, q32_dev, k_pool_dev, v_pool_dev, row_bytes, row_of_id_dev,
+                            pool_rows, n, alpha, ratio, flags, scores_dev, ids_dev, ids_stride,
+                            counts_dev, out_dev, status_dev, ws, hs::as_stream(stream));
 }
 
 int hs_selftest_f16_checksums(uint64_t* checksums_dev, void* stream) {

@@ -383,6 +383,24 @@ int hs_decode_layer(const uint16_t *q16_dev, const float *q32_dev,
                     hs_status_t *status_dev, void *workspace_dev,
                     void *stream);
 
+/* No counterpart in the reference: hs_decode_layer for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The same layer, same arguments but no workspace:
+ * its scratch is a library-owned device array (18 MiB, one per GPU, held
+ * until the process ends), so the call performs no allocation at all.
+ * n <= HS_NOALLOC_MAX_TOKENS (HS_ERR_ARGUMENT beyond it).  Every call on a
+ * GPU shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other threads) race; order them on one stream.  The first call on a device
+ * looks up the array's device address (no allocation). */
+#define HS_NOALLOC_MAX_TOKENS 32768
+int hs_decode_layer_noalloc(const uint16_t *q16_dev, const float *q32_dev,
+                            const uint8_t *k_pool_dev, const uint8_t *v_pool_dev,
+                            size_t row_bytes, const int32_t *row_of_id_dev, uint32_t pool_rows,
+                            uint32_t n, float alpha, float ratio, uint32_t flags,
+                            uint16_t *scores_dev, uint32_t *ids_dev, size_t ids_stride,
+                            uint32_t *counts_dev, float *out_dev, hs_status_t *status_dev,
+                            void *stream);
+
 /* ---- device self checks (conversion units) ------------------------------
  * Hardware F32->F16 (RNE) over all 2^32 patterns, folded into 65536
  * per-chunk checksums (chunk = high 16 bits); see tests for the fold. */
