@@ -4,36 +4,54 @@ Headline (BASELINE.json metric, configs[1]): GQA keys scored per second for a
 decode step of 30 sparse layers at N=32768 (32 query / 8 KV heads, D=128):
 per layer the ordered-FP32 scorer over that layer's own F16 K[32768,8,128]
 (RoPE-structured synthetic keys, theta 500000) and the head-0 alpha-margin
-selection at the 20 % cap.  30 distinct 64 MiB key buffers rotate, so the
-256 MB MALL cannot serve repeats.  The layers are pipelined as the
-reference prepares history one layer early: layer l's per-head selection
-and layer l+1's scoring share one launch (hs_gqa_select_then_score), the
-scoring on the CUs the selection leaves idle.  The same step one layer at a
-time is timed as well (serial_ms_per_step) and must select the same ids.
+selection at the 20 % cap, in the reference's rank order.  30 distinct
+64 MiB key sets rotate, so the 256 MB MALL cannot serve repeats.  The step
+is the schedule a decode runs when the next layer's rehearsal query is known
+one layer early (runtime/gqa_executor.cpp:291-295, policy/
+full_gqa_runtime.cpp:493-569): layer l+1's history (the N - 1 tokens before
+the current one) is scored while layer l's selection runs, in one call
+(hs_gqa_select_then_score), and each selection first scores its own current
+token (column N - 1) from the query and the appended K row.  The same step
+one layer at a time (serial_ms_per_step) must select the same ids.
 
-Also reported on the same line:
-  roofline      the scoring kernel (dominant): algorithmic bytes per launch
-                (N*2112 + 8192) / its average duration, from HIP events
-                bracketing 30*K back-to-back scoring launches (one per layer
-                buffer) right after the timed steps, on the same stream.
-  roofline_pipelined_call
-                the timed step's dominant launches (count + combined
-                select-then-score launch): the next layer's scoring bytes
-                plus this layer's selection bytes / the call's average
-                duration over 29*K back-to-back calls.
-  layer_step    configs[2]: one full sparse layer (score over the hot pool ->
-                select at the cap -> sparse attention), microseconds per layer
-                over 30 distinct hot pools held as K and V arrays (and, for
-                comparison, as 4096 B KV records), and its algorithmic HBM
-                rate; us_per_layer_pipelined: the same 30 layers with each
-                layer's selection co-launched with the next layer's scoring
-                and its attention merge with the next layer's selection
-                count (amortized per layer; the outputs must match).
+Also on the same JSON line:
+  roofline      the timed step's dominant call, hs_gqa_select_then_score
+                (count launch + selection beside the next layer's history
+                scoring; 29 of the step's 30 layers): algorithmic bytes per
+                call / its mean duration from HIP events over back-to-back
+                calls; traffic = FETCH + WRITE bytes per call from the
+                committed counter summary.  roofline_step: the same for the
+                whole timed step.
+  kernels       each entry point of the path alone, HIP events over
+                back-to-back calls on rotating inputs: microseconds per call,
+                bytes per call and the fraction of the HBM peak.
+  layer_step    configs[2]: one full sparse layer, score -> select -> sparse
+                attention, over 30 distinct hot pools held as K and V arrays
+                (and as the reference's 4096 B KV records): hs_decode_layer,
+                whose scoring pass also writes the attention's q.k dots so the
+                attention reads only V rows; the pipelined schedule (next
+                layer's history beside this layer's selection, attention
+                reading K and V); pack and gather into batch_layout at the
+                layer's 6560 slots.
+  batch_step    configs[3]: rehearsal query on MFMA + batched score + select.
+  tier_step     configs[4]: hot/cold chain with the cold rows over the host
+                link, checked bit for bit against an all-hot pool.
   cpu_baseline  the reference's own CPU path (FullGqaCpuScorer + scaling +
                 select_gqa_scores, compiled from the reference sources into
-                oracle/_ref) on a bounded sample, timed on this host.
+                oracle/_ref) on one layer, timed on this host: median of at
+                least --cpu-runs runs, at the reference's 3 hot-scorer threads
+                and at all host cores (at most --cpu-max-threads), scoring and
+                selection timed separately.
+
+Algorithmic bytes per unit of work: scoring 2048 B of K + 64 B of scores per
+key and 8 KiB of Q per call; selection 2*32*N B of scores read + 4*32*k B of
+ids; attention 512 B per selected (id, KV head) row of the union of the 4
+query heads, + 8 KiB Q + 16 KiB out.  Materialized pack and gather writes are
+not algorithmic: their rows report the bytes the kernel must move.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --only FAMILY [--steps K]  (profiling aid: one family's
+       loop, with one plain 64 MiB copy as the counter calibration kernel)
 """
 from __future__ import annotations
 
@@ -41,6 +59,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -54,7 +73,21 @@ ALPHA = 5.0
 RATIO = 0.2
 HBM_PEAK_GBS = 8000.0
 METRIC = "GQA keys scored/s + HBM GB/s at N=32768; per-layer sparse decode step µs"
+KMAX = math.floor(N * 0.2000000029802322)  # floor(N * double(0.2f)) = 6553
+SLOTS = max(32, (KMAX + 31) // 32 * 32)  # sparse_slots (runtime/gqa_executor.cpp:145) = 6560
+WORDS = (N + 31) // 32
 SCORE_BYTES = N * 2048 + N * 64 + 8192  # K scan + F16 scores out + Q
+HIST_BYTES = (N - 1) * 2048 + (N - 1) * 64 + 8192  # a pipelined layer's history scoring
+CURRENT_BYTES = 8192 + 2048 + 64  # the current token: Q, its K row, its 32 scores
+SELECT_BYTES = 2 * 32 * N + 4 * 32 * KMAX
+MEMBER_BYTES = 4 * 32 * WORDS
+DOTS_BYTES = 32 * N * 4  # the F32 q.k dots [32][N] of the fused layer
+STEP_FAMILIES = ["step", "score", "select", "select_id", "pipe"]
+LAYER_FAMILIES = ["layer", "layer_pipe", "score_logits", "attention", "attention_logits", "pack",
+                  "gather"]
+FAMILIES = STEP_FAMILIES + LAYER_FAMILIES + ["batch", "tier"]
+PIPE_PROFILE = "profiles/select_then_score_hbm_counters.md"
+STEP_PROFILE = "profiles/step_hbm_counters.md"
 
 
 def log(msg):
@@ -66,85 +99,495 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=40)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--cpu-seconds", type=float, default=10.0,
-                   help="bounded CPU-baseline sample duration")
     p.add_argument("--layer-steps", type=int, default=20)
-    p.add_argument("--only", choices=["score", "select", "select_id", "pipe", "layer", "batch",
-                                      "tier"],
-                   default=None,
-                   help="profiling aid: run just one kernel family over the 30 layers "
-                        "(prints its own timing line, not the benchmark JSON)")
+    p.add_argument("--cpu-runs", type=int, default=5,
+                   help="minimum CPU-baseline runs per thread setting (the median is reported)")
+    p.add_argument("--cpu-seconds", type=float, default=5.0,
+                   help="minimum CPU time per thread setting")
+    p.add_argument("--cpu-max-threads", type=int, default=16,
+                   help="cap on the all-cores setting (the GPU box's CPU share)")
+    p.add_argument("--only", choices=FAMILIES, default=None,
+                   help="profiling aid: run one family's loop only and print its time "
+                        "(not the benchmark line)")
     return p.parse_args()
 
 
-def union_bytes(hs, member, n):
-    """sum over KV heads g of |U_g| * 512 B, U_g = union of heads 4g..4g+3."""
-    import torch
-    words = (n + 31) // 32
-    m = member.view(32, words).to(torch.int64) & 0xFFFFFFFF
-    total = 0
-    for g in range(8):
-        u = m[4 * g] | m[4 * g + 1] | m[4 * g + 2] | m[4 * g + 3]
-        total += int(sum(bin(int(x)).count("1") for x in u.cpu().tolist()))
-    return total * 512, total
-
-
-def cpu_baseline(q16_host, k_host, seconds):
-    """Time the reference CPU scoring+selection on one layer's inputs."""
-    import numpy as np
-    import oracle
-    threads = os.cpu_count() or 1
-    ref = oracle.ref()
-    kind = "reference" if ref is not None else "port"
-    table = None
-    if ref is not None:
-        root = np.float32(math.sqrt(128.0))
-        table = np.array([ref.L.hsref_half_bits(float(np.float32(ref.L.hsref_half_value(b)) / root))
-                          for b in range(65536)], dtype=np.uint16)
-    port = oracle.port()
-    keys = 0
-    runs = 0
-    t0 = time.perf_counter()
-    while True:
-        if ref is not None:
-            raw = ref.score(q16_host, k_host, N, 1024, threads=threads, impl=0)
-            scaled = table[raw]
-            rc, *_ = ref.select(scaled, 32, N, N, ALPHA, RATIO, width=int(N * 0.2) + 1)
-        else:
-            raw = port.score(q16_host, k_host, N, 1024)
-            rc, *_ = port.select(port.scale(raw), 32, N, N, ALPHA, RATIO)
-        assert rc == 0
-        keys += N
-        runs += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = time.perf_counter() - t0
-    return {
-        "value": keys / dt, "unit": "keys/s", "cores": threads if kind == "reference" else 1,
-        "kind": kind,
-        "sample": (f"{runs} x one layer (N={N}, score with FullGqaCpuScorer automatic impl on "
-                   f"{threads} threads + scaling + select_gqa_scores alpha {ALPHA} cap 0.2) "
-                   f"= {keys} keys in {dt:.1f} s"),
-    }
-
-
-TRAFFIC_PROFILE = "profiles/score_kernel_hbm_counters.md"
-
-
-
-
-PIPE_TRAFFIC_PROFILE = "profiles/select_then_score_hbm_counters.md"
-
-
-def pmc_traffic(profile=TRAFFIC_PROFILE, key="traffic_bytes_per_launch"):
-    """HBM bytes per launch (or call) from a committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (copy-calibrated); None if absent."""
+def pmc_traffic(profile, key):
+    """HBM bytes from a committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (copy-calibrated); None if absent."""
     import re
-    path = Path(__file__).resolve().parent / profile
+    path = ROOT / profile
     if not path.exists():
         return None
     m = re.search(key + r":\s*(\d+)", path.read_text())
     return int(m.group(1)) if m else None
+
+
+class Gpu:
+    """Library, torch, the launch stream and the timing helper."""
+
+    def __init__(self):
+        import ctypes
+        import torch
+        import hillserve_amd as hs
+        from hillserve_amd import ops
+        assert torch.cuda.is_available(), "no GPU visible"
+        self.torch, self.hs, self.ops, self.ctypes = torch, hs, ops, ctypes
+        self.dev = torch.device("cuda:0")
+        torch.cuda.set_device(self.dev)
+        self.stream = torch.cuda.current_stream()
+        self.sp = ctypes.c_void_p(self.stream.cuda_stream)
+        self.L = hs.lib()
+
+    def vp(self, t):
+        return None if t is None else self.ctypes.c_void_p(t.data_ptr())
+
+    def timed_us(self, fn, reps, per_call=1):
+        """Mean microseconds per call: HIP events on the launch stream around
+        `reps` back-to-back runs of fn, each making `per_call` calls."""
+        torch = self.torch
+        b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        b.record(self.stream)
+        for _ in range(reps):
+            fn()
+        e.record(self.stream)
+        torch.cuda.synchronize()
+        return 1e3 * b.elapsed_time(e) / (reps * per_call)
+
+    def calibration_copy(self):
+        """One plain 64 MiB device copy (64 MiB read, 64 MiB written): the
+        HBM counters are scaled by what they read for it."""
+        src = self.torch.empty(N * 1024, dtype=self.torch.float16, device=self.dev)
+        self.torch.empty_like(src).copy_(src)
+        self.torch.cuda.synchronize()
+
+
+def kernel_row(family, call, us, nbytes, basis="algorithmic"):
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"family": family, "call": call, "us": round(us, 3), "bytes": nbytes,
+            "bytes_basis": basis, "gbps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def log_rows(rows):
+    for r in rows:
+        log(f"  {r['family']:>16s}: {r['us']:8.2f} us  {r['gbps']:6.0f} GB/s  "
+            f"({100 * r['frac']:.1f} %)  {r['call']}")
+
+
+def union_rows(torch, member):
+    """sum over KV heads of |U_g|, U_g = union of query heads 4g..4g+3."""
+    m = member.view(32, WORDS).to(torch.int64) & 0xFFFFFFFF
+    total = 0
+    for kv in range(8):
+        u = (m[4 * kv] | m[4 * kv + 1] | m[4 * kv + 2] | m[4 * kv + 3]).cpu().tolist()
+        total += sum(bin(int(x)).count("1") for x in u)
+    return total
+
+
+# ---- configs[1]: 30 layers of score + select ---------------------------------------
+
+class Step:
+    """30 layers of packed K, their queries, and the pipelined
+    calls bound once to fixed buffers."""
+
+    def __init__(self, g):
+        torch, ops, dev = g.torch, g.ops, g.dev
+        self.g = g
+        log("configs[1]: 30 layers of K[32768,8,128] F16 (1.9 GB) + queries")
+        self.keys = [torch.empty(N * 1024, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
+        self.qs = [torch.empty(4096, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
+        for layer in range(LAYERS):
+            ops.fill_rope_keys(self.keys[layer], N, 1024, 8, seed=1000 + layer, theta=500000.0)
+            ops.fill_gaussian(self.qs[layer], seed=5000 + layer)
+        self.raws = [torch.empty((32, N), dtype=torch.float16, device=dev) for _ in range(2)]
+        self.partials = [torch.empty((N + 63) // 64, dtype=torch.int32, device=dev)
+                         for _ in range(2)]
+        self.ids = torch.empty((32, KMAX), dtype=torch.int32, device=dev)
+        self.counts = torch.empty(32, dtype=torch.int32, device=dev)
+        self.member = torch.empty((32, WORDS), dtype=torch.int32, device=dev)
+        self.status = ops.new_status(dev)
+        # one status per layer: a failed selection of any layer of the step
+        # stays visible after the step
+        self.statuses = [ops.new_status(dev) for _ in range(LAYERS)]
+        self.ws = ops.workspace(ops.select_workspace_bytes(32, N), dev)
+        # the current token of each layer: column N - 1, the last K row
+        self.cur_keys = [self.keys[layer][(N - 1) * 1024:] for layer in range(LAYERS)]
+        self.pipe_calls = [ops.prepare_select_then_score([self.sel_job(l)], [self.history(l + 1)],
+                                                         32, ALPHA, RATIO, scale_raw=True)
+                           for l in range(LAYERS - 1)]
+        self.last_select = ops.prepare_select_batched([self.sel_job(LAYERS - 1)], 32, ALPHA,
+                                                      RATIO, scale_raw=True)
+        torch.cuda.synchronize()
+
+    def sel_job(self, l):
+        return dict(scores=self.raws[l % 2], n=N, head0_partial=self.partials[l % 2],
+                    ids=self.ids, ids_stride=KMAX, counts=self.counts, status=self.statuses[l],
+                    ws=self.ws, current_q=self.qs[l], current_key=self.cur_keys[l])
+
+    def history(self, l):
+        return dict(q16=self.qs[l], keys=self.keys[l], tokens=N - 1, out=self.raws[l % 2],
+                    score_stride=N, head0_partial=self.partials[l % 2])
+
+    def score_history0(self):
+        self.g.ops.score(self.qs[0], self.keys[0], N - 1, out=self.raws[0], score_stride=N,
+                         head0_partial=self.partials[0])
+
+    def step(self):
+        """The timed step: layer 0's history, then per layer its selection
+        (completing its current token) beside the next layer's history."""
+        self.score_history0()
+        for call in self.pipe_calls:
+            call()
+        self.last_select()
+
+    def serial_step(self):
+        """One layer at a time: score all N tokens, then select."""
+        for layer in range(LAYERS):
+            self.g.ops.score(self.qs[layer], self.keys[layer], N, out=self.raws[0],
+                             head0_partial=self.partials[0])
+            self.select(id_order=False)
+
+    def select(self, id_order, member=None):
+        self.g.ops.select(self.raws[0], 32, N, N, ALPHA, RATIO, scale_raw=True, id_order=id_order,
+                          head0_partial=self.partials[0], ids=self.ids, ids_stride=KMAX,
+                          counts=self.counts, member=member, status=self.status, ws=self.ws)
+
+    def check_statuses(self):
+        for l, stt in enumerate(self.statuses):
+            st = self.g.ops.read_status(stt)
+            assert st["code"] == 0 and st["k"] == KMAX, (l, st)
+
+    def families(self):
+        """name -> (callable, calls per run); each run rotates over the layers."""
+        ops = self.g.ops
+
+        def score():
+            for layer in range(LAYERS):
+                ops.score(self.qs[layer], self.keys[layer], N, out=self.raws[0],
+                          head0_partial=self.partials[0])
+
+        def select():
+            for _ in range(LAYERS):
+                self.select(id_order=False)
+
+        def select_id():
+            for _ in range(LAYERS):
+                self.select(id_order=True, member=self.member)
+
+        def pipe():
+            for call in self.pipe_calls:
+                call()
+
+        return {"step": (self.step, 1), "score": (score, LAYERS), "select": (select, LAYERS),
+                "select_id": (select_id, LAYERS), "pipe": (pipe, LAYERS - 1)}
+
+    def prepare(self, family):
+        """Inputs a family's loop expects: scores for the selections, layer 0's
+        history for the pipelined calls."""
+        if family in ("select", "select_id"):
+            self.g.ops.score(self.qs[0], self.keys[0], N, out=self.raws[0],
+                             head0_partial=self.partials[0])
+        elif family == "pipe":
+            self.score_history0()
+
+
+def step_leg(g, args):
+    torch = g.torch
+    s = Step(g)
+    for _ in range(args.warmup):
+        s.step()
+    s.check_statuses()
+    step_us = g.timed_us(s.step, args.steps)
+    s.check_statuses()
+    last_ids = s.ids.clone()
+    s.serial_step()
+    torch.cuda.synchronize()
+    assert torch.equal(s.ids, last_ids), "pipelined and serial selections differ"
+    serial_us = g.timed_us(s.serial_step, args.steps)
+
+    fams = s.families()
+    reps = max(4, args.steps // 2)
+    rows = []
+    specs = [
+        ("score", "hs_gqa_score: score_kernel, all N keys", SCORE_BYTES),
+        ("select", "hs_gqa_select, rank order: count_kernel + head_select_kernel",
+         SELECT_BYTES),
+        ("select_id", "hs_gqa_select, id order + membership: count_kernel + head_select_kernel",
+         SELECT_BYTES + MEMBER_BYTES),
+        ("pipe", "hs_gqa_select_then_score: count_kernel (+ current token) + select_score_kernel "
+                 "(selection beside the next layer's history scoring)",
+         HIST_BYTES + SELECT_BYTES + CURRENT_BYTES),
+    ]
+    pipe_us = None
+    for name, call, nbytes in specs:
+        s.prepare(name)
+        fn, per = fams[name]
+        fn()
+        us = g.timed_us(fn, reps, per)
+        rows.append(kernel_row(name, call, us, nbytes))
+        if name == "pipe":
+            pipe_us = us
+    s.check_statuses()
+    step_bytes = LAYERS * (HIST_BYTES + SELECT_BYTES + CURRENT_BYTES)
+    out = {
+        "step_us": step_us, "serial_us": serial_us, "pipe_us": pipe_us,
+        "step_bytes": step_bytes, "kernels": rows,
+        "q_host": s.qs[0].cpu().view(torch.int16).numpy(),
+        "k_host": s.keys[0].cpu().view(torch.int16).numpy(),
+    }
+    log(f"configs[1]: {step_us / 1e3:.3f} ms/step pipelined ({serial_us / 1e3:.3f} one layer at a "
+        f"time), {LAYERS * N / (step_us * 1e-6) / 1e9:.2f} G keys/s, "
+        f"{step_bytes / (step_us * 1e-6) / 1e9:.0f} GB/s algorithmic")
+    log_rows(rows)
+    return out
+
+
+# ---- configs[2]: full sparse layers over 30 hot pools --------------------------------
+
+class Pools:
+    """30 hot pools of N tokens: K and V arrays of 2048 B rows (split), or the
+    reference's 4096 B KV records holding the same rows."""
+
+    def __init__(self, g, split):
+        torch, ops, dev = g.torch, g.ops, g.dev
+        self.split = split
+        self.row_bytes = 2048 if split else 4096
+        log(f"configs[2]: 30 hot pools of {N} tokens as "
+            f"{'K and V arrays' if split else '4096 B KV records'} (3.8 GB)")
+        self.k, self.v = [], []
+        for layer in range(LAYERS):
+            if split:
+                kp = torch.empty(N * 1024, dtype=torch.float16, device=dev)
+                vpool = torch.empty(N * 1024, dtype=torch.float16, device=dev)
+                ops.fill_rope_keys(kp, N, 1024, 8, seed=2000 + layer, theta=500000.0)
+                ops.fill_gaussian(vpool, seed=3000 + layer)
+            else:
+                kp = torch.empty(N * 2048, dtype=torch.float16, device=dev)
+                ops.fill_rope_keys(kp, N, 2048, 8, seed=2000 + layer, theta=500000.0)
+                tmp = torch.empty((N, 1024), dtype=torch.float16, device=dev)
+                ops.fill_gaussian(tmp, seed=3000 + layer)
+                kp.view(N, 2048)[:, 1024:].copy_(tmp)
+                vpool = None
+            self.k.append(kp)
+            self.v.append(vpool)
+
+    def kv(self, l):
+        """(K base, V base) pointers as the C entry points take them."""
+        import ctypes
+        kp = self.k[l]
+        if self.split:
+            return ctypes.c_void_p(kp.data_ptr()), ctypes.c_void_p(self.v[l].data_ptr())
+        return ctypes.c_void_p(kp.data_ptr()), ctypes.c_void_p(kp.data_ptr() + 2048)
+
+
+class LayerBench:
+    """queries, the layer's buffers, the pipelined calls and the
+    pack / gather inputs over K and V array pools (and KV-record pools)."""
+
+    def __init__(self, g, records):
+        torch, ops, dev = g.torch, g.ops, g.dev
+        self.g = g
+        self.rec = Pools(g, split=False) if records else None
+        self.c = Pools(g, split=True)
+        self.qs = [ops.fill_gaussian(torch.empty(4096, dtype=torch.float16, device=dev), 5000 + l)
+                   for l in range(LAYERS)]
+        self.q32s = [torch.empty((32, 128), dtype=torch.float32, device=dev).normal_(
+            generator=torch.Generator(device=dev).manual_seed(l)) for l in range(LAYERS)]
+        self.raw = torch.empty((32, N), dtype=torch.float16, device=dev)
+        self.ids = torch.empty((32, KMAX), dtype=torch.int32, device=dev)
+        self.counts = torch.empty(32, dtype=torch.int32, device=dev)
+        self.out = torch.empty((32, 128), dtype=torch.float32, device=dev)
+        self.status = ops.new_status(dev)
+        self.lws = ops.workspace(ops.decode_layer_workspace_bytes(N), dev)
+        self.part = torch.empty((N + 63) // 64, dtype=torch.int32, device=dev)
+        self.member = torch.empty((32, WORDS), dtype=torch.int32, device=dev)
+        self.dots = torch.empty((32, N), dtype=torch.float32, device=dev)
+        self.aws = ops.workspace(ops.attention_workspace_bytes(N), dev)
+        # the pipelined schedule's buffers
+        self.raws = [torch.empty((32, N), dtype=torch.float16, device=dev) for _ in range(2)]
+        self.parts = [torch.empty((N + 63) // 64, dtype=torch.int32, device=dev) for _ in range(2)]
+        self.member_p = torch.empty((32, WORDS), dtype=torch.int32, device=dev)
+        self.sws = ops.workspace(ops.select_workspace_bytes(32, N), dev)
+        self.statuses = [ops.new_status(dev) for _ in range(LAYERS)]
+        flags = dict(scale_raw=True, require_k=True, id_order=True)
+        self.calls = [ops.prepare_select_then_score([self.job(l)], [self.hist(l + 1)], 32, ALPHA,
+                                                    RATIO, **flags) for l in range(LAYERS - 1)]
+        self.last_call = ops.prepare_select_batched([self.job(LAYERS - 1)], 32, ALPHA, RATIO,
+                                                    **flags)
+        # pack / gather at the layer's sparse_slots (one query position)
+        self.lens = torch.full((32,), KMAX, dtype=torch.int32, device=dev)
+        self.positions = torch.tensor([N - 1], dtype=torch.int64, device=dev)
+        self.pk = torch.empty(SLOTS * 32 * 128, dtype=torch.float16, device=dev)
+        self.pv = torch.empty_like(self.pk)
+        self.pm = torch.empty(32 * 64 * SLOTS, dtype=torch.float32, device=dev)
+        self.pst = ops.new_status(dev)
+        self.gmap = torch.full((32, SLOTS), -1, dtype=torch.int32, device=dev)
+        self.gst = ops.new_status(dev)
+        torch.cuda.synchronize()
+
+    def job(self, l):
+        return dict(scores=self.raws[l % 2], n=N, head0_partial=self.parts[l % 2], ids=self.ids,
+                    ids_stride=KMAX, counts=self.counts, member=self.member_p,
+                    status=self.statuses[l], ws=self.sws, current_q=self.qs[l],
+                    current_key=self.c.k[l][(N - 1) * 1024:])
+
+    def hist(self, l):
+        return dict(q16=self.qs[l], keys=self.c.k[l], tokens=N - 1, out=self.raws[l % 2],
+                    score_stride=N, head0_partial=self.parts[l % 2])
+
+    def decode_pass(self, pools):
+        ops = self.g.ops
+        for l in range(LAYERS):
+            ops.decode_layer(self.qs[l], self.q32s[l], pools.k[l], N, ALPHA, RATIO,
+                             scores=self.raw, ids=self.ids, ids_stride=KMAX, counts=self.counts,
+                             out=self.out, status=self.status, ws=self.lws, v_pool=pools.v[l],
+                             row_bytes=pools.row_bytes)
+
+    def pipelined_pass(self):
+        """Layer 0's history; per layer its selection (completing its current
+        token) beside the next layer's history, then its attention (K and V:
+        the current query is not known early, so no dots are precomputed)."""
+        ops = self.g.ops
+        ops.score(self.qs[0], self.c.k[0], N - 1, out=self.raws[0], score_stride=N,
+                  head0_partial=self.parts[0])
+        for l in range(LAYERS):
+            (self.calls[l] if l < LAYERS - 1 else self.last_call)()
+            ops.sparse_attention(self.q32s[l], self.c.k[l], N, self.member_p, out=self.out,
+                                 ws=self.aws, v_pool=self.c.v[l], row_bytes=2048)
+
+    def select_last(self):
+        """The last layer's scores, dots and id-order selection with
+        membership: the inputs of the attention, pack and gather loops."""
+        ops, l = self.g.ops, LAYERS - 1
+        ops.score_logits(self.qs[l], self.q32s[l], self.c.k[l], N, out=self.raw,
+                         head0_partial=self.part, logits=self.dots)
+        ops.select(self.raw, 32, N, N, ALPHA, RATIO, scale_raw=True, id_order=True,
+                   head0_partial=self.part, ids=self.ids, ids_stride=KMAX, counts=self.counts,
+                   member=self.member, status=self.status, ws=self.sws)
+        self.gmap[:, :KMAX] = self.ids
+        st = ops.read_status(self.status)
+        assert st["code"] == 0 and st["k"] == KMAX, st
+
+    def families(self):
+        g, ops, L = self.g, self.g.ops, self.g.L
+        c = self.c
+
+        def layer():
+            self.decode_pass(c)
+
+        def score_logits():
+            for l in range(LAYERS):
+                ops.score_logits(self.qs[l], self.q32s[l], c.k[l], N, out=self.raw,
+                                 head0_partial=self.part, logits=self.dots)
+
+        def attention():
+            for l in range(LAYERS):
+                ops.sparse_attention(self.q32s[l], c.k[l], N, self.member, out=self.out,
+                                     ws=self.aws, v_pool=c.v[l], row_bytes=2048)
+
+        def attention_logits():
+            for l in range(LAYERS):
+                ops.sparse_attention_logits(self.dots, c.v[l], N, self.member, out=self.out,
+                                            ws=self.aws)
+
+        def pack():
+            for l in range(LAYERS):
+                kp, vp = c.kv(l)
+                g.hs.check(L.hs_gqa_pack(kp, vp, 2048, N, None, N, g.vp(self.ids), g.vp(self.lens),
+                                         KMAX, g.vp(self.positions), 1, SLOTS, g.vp(self.pk),
+                                         g.vp(self.pv), g.vp(self.pm), g.vp(self.pst), g.sp))
+
+        def gather():
+            for l in range(LAYERS):
+                g.hs.check(L.hs_gqa_gather_rows(g.vp(self.rec.k[l]), N, None, 0, g.vp(self.gmap),
+                                                SLOTS, g.vp(self.pk), g.vp(self.pv),
+                                                g.vp(self.gst), g.sp))
+
+        fams = {"layer": (layer, LAYERS), "layer_pipe": (self.pipelined_pass, LAYERS),
+                "score_logits": (score_logits, LAYERS), "attention": (attention, LAYERS),
+                "attention_logits": (attention_logits, LAYERS), "pack": (pack, LAYERS)}
+        if self.rec is not None:
+            fams["gather"] = (gather, LAYERS)
+        return fams
+
+
+def layer_leg(g, args):
+    torch, ops = g.torch, g.ops
+    b = LayerBench(g, records=True)
+    b.decode_pass(b.rec)
+    st = ops.read_status(b.status)
+    assert st["code"] == 0 and st["k"] == KMAX, st
+    rec_us = g.timed_us(lambda: b.decode_pass(b.rec), args.layer_steps, LAYERS)
+    rec_out = b.out.clone()
+    b.decode_pass(b.c)
+    st = ops.read_status(b.status)
+    assert st["code"] == 0 and st["k"] == KMAX, st
+    # the arrays hold the records' rows: the same outputs, bit for bit
+    assert torch.equal(b.out, rec_out), "K and V arrays and 4096 B KV records disagree"
+    serial_out, serial_ids = b.out.clone(), b.ids.clone()
+    us = g.timed_us(lambda: b.decode_pass(b.c), args.layer_steps, LAYERS)
+
+    b.pipelined_pass()
+    torch.cuda.synchronize()
+    for stt in b.statuses:
+        assert ops.read_status(stt)["code"] == 0
+    assert torch.equal(b.ids, serial_ids), "pipelined and one-layer-at-a-time ids differ"
+    # the pipelined attention forms its dots itself (MFMA, split F32 query):
+    # the same output to about 1e-6 relative
+    rel = float(((b.out - serial_out).norm(dim=1) / serial_out.norm(dim=1)).max())
+    assert rel <= 1e-4, f"pipelined and fused-layer attention differ: {rel:.3g}"
+    pipe_us = g.timed_us(b.pipelined_pass, args.layer_steps, LAYERS)
+
+    b.select_last()
+    union = union_rows(torch, b.member)
+    ubytes = union * 512
+    fams = b.families()
+    reps = max(4, args.layer_steps // 2)
+    pack_read = 32 * KMAX * 512
+    pack_write = 2 * SLOTS * 32 * 128 * 2 + 4 * 32 * 64 * SLOTS
+    specs = [
+        ("score_logits", "hs_gqa_score_logits: score_logits_kernel (scores + F32 q.k dots "
+                         "on MFMA)", SCORE_BYTES + 16384 + DOTS_BYTES, "algorithmic + dots written"),
+        ("attention", "hs_gqa_sparse_attention: attn_partial_kernel (K and V rows) + "
+                      "attn_combine_kernel", ubytes + 8192 + 16384, "algorithmic"),
+        ("attention_logits", "hs_gqa_sparse_attention_logits: attn_v_kernel (V rows + the "
+                             "selected dots) + attn_combine_kernel",
+         union * 256 + 32 * KMAX * 4 + 16384, "V rows + selected dots + out"),
+        ("pack", f"hs_gqa_pack: {SLOTS} slots, 1 query position, K and V arrays",
+         pack_read + pack_write, "moved: rows read + K, V, mask written"),
+        ("gather", f"hs_gqa_gather_rows: {SLOTS} slots from 4096 B records",
+         pack_read + 2 * SLOTS * 32 * 128 * 2, "moved: rows read + K, V written"),
+    ]
+    rows = []
+    for name, call, nbytes, basis in specs:
+        fn, per = fams[name]
+        fn()
+        rows.append(kernel_row(name, call, g.timed_us(fn, reps, per), nbytes, basis))
+    assert ops.read_status(b.pst)["code"] == 0, ops.read_status(b.pst)
+    assert ops.read_status(b.gst)["code"] == 0, ops.read_status(b.gst)
+    # the layer's algorithmic bytes: scoring, the scores read by the
+    # selection, ids, every selected (id, KV head) K and V row once
+    layer_bytes = SCORE_BYTES + SELECT_BYTES + ubytes + 8192 + 16384
+    gbs = layer_bytes / (us * 1e-6) / 1e9
+    out = {
+        "workload": "configs[2]: score over the hot pool + select at the cap + sparse attention",
+        "pool_layout": "K and V arrays, 2048 B rows each",
+        "us_per_layer": us, "us_per_layer_kv_records": rec_us, "us_per_layer_pipelined": pipe_us,
+        "algorithmic_bytes": layer_bytes, "achieved_gbps": gbs,
+        "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
+        "pipelined_gbps": layer_bytes / (pipe_us * 1e-6) / 1e9,
+        "k": KMAX, "union_rows": union, "sparse_slots": SLOTS, "kernels": rows,
+        "schedule": "hs_decode_layer: score_logits_kernel -> count_kernel -> head_select_kernel "
+                    "(id order) -> attn_v_kernel -> attn_combine_kernel; pipelined: "
+                    "hs_gqa_select_then_score + hs_gqa_sparse_attention (K and V)",
+    }
+    log(f"configs[2]: {us:.1f} us/layer (K and V arrays; {rec_us:.1f} us over 4096 B records; "
+        f"{pipe_us:.1f} us per layer pipelined), {gbs:.0f} GB/s algorithmic "
+        f"({100 * gbs / HBM_PEAK_GBS:.1f} % of peak), union {union} rows")
+    log_rows(rows)
+    del b
+    return out
 
 
 BATCH = 16
@@ -152,7 +595,7 @@ REHEARSAL_FLOPS = 2 * BATCH * 4096 * 4096
 REHEARSAL_BYTES = 4096 * 4096 * 2 + 2 * BATCH * 4096 * 2  # Wq + hidden + q
 
 
-def batch_leg(args, hs, ops, torch, stream, dev):
+def batch_leg(g, args):
     """16 decode sequences (N_i in 8192..32768, multiples of 64).
     One step = rehearsal query (RMS norm, BF16 Wq on MFMA, RoPE) for the
     batch, batched ordered-FP32 scoring of every sequence's keys, batched
@@ -160,8 +603,9 @@ def batch_leg(args, hs, ops, torch, stream, dev):
     prebuilt job tables, so the timed loop is device work only."""
     import ctypes
     import numpy as np
-    g = np.random.default_rng(7)
-    ns = [int(x) * 64 for x in g.integers(8192 // 64, 32768 // 64 + 1, size=BATCH)]
+    hs, ops, torch, stream, dev = g.hs, g.ops, g.torch, g.stream, g.dev
+    rg = np.random.default_rng(7)
+    ns = [int(x) * 64 for x in rg.integers(8192 // 64, 32768 // 64 + 1, size=BATCH)]
     keys = [torch.empty(n * 1024, dtype=torch.float16, device=dev) for n in ns]
     for i, (k, n) in enumerate(zip(keys, ns)):
         ops.fill_rope_keys(k, n, 1024, 8, seed=7000 + i, theta=500000.0)
@@ -198,21 +642,24 @@ def batch_leg(args, hs, ops, torch, stream, dev):
     def scoring():
         hs.check(L.hs_gqa_score_batched(score_p, BATCH, sp))
 
+    def selection():
+        hs.check(L.hs_gqa_select_batched(sel_p, BATCH, 32, ALPHA, RATIO, hs.HS_SELECT_SCALE_RAW, sp))
+
     def step():
         rehearsal()
         scoring()
-        hs.check(L.hs_gqa_select_batched(sel_p, BATCH, 32, ALPHA, RATIO, hs.HS_SELECT_SCALE_RAW, sp))
+        selection()
 
     def timed(fn, reps):
-        b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        b.record(stream)
-        for _ in range(reps):
-            fn()
-        e.record(stream)
-        torch.cuda.synchronize()
-        return 1e3 * b.elapsed_time(e) / reps
+        return g.timed_us(fn, reps)
 
+    if args.only == "batch":
+        g.calibration_copy()
+        for _ in range(max(2, args.warmup)):
+            step()
+        print(f"only batch: {timed(step, args.steps):.2f} us per step", flush=True)
+        del keys
+        return {}
     for _ in range(max(2, args.warmup)):
         step()
     torch.cuda.synchronize()
@@ -232,13 +679,25 @@ def batch_leg(args, hs, ops, torch, stream, dev):
         rehearsal()
         e.record(stream)
         scoring()
-        hs.check(L.hs_gqa_select_batched(sel_p, BATCH, 32, ALPHA, RATIO, hs.HS_SELECT_SCALE_RAW, sp))
+        selection()
     torch.cuda.synchronize()
     rehearsal_us = 1e3 * sum(b.elapsed_time(e) for b, e in marks) / reps
     score_us = timed(scoring, reps)
+    select_us = timed(selection, reps)
     total = sum(ns)
     score_bytes = sum(n * 2112 + 8192 for n in ns)
+    select_bytes = sum(2 * 32 * n + 4 * 32 * k for n, k in zip(ns, kmaxes))
+    kernels = [
+        kernel_row("rehearsal", f"hs_rehearsal_query: rehearsal_kernel, batch {BATCH} (Wq cold), "
+                   f"{100 * REHEARSAL_FLOPS / (rehearsal_us * 1e-6) / 2.5e15:.2f} % of the dense "
+                   "bf16 MFMA peak", rehearsal_us, REHEARSAL_BYTES),
+        kernel_row("score_batched", f"hs_gqa_score_batched: {BATCH} sequences, {total} keys",
+                   score_us, score_bytes),
+        kernel_row("select_batched", f"hs_gqa_select_batched: {BATCH} sequences, rank order",
+                   select_us, select_bytes),
+    ]
     out = {
+        "kernels": kernels,
         "workload": "configs[3]: 16 sequences, rehearsal query on MFMA + batched score + "
                     "batched rank-order select",
         "sequences": BATCH, "tokens": ns, "total_keys": total,
@@ -248,11 +707,14 @@ def batch_leg(args, hs, ops, torch, stream, dev):
         "rehearsal_gbps": REHEARSAL_BYTES / (rehearsal_us * 1e-6) / 1e9,
         "score_batched_us": score_us,
         "score_batched_gbps": score_bytes / (score_us * 1e-6) / 1e9,
+        "select_batched_us": select_us,
     }
     log(f"configs[3]: {step_us:.1f} us/step for {total} keys over {BATCH} sequences = "
         f"{out['keys_per_s']/1e9:.2f} G keys/s; rehearsal {rehearsal_us:.2f} us "
         f"({out['rehearsal_gbps']:.0f} GB/s, MFMA {100*out['rehearsal_mfma_util']:.2f} %), "
-        f"batched score {score_us:.1f} us ({out['score_batched_gbps']:.0f} GB/s)")
+        f"batched score {score_us:.1f} us ({out['score_batched_gbps']:.0f} GB/s), batched "
+        f"select {select_us:.1f} us")
+    log_rows(kernels)
     del keys
     return out
 
@@ -260,7 +722,7 @@ def batch_leg(args, hs, ops, torch, stream, dev):
 TIER_SEQS, TIER_N, TIER_PHYS = 8, 32768, 2
 
 
-def tier_leg(args, hs, ops, torch, stream, dev):
+def tier_leg(g, args):
     """8 sequences x N = 32768, half of the 64-token blocks hot
     (seeded permutation).  Hot rows sit in an HBM pool followed by staging
     rows; cold rows sit in a pinned SegmentedKVStore image per sequence.  The
@@ -273,11 +735,12 @@ def tier_leg(args, hs, ops, torch, stream, dev):
     A step is 30 layers over TIER_PHYS distinct physical layers."""
     import ctypes
     import numpy as np
+    hs, ops, torch, stream, dev = g.hs, g.ops, g.torch, g.stream, g.dev
     L = hs.lib()
     vp = lambda t: ctypes.c_void_p(t.data_ptr())
-    g = np.random.default_rng(11)
+    rg = np.random.default_rng(11)
     blocks = TIER_N // 64
-    hot_blocks = [np.sort(g.permutation(blocks)[: blocks // 2]) for _ in range(TIER_SEQS)]
+    hot_blocks = [np.sort(rg.permutation(blocks)[: blocks // 2]) for _ in range(TIER_SEQS)]
     hot_rows = (blocks // 2) * 64
     cold_rows = TIER_N - hot_rows
     side = torch.cuda.Stream(device=dev)
@@ -451,7 +914,10 @@ def tier_leg(args, hs, ops, torch, stream, dev):
         "cold_key_scoring": "GPU: every token's K is HBM-resident (the raw-K score file held in HBM); "
                             "cold 4096 B rows come over the host link for the selected tokens",
         "ms_per_step": step_ms, "main_stream_ms": main_ms, "cold_fetch_ms": cold_ms,
-        "overlap_fraction": overlap, "cold_rows_per_seq_layer": sum(counts) / len(counts),
+        "overlap_fraction": overlap,
+        # at most the main stream's time can hide cold-fetch time
+        "overlap_ceiling": min(1.0, main_ms / cold_ms),
+        "cold_rows_per_seq_layer": sum(counts) / len(counts),
         "cold_link_gbps": cold_bytes / (cold_ms * 1e-3) / 1e9,
     }
     log(f"configs[4]: {step_ms:.1f} ms/step (main stream alone {main_ms:.1f} ms, cold fetch alone "
@@ -462,383 +928,167 @@ def tier_leg(args, hs, ops, torch, stream, dev):
     return out
 
 
-def profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status, ws, kmax,
-                 pipe_calls):
-    """Back-to-back launches of one kernel family over the 30 layers
-    (pipe: the 29 select-then-score calls of the pipelined step)."""
-    def run():
-        if args.only == "pipe":
-            for call in pipe_calls:
-                call()
-            return
-        for layer in range(LAYERS):
-            if args.only == "score":
-                ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
+
+
+# ---- the reference CPU path ------------------------------------------------------
+
+def cpu_baseline(args, q_host, k_host):
+    """The compiled reference (oracle/_ref): FullGqaCpuScorer (automatic
+    implementation) over one layer's N keys, then the scaling of
+    policy/full_gqa_runtime.cpp:571 and select_gqa_scores, timed
+    separately.  Median of at least --cpu-runs runs (and --cpu-seconds) per
+    setting: the reference's 3 hot-scorer threads (policy/
+    full_gqa_runtime.hpp:27; its 1 cold-scorer thread has no cold keys here)
+    and all host cores up to --cpu-max-threads.  Without the reference
+    build: the C restatement on one thread (kind "port")."""
+    import numpy as np
+    import oracle
+    ref = oracle.ref()
+    port = oracle.port()
+    q16 = q_host.view(np.uint16)
+    k16 = k_host.view(np.uint16)
+    host = os.cpu_count() or 1
+    all_cores = max(1, min(host, args.cpu_max_threads))
+    settings = sorted({min(3, all_cores), all_cores}) if ref is not None else [1]
+    table = None
+    if ref is not None:
+        root = np.float32(math.sqrt(128.0))
+        table = np.array([ref.L.hsref_half_bits(float(np.float32(ref.L.hsref_half_value(b)) / root))
+                          for b in range(65536)], dtype=np.uint16)
+    results = []
+    for threads in settings:
+        score_s, select_s = [], []
+        t_start = time.perf_counter()
+        while (len(score_s) < max(1, args.cpu_runs)
+               or time.perf_counter() - t_start < args.cpu_seconds):
+            t0 = time.perf_counter()
+            if ref is not None:
+                raw = ref.score(q16, k16, N, 1024, threads=threads, impl=0)
+                t1 = time.perf_counter()
+                rc, k, *_ = ref.select(table[raw], 32, N, N, ALPHA, RATIO, width=KMAX + 1)
             else:
-                ops.select(raw, 32, N, N, ALPHA, RATIO, scale_raw=True, head0_partial=partial,
-                           ids=ids, ids_stride=kmax, counts=counts, status=status, ws=ws,
-                           id_order=args.only == "select_id")
-    for layer in range(LAYERS):  # valid raw scores and partials for the select loop
-        ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
-    # calibration for HBM counters: one plain 64 MiB device copy (64 MiB read + written)
-    src = torch.empty(N * 1024, dtype=torch.float16, device=raw.device)
-    torch.empty_like(src).copy_(src)
+                raw = port.score(q16, k16, N, 1024)
+                t1 = time.perf_counter()
+                rc, k, *_ = port.select(port.scale(raw), 32, N, N, ALPHA, RATIO)
+            t2 = time.perf_counter()
+            assert rc == 0 and k == KMAX, (rc, k)
+            score_s.append(t1 - t0)
+            select_s.append(t2 - t1)
+        sc, se = statistics.median(score_s), statistics.median(select_s)
+        results.append({"threads": threads, "runs": len(score_s), "score_ms": round(1e3 * sc, 3),
+                        "select_ms": round(1e3 * se, 3), "keys_per_s": N / (sc + se)})
+        log(f"cpu baseline, {threads} threads: score {1e3 * sc:.1f} ms + scale and select "
+            f"{1e3 * se:.1f} ms per layer (median of {len(score_s)}) = "
+            f"{N / (sc + se) / 1e6:.3f} M keys/s")
+    best = max(results, key=lambda r: r["keys_per_s"])
+    what = ("FullGqaCpuScorer (automatic impl) + scaling + select_gqa_scores compiled from the "
+            "reference sources" if ref is not None else "the C restatement, one thread")
+    return {
+        "value": best["keys_per_s"], "unit": "keys/s", "cores": best["threads"],
+        "kind": "reference" if ref is not None else "port",
+        "sample": (f"one configs[1] layer (N={N}, layer 0's F16 Q and RoPE keys) scored, scaled "
+                   f"and selected (alpha {ALPHA}, cap 0.2f, k={KMAX}) by {what}; median of "
+                   f"{best['runs']} runs; settings: "
+                   + ", ".join(f"{r['threads']} threads {r['keys_per_s'] / 1e6:.3f} M keys/s"
+                               for r in results)),
+        "settings": results, "host_threads": host,
+    }
+
+
+# ---- profiling aid -------------------------------------------------------------------
+
+def only(g, args):
+    """Back-to-back runs of one family's loop (after one plain 64 MiB copy, the
+    calibration kernel of the HBM counters)."""
+    fam = args.only
+    if fam == "batch":
+        batch_leg(g, args)
+        return 0
+    if fam == "tier":
+        tier_leg(g, args)
+        return 0
+    if fam in STEP_FAMILIES:
+        s = Step(g)
+        s.prepare(fam)
+        fn, per = s.families()[fam]
+    else:
+        b = LayerBench(g, records=fam == "gather")
+        if fam in ("attention", "attention_logits", "pack", "gather"):
+            b.select_last()
+        fn, per = b.families()[fam]
+    g.calibration_copy()
     for _ in range(args.warmup):
-        run()
-    b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    b.record(stream)
-    for _ in range(args.steps):
-        run()
-    e.record(stream)
-    torch.cuda.synchronize()
-    us = 1e3 * b.elapsed_time(e) / (args.steps * (len(pipe_calls) if args.only == "pipe" else LAYERS))
-    extra = f", {SCORE_BYTES / (us * 1e-6) / 1e9:.0f} GB/s" if args.only == "score" else ""
-    print(f"only {args.only}: {us:.2f} us per launch (back to back, {LAYERS} layers x "
-          f"{args.steps} steps){extra}", flush=True)
+        fn()
+    us = g.timed_us(fn, args.steps, per)
+    print(f"only {fam}: {us:.2f} us per call ({per} calls per run, {args.steps} runs)", flush=True)
     return 0
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(every GPU box in this setup has one GPU; see DESIGN.md for how the path shards)",
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (every GPU "
+              "box in this setup has one GPU; the path's sharding is a design, not a run)",
               file=sys.stderr)
         return 2
-    import numpy as np
-    import torch
-    import hillserve_amd as hs
-    from hillserve_amd import ops
+    g = Gpu()
+    if args.only:
+        return only(g, args)
 
-    assert torch.cuda.is_available(), "no GPU visible"
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    stream = torch.cuda.current_stream()
-    kmax = math.floor(N * float(np.float32(RATIO)))
+    s1 = step_leg(g, args)
+    layer = layer_leg(g, args)
+    batch = batch_leg(g, args)
+    tier = tier_leg(g, args)
+    log("cpu baseline: the reference CPU path on one configs[1] layer")
+    cpu = cpu_baseline(args, s1.pop("q_host"), s1.pop("k_host"))
 
-    # ---- configs[1]: 30 layers of packed K -----------------------------------
-    log("allocating 30 layers of K[32768,8,128] F16 (1.9 GB) + queries")
-    keys = [torch.empty(N * 1024, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
-    qs = [torch.empty(4096, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
-    for layer in range(LAYERS):
-        ops.fill_rope_keys(keys[layer], N, 1024, 8, seed=1000 + layer, theta=500000.0)
-        ops.fill_gaussian(qs[layer], seed=5000 + layer)
-    raws = [torch.empty((32, N), dtype=torch.float16, device=dev) for _ in range(2)]
-    partials = [torch.empty((N + 63) // 64, dtype=torch.int32, device=dev) for _ in range(2)]
-    raw, partial = raws[0], partials[0]
-    ids = torch.empty((32, kmax), dtype=torch.int32, device=dev)
-    counts = torch.empty(32, dtype=torch.int32, device=dev)
-    status = ops.new_status(dev)
-    # one status per layer in the pipelined step: a failed selection of any
-    # layer stays visible after the step (a shared status would keep only the
-    # last layer's)
-    statuses = [ops.new_status(dev) for _ in range(LAYERS)]
-    ws = ops.workspace(ops.select_workspace_bytes(32, N), dev)
-    # the current token of each layer: column N - 1, whose K row is the last
-    # row of the layer's keys (appended at this step)
-    cur_keys = [keys[layer][(N - 1) * 1024:] for layer in range(LAYERS)]
-    torch.cuda.synchronize()
-
-    def new_event():
-        return torch.cuda.Event(enable_timing=True)
-
-    def select_layer(b):
-        ops.select(raws[b], 32, N, N, ALPHA, RATIO, scale_raw=True, head0_partial=partials[b],
-                   ids=ids, ids_stride=kmax, counts=counts, status=status, ws=ws)
-
-    def serial_step():
-        # one layer at a time: score, then select
-        for layer in range(LAYERS):
-            ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
-            select_layer(0)
-
-    # Pipelined as a decode can run it (the early history preparation of
-    # runtime/gqa_executor.cpp:291-295 and policy/full_gqa_runtime.cpp:
-    # 493-569): layer l+1's history, the N - 1 tokens before the current one,
-    # is scored while layer l's selection runs (hs_gqa_select_then_score);
-    # layer l's selection first completes its own current token, column
-    # N - 1, from the rehearsal query and the token's K row (the count
-    # launch's current-token completion).  The score buffers alternate.
-    def sel_job(l):
-        return dict(scores=raws[l % 2], n=N, head0_partial=partials[l % 2], ids=ids,
-                    ids_stride=kmax, counts=counts, status=statuses[l], ws=ws,
-                    current_q=qs[l], current_key=cur_keys[l])
-
-    def history(l):
-        return dict(q16=qs[l], keys=keys[l], tokens=N - 1, out=raws[l % 2], score_stride=N,
-                    head0_partial=partials[l % 2])
-
-    pipe_calls = [ops.prepare_select_then_score([sel_job(l)], [history(l + 1)], 32, ALPHA, RATIO,
-                                                scale_raw=True)
-                  for l in range(LAYERS - 1)]
-    last_select = ops.prepare_select_batched([sel_job(LAYERS - 1)], 32, ALPHA, RATIO,
-                                             scale_raw=True)
-
-    def step():
-        h0 = history(0)
-        ops.score(h0["q16"], h0["keys"], N - 1, out=h0["out"], score_stride=N,
-                  head0_partial=h0["head0_partial"])
-        for call in pipe_calls:
-            call()
-        last_select()
-
-    def check_statuses():
-        for l, stt in enumerate(statuses):
-            st = ops.read_status(stt)
-            assert st["code"] == 0 and st["k"] == kmax, (l, st)
-
-    if args.only == "batch":
-        batch_leg(args, hs, ops, torch, stream, dev)
-        return 0
-    if args.only == "tier":
-        tier_leg(args, hs, ops, torch, stream, dev)
-        return 0
-    if args.only in ("score", "select", "select_id", "pipe"):
-        return profile_only(args, ops, torch, stream, qs, keys, raw, partial, ids, counts, status,
-                            ws, kmax, pipe_calls)
-
-    for _ in range(args.warmup):
-        step()
-    check_statuses()
-    begin, end = new_event(), new_event()
-    torch.cuda.synchronize()
-    begin.record(stream)
-    for i in range(args.steps):
-        step()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms_per_step = begin.elapsed_time(end) / args.steps
-    check_statuses()
-    last_ids = ids.clone()
-    # the same step one layer at a time (no pipelining), for comparison
-    serial_step()
-    torch.cuda.synchronize()
-    assert torch.equal(ids, last_ids), "pipelined and serial selections differ"
-    sb, se = new_event(), new_event()
-    sb.record(stream)
-    for i in range(args.steps):
-        serial_step()
-    se.record(stream)
-    torch.cuda.synchronize()
-    serial_ms = sb.elapsed_time(se) / args.steps
-    # scoring kernel alone: 30*K back-to-back launches over the rotating layers
-    sb, se = new_event(), new_event()
-    sb.record(stream)
-    for _ in range(args.steps):
-        for layer in range(LAYERS):
-            ops.score(qs[layer], keys[layer], N, out=raw, head0_partial=partial)
-    se.record(stream)
-    torch.cuda.synchronize()
-    score_ms = [sb.elapsed_time(se) / (args.steps * LAYERS)]
-    # the pipelined step's own launches alone: 29*K back-to-back
-    # select-then-score calls (count launch + combined launch), each layer's
-    # selection beside the next layer's scoring
-    torch.cuda.synchronize()
-    h0 = history(0)
-    ops.score(h0["q16"], h0["keys"], N - 1, out=h0["out"], score_stride=N,
-              head0_partial=h0["head0_partial"])
-    pb, pe = new_event(), new_event()
-    pb.record(stream)
-    for _ in range(args.steps):
-        for call in pipe_calls:
-            call()
-    pe.record(stream)
-    torch.cuda.synchronize()
-    pipe_call_us = 1e3 * pb.elapsed_time(pe) / (args.steps * len(pipe_calls))
-    check_statuses()
-    # per call: the next layer's scoring plus this layer's selection
-    pipe_bytes = SCORE_BYTES + 2 * 32 * N * 2 + 4 * 32 * kmax
-    pipe_gbs = pipe_bytes / (pipe_call_us * 1e-6) / 1e9
-    keys_per_s = LAYERS * N / (ms_per_step / 1e3)
-    step_bytes = LAYERS * (SCORE_BYTES + 2 * 32 * N * 2 + 4 * 32 * kmax)
-    avg_score_us = 1e3 * sum(score_ms) / len(score_ms)
-    score_gbs = SCORE_BYTES / (avg_score_us * 1e-6) / 1e9
-    log(f"configs[1]: {ms_per_step:.3f} ms/step pipelined ({serial_ms:.3f} one layer at a time), "
-        f"{LAYERS} layers, {keys_per_s/1e9:.2f} G keys/s; "
-        f"score kernel {avg_score_us:.2f} us avg = {score_gbs:.0f} GB/s; "
-        f"select-then-score call {pipe_call_us:.2f} us = {pipe_gbs:.0f} GB/s")
-
-    # ---- configs[2]: full sparse layer over 30 hot pools ---------------------
-    # The hot pool as a K array and a V array (2048 B rows each, the layout
-    # this framework keeps in HBM: the scorer streams K contiguously), and,
-    # for comparison, as the reference's 4096 B KV records.
-    del keys
-    q32s = [torch.empty((32, 128), dtype=torch.float32, device=dev) for _ in range(LAYERS)]
-    for layer in range(LAYERS):
-        q32s[layer].normal_(generator=torch.Generator(device=dev).manual_seed(layer))
-    out = torch.empty((32, 128), dtype=torch.float32, device=dev)
-    lws = ops.workspace(ops.decode_layer_workspace_bytes(N), dev)
-
-    def layer_leg(split):
-        log(f"configs[2]: 30 hot pools of 32768 x 4096 B (3.8 GB) as "
-            f"{'K and V arrays' if split else '4096 B KV records'}")
-        k_pools, v_pools = [], []
-        for layer in range(LAYERS):
-            # K RoPE-structured, V Gaussian
-            if split:
-                kp = torch.empty(N * 1024, dtype=torch.float16, device=dev)
-                vpool = torch.empty(N * 1024, dtype=torch.float16, device=dev)
-                ops.fill_rope_keys(kp, N, 1024, 8, seed=2000 + layer, theta=500000.0)
-                ops.fill_gaussian(vpool, seed=3000 + layer)
-            else:
-                kp = torch.empty(N * 2048, dtype=torch.float16, device=dev)
-                ops.fill_rope_keys(kp, N, 2048, 8, seed=2000 + layer, theta=500000.0)
-                tmp = torch.empty((N, 1024), dtype=torch.float16, device=dev)
-                ops.fill_gaussian(tmp, seed=3000 + layer)
-                kp.view(N, 2048)[:, 1024:].copy_(tmp)
-                vpool = None
-            k_pools.append(kp)
-            v_pools.append(vpool)
-        torch.cuda.synchronize()
-        row_bytes = 2048 if split else 4096
-
-        def layer_pass():
-            for layer in range(LAYERS):
-                ops.decode_layer(qs[layer], q32s[layer], k_pools[layer], N, ALPHA, RATIO,
-                                 scores=raw, ids=ids, ids_stride=kmax, counts=counts, out=out,
-                                 status=status, ws=lws, v_pool=v_pools[layer], row_bytes=row_bytes)
-
-        layer_pass()
-        st = ops.read_status(status)
-        assert st["code"] == 0 and st["k"] == kmax, st
-        # member bitmaps of the last layer sit at the workspace's member slice
-        member_off = ((N + 63) // 64 * 4 + 255) // 256 * 256
-        member = lws[member_off: member_off + 32 * ((N + 31) // 32) * 4].view(torch.int32)
-        ubytes, utokens = union_bytes(hs, member, N)
-        b3, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        b3.record(stream)
-        for _ in range(args.layer_steps):
-            layer_pass()
-        e3.record(stream)
-        torch.cuda.synchronize()
-        us = 1e3 * b3.elapsed_time(e3) / (args.layer_steps * LAYERS)
-        pipe_us = None
-        if split:
-            # The same 30 layers pipelined as a decode can run them: layer
-            # l+1's history (N - 1 tokens) is scored beside layer l's
-            # selection, which first completes layer l's current token (column
-            # N - 1, K row N - 1 of the pool); then layer l's attention.  The
-            # next layer's selection cannot start before its current token
-            # exists, i.e. after this layer's attention (and the rest of the
-            # model layer), so nothing is co-launched with the attention.
-            last_out = out.clone()
-            member_p = torch.empty((32, (N + 31) // 32), dtype=torch.int32, device=dev)
-            aws = ops.workspace(ops.attention_workspace_bytes(N), dev)
-            flags = dict(scale_raw=True, require_k=True, id_order=True)
-
-            def job(l):
-                return dict(scores=raws[l % 2], n=N, head0_partial=partials[l % 2], ids=ids,
-                            ids_stride=kmax, counts=counts, member=member_p, status=statuses[l],
-                            ws=ws, current_q=qs[l], current_key=k_pools[l][(N - 1) * 1024:])
-
-            def hist(l):
-                return dict(q16=qs[l], keys=k_pools[l], tokens=N - 1, out=raws[l % 2],
-                            score_stride=N, head0_partial=partials[l % 2])
-
-            calls = [ops.prepare_select_then_score([job(l)], [hist(l + 1)], 32, ALPHA, RATIO,
-                                                   **flags)
-                     for l in range(LAYERS - 1)]
-            last_call = ops.prepare_select_batched([job(LAYERS - 1)], 32, ALPHA, RATIO, **flags)
-
-            def attend(l):
-                ops.sparse_attention(q32s[l], k_pools[l], N, member_p, out=out, ws=aws,
-                                     v_pool=v_pools[l], row_bytes=row_bytes)
-
-            def pipelined_pass():
-                h0 = hist(0)
-                ops.score(h0["q16"], h0["keys"], N - 1, out=h0["out"], score_stride=N,
-                          head0_partial=h0["head0_partial"])
-                for layer in range(LAYERS - 1):
-                    calls[layer]()
-                    attend(layer)
-                last_call()
-                attend(LAYERS - 1)
-
-            pipelined_pass()
-            torch.cuda.synchronize()
-            check_statuses()
-            assert torch.equal(out, last_out), "pipelined and one-layer-at-a-time outputs differ"
-            b3.record(stream)
-            for _ in range(args.layer_steps):
-                pipelined_pass()
-            e3.record(stream)
-            torch.cuda.synchronize()
-            pipe_us = 1e3 * b3.elapsed_time(e3) / (args.layer_steps * LAYERS)
-        del k_pools, v_pools
-        return us, ubytes, utokens, pipe_us
-
-    rec_us, _, _, _ = layer_leg(split=False)
-    layer_us, ubytes, utokens, layer_pipe_us = layer_leg(split=True)
-    layer_bytes = SCORE_BYTES + 2 * 32 * N * 2 + 4 * 32 * kmax + ubytes + 8192 + 16384
-    layer_gbs = layer_bytes / (layer_us * 1e-6) / 1e9
-    log(f"configs[2]: {layer_us:.1f} us/layer with K and V arrays ({rec_us:.1f} us with 4096 B "
-        f"KV records; {layer_pipe_us:.1f} us per layer pipelined over 30 layers), "
-        f"{layer_gbs:.0f} GB/s algorithmic (union {utokens} (id,KV-head) rows of the last layer)")
-
-    # ---- configs[3]: batched rehearsal + scoring + selection ----------------------
-    batch = batch_leg(args, hs, ops, torch, stream, dev)
-    tier = tier_leg(args, hs, ops, torch, stream, dev)
-
-    # ---- CPU baseline on a bounded sample ----------------------------------------
-    k_sample = torch.empty(N * 1024, dtype=torch.float16, device=dev)
-    ops.fill_rope_keys(k_sample, N, 1024, 8, seed=1000, theta=500000.0)
-    k_host = k_sample.cpu().view(torch.int16).numpy().view(np.uint16)
-    q_host = qs[0].cpu().view(torch.int16).numpy().view(np.uint16)
-    log(f"cpu baseline: ~{args.cpu_seconds:.0f} s of the reference CPU path")
-    cpu = cpu_baseline(q_host, k_host, args.cpu_seconds)
-
+    step_us, pipe_us = s1["step_us"], s1["pipe_us"]
+    pipe_bytes = HIST_BYTES + SELECT_BYTES + CURRENT_BYTES
+    pipe_gbs = pipe_bytes / (pipe_us * 1e-6) / 1e9
+    step_gbs = s1["step_bytes"] / (step_us * 1e-6) / 1e9
     result = {
         "metric": METRIC,
-        "value": keys_per_s,
+        "value": LAYERS * N / (step_us * 1e-6),
         "unit": "keys/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": step_us / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (device-generated RoPE-structured Gaussian F16 keys, Gaussian F16 queries)",
+        "data": "synthetic (device-generated RoPE-structured Gaussian F16 keys, Gaussian F16 "
+                "queries)",
         "config": {
             "workload": "configs[1]: score + select, 30 sparse layers per decode step, N=32768",
             "tokens": N, "layers": LAYERS, "query_heads": 32, "kv_heads": 8, "head_dim": 128,
-            "alpha": ALPHA, "cap_ratio": RATIO, "k": kmax, "io_dtype": "f16",
-            "schedule": "layer l's selection co-launched with layer l+1's scoring "
-                        "(hs_gqa_select_then_score)",
+            "alpha": ALPHA, "cap_ratio": RATIO, "k": KMAX, "io_dtype": "f16",
+            "schedule": "layer l's selection (completing its current token) beside layer l+1's "
+                        "history scoring (hs_gqa_select_then_score)",
         },
-        "serial_ms_per_step": serial_ms,
-        "serial_keys_per_s": LAYERS * N / (serial_ms / 1e3),
-        "hbm_gbps": step_bytes / (ms_per_step * 1e-3) / 1e9,
+        "serial_ms_per_step": s1["serial_us"] / 1e3,
+        "serial_keys_per_s": LAYERS * N / (s1["serial_us"] * 1e-6),
+        "hbm_gbps": step_gbs,
         "roofline": {
-            "bound": "hbm", "achieved": score_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": score_gbs / HBM_PEAK_GBS, "traffic": pmc_traffic(),
-            "traffic_source": TRAFFIC_PROFILE,
-            "kernel": "score_kernel", "avg_launch_us": avg_score_us,
-            "algorithmic_bytes_per_launch": SCORE_BYTES,
-        },
-        "roofline_pipelined_call": {
             "bound": "hbm", "achieved": pipe_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": pipe_gbs / HBM_PEAK_GBS,
-            "traffic": pmc_traffic(PIPE_TRAFFIC_PROFILE, "traffic_bytes_per_call"),
-            "traffic_source": PIPE_TRAFFIC_PROFILE,
-            "kernel": "count_kernel + select_score_kernel (hs_gqa_select_then_score)",
-            "avg_call_us": pipe_call_us, "algorithmic_bytes_per_call": pipe_bytes,
-            "note": "the timed step's dominant launches: one layer's selection (scores read, "
-                    "order keys written and read, ids written) beside the next layer's scoring",
+            "traffic": pmc_traffic(PIPE_PROFILE, "traffic_bytes_per_call"),
+            "traffic_source": PIPE_PROFILE,
+            "kernel": "count_kernel + select_score_kernel (one hs_gqa_select_then_score call)",
+            "avg_launch_us": pipe_us, "algorithmic_bytes_per_launch": pipe_bytes,
+            "note": "the timed step's dominant call (29 of its 30 layers): one layer's selection "
+                    "and current token beside the next layer's history scoring",
         },
-        "layer_step": {
-            "workload": "configs[2]: score over hot pool + select at cap + sparse attention",
-            "pool_layout": "K and V arrays, 2048 B rows each",
-            "us_per_layer": layer_us, "us_per_layer_kv_records": rec_us,
-            "us_per_layer_pipelined": layer_pipe_us,
-            "pipelined_gbps": layer_bytes / (layer_pipe_us * 1e-6) / 1e9,
-            "algorithmic_bytes": layer_bytes,
-            "achieved_gbps": layer_gbs, "frac_of_hbm_peak": layer_gbs / HBM_PEAK_GBS,
-            "union_rows": utokens,
+        "roofline_step": {
+            "bound": "hbm", "achieved": step_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": step_gbs / HBM_PEAK_GBS,
+            "traffic": pmc_traffic(STEP_PROFILE, "traffic_bytes_per_step"),
+            "traffic_source": STEP_PROFILE,
+            "step_us": step_us, "algorithmic_bytes_per_step": s1["step_bytes"],
         },
+        "kernels": s1["kernels"] + layer["kernels"] + batch.pop("kernels"),
+        "layer_step": {k: v for k, v in layer.items() if k != "kernels"},
         "batch_step": batch,
         "tier_step": tier,
         "cpu_baseline": cpu,

@@ -409,45 +409,67 @@ void pack_gqa_workspace(const std::vector<std::vector<std::uint64_t>>& ids,
 
 // ---- chunked stream planner (smartssd/stream_layout.hpp:18-51) --------------------
 
+// The cold keys form one byte stream: the regions in order, K rows of
+// 2048 B, at most 32768 tokens.  Consecutive regions that continue each other
+// in the same file are joined into one extent first; each chunk is then the
+// stream window [chunk_begin, chunk_end) cut out of the extents it overlaps,
+// one read per overlapped extent, placed at its offset inside the window.
+// Joining before cutting gives the same reads as joining pieces inside each
+// chunk, because only stream-adjacent pieces can be joined either way.
 std::vector<DirectChunkPlan> plan_raw_gqa_stream(const std::vector<ScoreFileRegion>& regions,
                                                  std::size_t chunk_tokens) {
-    constexpr std::size_t kKeyBytes = kKvHeads * kDim * 2, kBlockBytes = 64 * kKeyBytes;
-    if (regions.empty() || chunk_tokens == 0 || chunk_tokens > 32768 || chunk_tokens % 64)
-        throw std::invalid_argument("CSS requires nonempty64-token regions and64<=chunk<=32768");
-    std::size_t total = 0;
-    for (const auto& r : regions) {
-        if (r.fd < 0 || r.bytes == 0 || r.offset % 4096 || r.bytes % kBlockBytes ||
-            r.offset > std::numeric_limits<std::uint64_t>::max() - r.bytes)
-            throw std::invalid_argument("CSS region must be aligned exact64-token raw GQA blocks");
-        if (r.bytes / kKeyBytes > 32768 - total) throw std::length_error("CSS pilot exceeds32768 cold tokens");
-        total += r.bytes / kKeyBytes;
+    constexpr std::uint64_t kRowBytes = kKvHeads * kDim * 2, kBlockBytes = 64 * kRowBytes;
+    constexpr std::uint64_t kMaxTokens = 32768;
+    const bool chunk_ok = chunk_tokens >= 64 && chunk_tokens <= kMaxTokens && chunk_tokens % 64 == 0;
+    if (regions.empty() || !chunk_ok)
+        throw std::invalid_argument(
+            "raw GQA stream: needs at least one region and a chunk of 64..32768 tokens, "
+            "a multiple of 64");
+
+    struct Extent {
+        int fd;
+        std::uint64_t file_offset, stream_begin, stream_end;
+    };
+    std::vector<Extent> extents;
+    std::uint64_t stream_bytes = 0;
+    for (const ScoreFileRegion& r : regions) {
+        const bool placed = r.fd >= 0 && r.offset % 4096 == 0 &&
+                            r.offset <= std::numeric_limits<std::uint64_t>::max() - r.bytes;
+        if (!placed || r.bytes == 0 || r.bytes % kBlockBytes != 0)
+            throw std::invalid_argument(
+                "raw GQA stream: a region must be 4096-byte aligned and hold whole 64-token "
+                "K blocks");
+        if (r.bytes / kRowBytes > kMaxTokens - stream_bytes / kRowBytes)
+            throw std::length_error("raw GQA stream: more than 32768 cold tokens");
+        const bool continues = !extents.empty() && extents.back().fd == r.fd &&
+                               extents.back().file_offset +
+                                       (extents.back().stream_end - extents.back().stream_begin) ==
+                                   r.offset;
+        if (continues)
+            extents.back().stream_end += r.bytes;
+        else
+            extents.push_back(Extent{r.fd, r.offset, stream_bytes, stream_bytes + r.bytes});
+        stream_bytes += r.bytes;
     }
-    std::vector<DirectChunkPlan> plan;
-    std::size_t region = 0;
-    std::uint64_t used = 0;  // bytes of `region` already planned
-    for (std::size_t first = 0; first < total; first += chunk_tokens) {
-        DirectChunkPlan chunk;
-        chunk.token_offset = first;
-        chunk.tokens = std::min(chunk_tokens, total - first);
-        std::size_t left = chunk.tokens * kKeyBytes, dest = 0;
-        while (left) {
-            const ScoreFileRegion& r = regions[region];
-            const std::size_t take = static_cast<std::size_t>(std::min<std::uint64_t>(left, r.bytes - used));
-            const std::uint64_t at = r.offset + used;
-            DirectChunkRead* last = chunk.reads.empty() ? nullptr : &chunk.reads.back();
-            if (last && last->fd == r.fd && last->offset + last->bytes == at)
-                last->bytes += take;  // contiguous in the same file: one read
-            else
-                chunk.reads.push_back(DirectChunkRead{r.fd, at, take, dest});
-            left -= take;
-            dest += take;
-            used += take;
-            if (used == r.bytes) {
-                ++region;
-                used = 0;
-            }
+
+    const std::uint64_t tokens = stream_bytes / kRowBytes;
+    std::vector<DirectChunkPlan> plan((tokens + chunk_tokens - 1) / chunk_tokens);
+    std::size_t e = 0;  // first extent that can overlap the current window
+    for (std::size_t c = 0; c < plan.size(); ++c) {
+        DirectChunkPlan& chunk = plan[c];
+        chunk.token_offset = c * chunk_tokens;
+        chunk.tokens = static_cast<std::size_t>(
+            std::min<std::uint64_t>(chunk_tokens, tokens - chunk.token_offset));
+        const std::uint64_t begin = chunk.token_offset * kRowBytes;
+        const std::uint64_t end = begin + chunk.tokens * kRowBytes;
+        while (extents[e].stream_end <= begin) ++e;
+        for (std::size_t x = e; x < extents.size() && extents[x].stream_begin < end; ++x) {
+            const std::uint64_t lo = std::max(begin, extents[x].stream_begin);
+            const std::uint64_t hi = std::min(end, extents[x].stream_end);
+            chunk.reads.push_back(DirectChunkRead{
+                extents[x].fd, extents[x].file_offset + (lo - extents[x].stream_begin),
+                static_cast<std::size_t>(hi - lo), static_cast<std::size_t>(lo - begin)});
         }
-        plan.push_back(std::move(chunk));
     }
     return plan;
 }

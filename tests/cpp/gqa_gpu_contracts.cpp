@@ -110,23 +110,23 @@ void selector_contracts() {
     std::vector<std::uint16_t> score;
     for (float x : {10.f, 9.f, 8.f, 7.f, 1.f, 1.f, 1.f, 1.f}) score.push_back(half_bits(x));
     auto x = select_gqa_scores(score, 2, 4, 4, 2.f, 1.f);
-    check(x.counts == std::vector<std::uint32_t>({3, 0}) && x.k == 1, "head0/inclusive/count floor semantics");
-    check(x.ids[0][0] == 0 && x.ids[1][0] == 0, "deterministic original-ID ties");
+    check(x.counts == std::vector<std::uint32_t>({3, 0}) && x.k == 1, "head-0 threshold, inclusive counts and the floor of the mean");
+    check(x.ids[0][0] == 0 && x.ids[1][0] == 0, "equal scores rank by ascending id");
     // capacity padding beyond valid tokens is not a candidate (:29-30)
     std::vector<std::uint16_t> padded(2 * 8, half_bits(1000));
     for (std::size_t h = 0; h < 2; ++h)
         for (std::size_t t = 0; t < 5; ++t) padded[h * 8 + t] = half_bits(float(t));
     auto p = select_gqa_scores(padded, 2, 8, 5, 10, 0.4f);
-    check(p.k == 2 && p.ids[0] == std::vector<std::uint64_t>({4, 3}), "padding/current candidate selection");
+    check(p.k == 2 && p.ids[0] == std::vector<std::uint64_t>({4, 3}), "padding columns excluded, the current column included");
     // F16 count rounding at 2049 (:32)
     std::vector<std::uint16_t> many(2049, half_bits(0));
     auto rounded = select_gqa_scores(many, 1, 2049, 2049, 0, 1);
-    check(rounded.counts[0] == 2049 && rounded.k == 2048, "F16 count2049 rounds2048");
+    check(rounded.counts[0] == 2049 && rounded.k == 2048, "an F16 count of 2049 is 2048");
     // long addressing (:34)
     std::vector<std::uint16_t> long_scores(131072, half_bits(-10));
     long_scores.back() = half_bits(1);
     auto last = select_gqa_scores(long_scores, 1, long_scores.size(), long_scores.size(), 0, 1);
-    check(last.k == 1 && last.ids[0][0] == 131071, "global long-token ID not truncated");
+    check(last.k == 1 && last.ids[0][0] == 131071, "ids beyond 65535 survive the selection");
     // F16 count overflow and the FP32-count extension (:35-41)
     std::vector<std::uint16_t> overflow(65520, half_bits(0));
     rejects([&] { select_gqa_scores(overflow, 1, overflow.size(), overflow.size(), 0, 1); },
@@ -135,7 +135,7 @@ void selector_contracts() {
     check(wide.counts[0] == 65520 && wide.k == 13104 && wide.ids[0].front() == 0 && wide.ids[0].back() == 13103,
           "explicit FP32 count extension keeps ordered cap");
     auto exact = select_gqa_scores(many, 1, 2049, 2049, 0, 1, true);
-    check(exact.k == 2049, "explicit FP32 count has no hidden F16 rounding");
+    check(exact.k == 2049, "FP32 counts are exact");
     // random orders with signed zeros (:49-57)
     std::mt19937 rng(1741);
     for (int trial = 0; trial < 24; ++trial) {
@@ -160,10 +160,10 @@ void selector_contracts() {
     const std::array<std::uint32_t, 4> counts{3, 6, 11, 26};
     for (std::size_t a = 0; a < alphas.size(); ++a) {
         auto s = select_gqa_scores(scores, H, P, P, alphas[a], .2f);
-        check(s.k == expected[a], "alpha/count/20percent-cap changed on same input");
+        check(s.k == expected[a], "margin, count or cap differ between two runs on one input");
         for (std::size_t h = 0; h < H; ++h) {
-            check(s.counts[h] == counts[a], "inclusive threshold count changed");
-            for (std::size_t t = 0; t < s.k; ++t) check(s.ids[h][t] == t, "alpha changed score ranking");
+            check(s.counts[h] == counts[a], "a score equal to the threshold is counted");
+            for (std::size_t t = 0; t < s.k; ++t) check(s.ids[h][t] == t, "a larger margin must not reorder the selected ids");
         }
     }
     for (float alpha : alphas) {
@@ -502,26 +502,26 @@ void pack_contracts() {
 void stream_layout_contracts() {
     constexpr std::size_t block = 64 * 8 * 128 * 2;
     auto plan = plan_raw_gqa_stream({{3, 0, block, false}, {3, 3 * block, block, false}, {3, 7 * block, block, false}}, 128);
-    check(plan.size() == 2 && plan[0].tokens == 128 && plan[1].tokens == 64, "tail shape");
-    check(plan[1].token_offset == 128 && plan[0].reads.size() == 2, "cold index map");
-    check(plan[0].reads[1].offset == 3 * block && plan[0].reads[1].destination_offset == block, "noncontiguous direct placement");
-    check(plan[1].reads[0].offset == 7 * block && plan[1].reads[0].destination_offset == 0, "tail original identity");
+    check(plan.size() == 2 && plan[0].tokens == 128 && plan[1].tokens == 64, "chunk count and the short last chunk");
+    check(plan[1].token_offset == 128 && plan[0].reads.size() == 2, "second chunk offset and first chunk read count");
+    check(plan[0].reads[1].offset == 3 * block && plan[0].reads[1].destination_offset == block, "a read after a gap lands right after the previous bytes");
+    check(plan[1].reads[0].offset == 7 * block && plan[1].reads[0].destination_offset == 0, "the last chunk reads the last region from its start");
     plan = plan_raw_gqa_stream({{3, block, block, false}, {3, 2 * block, 4 * block, false}}, 128);
-    check(plan.size() == 3 && plan[0].reads.size() == 1 && plan[0].reads[0].bytes == 2 * block, "coalescing");
-    check(plan[1].reads[0].offset == 3 * block && plan[2].reads[0].offset == 5 * block, "split coverage");
+    check(plan.size() == 3 && plan[0].reads.size() == 1 && plan[0].reads[0].bytes == 2 * block, "adjacent regions of one file join into one read");
+    check(plan[1].reads[0].offset == 3 * block && plan[2].reads[0].offset == 5 * block, "a long region is split across chunks in order");
     std::size_t read_bytes = 0;
     for (const auto& chunk : plan) {
         std::size_t dest = 0;
         for (const auto& read : chunk.reads) {
-            check(read.destination_offset == dest && read.offset % 4096 == 0 && read.bytes % 4096 == 0, "direct alignment/coverage");
+            check(read.destination_offset == dest && read.offset % 4096 == 0 && read.bytes % 4096 == 0, "reads are page aligned and back to back in the chunk");
             dest += read.bytes;
         }
-        check(dest == chunk.tokens * 8 * 128 * 2, "chunk exact coverage");
+        check(dest == chunk.tokens * 8 * 128 * 2, "a chunk's reads cover exactly its tokens");
         read_bytes += dest;
     }
-    check(read_bytes == 5 * block, "total byte coverage");
+    check(read_bytes == 5 * block, "every region byte is read once");
     plan = plan_raw_gqa_stream({{3, 0, block, false}, {4, block, block, false}}, 128);
-    check(plan[0].reads.size() == 2, "different fd must not coalesce");
+    check(plan[0].reads.size() == 2, "regions of two files stay two reads");
     rejects([&] { plan_raw_gqa_stream({}, 64); }, "empty regions");
     rejects([&] { plan_raw_gqa_stream({{3, 0, block, false}}, 0); }, "chunk 0");
     rejects([&] { plan_raw_gqa_stream({{3, 0, block, false}}, 65); }, "chunk not 64-aligned");
@@ -532,6 +532,62 @@ void stream_layout_contracts() {
     rejects([&] { plan_raw_gqa_stream({{3, 0, 0, false}}, 64); }, "empty region");
     rejects([&] { plan_raw_gqa_stream({{3, 0, 513 * block, false}}, 64); }, "beyond 32768 tokens");
     rejects([&] { plan_raw_gqa_stream({{3, std::numeric_limits<std::uint64_t>::max() - 4095, block, false}}, 64); }, "offset overflow");
+    bool length = false;
+    try {
+        plan_raw_gqa_stream({{3, 0, 256 * block, false}, {4, 0, 257 * block, false}}, 64);
+    } catch (const std::length_error&) {
+        length = true;
+    }
+    check(length, "more than 32768 tokens over two regions is a length error");
+
+    // Random region lists against a token-by-token restatement: token t of
+    // the stream is K row (t - first token of its region) of its region, and
+    // a read maps its bytes onto the chunk in stream order.  Reads of one
+    // chunk never continue each other in one file (they would be one read).
+    std::mt19937 rng(4242);
+    constexpr std::size_t row = 8 * 128 * 2;
+    for (int trial = 0; trial < 200; ++trial) {
+        std::vector<ScoreFileRegion> regions;
+        std::size_t tokens = 0;
+        const int count = 1 + int(rng() % 6);
+        for (int r = 0; r < count; ++r) {
+            const int fd = 3 + int(rng() % 2);
+            std::uint64_t offset = std::uint64_t(rng() % 64) * 4096;
+            if (!regions.empty() && rng() % 2 == 0 && regions.back().fd == fd)
+                offset = regions.back().offset + regions.back().bytes;  // continues the last one
+            const std::size_t blocks = 1 + rng() % 12;
+            regions.push_back({fd, offset, blocks * block, false});
+            tokens += blocks * 64;
+        }
+        const std::size_t chunk = 64 * (1 + rng() % 10);
+        std::vector<std::pair<int, std::uint64_t>> where;  // (fd, file offset) of each token
+        for (const auto& r : regions)
+            for (std::uint64_t b = 0; b < r.bytes; b += row) where.push_back({r.fd, r.offset + b});
+        const auto plan = plan_raw_gqa_stream(regions, chunk);
+        check(plan.size() == (tokens + chunk - 1) / chunk, "one chunk per chunk_tokens tokens");
+        for (std::size_t c = 0; c < plan.size(); ++c) {
+            check(plan[c].token_offset == c * chunk &&
+                      plan[c].tokens == std::min(chunk, tokens - c * chunk),
+                  "chunk offsets and sizes");
+            std::size_t placed = 0;
+            for (std::size_t i = 0; i < plan[c].reads.size(); ++i) {
+                const auto& rd = plan[c].reads[i];
+                check(rd.destination_offset == placed && rd.bytes % row == 0, "reads back to back");
+                for (std::size_t b = 0; b < rd.bytes; b += row) {
+                    const auto& w = where[plan[c].token_offset + (placed + b) / row];
+                    check(w.first == rd.fd && w.second == rd.offset + b, "token read from its region row");
+                }
+                if (i > 0) {
+                    const auto& prev = plan[c].reads[i - 1];
+                    check(!(prev.fd == rd.fd && prev.offset + prev.bytes == rd.offset),
+                          "continuing reads are joined");
+                }
+                placed += rd.bytes;
+            }
+            check(placed == plan[c].tokens * row, "chunk fully read");
+        }
+        ++cases;
+    }
 }
 
 // GPU streaming of file regions: the chunks concatenate to the one-shot
@@ -619,7 +675,7 @@ void cover_contracts() {
     for (std::size_t h = 0; h < H; ++h)
         for (std::size_t j = 0; j < 5; ++j) sparse[h * capacity + 40 + 300 * j + h] = half_bits(500.f + float(j));
     const auto small = history_cover_gqa(sparse, H, capacity, position, 1.f);
-    check(small.bound == 6, "F16 threshold-count upper bound includes unknown current contribution");
+    check(small.bound == 6, "the F16 count bound covers the current token's unknown score");
     rejects([&] { history_cover_gqa(raw, H, capacity, 1, 1.f); }, "cap 0 rejected");
     rejects([&] { history_cover_gqa(raw, H, capacity, capacity, 1.f); }, "no room for the current token");
     auto inf = raw;
