@@ -58,19 +58,49 @@ __device__ __forceinline__ bool finite_half(uint32_t bits) {
     return (bits & 0x7c00u) != 0x7c00u;
 }
 
-// Wave64 reductions over ds_swizzle-free cross-lane moves.
+// Integer wave64 scans and reductions on DPP row moves, which stay in the
+// VALU (a __shfl is an LDS permute with its own round trip): row_shr 1, 2,
+// 4, 8 scan each row of 16 lanes; row_bcast:15 then adds row 0's total to
+// row 1 and row 2's to row 3, and row_bcast:31 adds lanes 0..31's total to
+// rows 2 and 3.  Lanes whose source lies outside the row read 0, the
+// identity of both + and unsigned max.
+namespace dpp {
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ uint32_t move(uint32_t v) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, kRowMask, 0xf, false));
+}
+}  // namespace dpp
+
+// Inclusive prefix sum over the lanes of the wave (lane 0 first).
+__device__ __forceinline__ uint32_t wave_inclusive_sum_u32(uint32_t x) {
+    x += dpp::move<dpp::kRowShr1>(x);
+    x += dpp::move<dpp::kRowShr2>(x);
+    x += dpp::move<dpp::kRowShr4>(x);
+    x += dpp::move<dpp::kRowShr8>(x);
+    x += dpp::move<dpp::kRowBcast15, 0xa>(x);
+    x += dpp::move<dpp::kRowBcast31, 0xc>(x);
+    return x;
+}
+__device__ __forceinline__ uint32_t wave_inclusive_max_u32(uint32_t x) {
+    x = max(x, dpp::move<dpp::kRowShr1>(x));
+    x = max(x, dpp::move<dpp::kRowShr2>(x));
+    x = max(x, dpp::move<dpp::kRowShr4>(x));
+    x = max(x, dpp::move<dpp::kRowShr8>(x));
+    x = max(x, dpp::move<dpp::kRowBcast15, 0xa>(x));
+    x = max(x, dpp::move<dpp::kRowBcast31, 0xc>(x));
+    return x;
+}
+// Reductions: lane 63 of the inclusive scan, the same in every lane.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        const uint32_t other = __shfl_xor(v, offset, 64);
-        v = v > other ? v : other;
-    }
-    return v;
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(wave_inclusive_max_u32(v)), 63));
 }
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
-    return v;
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(wave_inclusive_sum_u32(v)), 63));
 }
 __device__ __forceinline__ float wave_max_f32(float v) {
 #pragma unroll

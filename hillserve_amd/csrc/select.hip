@@ -267,12 +267,7 @@ __device__ uint32_t block_sum(uint32_t v, uint32_t* tmp) {
 template <uint32_t kT = kThreads>
 __device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* tmp) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    uint32_t x = v;
-#pragma unroll
-    for (uint32_t off = 1; off < 64; off <<= 1) {
-        const uint32_t y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
-    }
+    const uint32_t x = wave_inclusive_sum_u32(v);
     if (lane == 63) tmp[wave] = x;
     __syncthreads();
     uint32_t before = 0;
@@ -294,12 +289,7 @@ __device__ void find_bucket(const uint32_t* hist, uint32_t need, uint32_t* out_b
             local[j] = hist[255 - (4 * lane + j)];
             sum += local[j];
         }
-        uint32_t x = sum;
-#pragma unroll
-        for (uint32_t off = 1; off < 64; off <<= 1) {
-            const uint32_t y = __shfl_up(x, off, 64);
-            if (lane >= off) x += y;
-        }
+        const uint32_t x = wave_inclusive_sum_u32(sum);
         const uint32_t before = x - sum;
         if (before < need && need <= x) {
             uint32_t running = before;
@@ -331,6 +321,63 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t digit, bool valid) {
 template <uint32_t kWords>
 __device__ __forceinline__ uint32_t half_at(const uint32_t (&packed)[kWords], uint32_t j) {
     return (packed[j >> 1] >> ((j & 1u) * 16u)) & 0xffffu;
+}
+
+// Packed 16-bit integer ALU on both halves of a word at once.  Written as
+// instructions because the compiler turns min(sat(a - b), 1) back into two
+// compares and two selects per word.
+__device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
+    uint32_t d;
+    asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+__device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
+    uint32_t d;
+    asm("v_pk_sub_u16 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+__device__ __forceinline__ uint32_t pk_min1_u16(uint32_t a) {  // min(half, 1) per half
+    uint32_t d;
+    asm("v_pk_min_u16 %0, %1, 1 op_sel_hi:[1,0]" : "=v"(d) : "v"(a));
+    return d;
+}
+__device__ __forceinline__ uint32_t pk_shift_in_u16(uint32_t acc, uint32_t bits) {  // 2 acc + bits
+    uint32_t d;
+    asm("v_pk_mad_u16 %0, %1, 2, %2 op_sel_hi:[1,0,1]" : "=v"(d) : "v"(acc), "v"(bits));
+    return d;
+}
+// Bit 2i of the result = bit i of the low half, bit 2i+1 = bit i of the
+// high half (the outer perfect shuffle of a word).
+__device__ __forceinline__ uint32_t interleave_halves(uint32_t x) {
+    uint32_t t = (x ^ (x >> 8)) & 0x0000ff00u;
+    x ^= t ^ (t << 8);
+    t = (x ^ (x >> 4)) & 0x00f000f0u;
+    x ^= t ^ (t << 4);
+    t = (x ^ (x >> 2)) & 0x0c0c0c0cu;
+    x ^= t ^ (t << 2);
+    t = (x ^ (x >> 1)) & 0x22222222u;
+    x ^= t ^ (t << 1);
+    return x;
+}
+// Bit j of `above` / `tie`: key j of the 2 kWords keys packed two per word
+// (key 2i in the low half of word i) is > / == kstar.  Per half, the
+// saturating difference key - kstar is nonzero iff key > kstar and the
+// wrapping one is zero iff key == kstar; the 0/1 halves are shifted into a
+// low-half accumulator (even keys) and a high-half one (odd keys), which the
+// shuffle interleaves.
+template <uint32_t kWords>
+__device__ __forceinline__ void key_masks(const uint32_t (&keys)[kWords], uint32_t kstar,
+                                          uint32_t& above, uint32_t& tie) {
+    static_assert(kWords == 16, "32 keys: one bit each");
+    const uint32_t ks = kstar * 0x10001u;
+    uint32_t gt = 0, ne = 0;
+#pragma unroll
+    for (int i = kWords - 1; i >= 0; --i) {
+        gt = pk_shift_in_u16(gt, pk_min1_u16(pk_sub_sat_u16(keys[i], ks)));
+        ne = pk_shift_in_u16(ne, pk_min1_u16(pk_sub_u16(keys[i], ks)));
+    }
+    above = interleave_halves(gt);
+    tie = ~interleave_halves(ne);
 }
 
 // This thread's kR consecutive ids of head h from `begin` into registers
@@ -569,17 +616,19 @@ __device__ int derive_k(const SelectArgs& a, const uint32_t* head_count, const u
         // count gets the current token's possible +1, the mean must be >= 1,
         // and the cap is that of n + 1 columns
         if (!isfinite(thr)) return HS_ERR_THRESHOLD;
-        float total = 0.0f;
+        uint32_t total = 0;
         for (uint32_t first = 0; first < a.heads && code == HS_OK; first += 64) {
             const uint32_t hh = first + lane;
             const bool valid = hh < a.heads;
             const float c = valid ? static_cast<float>(head_count[hh] + 1u) : 0.0f;
             const float rounded = fp32_counts ? c : h2f(f2h(c));
-            if (__ballot(valid && !isfinite(rounded))) code = HS_ERR_COUNT;
-            total += wave_sum_f32(valid ? rounded : 0.0f);
+            const bool err = valid && !isfinite(rounded);
+            if (__ballot(err)) code = HS_ERR_COUNT;
+            total += wave_sum_u32(valid && !err ? static_cast<uint32_t>(rounded) : 0u);
         }
         if (code != HS_OK) return code;
-        const float q = __fdiv_rn(total, static_cast<float>(a.heads));
+        // integer counts below 2^24 in total: the conversion is exact
+        const float q = __fdiv_rn(static_cast<float>(total), static_cast<float>(a.heads));
         const float mean = fp32_counts ? q : h2f(f2h(q));
         if (!isfinite(mean) || !(mean >= 1.0f)) return HS_ERR_MEAN;
         uint64_t cap_k = static_cast<uint64_t>(
@@ -591,7 +640,7 @@ __device__ int derive_k(const SelectArgs& a, const uint32_t* head_count, const u
     }
     if (head_bad[0]) return HS_ERR_NONFINITE;
     if (!isfinite(thr)) return HS_ERR_THRESHOLD;
-    float total = 0.0f;
+    uint32_t total = 0;
     for (uint32_t first = 0; first < a.heads && code == HS_OK; first += 64) {
         const uint32_t hh = first + lane;
         const bool valid = hh < a.heads;
@@ -600,14 +649,17 @@ __device__ int derive_k(const SelectArgs& a, const uint32_t* head_count, const u
         const float rounded = fp32_counts ? static_cast<float>(c) : h2f(f2h(static_cast<float>(c)));
         const bool err = valid && (hb || !isfinite(rounded));
         const uint64_t errs = __ballot(err);
-        if (errs) {
-            const uint32_t at = static_cast<uint32_t>(__ffsll(static_cast<long long>(errs))) - 1;
-            code = __shfl(hb ? 1 : 0, at, 64) ? HS_ERR_NONFINITE : HS_ERR_COUNT;
+        if (errs) {  // the first failing head decides the code
+            const uint64_t bad_heads = __ballot(hb);
+            code = (bad_heads & (errs & (0ull - errs))) ? HS_ERR_NONFINITE : HS_ERR_COUNT;
         }
-        total += wave_sum_f32(valid && !err ? rounded : 0.0f);
+        // the rounded counts are integers (<= 65504, or <= n <= 131072 with
+        // FP32 counts) over <= 128 heads: the integer total is <= 2^24 and
+        // converts to FP32 exactly, the total of any FP32 summation order
+        total += wave_sum_u32(valid && !err ? static_cast<uint32_t>(rounded) : 0u);
     }
     if (code != HS_OK) return code;
-    const float q = __fdiv_rn(total, static_cast<float>(a.heads));
+    const float q = __fdiv_rn(static_cast<float>(total), static_cast<float>(a.heads));
     const float mean = fp32_counts ? q : h2f(f2h(q));
     if (!isfinite(mean)) return HS_ERR_MEAN;
     uint64_t kk = static_cast<uint64_t>(mean);
@@ -1067,8 +1119,9 @@ struct HeadSelectLds {
     uint32_t tmp[kHWaves];
     uint32_t sh[8];
     uint32_t sort_lds[kRankOrder ? 2 * kHeadMaxK : 1];
-    uint32_t tables[kRankOrder ? 2 * kSortRange : 1];
+    alignas(16) uint32_t tables[kRankOrder ? 2 * kSortRange : 1];
     uint32_t whist[kRankOrder ? kHWaves : 1][256];
+    uint32_t stage[kRankOrder ? 1 : kHeadMaxK];  // id order: the ids before their store
 };
 
 // The selection of head h of job `job` by one kHThreads workgroup.
@@ -1200,13 +1253,8 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
     // (bit j = id begin + j, shifted in from the top id down)
     const uint32_t valid = begin + kHRun <= n ? 0xffffffffu
                                                : (begin < n ? (1u << (n - begin)) - 1u : 0u);
-    uint32_t above_mask = 0, tie_mask = 0;
-#pragma unroll
-    for (int j = kHRun - 1; j >= 0; --j) {
-        const uint32_t key = half_at(keys, static_cast<uint32_t>(j));
-        above_mask = (above_mask << 1) + (key > kstar ? 1u : 0u);
-        tie_mask = (tie_mask << 1) + (key == kstar ? 1u : 0u);
-    }
+    uint32_t above_mask, tie_mask;
+    key_masks(keys, kstar, above_mask, tie_mask);
     above_mask &= valid;
     tie_mask &= valid;
     // one scan of both counts (each total <= 32768 fits its 16 bits): the ties
@@ -1240,8 +1288,18 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
     if (a.member && tid < words) a.member[static_cast<size_t>(h) * words + tid] = bits32;
     uint32_t* out = a.ids + static_cast<size_t>(h) * a.ids_stride;
     if constexpr (!kRankOrder) {
-        for (uint32_t sel = bits32; sel != 0; sel &= sel - 1)
-            out[pos++] = begin + static_cast<uint32_t>(__ffs(sel)) - 1;
+        if (k <= kHeadMaxK) {
+            // into LDS at their places, then out in row order: the stores of a
+            // wave cover 256 consecutive bytes instead of 64 scattered places
+            uint32_t* stage = lds.stage;
+            for (uint32_t sel = bits32; sel != 0; sel &= sel - 1)
+                stage[pos++] = begin + static_cast<uint32_t>(__ffs(sel)) - 1;
+            __syncthreads();
+            for (uint32_t r = tid; r < k; r += kHThreads) out[r] = stage[r];
+        } else {
+            for (uint32_t sel = bits32; sel != 0; sel &= sel - 1)
+                out[pos++] = begin + static_cast<uint32_t>(__ffs(sel)) - 1;
+        }
     } else {
         // Rank order (k <= kHeadMaxK here): a counting sort by key over the
         // table's bins, larger keys first.  Bins above K*'s hold every key,
@@ -1252,25 +1310,38 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
         uint32_t* cursor = tables + kSortRange;
         constexpr uint32_t kPer = kSortRange / kHThreads;
         const uint32_t first = (kHThreads - 1 - tid) * kPer;
+        // a thread's bins move as 16-byte LDS accesses: word accesses at the
+        // 8-word stride between lanes would conflict 16 ways
+        static_assert(kPer == 8, "two 16-byte accesses per thread");
         uint32_t c[kPer], sum = 0, big = 0;
+        {
+            const uint4 b0 = *reinterpret_cast<const uint4*>(table + first);
+            const uint4 b1 = *reinterpret_cast<const uint4*>(table + first + 4);
+            const uint32_t in[kPer] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
-        for (uint32_t i = 0; i < kPer; ++i) {
-            const uint32_t bin = first + i;
-            c[i] = bin > tie_bin ? table[bin] : (bin == tie_bin ? t_need : 0u);
-            sum += c[i];
-            big = max(big, c[i]);
+            for (uint32_t i = 0; i < kPer; ++i) {
+                const uint32_t bin = first + i;
+                c[i] = bin > tie_bin ? in[i] : (bin == tie_bin ? t_need : 0u);
+                sum += c[i];
+                big = max(big, c[i]);
+            }
         }
         if (big > kGroupCap) sh[kFlag] = 1u;  // read after the scan's barriers
         const uint32_t higher = block_exclusive_scan<kHThreads>(sum, tmp);
         uint32_t* B = sort_lds;
         if (sh[kFlag] == 0) {
-            uint32_t run = higher + sum;
+            uint32_t run = higher + sum, at[kPer];
 #pragma unroll
             for (uint32_t i = 0; i < kPer; ++i) {
                 run -= c[i];
-                table[first + i] = run;  // the bin's first position
-                cursor[first + i] = run;
+                at[i] = run;  // the bin's first position
             }
+            const uint4 a0 = make_uint4(at[0], at[1], at[2], at[3]);
+            const uint4 a1 = make_uint4(at[4], at[5], at[6], at[7]);
+            *reinterpret_cast<uint4*>(table + first) = a0;
+            *reinterpret_cast<uint4*>(table + first + 4) = a1;
+            *reinterpret_cast<uint4*>(cursor + first) = a0;
+            *reinterpret_cast<uint4*>(cursor + first + 4) = a1;
             if (tid < 8) B[m + tid] = 0xffffffffu;  // past every composite
             __syncthreads();
             // each selected composite ((0xffff - key) << 16 | id) into its key's group
