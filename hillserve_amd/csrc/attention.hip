@@ -278,11 +278,9 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
 
     // ---- the 4 row groups share m: add their o; l from the row lanes ------
 #pragma unroll
-    for (uint32_t off = 16; off < 64; off <<= 1)
+    for (uint32_t j = 0; j < 4; ++j)
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j)
-#pragma unroll
-            for (uint32_t c = 0; c < 8; ++c) o[j][c] += __shfl_xor(o[j][c], off, 64);
+        for (uint32_t c = 0; c < 8; ++c) o[j][c] = rows_sum_f32(o[j][c]);
     float l[4];
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j) l[j] = first_lane(row_sum16(lsum[j]));
@@ -467,11 +465,9 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
         }
     }
 #pragma unroll
-    for (uint32_t off = 16; off < 64; off <<= 1)
+    for (uint32_t j = 0; j < 4; ++j)
 #pragma unroll
-        for (uint32_t j = 0; j < 4; ++j)
-#pragma unroll
-            for (uint32_t c = 0; c < 8; ++c) o[j][c] += __shfl_xor(o[j][c], off, 64);
+        for (uint32_t c = 0; c < 8; ++c) o[j][c] = rows_sum_f32(o[j][c]);
     if (lane < 16) {
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {

@@ -102,15 +102,43 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
     return static_cast<uint32_t>(
         __builtin_amdgcn_readlane(static_cast<int>(wave_inclusive_sum_u32(v)), 63));
 }
+// The same DPP pattern over floats (the `identity` fills lanes whose source
+// lies outside the row): the maximum is exact in any order (fmaxf drops NaN
+// as the butterfly did); the sum is one fixed summation order.
+template <int kCtrl, int kRowMask = 0xf>
+__device__ __forceinline__ float dpp_move_f32(float v, float identity) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(v),
+                                                      kCtrl, kRowMask, 0xf, false));
+}
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
-    return v;
+    constexpr float kLow = -INFINITY;
+    v = fmaxf(v, dpp_move_f32<dpp::kRowShr1>(v, kLow));
+    v = fmaxf(v, dpp_move_f32<dpp::kRowShr2>(v, kLow));
+    v = fmaxf(v, dpp_move_f32<dpp::kRowShr4>(v, kLow));
+    v = fmaxf(v, dpp_move_f32<dpp::kRowShr8>(v, kLow));
+    v = fmaxf(v, dpp_move_f32<dpp::kRowBcast15, 0xa>(v, kLow));
+    v = fmaxf(v, dpp_move_f32<dpp::kRowBcast31, 0xc>(v, kLow));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
-    return v;
+    v += dpp_move_f32<dpp::kRowShr1>(v, 0.0f);
+    v += dpp_move_f32<dpp::kRowShr2>(v, 0.0f);
+    v += dpp_move_f32<dpp::kRowShr4>(v, 0.0f);
+    v += dpp_move_f32<dpp::kRowShr8>(v, 0.0f);
+    v += dpp_move_f32<dpp::kRowBcast15, 0xa>(v, 0.0f);
+    v += dpp_move_f32<dpp::kRowBcast31, 0xc>(v, 0.0f);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// Sum over the 4 rows of 16 lanes, the result in every row: rows 0+1 and
+// 2+3 first, then the two pairs (the order of xor-16 then xor-32 butterfly
+// steps), with the gfx950 lane swaps instead of LDS permutes.
+__device__ __forceinline__ float rows_sum_f32(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Number of set lanes below the calling lane in a 64-bit ballot.
