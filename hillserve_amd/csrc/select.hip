@@ -514,7 +514,11 @@ struct CountLds {
     uint32_t current;  // raw bits of this head's current-token score
 };
 
-// Group g (head, slice) of job `job` by one kThreads workgroup.
+// Group g (head, slice) of job `job` by one kThreads workgroup.  kCurrent:
+// some job of the batch completes its current token (the scoring call it
+// makes takes more registers than the rest of the count: batches without
+// one run the leaner instance, four workgroups per CU).
+template <bool kCurrent>
 __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, uint32_t job,
                                             CountLds& lds) {
     auto& whist = lds.whist;
@@ -534,8 +538,9 @@ __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, ui
     // its head (wave 1, on another SIMD), writes it into the scores and
     // counts it in place of what the column held.
     const uint32_t last = a.n - 1u;
-    const bool holds_last = a.cur_key && last >= s * kSlice && last < s * kSlice + kSlice;
-    if (a.cur_key) {
+    const bool holds_last =
+        kCurrent && a.cur_key && last >= s * kSlice && last < s * kSlice + kSlice;
+    if (kCurrent && a.cur_key) {
         if (tid == 0) {
             const uint32_t c0 = score_current(a.cur_q, a.cur_key, 0);
             if (!is_nan_half(c0)) best = max(best, order_key(c0));
@@ -597,9 +602,10 @@ __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, ui
     }
 }
 
+template <bool kCurrent>
 __global__ void __launch_bounds__(kThreads) count_kernel(const SelectJobs js) {
     __shared__ CountLds lds;
-    count_group(js, blockIdx.x, blockIdx.y, lds);
+    count_group<kCurrent>(js, blockIdx.x, blockIdx.y, lds);
 }
 
 // k from every head's count and nonfinite flag (policy/gqa_policy.cpp:51-63),
@@ -1617,6 +1623,7 @@ __global__ void __launch_bounds__(kThreads) rank_kernel(SelectArgs a) {
 // heads x 4 channel groups) and the next layer's selection count (the
 // others: (head, slice) groups x jobs) in one launch; both are short and
 // latency-bound, and neither reads what the other writes.
+template <bool kCurrent>
 __global__ void __launch_bounds__(kThreads)
 combine_count_kernel(const float* __restrict__ part, uint32_t chunks, float* __restrict__ out,
                      const SelectJobs js, uint32_t groups) {
@@ -1631,7 +1638,7 @@ combine_count_kernel(const float* __restrict__ part, uint32_t chunks, float* __r
         return;
     }
     const uint32_t b = blockIdx.x - kMergers;
-    count_group(js, b % groups, b / groups, lds.count);
+    count_group<kCurrent>(js, b % groups, b / groups, lds.count);
 }
 
 }  // namespace
@@ -1687,7 +1694,7 @@ bool per_head_path(uint32_t n, float ratio, uint32_t flags) {
 // What the launches of a batch need to know about its jobs.
 struct BatchShape {
     uint32_t max_partials = 0, max_groups = 0;
-    bool any_own_partial = false, all_per_head = true;
+    bool any_own_partial = false, all_per_head = true, any_current = false;
 };
 BatchShape batch_shape(const SelectJobs& js) {
     BatchShape b;
@@ -1696,6 +1703,7 @@ BatchShape batch_shape(const SelectJobs& js) {
         b.max_partials = std::max(b.max_partials, p.partials);
         b.max_groups = std::max(b.max_groups, p.groups);
         b.any_own_partial |= js.job[j].partial == nullptr;
+        b.any_current |= js.job[j].cur_key != nullptr;
         b.all_per_head &= per_head_path(js.job[j].n, js.ratio, js.flags);
     }
     return b;
@@ -1708,7 +1716,12 @@ void launch_counts(const SelectJobs& js, const BatchShape& b, hipStream_t stream
     if (b.any_own_partial)
         hipLaunchKernelGGL(head0_max_kernel, dim3((b.max_partials + 3) / 4, js.count), dim3(256), 0,
                            stream, js);
-    hipLaunchKernelGGL(count_kernel, dim3(b.max_groups, js.count), dim3(kThreads), 0, stream, js);
+    if (b.any_current)
+        hipLaunchKernelGGL(count_kernel<true>, dim3(b.max_groups, js.count), dim3(kThreads), 0,
+                           stream, js);
+    else
+        hipLaunchKernelGGL(count_kernel<false>, dim3(b.max_groups, js.count), dim3(kThreads), 0,
+                           stream, js);
 }
 
 // Launches for the checked jobs of `js`.  Batches whose jobs all take the
@@ -1942,8 +1955,13 @@ int launch_attention_then_count(const float* q, const uint8_t* k_pool, const uin
     if (b.any_own_partial)
         hipLaunchKernelGGL(head0_max_kernel, dim3((b.max_partials + 3) / 4, js.count), dim3(256), 0,
                            stream, js);
-    hipLaunchKernelGGL(combine_count_kernel, dim3(32 * 4 + b.max_groups * js.count), dim3(kThreads),
-                       0, stream, static_cast<const float*>(workspace), chunks, out, js, b.max_groups);
+    const dim3 grid(32 * 4 + b.max_groups * js.count);
+    if (b.any_current)
+        hipLaunchKernelGGL(combine_count_kernel<true>, grid, dim3(kThreads), 0, stream,
+                           static_cast<const float*>(workspace), chunks, out, js, b.max_groups);
+    else
+        hipLaunchKernelGGL(combine_count_kernel<false>, grid, dim3(kThreads), 0, stream,
+                           static_cast<const float*>(workspace), chunks, out, js, b.max_groups);
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "attention-then-count launch");
 }
