@@ -35,7 +35,8 @@ Also on the same JSON line:
                 layer's 6560 slots.
   batch_step    configs[3]: rehearsal query on MFMA + batched score + select.
   tier_step     configs[4]: hot/cold chain with the cold rows over the host
-                link, checked bit for bit against an all-hot pool.
+                link (a copy kernel, and the copy engines), checked bit for
+                bit against an all-hot pool.
   cpu_baseline  the reference's own CPU path (FullGqaCpuScorer + scaling +
                 select_gqa_scores, compiled from the reference sources into
                 oracle/_ref) on one layer, timed on this host: median of at
@@ -732,7 +733,12 @@ def tier_leg(g, args):
     sequence; on a side stream: the cold fetch of that layer (identity and
     FNV-1a checked), overlapped with the next layer's score and selection;
     attention of the layer runs on the main stream once its cold rows are in.
-    A step is 30 layers over TIER_PHYS distinct physical layers."""
+    A step is 30 layers over TIER_PHYS distinct physical layers.  The same
+    step runs twice: with the device read of hs_kv_cold_fetch (a kernel
+    copies the selected cold records over the host link), and with the copy
+    engines (hs_kv_cold_fetch_runs: every cold row of the layer, one
+    hipMemcpyAsync per run of consecutive cold positions, checked in HBM;
+    attention through a static row map)."""
     import ctypes
     import numpy as np
     hs, ops, torch, stream, dev = g.hs, g.ops, g.torch, g.stream, g.dev
@@ -792,7 +798,17 @@ def tier_leg(g, args):
                 out=torch.empty((32, 128), dtype=torch.float32, device=dev),
                 aws=ops.workspace(ops.attention_workspace_bytes(TIER_N), dev)))
             del rows, v, host_rows
-        seqs.append(dict(image=image, layers=layers))
+        # the copy-engine variant stages every cold row of a layer: its runs of
+        # consecutive cold positions, their expected positions on the device,
+        # and the static row map (hot token -> slot, cold token -> staging row)
+        cold = np.nonzero(slot < 0)[0]
+        static_map = slot.copy()
+        static_map[cold] = hot_rows + np.arange(cold.size, dtype=np.int32)
+        for d in layers:
+            d["raw"] = torch.empty((cold_rows, 4128), dtype=torch.uint8, device=dev)
+        seqs.append(dict(image=image, layers=layers, runs=ops.cold_runs(cold),
+                         cold_dev=torch.from_numpy(cold.astype(np.int32)).to(dev),
+                         static_map=torch.from_numpy(static_map).to(dev)))
     torch.cuda.synchronize()
     sp, sside = ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p(side.cuda_stream)
     score_tabs, sel_tabs = [], []
@@ -814,11 +830,13 @@ def tier_leg(g, args):
     score_ptr = [score_tabs[2 * l] for l in range(TIER_PHYS)]
     sel_ptr = [sel_tabs[2 * l] for l in range(TIER_PHYS)]
 
-    def front(l):  # main stream: score, select, cold plan of layer l
+    def front(l, plan=True):  # main stream: score, select (and cold plan) of layer l
         p = l % TIER_PHYS
         hs.check(L.hs_gqa_score_batched(score_ptr[p], TIER_SEQS, sp))
         hs.check(L.hs_gqa_select_batched(sel_ptr[p], TIER_SEQS, 32, ALPHA, RATIO,
                                          hs.HS_SELECT_SCALE_RAW | hs.HS_SELECT_ID_ORDER, sp))
+        if not plan:
+            return
         for sq in seqs:
             d = sq["layers"][p]
             hs.check(L.hs_gqa_cold_plan(vp(d["member"]), 32, TIER_N, vp(d["slot"]), hot_rows,
@@ -833,39 +851,66 @@ def tier_leg(g, args):
                                         ctypes.c_void_p(staging.data_ptr() + 2048), 4096,
                                         vp(d["cstatus"]), vp(d["cws"]), strm))
 
-    def attend(l):
+    def cold_engines(l, strm):  # every cold row of the layer, by the copy engines
         p = l % TIER_PHYS
         for sq in seqs:
             d = sq["layers"][p]
+            first, count_arr, nruns = sq["runs"]
+            staging = d["pool"][hot_rows:]
+            hs.check(L.hs_kv_cold_fetch_runs(vp(sq["image"]), p, ctypes.cast(first, ctypes.c_void_p),
+                                             ctypes.cast(count_arr, ctypes.c_void_p), nruns,
+                                             vp(d["raw"]), vp(sq["cold_dev"]), cold_rows,
+                                             vp(staging), ctypes.c_void_p(staging.data_ptr() + 2048),
+                                             4096, vp(d["cstatus"]), vp(d["cws"]), strm))
+
+    def attend(l, static=False, marks=None):
+        p = l % TIER_PHYS
+        if marks is not None:
+            b = torch.cuda.Event(enable_timing=True)
+            b.record(stream)
+        for sq in seqs:
+            d = sq["layers"][p]
+            rowmap = sq["static_map"] if static else d["rowmap"]
             hs.check(L.hs_gqa_sparse_attention(vp(d["q32"]), vp(d["pool"]),
                                                ctypes.c_void_p(d["pool"].data_ptr() + 2048), 4096,
-                                               vp(d["rowmap"]), hot_rows + cold_rows,
+                                               vp(rowmap), hot_rows + cold_rows,
                                                vp(d["member"]), TIER_N, vp(d["out"]), vp(d["aws"]),
                                                sp))
+        if marks is not None:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record(stream)
+            marks.append((b, e))
 
-    def step(with_cold=True):
+    def step(with_cold=True, engines=False, marks=None):
         pending = None
         for l in range(LAYERS):
-            front(l)
+            front(l, plan=not engines)
             ev = torch.cuda.Event()
             ev.record(stream)
             if with_cold:
                 side.wait_event(ev)
-                cold(l, sside)
+                (cold_engines if engines else cold)(l, sside)
                 done = torch.cuda.Event()
                 done.record(side)
             if pending is not None:
                 if with_cold:
                     stream.wait_event(pending[1])
-                attend(pending[0])
+                attend(pending[0], engines, marks)
             pending = (l, done if with_cold else None)
         if with_cold:
             stream.wait_event(pending[1])
-        attend(pending[0])
+        attend(pending[0], engines, marks)
 
-    def cold_only():
+    def cold_only(engines=False):
         for l in range(LAYERS):
-            cold(l, sp)
+            (cold_engines if engines else cold)(l, sp)
+
+    def attention_us(fn):
+        """Mean µs of one attention call (of the TIER_SEQS per layer) inside fn."""
+        marks = []
+        fn(marks)
+        torch.cuda.synchronize()
+        return 1e3 * sum(b.elapsed_time(e) for b, e in marks) / (len(marks) * TIER_SEQS)
 
     def timed(fn, reps):
         b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -892,22 +937,44 @@ def tier_leg(g, args):
     full = torch.empty((TIER_N, 2048), dtype=torch.float16, device=dev)
     fstatus = ops.new_status(dev)
     fws = ops.workspace(L.hs_kv_cold_fetch_workspace_bytes(TIER_N), dev)
+    refs = []
     for sq in seqs:
         d = sq["layers"][last]
         hs.check(L.hs_kv_cold_fetch(vp(sq["image"]), last, vp(every), TIER_N, vp(full),
                                     ctypes.c_void_p(full.data_ptr() + 2048), 4096, vp(fstatus),
                                     vp(fws), sp))
-        ref = ops.sparse_attention(d["q32"], full.reshape(-1), TIER_N, d["member"], stream=stream)
+        refs.append(ops.sparse_attention(d["q32"], full.reshape(-1), TIER_N, d["member"],
+                                         stream=stream))
         assert ops.read_status(fstatus)["code"] == 0
-        assert torch.equal(ref.view(torch.int32), d["out"].view(torch.int32)), \
-            "configs[4]: hot + fetched-cold attention differs from the all-hot attention"
+
+    def check_outputs(what):
+        for sq, ref in zip(seqs, refs):
+            d = sq["layers"][last]
+            for dd in sq["layers"]:
+                assert ops.read_status(dd["cstatus"])["code"] == 0, (what, ops.read_status(dd["cstatus"]))
+            assert torch.equal(ref.view(torch.int32), d["out"].view(torch.int32)), \
+                f"configs[4] ({what}): hot + fetched-cold attention differs from the all-hot attention"
+
+    check_outputs("kernel copy")
+    step(engines=True)
+    torch.cuda.synchronize()
+    check_outputs("copy engines")
     del full, fws
     reps = 2
     step_ms = timed(step, reps)
     main_ms = timed(lambda: step(False), reps)
     cold_ms = timed(cold_only, reps)
+    ce_step_ms = timed(lambda: step(engines=True), reps)
+    ce_main_ms = timed(lambda: step(False, engines=True), reps)
+    ce_cold_ms = timed(lambda: cold_only(True), reps)
+    attn_alone_us = 1e3 * timed(lambda: [attend(l, True) for l in range(LAYERS)], reps) / (
+        LAYERS * TIER_SEQS)
+    attn_kernel_us = attention_us(lambda m: step(marks=m))
+    attn_engines_us = attention_us(lambda m: step(engines=True, marks=m))
     cold_bytes = sum(counts) / len(counts) * TIER_SEQS * LAYERS * 4128
     overlap = max(0.0, min(1.0, (main_ms + cold_ms - step_ms) / cold_ms))
+    ce_bytes = cold_rows * TIER_SEQS * LAYERS * 4128
+    ce_overlap = max(0.0, min(1.0, (ce_main_ms + ce_cold_ms - ce_step_ms) / ce_cold_ms))
     out = {
         "workload": "configs[4]: 8 sequences x N=32768, 50% of 64-token blocks in HBM, cold rows in "
                     "pinned SegmentedKVStore images, 30 layers per step",
@@ -919,11 +986,29 @@ def tier_leg(g, args):
         "overlap_ceiling": min(1.0, main_ms / cold_ms),
         "cold_rows_per_seq_layer": sum(counts) / len(counts),
         "cold_link_gbps": cold_bytes / (cold_ms * 1e-3) / 1e9,
+        "attention_us_in_step": attn_kernel_us,
+        "attention_us_alone": attn_alone_us,
+        "copy_engines": {
+            "what": "every cold row of a layer staged by hs_kv_cold_fetch_runs (one hipMemcpyAsync "
+                    "per run of consecutive cold positions), checked and split in HBM, attention "
+                    "through a static row map (no cold plan)",
+            "ms_per_step": ce_step_ms, "main_stream_ms": ce_main_ms, "cold_fetch_ms": ce_cold_ms,
+            "cold_link_gbps": ce_bytes / (ce_cold_ms * 1e-3) / 1e9,
+            "overlap_fraction": ce_overlap,
+            "overlap_ceiling": min(1.0, ce_main_ms / ce_cold_ms),
+            "attention_us_in_step": attn_engines_us,
+            "runs_per_seq": sum(sq["runs"][2] for sq in seqs) / len(seqs),
+        },
     }
     log(f"configs[4]: {step_ms:.1f} ms/step (main stream alone {main_ms:.1f} ms, cold fetch alone "
         f"{cold_ms:.1f} ms = {out['cold_link_gbps']:.1f} GB/s over the host link, "
         f"{out['cold_rows_per_seq_layer']:.0f} cold rows per sequence-layer); overlap "
-        f"fraction {overlap:.3f}")
+        f"fraction {overlap:.3f}; attention {attn_kernel_us:.1f} us per call in the step, "
+        f"{attn_alone_us:.1f} us alone")
+    log(f"configs[4] copy engines: {ce_step_ms:.1f} ms/step (main {ce_main_ms:.1f} ms, cold "
+        f"{ce_cold_ms:.1f} ms = {out['copy_engines']['cold_link_gbps']:.1f} GB/s, "
+        f"{out['copy_engines']['runs_per_seq']:.0f} runs per sequence-layer); overlap "
+        f"{ce_overlap:.3f}; attention {attn_engines_us:.1f} us per call in the step")
     del seqs
     return out
 

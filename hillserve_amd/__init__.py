@@ -134,6 +134,7 @@ SIGNATURES = {
     "hs_kv_store_append": (_I, [_P, _U32, _U32, _P, _U32]),
     "hs_kv_cold_fetch_workspace_bytes": (_SZ, [_U32]),
     "hs_kv_cold_fetch": (_I, [_P, _U32, _P, _U32, _P, _P, _SZ, _P, _P, _P]),
+    "hs_kv_cold_fetch_runs": (_I, [_P, _U32, _P, _P, _U32, _P, _P, _U32, _P, _P, _SZ, _P, _P, _P]),
     "hs_gqa_cold_plan": (_I, [_P, _U32, _U32, _P, _U32, _U32, _P, _P, _P, _P]),
     "hs_gqa_union_workspace_bytes": (_SZ, [_U32]),
     "hs_gqa_physical_union": (_I, [_P, _P, _SZ, _U32, _P, _P, _P, _P, _P]),

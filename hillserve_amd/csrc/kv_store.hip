@@ -24,6 +24,11 @@
 //                       in byte order (FNV-1a is sequential within a record)
 //                       and compares the digest;
 //   cold_status_kernel: folds the per-record flags into the status.
+// hs_kv_cold_fetch_runs moves the same records over the host link with the
+// copy engines instead: one hipMemcpyAsync per run of consecutive positions
+// into a raw staging buffer in HBM (4128 B records, back to back), after
+// which the same three kernels check and split them there, so no CU waits
+// on the host link.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -60,6 +65,10 @@ struct RecordHeader {
 static_assert(sizeof(RecordHeader) == kHeader, "32-byte record header");
 
 // One wave per record: payload 4096 B = 64 lanes x 4 x 16 B, header by 2 lanes.
+// kStaged: record i is the i-th of `image` laid back to back (the raw
+// staging buffer of hs_kv_cold_fetch_runs), expected at position
+// positions[i]; otherwise record (layer, positions[i]) of the image.
+template <bool kStaged>
 __global__ void __launch_bounds__(256)
 cold_copy_kernel(const uint8_t* __restrict__ image, uint32_t layer, uint32_t capacity,
                  uint64_t request, const uint32_t* __restrict__ positions, uint32_t count,
@@ -76,7 +85,8 @@ cold_copy_kernel(const uint8_t* __restrict__ image, uint32_t layer, uint32_t cap
         }
         return;
     }
-    const uint8_t* rec = image + 4096ull + (uint64_t(layer) * capacity + p) * kStride;
+    const uint8_t* rec = kStaged ? image + uint64_t(i) * kStride
+                                 : image + 4096ull + (uint64_t(layer) * capacity + p) * kStride;
     uint4 v[4];
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j)
@@ -205,9 +215,12 @@ size_t cold_fetch_workspace_bytes(uint32_t count) {
     return align256(sizeof(uint64_t) * n) + align256(sizeof(uint32_t) * n);
 }
 
-int launch_cold_fetch(const void* image, uint32_t layer, const uint32_t* positions,
-                      uint32_t count, uint8_t* k_out, uint8_t* v_out, size_t row_bytes,
-                      hs_status_t* status, void* workspace, hipStream_t stream) {
+// Host checks shared by both reads; the image header is host memory, so the
+// geometry comes from it, as the reference's reader takes it from the
+// file's first page.  On success h[] holds the header.
+int check_cold_read(const void* image, uint32_t layer, const uint32_t* positions, uint32_t count,
+                    const uint8_t* k_out, const uint8_t* v_out, size_t row_bytes,
+                    const hs_status_t* status, const void* workspace, uint64_t (&h)[8]) {
     if (!image || !positions || !k_out || !v_out || !status || !workspace)
         return reject("cold fetch: null pointer");
     if (count == 0) return reject("cold fetch: count must be >= 1");
@@ -216,27 +229,77 @@ int launch_cold_fetch(const void* image, uint32_t layer, const uint32_t* positio
         return reject("cold fetch: image, K and V rows must be 16-byte aligned");
     if (row_bytes < 2048 || row_bytes % 16 != 0 || row_bytes > (1u << 20))
         return reject("cold fetch: row_bytes must be 2048..1 MiB and a multiple of 16");
-    const int64_t v_delta = reinterpret_cast<intptr_t>(v_out) - reinterpret_cast<intptr_t>(k_out);
-    // the image header is host memory: geometry comes from it, as the
-    // reference's reader takes it from the file's first page
-    uint64_t h[8];
     std::memcpy(h, image, sizeof h);
     if (h[0] != kMagic || h[1] != 1 || h[5] != kRow || h[6] != kStride || h[3] == 0 ||
         h[3] > kMaxLayers || h[4] == 0 || h[4] > kMaxPositions || h[7] != extent_of(h[3], h[4]))
         return reject("cold fetch: not a SegmentedKVStore v1 image of 4096 B records");
     if (layer >= h[3]) return reject("cold fetch: layer beyond the image");
+    return HS_OK;
+}
+
+// The check and split of `count` records (the copy kernel reads the image or
+// the staged records), the digest and the status.
+template <bool kStaged>
+int launch_cold_checks(const uint8_t* records, uint32_t layer, const uint64_t (&h)[8],
+                       const uint32_t* positions, uint32_t count, uint8_t* k_out, uint8_t* v_out,
+                       size_t row_bytes, hs_status_t* status, void* workspace, hipStream_t stream) {
+    const int64_t v_delta = reinterpret_cast<intptr_t>(v_out) - reinterpret_cast<intptr_t>(k_out);
     uint64_t* digests = static_cast<uint64_t*>(workspace);
     uint32_t* flags = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) +
                                                   align256(sizeof(uint64_t) * count));
-    hipLaunchKernelGGL(cold_copy_kernel, dim3((count + 3) / 4), dim3(256), 0, stream,
-                       static_cast<const uint8_t*>(image), layer, static_cast<uint32_t>(h[4]),
-                       h[2], positions, count, k_out, static_cast<uint32_t>(row_bytes), v_delta,
-                       digests, flags);
+    hipLaunchKernelGGL(cold_copy_kernel<kStaged>, dim3((count + 3) / 4), dim3(256), 0, stream,
+                       records, layer, static_cast<uint32_t>(h[4]), h[2], positions, count, k_out,
+                       static_cast<uint32_t>(row_bytes), v_delta, digests, flags);
     hipLaunchKernelGGL(cold_digest_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, k_out,
                        static_cast<uint32_t>(row_bytes), v_delta, digests, count, flags);
     hipLaunchKernelGGL(cold_status_kernel, dim3(1), dim3(256), 0, stream, flags, count, status);
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "cold fetch launch");
+}
+
+int launch_cold_fetch(const void* image, uint32_t layer, const uint32_t* positions,
+                      uint32_t count, uint8_t* k_out, uint8_t* v_out, size_t row_bytes,
+                      hs_status_t* status, void* workspace, hipStream_t stream) {
+    uint64_t h[8];
+    const int rc = check_cold_read(image, layer, positions, count, k_out, v_out, row_bytes, status,
+                                   workspace, h);
+    if (rc != HS_OK) return rc;
+    return launch_cold_checks<false>(static_cast<const uint8_t*>(image), layer, h, positions,
+                                     count, k_out, v_out, row_bytes, status, workspace, stream);
+}
+
+int launch_cold_fetch_runs(const void* image, uint32_t layer, const uint32_t* run_first,
+                           const uint32_t* run_count, uint32_t runs, uint8_t* raw,
+                           const uint32_t* positions, uint32_t count, uint8_t* k_out,
+                           uint8_t* v_out, size_t row_bytes, hs_status_t* status, void* workspace,
+                           hipStream_t stream) {
+    uint64_t h[8];
+    int rc = check_cold_read(image, layer, positions, count, k_out, v_out, row_bytes, status,
+                             workspace, h);
+    if (rc != HS_OK) return rc;
+    if (!raw || !run_first || !run_count || runs == 0) return reject("cold fetch runs: null pointer or no run");
+    uint64_t total = 0;
+    for (uint32_t r = 0; r < runs; ++r) {
+        if (run_count[r] == 0 || run_first[r] >= h[4] || run_count[r] > h[4] - run_first[r])
+            return reject("cold fetch runs: a run outside the layer's positions");
+        total += run_count[r];
+    }
+    if (total != count) return reject("cold fetch runs: the runs must hold exactly count records");
+    // one copy per run, back to back in the staging buffer (the copy
+    // engines move pinned host memory; no kernel waits on the link).  The
+    // batched copy call of newer HIP runtimes is not used: a process may run
+    // this library on an older runtime (the one a framework ships).
+    const uint8_t* base = static_cast<const uint8_t*>(image);
+    uint64_t at = 0;
+    for (uint32_t r = 0; r < runs; ++r) {
+        const uint64_t bytes = uint64_t(run_count[r]) * kStride;
+        const hipError_t e = hipMemcpyAsync(raw + at, base + record_offset(layer, uint32_t(h[4]), run_first[r]),
+                                            bytes, hipMemcpyHostToDevice, stream);
+        if (e != hipSuccess) return hip_fail(e, "cold fetch runs: copy");
+        at += bytes;
+    }
+    return launch_cold_checks<true>(raw, layer, h, positions, count, k_out, v_out, row_bytes,
+                                    status, workspace, stream);
 }
 
 int launch_cold_plan(const uint32_t* member, uint32_t heads, uint32_t n, const int32_t* slot,
@@ -312,6 +375,17 @@ int hs_kv_cold_fetch(const void* image, uint32_t layer, const uint32_t* position
     hs::clear_error();
     return hs::launch_cold_fetch(image, layer, positions_dev, count, k_out_dev, v_out_dev,
                                  row_bytes, status_dev, workspace_dev, hs::as_stream(stream));
+}
+
+int hs_kv_cold_fetch_runs(const void* image, uint32_t layer, const uint32_t* run_first,
+                          const uint32_t* run_count, uint32_t runs, uint8_t* raw_dev,
+                          const uint32_t* positions_dev, uint32_t count, uint8_t* k_out_dev,
+                          uint8_t* v_out_dev, size_t row_bytes, hs_status_t* status_dev,
+                          void* workspace_dev, void* stream) {
+    hs::clear_error();
+    return hs::launch_cold_fetch_runs(image, layer, run_first, run_count, runs, raw_dev,
+                                      positions_dev, count, k_out_dev, v_out_dev, row_bytes,
+                                      status_dev, workspace_dev, hs::as_stream(stream));
 }
 
 }  // extern "C"

@@ -525,6 +525,50 @@ def kv_cold_fetch(image, layer, positions, k_out, *, v_out=None, row_bytes=4096,
     return status
 
 
+def cold_runs(positions):
+    """(run_first, run_count) ctypes arrays of the consecutive runs of an
+    ascending host list of positions."""
+    firsts, counts = [], []
+    for p in positions:
+        p = int(p)
+        if firsts and firsts[-1] + counts[-1] == p:
+            counts[-1] += 1
+        else:
+            firsts.append(p)
+            counts.append(1)
+    n = max(1, len(firsts))
+    return (ctypes.c_uint32 * n)(*firsts), (ctypes.c_uint32 * n)(*counts), len(firsts)
+
+
+def kv_cold_fetch_runs(image, layer, runs, raw, positions, k_out, *, v_out=None, row_bytes=4096,
+                       status=None, ws=None, stream=None):
+    """hs_kv_cold_fetch_runs: the records of `runs` (from cold_runs) copied
+    from the pinned image into `raw` (uint8, count x 4128) by the copy
+    engines, then checked and split into k_out / v_out as kv_cold_fetch does;
+    positions: the expected position of each staged record (device)."""
+    _need_cuda(raw, positions, k_out, v_out)
+    if image.is_cuda or not image.is_pinned():
+        raise ValueError("the store image must be pinned host memory")
+    first, count_arr, nruns = runs
+    count = positions.numel()
+    if v_out is None:
+        if row_bytes != 4096:
+            raise ValueError("a single output tensor holds 4096 B KV records")
+        kp, vp = _p(k_out), ctypes.c_void_p(k_out.data_ptr() + 2048)
+    else:
+        kp, vp = _p(k_out), _p(v_out)
+    if status is None:
+        status = new_status(k_out.device, stream)
+    if ws is None:
+        ws = _scratch(lib().hs_kv_cold_fetch_workspace_bytes(count), k_out.device, stream)
+    check(lib().hs_kv_cold_fetch_runs(ctypes.c_void_p(image.data_ptr()), layer,
+                                      ctypes.cast(first, ctypes.c_void_p),
+                                      ctypes.cast(count_arr, ctypes.c_void_p), nruns, _p(raw),
+                                      _p(positions), count, kp, vp, row_bytes, _p(status), _p(ws),
+                                      _s(stream)))
+    return status
+
+
 # ---- device checks and synthetic data -------------------------------------------------
 
 def selftest_f16_checksums(stream=None):

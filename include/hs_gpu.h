@@ -258,6 +258,23 @@ int hs_kv_cold_fetch(const void *image, uint32_t layer, const uint32_t *position
                      uint32_t count, uint8_t *k_out_dev, uint8_t *v_out_dev, size_t row_bytes,
                      hs_status_t *status_dev, void *workspace_dev, void *stream);
 
+/* The same read with the copy engines crossing the host link (configs[4]'s
+ * "selected cold blocks via hipMemcpyAsync on a side stream"; the same
+ * SegmentedKVStore::fetch checks, storage/segmented_store.cpp:85-95): the
+ * records of positions [run_first[r], run_first[r] + run_count[r]) of one
+ * layer, run after run, are copied from the pinned image with one
+ * hipMemcpyAsync per run into raw_dev (count x 4128 B records back to back,
+ * count = the runs' total), then checked and split on the device as
+ * hs_kv_cold_fetch does, staged record i expected at positions_dev[i]
+ * (normally the runs' positions in order).  No CU waits on the link.
+ * run_first / run_count are host arrays, read by the call.  Same workspace
+ * and status as hs_kv_cold_fetch; raw_dev 16-byte aligned. */
+int hs_kv_cold_fetch_runs(const void *image, uint32_t layer, const uint32_t *run_first,
+                          const uint32_t *run_count, uint32_t runs, uint8_t *raw_dev,
+                          const uint32_t *positions_dev, uint32_t count, uint8_t *k_out_dev,
+                          uint8_t *v_out_dev, size_t row_bytes, hs_status_t *status_dev,
+                          void *workspace_dev, void *stream);
+
 /* Cold plan of one sequence after its selection (the hot/prefetched/cold
  * split of FullGqaRuntimePolicy::fetch, policy/full_gqa_runtime.cpp:
  * 640-660, for device consumers): member_dev [heads][ceil(n/32)] bitmaps,

@@ -128,3 +128,74 @@ def test_cold_plan_and_padded_fetch(hs):
     o = out.cpu().numpy()
     assert np.array_equal(o[: want.size], data[want])
     assert not o[want.size:].any()  # padding rows untouched
+
+
+def runs_fetch(hs, image, layer, positions, split=False):
+    """The same read through hs_kv_cold_fetch_runs (the copy engines move the
+    runs of consecutive positions into a raw staging buffer)."""
+    pos = torch.tensor(positions, dtype=torch.int32, device="cuda")
+    raw = torch.empty((len(positions), 4128), dtype=torch.uint8, device="cuda")
+    runs = hs.ops.cold_runs(positions)
+    if split:
+        k_out = torch.empty((len(positions), 2048), dtype=torch.uint8, device="cuda")
+        v_out = torch.empty((len(positions), 2048), dtype=torch.uint8, device="cuda")
+        status = hs.ops.kv_cold_fetch_runs(image, layer, runs, raw, pos, k_out, v_out=v_out,
+                                           row_bytes=2048)
+        out = torch.cat([k_out, v_out], dim=1)
+    else:
+        out = torch.empty((len(positions), 4096), dtype=torch.uint8, device="cuda")
+        status = hs.ops.kv_cold_fetch_runs(image, layer, runs, raw, pos, out)
+    return out.cpu().numpy(), hs.ops.read_status(status), runs[2]
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_runs_fetch_equals_kernel_fetch(hs, split):
+    """Ascending positions in runs of random lengths (64-token blocks and
+    single rows): the staged rows equal the kernel read's byte for byte."""
+    g = rng(3)
+    n = 4096
+    rows = g.integers(0, 256, size=(n, 4096), dtype=np.uint8)
+    image = pinned_image(hs, 91, 2, n, 1, rows)
+    blocks = np.sort(g.permutation(n // 64)[: n // 128])
+    positions = sorted({int(b) * 64 + t for b in blocks for t in range(64)} |
+                       {int(x) for x in g.integers(0, n, size=200)})
+    want, st_k = cold_fetch(hs, image, 1, positions, split=split)
+    got, st_r, runs = runs_fetch(hs, image, 1, positions, split=split)
+    assert runs > 1
+    assert st_k["code"] == 0 and st_r["code"] == 0 and st_r["k"] == 0
+    assert np.array_equal(got, want)
+    assert np.array_equal(got, rows[positions])
+
+
+def test_runs_fetch_corruption_and_rejections(hs):
+    g = rng(4)
+    rows = g.integers(0, 256, size=(128, 4096), dtype=np.uint8)
+    image = pinned_image(hs, 6, 1, 128, 0, rows)
+    raw = image.numpy()
+    rec = lambda p: 4096 + p * 4128
+    raw[rec(70) + 32 + 17] ^= 0x80           # payload: digest mismatch
+    raw[rec(90) + 8] ^= 1                     # position field
+    positions = list(range(64, 128))
+    _, st, _ = runs_fetch(hs, image, 0, positions)
+    assert st["code"] == hs.HS_ERR_CORRUPT and st["k"] == 2
+    # an expected position that differs from the staged record's is an identity failure
+    L = hs.lib()
+    pos = torch.tensor(positions[:8], dtype=torch.int32, device="cuda")
+    wrong = torch.tensor([64, 65, 66, 67, 68, 69, 71, 71], dtype=torch.int32, device="cuda")
+    out = torch.empty((8, 4096), dtype=torch.uint8, device="cuda")
+    stage = torch.empty((8, 4128), dtype=torch.uint8, device="cuda")
+    st = hs.ops.kv_cold_fetch_runs(image, 0, hs.ops.cold_runs(range(64, 72)), stage, wrong, out)
+    assert hs.ops.read_status(st) == {"code": hs.HS_ERR_CORRUPT, "k": 1, "boundary_tied_heads": 0,
+                                      "head0_max_key": 0}
+    # runs that do not hold exactly `count` records, or leave the layer
+    ws = hs.ops.workspace(L.hs_kv_cold_fetch_workspace_bytes(8))
+    status = hs.ops.new_status()
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    for firsts, counts in (([64], [7]), ([64], [9]), ([124], [8]), ([200], [8])):
+        f = (ctypes.c_uint32 * 1)(*firsts)
+        c = (ctypes.c_uint32 * 1)(*counts)
+        rc = L.hs_kv_cold_fetch_runs(vp(image), 0, ctypes.cast(f, ctypes.c_void_p),
+                                     ctypes.cast(c, ctypes.c_void_p), 1, vp(stage), vp(pos), 8,
+                                     vp(out), ctypes.c_void_p(out.data_ptr() + 2048), 4096,
+                                     vp(status), vp(ws), None)
+        assert rc == hs.HS_ERR_ARGUMENT, (firsts, counts)

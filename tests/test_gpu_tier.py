@@ -122,6 +122,42 @@ def test_hot_cold_chain(hs, port, n):
         assert err <= TOL, err
 
 
+@pytest.mark.parametrize("n", [4096])
+def test_hot_cold_chain_copy_engines(hs, port, n):
+    """configs[4]'s copy-engine variant: every cold row of the layer staged by
+    hs_kv_cold_fetch_runs (runs of consecutive cold positions, one
+    hipMemcpyAsync each), a static row map (hot token -> its slot, cold token
+    -> staging row of its rank among the cold positions), attention through
+    it.  Output bit for bit the all-hot attention."""
+    g = rng(5400 + n)
+    k, rows, slot, hot = _sequence(g, n, 333)
+    q16 = f16_bits(g.standard_normal((32, 128)))
+    q32 = g.standard_normal((32, 128)).astype(np.float32)
+    part = torch.empty((n + 63) // 64, dtype=torch.int32, device="cuda")
+    raw = hs.ops.score(to_dev(q16.reshape(-1)), to_dev(k.reshape(-1)), n, head0_partial=part)
+    member = torch.empty((32, (n + 31) // 32), dtype=torch.int32, device="cuda")
+    _, _, _, status = hs.ops.select(raw, 32, n, n, ALPHA, RATIO, scale_raw=True, id_order=True,
+                                    require_k=True, head0_partial=part, member=member)
+    assert hs.ops.read_status(status)["code"] == 0
+    cold = np.nonzero(slot < 0)[0]
+    hot_rows = n - cold.size
+    pool = torch.zeros((n, 2048), dtype=torch.float16, device="cuda")
+    pool[:hot_rows] = to_dev(rows[hot])
+    rowmap = slot.astype(np.int32).copy()
+    rowmap[cold] = hot_rows + np.arange(cold.size, dtype=np.int32)
+    image = _image(hs, rows, 77)
+    runs = hs.ops.cold_runs(cold)
+    assert runs[2] > 1
+    stage = torch.empty((cold.size, 4128), dtype=torch.uint8, device="cuda")
+    cstatus = hs.ops.kv_cold_fetch_runs(image, 0, runs, stage, to_dev(cold.astype(np.int32)),
+                                        pool[hot_rows:])
+    q = torch.from_numpy(q32).cuda()
+    out = hs.ops.sparse_attention(q, pool.reshape(-1), n, member, rows=to_dev(rowmap))
+    assert hs.ops.read_status(cstatus)["code"] == 0
+    ref_dev = hs.ops.sparse_attention(q, to_dev(rows.reshape(-1)), n, member)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref_dev.cpu().numpy().view(np.uint32))
+
+
 def test_corrupt_cold_record_surfaces(hs):
     """A damaged cold record in the chain is reported by the fetch status
     (the reference's fetch throws), not consumed silently."""
