@@ -187,21 +187,51 @@ pack_kernel(PoolSource ps, MapSource ms, const uint64_t* __restrict__ positions,
             reinterpret_cast<uint4*>(k_out + (static_cast<size_t>(s0 + s) * 32 + h) * 128)[c] = kw;
     }
     __syncthreads();
-    // V[h][d][s]: 128 channel rows x 64 slots
+    // V[h][d][s]: 128 channel rows x 64 slots.  A thread gathers 8
+    // consecutive slots of one channel from the tile and stores them as one
+    // 16-byte word (8 threads cover a channel row's 128 B); rows whose start
+    // is not 16-byte aligned (count % 8 != 0) or that end inside the group
+    // store element by element.
     const uint16_t* vt = reinterpret_cast<const uint16_t*>(&vtile[0][0]);
-    for (uint32_t i = tid; i < 128 * 64; i += 256) {
-        const uint32_t d = i >> 6, s = i & 63u;
-        if (s0 + s < count)
-            v_out[(static_cast<size_t>(h) * 128 + d) * count + s0 + s] = vt[s * (17 * 8) + d];
+    const bool wide = (count & 7u) == 0 && (reinterpret_cast<uintptr_t>(v_out) & 15u) == 0;
+    for (uint32_t i = tid; i < 128 * 8; i += 256) {
+        const uint32_t d = i >> 3, sg = (i & 7u) * 8;
+        uint32_t w[4];
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j)
+            w[j] = uint32_t(vt[(sg + 2 * j) * (17 * 8) + d]) |
+                   (uint32_t(vt[(sg + 2 * j + 1) * (17 * 8) + d]) << 16);
+        uint16_t* dst = v_out + (static_cast<size_t>(h) * 128 + d) * count + s0 + sg;
+        if (wide && s0 + sg + 8 <= count) {
+            *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j)
+                if (s0 + sg + j < count) dst[j] = static_cast<uint16_t>(w[j >> 1] >> ((j & 1u) * 16u));
+        }
     }
     if (kPack) {
+        // mask rows, 4 slots (16 B) per thread where the row allows
         const uint32_t qpad = (nq + 63) / 64 * 64;
-        for (uint32_t i = tid; i < qpad * 64; i += 256) {
-            const uint32_t qi = i >> 6, s = i & 63u;
-            if (s0 + s >= count) continue;
-            const uint32_t id = slot_id[s];
-            const bool open = id != 0xffffffffu && qi < nq && id <= positions[qi];
-            mask[(static_cast<size_t>(h) * qpad + qi) * count + s0 + s] = open ? 0.0f : -INFINITY;
+        const bool wide_mask = (count & 3u) == 0 && (reinterpret_cast<uintptr_t>(mask) & 15u) == 0;
+        for (uint32_t i = tid; i < qpad * 16; i += 256) {
+            const uint32_t qi = i >> 4, sg = (i & 15u) * 4;
+            const uint64_t pos = qi < nq ? positions[qi] : 0;
+            float m[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                const uint32_t id = slot_id[sg + j];
+                const bool open = id != 0xffffffffu && qi < nq && id <= pos;
+                m[j] = open ? 0.0f : -INFINITY;
+            }
+            float* dst = mask + (static_cast<size_t>(h) * qpad + qi) * count + s0 + sg;
+            if (wide_mask && s0 + sg + 4 <= count) {
+                *reinterpret_cast<float4*>(dst) = make_float4(m[0], m[1], m[2], m[3]);
+            } else {
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j)
+                    if (s0 + sg + j < count) dst[j] = m[j];
+            }
         }
     }
 }
