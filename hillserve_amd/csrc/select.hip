@@ -380,57 +380,84 @@ __device__ __forceinline__ void key_masks(const uint32_t (&keys)[kWords], uint32
     tie = ~interleave_halves(ne);
 }
 
-// This thread's kR consecutive ids of head h from `begin` into registers
-// (scaled when asked); ids past n read as 0 and are masked by the callers.
-template <uint32_t kR>
-__device__ __forceinline__ void load_run(const SelectArgs& a, uint32_t h, uint32_t begin,
-                                         uint32_t (&packed)[kR / 2]) {
+// kRuns runs of kR consecutive ids of head h, from `begin` and kGap ids
+// apart, into registers (scaled when asked); ids past n read as 0 and are
+// masked by the callers.  Every 16-byte word of every run is requested before
+// any is used, so the runs cost one memory round trip, not one each.
+// kAligned: the caller has checked that the row is 16-byte aligned and
+// n >= 8 (the per-id path for other rows is not compiled).  kScale = false
+// leaves the scaling to the caller.
+template <uint32_t kR, uint32_t kRuns = 1, uint32_t kGap = 0, bool kAligned = false,
+          bool kScale = true>
+__device__ __forceinline__ void load_runs(const SelectArgs& a, uint32_t h, uint32_t begin,
+                                          uint32_t (&packed)[kRuns][kR / 2]) {
     static_assert(kR % 8 == 0, "runs are whole 16-byte words");
     const uint16_t* row = a.scores + static_cast<size_t>(h) * a.stride;
     const uint32_t n = a.n;
     // 16-byte loads when the row is aligned (uniform over the workgroup);
     // every load is straight-line, its address clamped into the row
-    const bool vec = (reinterpret_cast<uintptr_t>(row) & 15u) == 0 && n >= 8;
+    const bool vec = kAligned || ((reinterpret_cast<uintptr_t>(row) & 15u) == 0 && n >= 8);
     if (vec) {
+        uint4 x[kRuns][kR / 8];
 #pragma unroll
-        for (uint32_t v = 0; v < kR / 8; ++v) {
-            const uint32_t at = begin + 8 * v;
-            const bool full = at + 8 <= n;
-            const uint4 x = *reinterpret_cast<const uint4*>(row + (full ? at : 0u));
-            uint32_t* w = packed + 4 * v;
-            w[0] = full ? x.x : 0u; w[1] = full ? x.y : 0u;
-            w[2] = full ? x.z : 0u; w[3] = full ? x.w : 0u;
-        }
-        if (begin + kR > n && begin < n) {  // the row's last, partial word
+        for (uint32_t r = 0; r < kRuns; ++r)
 #pragma unroll
             for (uint32_t v = 0; v < kR / 8; ++v) {
-                const uint32_t at = begin + 8 * v;
-                if (at < n && at + 8 > n) {
+                const uint32_t at = begin + r * kGap + 8 * v;
+                x[r][v] = *reinterpret_cast<const uint4*>(row + (at + 8 <= n ? at : 0u));
+            }
 #pragma unroll
-                    for (uint32_t c = 0; c < 4; ++c) {
-                        const uint32_t lo = at + 2 * c < n ? row[at + 2 * c] : 0u;
-                        const uint32_t hi = at + 2 * c + 1 < n ? row[at + 2 * c + 1] : 0u;
-                        packed[4 * v + c] = lo | (hi << 16);
+        for (uint32_t r = 0; r < kRuns; ++r)
+#pragma unroll
+            for (uint32_t v = 0; v < kR / 8; ++v) {
+                const bool full = begin + r * kGap + 8 * v + 8 <= n;
+                uint32_t* w = packed[r] + 4 * v;
+                w[0] = full ? x[r][v].x : 0u; w[1] = full ? x[r][v].y : 0u;
+                w[2] = full ? x[r][v].z : 0u; w[3] = full ? x[r][v].w : 0u;
+            }
+#pragma unroll
+        for (uint32_t r = 0; r < kRuns; ++r) {
+            const uint32_t b = begin + r * kGap;
+            if (b + kR > n && b < n) {  // the row's last, partial word
+#pragma unroll
+                for (uint32_t v = 0; v < kR / 8; ++v) {
+                    const uint32_t at = b + 8 * v;
+                    if (at < n && at + 8 > n) {
+#pragma unroll
+                        for (uint32_t c = 0; c < 4; ++c) {
+                            const uint32_t lo = at + 2 * c < n ? row[at + 2 * c] : 0u;
+                            const uint32_t hi = at + 2 * c + 1 < n ? row[at + 2 * c + 1] : 0u;
+                            packed[r][4 * v + c] = lo | (hi << 16);
+                        }
                     }
                 }
             }
         }
     } else {
 #pragma unroll
-        for (uint32_t v = 0; v < kR / 8; ++v) {
+        for (uint32_t r = 0; r < kRuns; ++r)
 #pragma unroll
-            for (uint32_t c = 0; c < 4; ++c) {
-                const uint32_t e = begin + 8 * v + 2 * c;
-                const uint32_t lo = row[e < n ? e : n - 1u], hi = row[e + 1 < n ? e + 1 : n - 1u];
-                packed[4 * v + c] = (e < n ? lo : 0u) | ((e + 1 < n ? hi : 0u) << 16);
+            for (uint32_t v = 0; v < kR / 8; ++v) {
+#pragma unroll
+                for (uint32_t c = 0; c < 4; ++c) {
+                    const uint32_t e = begin + r * kGap + 8 * v + 2 * c;
+                    const uint32_t lo = row[e < n ? e : n - 1u], hi = row[e + 1 < n ? e + 1 : n - 1u];
+                    packed[r][4 * v + c] = (e < n ? lo : 0u) | ((e + 1 < n ? hi : 0u) << 16);
+                }
             }
-        }
     }
-    if (a.flags & HS_SELECT_SCALE_RAW) {
+    if (kScale && (a.flags & HS_SELECT_SCALE_RAW)) {
 #pragma unroll
-        for (uint32_t c = 0; c < kR / 2; ++c)
-            packed[c] = scale_raw(packed[c] & 0xffffu) | (scale_raw(packed[c] >> 16) << 16);
+        for (uint32_t r = 0; r < kRuns; ++r)
+#pragma unroll
+            for (uint32_t c = 0; c < kR / 2; ++c)
+                packed[r][c] = scale_raw(packed[r][c] & 0xffffu) | (scale_raw(packed[r][c] >> 16) << 16);
     }
+}
+template <uint32_t kR>
+__device__ __forceinline__ void load_run(const SelectArgs& a, uint32_t h, uint32_t begin,
+                                         uint32_t (&packed)[kR / 2]) {
+    load_runs<kR>(a, h, begin, reinterpret_cast<uint32_t (&)[1][kR / 2]>(packed));
 }
 
 // Order-key histograms: 4 copies per wave, 257 words apart, so lanes that hit
@@ -495,43 +522,78 @@ __device__ __noinline__ uint32_t score_current(const uint16_t* q, const uint16_t
     return f2h(s);
 }
 
-// Maximum of the head-0 per-tile maxima (at most kMaxN / 64 of them).
-__device__ __forceinline__ uint32_t partial_max(const SelectArgs& a) {
-    constexpr uint32_t kLoads = kMaxN / 64 / kThreads;
-    uint32_t v[kLoads];
+// This thread's share of the head-0 per-tile maxima (at most kMaxN / 64 of
+// them), zeros past the end.  No branch: with no tile maxima the loads read
+// the plan record instead (always there) and are discarded.
+constexpr uint32_t kPartialLoads = kMaxN / 64 / kThreads;
+template <uint32_t kLoads = kPartialLoads>
+__device__ __forceinline__ void partial_loads(const SelectArgs& a, uint32_t (&v)[kLoads]) {
+    const uint32_t np = a.partials;
+    const uint32_t* p = np ? a.partial : reinterpret_cast<const uint32_t*>(a.plan);
+    const uint32_t last = np ? np - 1u : 0u;
 #pragma unroll
-    for (uint32_t u = 0; u < kLoads; ++u) v[u] = load_or_zero(a.partial, threadIdx.x + u * kThreads, a.partials);
-    uint32_t best = 0;
-#pragma unroll
-    for (uint32_t u = 0; u < kLoads; ++u) best = v[u] > best ? v[u] : best;
-    return best;
+    for (uint32_t u = 0; u < kLoads; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
+        const uint32_t x = p[i < last ? i : last];
+        v[u] = i < np ? x : 0u;
+    }
 }
 
 // ---- 1. count ---------------------------------------------------------------
+// A count group covers kR consecutive slices of one head; it publishes each
+// slice's count, nonfinite flag and high-byte histogram, the same records
+// whatever kR is.  kR = kWideCount serves large batches: one round of fewer,
+// fuller groups amortises each group's fixed latency (the head-0 maximum and
+// two barriers) over more ids.
+constexpr uint32_t kWideCount = 4;
+// Histograms: one per slice, each in 4 copies 257 words apart, so the lanes
+// of one instruction that hit the same bucket spread over 4 banks and 4
+// addresses.  The waves share the copies: LDS atomics conflict only within
+// an instruction.
+constexpr uint32_t kCountCopies = 4, kCountCopyStride = 257;
+constexpr uint32_t kCountHist = kCountCopies * kCountCopyStride;  // words per slice
 struct CountLds {
-    uint32_t whist[kHistWords];
+    uint32_t whist[kWideCount * kCountHist];
     uint32_t tmp[kWaves];
+    uint32_t sums[2][kWaves];
+    uint32_t bad;      // bit r: slice r of the group holds a nonfinite score
     uint32_t current;  // raw bits of this head's current-token score
 };
 
-// Group g (head, slice) of job `job` by one kThreads workgroup.  kCurrent:
-// some job of the batch completes its current token (the scoring call it
-// makes takes more registers than the rest of the count: batches without
-// one run the leaner instance, four workgroups per CU).
-template <bool kCurrent>
+// Count group g of job `job` by one kThreads workgroup: slices kR * t ..
+// kR * t + kR - 1 of head h (g = h * ceil(S / kR) + t), each thread kRun
+// consecutive ids of every slice, so every load and key store of a wave
+// covers whole consecutive lines.  kR > 1 only for batches whose score rows
+// are all 16-byte aligned with n >= 8 (checked by the host).  kCurrent: some job of the batch completes
+// its current token (the scoring call it makes takes more registers than the
+// rest of the count: batches without one run the leaner instance, four
+// workgroups per CU).
+template <bool kCurrent, uint32_t kR>
 __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, uint32_t job,
                                             CountLds& lds) {
+    static_assert(kR == 1 || kR == 2 || kR == kWideCount, "packed slice counts");
+    static_assert(kSlice < 65536, "a slice count fits 16 bits");
     auto& whist = lds.whist;
     auto& tmp = lds.tmp;
     const SelectArgs a = job_args(js, job);
     const uint32_t tid = threadIdx.x;
-    if (g >= a.heads * a.S) return;  // a shorter job of the batch
-    const uint32_t h = g / a.S, s = g - h * a.S;
-    const uint32_t begin = s * kSlice + tid * kRun;
-    uint32_t best = partial_max(a);
-    uint32_t packed[kRun / 2];
-    load_run<kRun>(a, h, begin, packed);
-    hist_clear(whist);
+    const uint32_t per_head = (a.S + kR - 1) / kR;
+    if (g >= a.heads * per_head) return;  // a shorter job of the batch
+    const uint32_t h = g / per_head, first = (g - h * per_head) * kR;
+    // the head-0 tile maxima and every run requested before any is used
+    // (kR > 1: every job is on the per-head path, n <= 32768, so at most
+    // 512 tile maxima, one per thread)
+    constexpr uint32_t kLoads = kR > 1 ? kHeadMaxN / 64 / kThreads : kPartialLoads;
+    uint32_t pv[kLoads];
+    partial_loads<kLoads>(a, pv);
+    uint32_t packed[kR][kRun / 2];  // ids past n (slices past S) read as zeros
+    load_runs<kRun, kR, kSlice, (kR > 1), false>(a, h, first * kSlice + tid * kRun, packed);
+    const bool scale = (a.flags & HS_SELECT_SCALE_RAW) != 0;
+    uint32_t best = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < kLoads; ++u) best = max(best, pv[u]);
+    for (uint32_t i = tid; i < kR * kCountHist; i += kThreads) whist[i] = 0;
+    if (tid == 0) lds.bad = 0;
     // Current-token completion: column n - 1 is scored here from the query
     // and the appended K row.  Every group folds its head-0 score into the
     // threshold maximum (wave 0); the group holding the column scores it for
@@ -539,7 +601,7 @@ __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, ui
     // counts it in place of what the column held.
     const uint32_t last = a.n - 1u;
     const bool holds_last =
-        kCurrent && a.cur_key && last >= s * kSlice && last < s * kSlice + kSlice;
+        kCurrent && a.cur_key && last >= first * kSlice && last < (first + kR) * kSlice;
     if (kCurrent && a.cur_key) {
         if (tid == 0) {
             const uint32_t c0 = score_current(a.cur_q, a.cur_key, 0);
@@ -553,47 +615,83 @@ __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, ui
         }
     }
     best = block_max(best, tmp);  // its barrier also orders the histogram clear
-    if (holds_last && last >= begin && last < begin + kRun) {
-        uint32_t bits = lds.current;
-        if (a.flags & HS_SELECT_SCALE_RAW) bits = scale_raw(bits);
+    if (holds_last) {
+        const uint32_t bits = lds.current;  // raw, scaled below with the rest
 #pragma unroll
-        for (uint32_t j = 0; j < kRun; ++j) {  // constant indices: packed stays in registers
-            constexpr uint32_t kLow = 0xffffu;
-            if (begin + j == last)
-                packed[j >> 1] = (packed[j >> 1] & ~(kLow << ((j & 1u) * 16u))) | (bits << ((j & 1u) * 16u));
+        for (uint32_t r = 0; r < kR; ++r) {
+            const uint32_t begin = (first + r) * kSlice + tid * kRun;
+#pragma unroll
+            for (uint32_t j = 0; j < kRun; ++j) {  // constant indices: packed stays in registers
+                constexpr uint32_t kLow = 0xffffu;
+                if (begin + j == last)
+                    packed[r][j >> 1] = (packed[r][j >> 1] & ~(kLow << ((j & 1u) * 16u))) |
+                                        (bits << ((j & 1u) * 16u));
+            }
         }
     }
     if (g == 0 && tid == 0) a.plan->head_max = best;
     const float thr = threshold_from_key(best, (a.flags & HS_SELECT_SCALE_RAW) != 0, a.alpha);
     // the history cover does not reject nonfinite scores (NaN counts as below)
     const bool cover = (a.flags & HS_SELECT_COVER) != 0;
-    uint32_t count = 0, bad = 0;
-    uint32_t keyw[kRun / 2] = {};
+    uint32_t* copy = whist + (tid & (kCountCopies - 1)) * kCountCopyStride;
+    uint32_t counts[kR], bad = 0;
 #pragma unroll
-    for (uint32_t j = 0; j < kRun; ++j) {
-        const uint32_t b = half_at(packed, j);
-        keyw[j >> 1] |= order_key(b) << ((j & 1u) * 16u);
-        if (begin + j < a.n) {
-            if (!cover && !finite_half(b)) {
-                bad = 1;
-            } else {
-                count += h2f(b) >= thr ? 1u : 0u;
-                hist_add(whist, order_key(b) >> 8);
+    for (uint32_t r = 0; r < kR; ++r) {
+        const uint32_t begin = (first + r) * kSlice + tid * kRun;
+        uint32_t keyw[kRun / 2] = {};
+        counts[r] = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < kRun; ++j) {
+            const uint32_t b = scale ? scale_raw(half_at(packed[r], j)) : half_at(packed[r], j);
+            keyw[j >> 1] |= order_key(b) << ((j & 1u) * 16u);
+            if (begin + j < a.n) {
+                if (!cover && !finite_half(b)) {
+                    bad |= 1u << r;
+                } else {
+                    counts[r] += h2f(b) >= thr ? 1u : 0u;
+                    atomicAdd(&copy[r * kCountHist + (order_key(b) >> 8)], 1u);
+                }
             }
         }
+        // the per-head path reads these order keys instead of rescaling
+        if (a.g_key16 && begin < a.key_stride)
+            *reinterpret_cast<uint4*>(a.g_key16 + static_cast<size_t>(h) * a.key_stride + begin) =
+                make_uint4(keyw[0], keyw[1], keyw[2], keyw[3]);
     }
-    // the per-head path reads these order keys instead of rescaling
-    if (a.g_key16 && begin < a.key_stride)
-        *reinterpret_cast<uint4*>(a.g_key16 + static_cast<size_t>(h) * a.key_stride + begin) =
-            make_uint4(keyw[0], keyw[1], keyw[2], keyw[3]);
-    // one reduction of both: the slice's count (<= kSlice) in the low 16
-    // bits, its threads' nonfinite flags summed above them
-    static_assert(kSlice < 65536 && kThreads < 65536, "count and flags share a word");
-    const uint32_t both = block_sum((bad << 16) | count, tmp);
-    if (tid < 256) a.g_hi[static_cast<size_t>(g) * 256 + tid] = hist_total(whist, tid);
-    if (tid == 0) {
-        a.g_count[g] = both & 0xffffu;
-        a.g_bad[g] = both >> 16 ? 1u : 0u;
+    // the slices' counts (<= kSlice each) two to a word, summed in one
+    // reduction; the nonfinite flags OR-ed into LDS before its barrier
+    uint32_t bad_wave = 0;
+#pragma unroll
+    for (uint32_t r = 0; r < kR; ++r) bad_wave |= __ballot((bad >> r) & 1u) ? 1u << r : 0u;
+    if ((tid & 63u) == 0 && bad_wave) atomicOr(&lds.bad, bad_wave);
+    uint32_t lo = counts[0], hi = 0;
+    if constexpr (kR >= 2) lo |= counts[1] << 16;
+    if constexpr (kR == 4) hi = counts[2] | (counts[3] << 16);
+    lo = wave_sum_u32(lo);
+    hi = wave_sum_u32(hi);
+    if ((tid & 63u) == 0) {
+        lds.sums[0][tid >> 6] = lo;
+        lds.sums[1][tid >> 6] = hi;
+    }
+    __syncthreads();
+    lo = hi = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < kWaves; ++w) {
+        lo += lds.sums[0][w];
+        hi += lds.sums[1][w];
+    }
+    const uint32_t slices_here = min(kR, a.S - first);
+    for (uint32_t i = tid; i < slices_here * 256; i += kThreads) {
+        const uint32_t r = i >> 8, bucket = i & 255u;
+        uint32_t c = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < kCountCopies; ++k) c += whist[r * kCountHist + k * kCountCopyStride + bucket];
+        a.g_hi[static_cast<size_t>(h * a.S + first + r) * 256 + bucket] = c;
+    }
+    if (tid < slices_here) {
+        const uint32_t word = tid < 2 ? lo : hi;
+        a.g_count[h * a.S + first + tid] = (word >> ((tid & 1u) * 16u)) & 0xffffu;
+        a.g_bad[h * a.S + first + tid] = (lds.bad >> tid) & 1u;
     }
     // the tie records the next launch accumulates into start from zero here
     if (g == 0) {
@@ -602,10 +700,10 @@ __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, ui
     }
 }
 
-template <bool kCurrent>
+template <bool kCurrent, uint32_t kR>
 __global__ void __launch_bounds__(kThreads) count_kernel(const SelectJobs js) {
     __shared__ CountLds lds;
-    count_group<kCurrent>(js, blockIdx.x, blockIdx.y, lds);
+    count_group<kCurrent, kR>(js, blockIdx.x, blockIdx.y, lds);
 }
 
 // k from every head's count and nonfinite flag (policy/gqa_policy.cpp:51-63),
@@ -1623,7 +1721,7 @@ __global__ void __launch_bounds__(kThreads) rank_kernel(SelectArgs a) {
 // heads x 4 channel groups) and the next layer's selection count (the
 // others: (head, slice) groups x jobs) in one launch; both are short and
 // latency-bound, and neither reads what the other writes.
-template <bool kCurrent>
+template <bool kCurrent, uint32_t kR>
 __global__ void __launch_bounds__(kThreads)
 combine_count_kernel(const float* __restrict__ part, uint32_t chunks, float* __restrict__ out,
                      const SelectJobs js, uint32_t groups) {
@@ -1638,7 +1736,7 @@ combine_count_kernel(const float* __restrict__ part, uint32_t chunks, float* __r
         return;
     }
     const uint32_t b = blockIdx.x - kMergers;
-    count_group<kCurrent>(js, b % groups, b / groups, lds.count);
+    count_group<kCurrent, kR>(js, b % groups, b / groups, lds.count);
 }
 
 }  // namespace
@@ -1693,20 +1791,44 @@ bool per_head_path(uint32_t n, float ratio, uint32_t flags) {
 
 // What the launches of a batch need to know about its jobs.
 struct BatchShape {
-    uint32_t max_partials = 0, max_groups = 0;
-    bool any_own_partial = false, all_per_head = true, any_current = false;
+    uint32_t heads = 0, max_partials = 0, max_groups = 0, max_slices = 0, slices = 0;
+    bool any_own_partial = false, all_per_head = true, any_current = false, all_aligned = true;
+    // slices per count group: kWideCount when a per-head batch of 16-byte
+    // aligned score rows has more (head, slice) pairs than one round of count
+    // groups holds (four workgroups on each of 256 CUs)
+    uint32_t count_width() const {
+        return all_per_head && all_aligned && slices > 1024 ? kWideCount : 1u;
+    }
+    uint32_t count_groups() const {
+        const uint32_t r = count_width();
+        return heads * ((max_slices + r - 1) / r);
+    }
 };
 BatchShape batch_shape(const SelectJobs& js) {
     BatchShape b;
+    b.heads = js.heads;
     for (uint32_t j = 0; j < js.count; ++j) {
         const SelectPlan p = plan_select(js.heads, js.job[j].n, kmax_of(js.job[j].n, js.ratio, js.flags));
         b.max_partials = std::max(b.max_partials, p.partials);
         b.max_groups = std::max(b.max_groups, p.groups);
+        b.max_slices = std::max(b.max_slices, p.S);
+        b.slices += p.groups;
         b.any_own_partial |= js.job[j].partial == nullptr;
         b.any_current |= js.job[j].cur_key != nullptr;
         b.all_per_head &= per_head_path(js.job[j].n, js.ratio, js.flags);
+        b.all_aligned &= (reinterpret_cast<uintptr_t>(js.job[j].scores) & 15u) == 0 &&
+                         js.job[j].stride % 8 == 0 && js.job[j].n >= 8;
     }
     return b;
+}
+
+template <uint32_t kR>
+void launch_count_kernel(const SelectJobs& js, const BatchShape& b, hipStream_t stream) {
+    const dim3 grid(b.count_groups(), js.count);
+    if (b.any_current)
+        hipLaunchKernelGGL((count_kernel<true, kR>), grid, dim3(kThreads), 0, stream, js);
+    else
+        hipLaunchKernelGGL((count_kernel<false, kR>), grid, dim3(kThreads), 0, stream, js);
 }
 
 // The head-0 maxima (jobs without the scorer's) and the count launch, unless
@@ -1716,12 +1838,10 @@ void launch_counts(const SelectJobs& js, const BatchShape& b, hipStream_t stream
     if (b.any_own_partial)
         hipLaunchKernelGGL(head0_max_kernel, dim3((b.max_partials + 3) / 4, js.count), dim3(256), 0,
                            stream, js);
-    if (b.any_current)
-        hipLaunchKernelGGL(count_kernel<true>, dim3(b.max_groups, js.count), dim3(kThreads), 0,
-                           stream, js);
+    if (b.count_width() == kWideCount)
+        launch_count_kernel<kWideCount>(js, b, stream);
     else
-        hipLaunchKernelGGL(count_kernel<false>, dim3(b.max_groups, js.count), dim3(kThreads), 0,
-                           stream, js);
+        launch_count_kernel<1>(js, b, stream);
 }
 
 // Launches for the checked jobs of `js`.  Batches whose jobs all take the
@@ -1955,13 +2075,22 @@ int launch_attention_then_count(const float* q, const uint8_t* k_pool, const uin
     if (b.any_own_partial)
         hipLaunchKernelGGL(head0_max_kernel, dim3((b.max_partials + 3) / 4, js.count), dim3(256), 0,
                            stream, js);
-    const dim3 grid(32 * 4 + b.max_groups * js.count);
-    if (b.any_current)
-        hipLaunchKernelGGL(combine_count_kernel<true>, grid, dim3(kThreads), 0, stream,
-                           static_cast<const float*>(workspace), chunks, out, js, b.max_groups);
+    const uint32_t groups = b.count_groups();
+    const dim3 grid(32 * 4 + groups * js.count);
+    const float* part = static_cast<const float*>(workspace);
+    const bool wide = b.count_width() == kWideCount;
+    if (b.any_current && wide)
+        hipLaunchKernelGGL((combine_count_kernel<true, kWideCount>), grid, dim3(kThreads), 0,
+                           stream, part, chunks, out, js, groups);
+    else if (b.any_current)
+        hipLaunchKernelGGL((combine_count_kernel<true, 1>), grid, dim3(kThreads), 0, stream, part,
+                           chunks, out, js, groups);
+    else if (wide)
+        hipLaunchKernelGGL((combine_count_kernel<false, kWideCount>), grid, dim3(kThreads), 0,
+                           stream, part, chunks, out, js, groups);
     else
-        hipLaunchKernelGGL(combine_count_kernel<false>, grid, dim3(kThreads), 0, stream,
-                           static_cast<const float*>(workspace), chunks, out, js, b.max_groups);
+        hipLaunchKernelGGL((combine_count_kernel<false, 1>), grid, dim3(kThreads), 0, stream, part,
+                           chunks, out, js, groups);
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "attention-then-count launch");
 }

@@ -270,3 +270,34 @@ def test_select_then_score_history_cover(hs):
     assert torch.equal(job["counts"], counts)
     assert torch.equal(job["member"], member)
     assert torch.equal(out_b.view(torch.int16), want_b.view(torch.int16))
+
+
+def test_counted_wide_batch_then_single_selections(hs):
+    # hs_gqa_attention_then_count over a batch of 16 next jobs (more (head,
+    # slice) pairs than one round of count groups: 4 slices per workgroup)
+    # feeds counted selections made one job at a time: the count records do
+    # not depend on how the count launch grouped the slices
+    ns = batch_ns(31)
+    assert sum(32 * -(-n // 4096) for n in ns) > 1024
+    nxt = make_jobs(hs, ns, 7900)
+    raws = [scored_layer(hs, j) for j in nxt]
+    wants = [expected_select(hs, select_job(hs, r, j["tokens"], j["head0_partial"]), False)
+             for r, j in zip(raws, nxt)]
+    n = 4096
+    L = kv_layers(hs, n, 1, 7950)[0]
+    member = torch.full((32, n // 32), -1, dtype=torch.int32, device="cuda")  # every id
+    want_out = hs.ops.sparse_attention(L["q32"], L["k"], n, member, v_pool=L["v"], row_bytes=2048)
+    jobs = [select_job(hs, r, j["tokens"], j["head0_partial"]) for r, j in zip(raws, nxt)]
+    out = torch.empty((32, 128), device="cuda")
+    aws = hs.ops.workspace(hs.ops.attention_workspace_bytes(n), "cuda")
+    hs.ops.prepare_attention_then_count(L["q32"], L["k"], n, member, jobs, 32, ALPHA, RATIO,
+                                        out=out, ws=aws, v_pool=L["v"], row_bytes=2048,
+                                        scale_raw=True)()
+    for j in jobs:
+        hs.ops.select(j["scores"], 32, j["n"], j["n"], ALPHA, RATIO, scale_raw=True, counted=True,
+                      head0_partial=j["head0_partial"], ids=j["ids"], counts=j["counts"],
+                      member=j["member"], status=j["status"], ws=j["ws"])
+    torch.cuda.synchronize()
+    assert torch.equal(out, want_out)
+    for j, w in zip(jobs, wants):
+        assert_select_equal(hs, j, w)
