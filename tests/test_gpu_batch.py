@@ -79,18 +79,23 @@ def test_batched_select_mixed_sizes_and_cover(hs):
 
 
 # Sizes of a batch with more (head, slice) pairs than one round of count
-# groups (> 1024): the count launch covers 4 slices per workgroup.  Ragged
+# groups (> 1024): with every score row 16-byte aligned (a stride that is a
+# multiple of 8) the count launch covers 4 slices per workgroup.  Ragged
 # sizes leave groups with 1..3 slices and slices with partial runs.
 WIDE_NS = [32768, 30001, 4097, 4096, 12289, 20000, 8229, 28672, 16384, 9999, 31000, 24576,
            17000, 6000, 32767, 25000]
 
 
+def _wide_stride(n):
+    return -(-n // 8) * 8
+
+
 def _single_select(hs, sj, id_order):
     words = (sj["n"] + 31) // 32
     m1 = torch.zeros((32, words), dtype=torch.int32, device="cuda")
-    ids1, counts1, _, status1 = hs.ops.select(sj["scores"], 32, sj["n"], sj["n"], 5.0, 0.2,
-                                              scale_raw=True, id_order=id_order, member=m1,
-                                              head0_partial=sj.get("head0_partial"))
+    ids1, counts1, _, status1 = hs.ops.select(sj["scores"], 32, sj["scores"].shape[-1], sj["n"],
+                                              5.0, 0.2, scale_raw=True, id_order=id_order,
+                                              member=m1, head0_partial=sj.get("head0_partial"))
     return ids1, counts1, m1, hs.ops.read_status(status1)
 
 
@@ -98,6 +103,8 @@ def _single_select(hs, sj, id_order):
 def test_wide_count_batch_matches_single_calls(hs, id_order):
     assert sum(32 * -(-n // 4096) for n in WIDE_NS) > 1024
     jobs = make_jobs(hs, WIDE_NS, 4000)
+    for j in jobs:
+        j["score_stride"] = _wide_stride(j["tokens"])
     outs = hs.ops.score_batched(jobs)
     # nonfinite scores in the third and fourth slice of a count group, and in
     # head 0 of another job: those jobs fail as the single calls do
@@ -138,15 +145,16 @@ def test_wide_count_batch_with_current_tokens(hs):
         hs.ops.score(j["q16"], j["keys"], n, out=full, head0_partial=part_full)
         wants.append((full, _single_select(hs, dict(scores=full, n=n, head0_partial=part_full),
                                            False)))
-        raw = torch.full((32, n), float("nan"), dtype=torch.float16, device="cuda")
+        stride = _wide_stride(n)
+        raw = torch.full((32, stride), float("nan"), dtype=torch.float16, device="cuda")
         part = torch.empty((n - 1 + 63) // 64, dtype=torch.int32, device="cuda")
-        hs.ops.score(j["q16"], j["keys"], n - 1, out=raw, score_stride=n, head0_partial=part)
+        hs.ops.score(j["q16"], j["keys"], n - 1, out=raw, score_stride=stride, head0_partial=part)
         sel_jobs.append(dict(scores=raw, n=n, head0_partial=part, current_q=j["q16"],
                              current_key=j["keys"][(n - 1) * 1024:]))
     res = hs.ops.select_batched(sel_jobs, 32, 5.0, 0.2, scale_raw=True)
     for sj, (ids, counts, _, status), (full, (ids1, counts1, _, st1)) in zip(sel_jobs, res, wants):
         st = hs.ops.read_status(status)
-        assert torch.equal(sj["scores"].view(torch.int16), full.view(torch.int16))
+        assert torch.equal(sj["scores"][:, :sj["n"]].view(torch.int16), full.view(torch.int16))
         assert st == st1 and st["code"] == 0
         k = st["k"]
         assert torch.equal(ids[:, :k], ids1[:, :k])
