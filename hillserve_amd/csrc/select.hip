@@ -17,7 +17,8 @@
 //
 // Work split: each head is cut into S <= 32 slices of 4096 consecutive ids;
 // every (head, slice) pair is one 512-thread workgroup whose threads own 8
-// consecutive ids each.  The phases that need a head-wide or device-wide view
+// consecutive ids each (the count launch of a large batch gives a workgroup
+// four slices of a head).  The phases that need a head-wide or device-wide view
 // are separate launches on the caller's stream: a kernel boundary is the
 // cheapest device-wide barrier on this part (one cache flush per launch,
 // where in-kernel barriers across the XCDs' separate L2 caches pay an L2
