@@ -15,6 +15,9 @@ token (column N - 1) from the query and the appended K row.  The same step
 one layer at a time (serial_ms_per_step) must select the same ids.
 
 Also on the same JSON line:
+  host_ms_per_step  the timed loop's host-observed time per step (first launch
+                to the end of the final synchronisation); ms_per_step is the
+                HIP events' device time of the same loop.
   roofline      the timed step's dominant call, hs_gqa_select_then_score
                 (count launch + selection beside the next layer's history
                 scoring; 29 of the step's 30 layers): algorithmic bytes per
@@ -145,15 +148,19 @@ class Gpu:
 
     def timed_us(self, fn, reps, per_call=1):
         """Mean microseconds per call: HIP events on the launch stream around
-        `reps` back-to-back runs of fn, each making `per_call` calls."""
+        `reps` back-to-back runs of fn, each making `per_call` calls.  The
+        host-observed time of the same loop (from the first launch to the
+        end of the final synchronisation) is kept in self.host_us."""
         torch = self.torch
         b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        t0 = time.perf_counter()
         b.record(self.stream)
         for _ in range(reps):
             fn()
         e.record(self.stream)
         torch.cuda.synchronize()
+        self.host_us = (time.perf_counter() - t0) * 1e6 / (reps * per_call)
         return 1e3 * b.elapsed_time(e) / (reps * per_call)
 
     def calibration_copy(self):
@@ -300,6 +307,7 @@ def step_leg(g, args):
         s.step()
     s.check_statuses()
     step_us = g.timed_us(s.step, args.steps)
+    step_host_us = g.host_us
     s.check_statuses()
     last_ids = s.ids.clone()
     s.serial_step()
@@ -332,12 +340,13 @@ def step_leg(g, args):
     s.check_statuses()
     step_bytes = LAYERS * (HIST_BYTES + SELECT_BYTES + CURRENT_BYTES)
     out = {
-        "step_us": step_us, "serial_us": serial_us, "pipe_us": pipe_us,
+        "step_us": step_us, "step_host_us": step_host_us, "serial_us": serial_us, "pipe_us": pipe_us,
         "step_bytes": step_bytes, "kernels": rows,
         "q_host": s.qs[0].cpu().view(torch.int16).numpy(),
         "k_host": s.keys[0].cpu().view(torch.int16).numpy(),
     }
-    log(f"configs[1]: {step_us / 1e3:.3f} ms/step pipelined ({serial_us / 1e3:.3f} one layer at a "
+    log(f"configs[1]: {step_us / 1e3:.3f} ms/step pipelined ({step_host_us / 1e3:.3f} host-observed; "
+        f"{serial_us / 1e3:.3f} one layer at a "
         f"time), {LAYERS * N / (step_us * 1e-6) / 1e9:.2f} G keys/s, "
         f"{step_bytes / (step_us * 1e-6) / 1e9:.0f} GB/s algorithmic")
     log_rows(rows)
@@ -1152,6 +1161,7 @@ def main():
             "schedule": "layer l's selection (completing its current token) beside layer l+1's "
                         "history scoring (hs_gqa_select_then_score)",
         },
+        "host_ms_per_step": s1["step_host_us"] / 1e3,
         "serial_ms_per_step": s1["serial_us"] / 1e3,
         "serial_keys_per_s": LAYERS * N / (s1["serial_us"] * 1e-6),
         "hbm_gbps": step_gbs,

@@ -317,3 +317,50 @@ def test_failed_selection_clears_member(hs, n):
                                         id_order=id_order)
         assert hs.ops.read_status(status)["code"] == hs.HS_ERR_NONFINITE
         assert not from_dev(member).any()
+
+
+def test_random_sweep_against_oracle(hs, port):
+    # seeded shapes and parameters across both launch paths: heads 1..128,
+    # n up to 40000 (the slice chain past 32768), strides with padding,
+    # quantized scores (ties) or Gaussian ones, FP32 counts on and off
+    g = rng(9091)
+    for case in range(12):
+        heads = int(g.choice([1, 3, 8, 32, 100, 128]))
+        n = int(g.integers(1, 40001)) if case % 3 else int(g.integers(1, 300))
+        if heads * n > 2_000_000:
+            n = 2_000_000 // heads
+        stride = n + int(g.integers(0, 40))
+        alpha = float(g.choice([0.0, 0.5, 2.0, 5.0, 8.0]))
+        ratio = float(np.float32(g.choice([0.05, 0.2, 0.5, 1.0])))
+        fp32 = bool(case % 2)
+        s = np.full((heads, stride), hb(-60000), dtype=np.uint16)
+        if case % 4 == 0:
+            vals = (g.integers(0, 64, size=(heads, n)) - 32) / 4.0  # heavy ties
+        else:
+            vals = g.standard_normal((heads, n)) * 3.0
+        s[:, :n] = f16_bits(vals)
+        check_against_port(hs, port, s, heads, stride, n, alpha, ratio, fp32)
+
+
+def test_random_batch_sweep_against_oracle(hs, port):
+    # a batch of 16 raw-score jobs with 16-byte aligned rows (four slices per
+    # count group) and one with a ragged stride, each against the oracle over
+    # its scaled scores
+    g = rng(9092)
+    for wide in (True, False):
+        jobs, raws = [], []
+        for i in range(16):
+            n = int(g.integers(8, 32769))
+            stride = -(-n // 8) * 8 if wide or i else n | 1
+            raw = np.full((32, stride), hb(0), dtype=np.uint16)
+            raw[:, :n] = f16_bits(g.standard_normal((32, n)) * 20.0)
+            raws.append((raw, n, stride))
+            jobs.append(dict(scores=to_dev(raw.reshape(-1)).view(32, stride), n=n))
+        res = hs.ops.select_batched(jobs, 32, 3.0, 0.2, scale_raw=True)
+        for (raw, n, stride), (ids, counts, _, status) in zip(raws, res):
+            st = hs.ops.read_status(status)
+            rc, k, pids, pcounts, tied = port.select(port.scale(raw), 32, stride, n, 3.0, 0.2)
+            assert st["code"] == rc == 0
+            assert st["k"] == k and st["boundary_tied_heads"] == tied
+            assert np.array_equal(from_dev(counts), pcounts)
+            assert np.array_equal(from_dev(ids)[:, :k], pids)
