@@ -31,6 +31,7 @@
 // on the host link.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 
 #include "hs_device.hpp"
@@ -45,6 +46,11 @@ constexpr uint32_t kRow = 4096, kHeader = 32, kStride = kRow + kHeader;
 constexpr uint32_t kMaxLayers = 128, kMaxPositions = 66048;  // segmented_store.cpp:31
 constexpr uint32_t kPad = 0xffffffffu;  // a position list's padding entry: no record
 constexpr uint32_t kPadFlag = 4u;
+// Workgroups (4 waves each) of a copy over the host link: 96 records of
+// 4 KiB in flight keep it at ~52 GB/s (16 workgroups: 50.5 GB/s, 8: 31)
+// while the CUs left free run the main stream's attention within 2x of its
+// speed alone (one wave per record over the whole chip: 7x).
+constexpr uint32_t kLinkBlocks = 24;
 
 uint64_t extent_of(uint32_t layers, uint32_t capacity) {
     return (4096ull + uint64_t(layers) * capacity * kStride + 4095) / 4096 * 4096;
@@ -64,19 +70,14 @@ struct RecordHeader {
 };
 static_assert(sizeof(RecordHeader) == kHeader, "32-byte record header");
 
-// One wave per record: payload 4096 B = 64 lanes x 4 x 16 B, header by 2 lanes.
-// kStaged: record i is the i-th of `image` laid back to back (the raw
-// staging buffer of hs_kv_cold_fetch_runs), expected at position
-// positions[i]; otherwise record (layer, positions[i]) of the image.
+// Record i (position positions[i]) into its staging row: copy, header identity.
 template <bool kStaged>
-__global__ void __launch_bounds__(256)
-cold_copy_kernel(const uint8_t* __restrict__ image, uint32_t layer, uint32_t capacity,
-                 uint64_t request, const uint32_t* __restrict__ positions, uint32_t count,
-                 uint8_t* k_out, uint32_t row_bytes, int64_t v_delta,
-                 uint64_t* __restrict__ digests, uint32_t* __restrict__ flags) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t i = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (i >= count) return;
+__device__ __forceinline__ void copy_record(const uint8_t* __restrict__ image, uint32_t layer,
+                                            uint32_t capacity, uint64_t request,
+                                            const uint32_t* __restrict__ positions, uint32_t i,
+                                            uint8_t* k_out, uint32_t row_bytes, int64_t v_delta,
+                                            uint64_t* __restrict__ digests,
+                                            uint32_t* __restrict__ flags, uint32_t lane) {
     const uint32_t p = positions[i];
     if (p == kPad || p >= capacity) {  // padding entry, or nothing to read
         if (lane == 0) {
@@ -106,6 +107,26 @@ cold_copy_kernel(const uint8_t* __restrict__ image, uint32_t layer, uint32_t cap
         flags[i] = ok ? 0u : 1u;
         digests[i] = a;
     }
+}
+
+// One wave per record at a time: payload 4096 B = 64 lanes x 4 x 16 B,
+// header by 2 lanes.  The waves stride over the records, so a launch over the
+// host link can hold a few CUs only: the link, not the CUs, bounds the copy,
+// and the CUs left free run the main stream's work beside it.
+// kStaged: record i is the i-th of `image` laid back to back (the raw
+// staging buffer of hs_kv_cold_fetch_runs), expected at position
+// positions[i]; otherwise record (layer, positions[i]) of the image.
+template <bool kStaged>
+__global__ void __launch_bounds__(256)
+cold_copy_kernel(const uint8_t* __restrict__ image, uint32_t layer, uint32_t capacity,
+                 uint64_t request, const uint32_t* __restrict__ positions, uint32_t count,
+                 uint8_t* k_out, uint32_t row_bytes, int64_t v_delta,
+                 uint64_t* __restrict__ digests, uint32_t* __restrict__ flags) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t waves = gridDim.x * 4;
+    for (uint32_t i = blockIdx.x * 4 + (threadIdx.x >> 6); i < count; i += waves)
+        copy_record<kStaged>(image, layer, capacity, request, positions, i, k_out, row_bytes,
+                             v_delta, digests, flags, lane);
 }
 
 // One lane per record: FNV-1a 64 over the staged row (K half, then V half),
@@ -247,7 +268,10 @@ int launch_cold_checks(const uint8_t* records, uint32_t layer, const uint64_t (&
     uint64_t* digests = static_cast<uint64_t*>(workspace);
     uint32_t* flags = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) +
                                                   align256(sizeof(uint64_t) * count));
-    hipLaunchKernelGGL(cold_copy_kernel<kStaged>, dim3((count + 3) / 4), dim3(256), 0, stream,
+    // over the host link a few workgroups keep the link busy (the copy is its
+    // rate, not theirs); staged records in HBM take the whole chip
+    const uint32_t blocks = kStaged ? (count + 3) / 4 : std::min((count + 3) / 4, kLinkBlocks);
+    hipLaunchKernelGGL(cold_copy_kernel<kStaged>, dim3(blocks), dim3(256), 0, stream,
                        records, layer, static_cast<uint32_t>(h[4]), h[2], positions, count, k_out,
                        static_cast<uint32_t>(row_bytes), v_delta, digests, flags);
     hipLaunchKernelGGL(cold_digest_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, k_out,
