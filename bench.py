@@ -559,7 +559,7 @@ def layer_leg(g, args):
     specs = [
         ("score_logits", "hs_gqa_score_logits: score_logits_kernel (scores + F32 q.k dots "
                          "on MFMA)", SCORE_BYTES + 16384 + DOTS_BYTES, "algorithmic + dots written"),
-        ("attention", "hs_gqa_sparse_attention: attn_partial_kernel (K and V rows) + "
+        ("attention", "hs_gqa_sparse_attention: attn_kv_kernel (K and V rows) + "
                       "attn_combine_kernel", ubytes + 8192 + 16384, "algorithmic"),
         ("attention_logits", "hs_gqa_sparse_attention_logits: attn_v_kernel (V rows + the "
                              "selected dots) + attn_combine_kernel",

@@ -19,12 +19,14 @@
 //    and V row exactly once for all of its query heads -> HBM bytes =
 //    sum_g |U_g|*512.  The 8 waves read the 8 heads' segments of the same
 //    pool rows at about the same time.
-//  * one pass over tiles of 16 union rows: a row's K and V segments are
-//    requested together (which streamed ~1.4x faster than a K pass followed
-//    by a V pass), the next tile before the current one is used.  Scores
-//    come from MFMA (q split into F16 hi and lo parts, FP32 products and
-//    sums), softmax is online per tile with a wave-uniform running maximum,
-//    and p*V accumulates in FP32 registers.
+//  * every K segment of the wave's union is requested at once; each tile of
+//    16 rows is scored on MFMA as it lands (q split into F16 hi and lo
+//    parts, FP32 products and sums) and its V segments are then requested
+//    into the registers its K held, so a wave waits for two waves of loads
+//    instead of one per tile.  The softmax takes the chunk's exact maximum
+//    per head (no running maximum), and p*V accumulates in FP32 registers.
+//    attn_v_kernel is the same with the scoring pass's dots in place of the
+//    K rows.
 //  * the (m, l, o[128]) partials of all chunks are merged by attn_combine.
 #include <hip/hip_runtime.h>
 
@@ -43,34 +45,6 @@ constexpr uint32_t kThreads = 512; // 8 waves: one per KV head
 constexpr uint32_t kRecord = kAttnRecord;
 constexpr float kScale = 0.088388347648318440550f;  // 1/sqrt(128)
 
-// Sum over the 16 lanes of a DPP row (one 16-lane group), returned to every
-// lane with the same bits: quad xor 1, quad xor 2, then the row mirror
-// (quad a <-> 3-a) and the half-row mirror (quad a <-> a^1).  Each step adds
-// two equal-order partial sums, so the result does not depend on the lane.
-template <int kCtrl>
-__device__ __forceinline__ float dpp_f32(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float row_sum16(float v) {
-    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
-    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
-    v += dpp_f32<0x140>(v);  // row_mirror
-    v += dpp_f32<0x141>(v);  // row_half_mirror
-    return v;
-}
-
-template <int kCtrl>
-__device__ __forceinline__ float dpp_max(float v) {
-    return fmaxf(v, dpp_f32<kCtrl>(v));
-}
-// Maximum over the 16 lanes of a DPP row, the same bits in every lane.
-__device__ __forceinline__ float row_max16(float v) {
-    v = dpp_max<0xB1>(v);
-    v = dpp_max<0x4E>(v);
-    v = dpp_max<0x140>(v);
-    v = dpp_max<0x141>(v);
-    return v;
-}
 __device__ __forceinline__ float first_lane(float v) {
     return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
@@ -78,46 +52,34 @@ __device__ __forceinline__ float first_lane(float v) {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// One pass over the selected rows.  A workgroup owns kChunk consecutive ids
-// and all 8 KV heads, one wave per KV head, so the 8 heads' segments of the
-// same pool rows are requested close together in time.  A wave walks its
-// union in tiles of 16 rows, the next tile's K and V requested before the
-// current tile is used:
-//  * scores on MFMA: S = Q . K^T with v_mfma_f32_16x16x32_f16, A = the 4
-//    query rows of the wave (rows 4..15 zero), B = K^T of the tile (lane l
-//    supplies channels 32s + 8(l/16) .. +7 of row l%16 at step s: 16
-//    contiguous bytes).  q is split into F16 hi = f16(q) and lo =
-//    f16(q - hi), two products per step, so the scores carry ~22 bits of q;
-//    products and sums are FP32.  Lanes 0..15 then hold S[0..3][row l];
-//  * softmax per tile: the tile's maximum per head (DPP over those 16
-//    lanes) updates the wave-uniform running maximum; o and the lanes'
-//    partial sums are rescaled only when it rises; p = exp(s - m) goes to
-//    LDS (16 B per row);
-//  * p * V on VALU: lane (row group l/16, channel group l%16) adds 4 rows of
-//    the tile for its 8 channels and 4 heads.
-// At the end the 4 row groups' o are added (they share m) and the wave
-// writes the chunk's record.
+// ---- K and V rows in two waves of loads -------------------------------------
+// One workgroup per kChunk ids, one wave per KV head g; the union's loads
+// go out in two waves:
+//  1. the union is compacted in id order into LDS (pool row and head mask);
+//  2. every K segment of the union is requested at once: tile t = union rows
+//     16t .. 16t+15 in the MFMA B layout (lane l: channels 32s + 8(l/16) ..
+//     +7 of row 16t + l%16, 16 B per step s);
+//  3. per tile: S = Q.K^T on MFMA (q split into F16 hi and lo, as above), the
+//     scaled, masked scores into LDS, then the tile's V segments requested
+//     into the registers its K held (lane (row group l/16, channel group
+//     l%16): 16 B of rows 16t + 4i + l/16);
+//  4. the chunk's exact maximum per head, p = exp(s - m) and l = sum p (no
+//     running maximum), then o += p * V as the rows land, and the record.
 template <bool kRows>
 __global__ void __launch_bounds__(kThreads)
-attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ pool,
-                    uint32_t row_bytes, int64_t v_delta, const int32_t* __restrict__ rows,
-                    uint32_t pool_rows,
-                    const uint32_t* __restrict__ member, uint32_t n, uint32_t chunks,
-                    float* __restrict__ part) {
-    __shared__ uint32_t sel_row[8][kChunk];
+attn_kv_kernel(const float* __restrict__ q, const uint8_t* __restrict__ pool, uint32_t row_bytes,
+               int64_t v_delta, const int32_t* __restrict__ rows, uint32_t pool_rows,
+               const uint32_t* __restrict__ member, uint32_t n, uint32_t chunks,
+               float* __restrict__ part) {
+    // union row e's pool row at sel_row[g][e % 4][e / 4] (the V row groups
+    // read 4 consecutive entries of one plane), its head mask at sel_mask[g][e]
+    __shared__ uint4 sel_row[8][4][kChunk / 16];
     __shared__ uint8_t sel_mask[8][kChunk];
-    __shared__ float4 ptile[8][16];
-
-    const uint32_t chunk = blockIdx.x;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    __shared__ float4 sel_p[8][kChunk];  // scaled scores of the union rows, then their p
+    const uint32_t chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63u;
     const uint32_t g = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave = KV head
-    const uint32_t words = (n + 31) / 32;
-    const uint32_t base = chunk * kChunk;
-
+    const uint32_t words = (n + 31) / 32, base = chunk * kChunk;
     const uint32_t r16 = lane & 15u, q16 = lane >> 4;
-    // ---- union of the 4 query heads' selections, compacted in id order ----
-    // (every membership word is requested before any is used: straight-line
-    // loads, the index clamped to the last id)
     constexpr uint32_t kSteps = kChunk / 64;
     uint32_t mw[kSteps][4];
 #pragma unroll
@@ -142,7 +104,7 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
         const uint64_t any = __ballot(mk != 0);
         if (mk) {
             const uint32_t at = total + lanes_below(any);
-            sel_row[g][at] = r;
+            reinterpret_cast<uint32_t*>(&sel_row[g][at & 3u][0])[at >> 2] = r;
             sel_mask[g][at] = static_cast<uint8_t>(mk);
         }
         total += static_cast<uint32_t>(__popcll(any));
@@ -163,99 +125,16 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
         }
         return;
     }
-
-    half8 ahi[4], alo[4];  // the MFMA A operands (filled below)
+    auto row_at = [&](uint32_t e) {  // pool row of union row e (e < total)
+        return reinterpret_cast<const uint32_t*>(&sel_row[g][e & 3u][0])[e >> 2];
+    };
     const uint32_t head_off = g * 256;  // the wave's KV head within a row
-    // tile t: K rows 16t + l%16 (MFMA B layout) and V rows 16t + l/16 + 4i
-    // (16 B per lane at channel group l%16); rows past the union re-read its
-    // last row and are masked out
-    auto load_tile = [&](uint32_t t, uint4 (&kw)[4], uint4 (&vw)[4]) {
-        const uint32_t ek = min(16 * t + r16, total - 1);
-        const uint8_t* krow = pool + static_cast<size_t>(sel_row[g][ek]) * row_bytes + head_off +
-                              16 * q16;
-#pragma unroll
-        for (uint32_t s = 0; s < 4; ++s) kw[s] = *reinterpret_cast<const uint4*>(krow + 64 * s);
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-            const uint32_t ev = min(16 * t + q16 + 4 * i, total - 1);
-            const uint8_t* vrow = pool + static_cast<size_t>(sel_row[g][ev]) * row_bytes;
-            vw[i] = *reinterpret_cast<const uint4*>(vrow + v_delta + head_off + 16 * r16);
-        }
-    };
-    float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // wave-uniform
-    float lsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // lanes 0..15: their rows' p sums
-    float o[4][8];
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j)
-#pragma unroll
-        for (uint32_t c = 0; c < 8; ++c) o[j][c] = 0.0f;
-
-    auto use_tile = [&](uint32_t t, const uint4 (&kw)[4], const uint4 (&vw)[4]) {
-        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (uint32_t s = 0; s < 4; ++s) {
-            const half8 kb = __builtin_bit_cast(half8, kw[s]);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[s], kb, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[s], kb, acc, 0, 0, 0);
-        }
-        // lanes 0..15: row 16t + l of the union, heads 0..3
-        const uint32_t e = 16 * t + r16;
-        const uint32_t mk_at = sel_mask[g][min(e, total - 1)];
-        const uint32_t mk = (q16 == 0 && e < total) ? mk_at : 0u;
-        float sc[4];
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) sc[j] = ((mk >> j) & 1u) ? acc[j] * kScale : -INFINITY;
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-            const float mn = fmaxf(m[j], first_lane(row_max16(sc[j])));
-            if (mn > m[j]) {  // wave-uniform
-                // scale 0 while head j had no selected row (m = -inf)
-                const float scale = m[j] == -INFINITY ? 0.0f : __expf(m[j] - mn);
-                lsum[j] *= scale;
-#pragma unroll
-                for (uint32_t c = 0; c < 8; ++c) o[j][c] *= scale;
-                m[j] = mn;
-            }
-        }
-        float p[4];
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-            p[j] = sc[j] == -INFINITY ? 0.0f : __expf(sc[j] - m[j]);
-            lsum[j] += p[j];
-        }
-        if (q16 == 0) ptile[g][r16] = make_float4(p[0], p[1], p[2], p[3]);
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-            const float4 pp = ptile[g][q16 + 4 * i];
-            const uint32_t vwords[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
-#pragma unroll
-            for (uint32_t c2 = 0; c2 < 4; ++c2) {
-                const float v0 = h2f(vwords[c2] & 0xffffu), v1 = h2f(vwords[c2] >> 16);
-                o[0][2 * c2] = __builtin_fmaf(pp.x, v0, o[0][2 * c2]);
-                o[1][2 * c2] = __builtin_fmaf(pp.y, v0, o[1][2 * c2]);
-                o[2][2 * c2] = __builtin_fmaf(pp.z, v0, o[2][2 * c2]);
-                o[3][2 * c2] = __builtin_fmaf(pp.w, v0, o[3][2 * c2]);
-                o[0][2 * c2 + 1] = __builtin_fmaf(pp.x, v1, o[0][2 * c2 + 1]);
-                o[1][2 * c2 + 1] = __builtin_fmaf(pp.y, v1, o[1][2 * c2 + 1]);
-                o[2][2 * c2 + 1] = __builtin_fmaf(pp.z, v1, o[2][2 * c2 + 1]);
-                o[3][2 * c2 + 1] = __builtin_fmaf(pp.w, v1, o[3][2 * c2 + 1]);
-            }
-        }
-        __builtin_amdgcn_wave_barrier();  // the tile's p are read before the next tile writes
-    };
-    // Pairs of tiles (the loop bound is wave-uniform; an odd tile count ends
-    // with one fully masked tile).  Each tile is requested, unconditionally,
-    // before the previous one is used, and no exit test sits between a
-    // tile's loads and its use, so the waits before each use leave the next
-    // tile in flight.
-    uint4 ka[4], va[4], kb[4], vb[4];
-    const uint32_t tiles = (total + 15) / 16;
-    const uint32_t pairs = (tiles + 1) / 2;
-    load_tile(0, ka, va);
-    __builtin_amdgcn_sched_barrier(0);
+    constexpr uint32_t kTiles = kChunk / 16;
+    const uint32_t tiles = (total + 15) / 16;  // wave-uniform
     // A operands: this wave's query rows, hi and lo parts (lanes with
-    // l%16 >= 4 hold the zero rows), read while the first tile is in flight
+    // l%16 >= 4 hold the zero rows); the query is requested before the K
+    // rows, so the first tile's MFMAs wait for that tile alone
+    half8 ahi[4], alo[4];
 #pragma unroll
     for (uint32_t s = 0; s < 4; ++s) {
 #pragma unroll
@@ -267,24 +146,120 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
             alo[s][e] = static_cast<_Float16>(x - static_cast<float>(hi));
         }
     }
-    for (uint32_t pi = 0; pi < pairs; ++pi) {
-        load_tile(2 * pi + 1, kb, vb);
-        __builtin_amdgcn_sched_barrier(0);
-        use_tile(2 * pi, ka, va);
-        load_tile(2 * pi + 2, ka, va);
-        __builtin_amdgcn_sched_barrier(0);
-        use_tile(2 * pi + 1, kb, vb);
+    // ---- every K segment of the union in flight ----
+    // (unconditional loads, past the union the last row again: no branch
+    // between them, so each tile's MFMAs wait for that tile's loads only)
+    uint4 kw[kTiles][4];
+#pragma unroll
+    for (uint32_t t = 0; t < kTiles; ++t) {
+        const uint8_t* krow = pool + static_cast<size_t>(row_at(min(16 * t + r16, total - 1))) *
+                                         row_bytes + head_off + 16 * q16;
+#pragma unroll
+        for (uint32_t s = 0; s < 4; ++s) kw[t][s] = *reinterpret_cast<const uint4*>(krow + 64 * s);
     }
-
-    // ---- the 4 row groups share m: add their o; l from the row lanes ------
+    // ---- per tile: scores on MFMA, then the tile's V rows requested ----
+    uint4 vw[kTiles][4];
+    const uint8_t* vbase = pool + v_delta + head_off + 16 * r16;
+    const uint32_t last_row = row_at(total - 1);
+#pragma unroll
+    for (uint32_t t = 0; t < kTiles; ++t) {
+        if (t < tiles) {
+            floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t s = 0; s < 4; ++s) {
+                const half8 kb = __builtin_bit_cast(half8, kw[t][s]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[s], kb, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[s], kb, acc, 0, 0, 0);
+            }
+            // lanes 0..15: row 16t + l of the union, heads 0..3
+            const uint32_t e = 16 * t + r16;
+            if (q16 == 0 && e < total) {
+                const uint32_t mk = sel_mask[g][e];
+                float sc[4];
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j) sc[j] = ((mk >> j) & 1u) ? acc[j] * kScale : -INFINITY;
+                sel_p[g][e] = make_float4(sc[0], sc[1], sc[2], sc[3]);
+            }
+            // rows 16t + 4i + q16, i < 4: entries 4t .. 4t+3 of plane q16, one
+            // LDS read; a row past the union reads the union's last row again
+            const uint4 r4 = sel_row[g][q16][t];
+            const uint32_t rr[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) {
+                const uint32_t r = 16 * t + 4 * i + q16 < total ? rr[i] : last_row;
+                vw[t][i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(r) * row_bytes);
+            }
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // ---- the chunk's exact maximum per head, then p and l ----
+    float m[4], lsum[4];
+    {
+        float4 a[kSteps];
+        float top[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+        for (uint32_t c = 0; c < kSteps; ++c) {
+            const uint32_t e = 64 * c + lane;
+            a[c] = e < total ? sel_p[g][e] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            top[0] = fmaxf(top[0], a[c].x);
+            top[1] = fmaxf(top[1], a[c].y);
+            top[2] = fmaxf(top[2], a[c].z);
+            top[3] = fmaxf(top[3], a[c].w);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) m[j] = first_lane(wave_max_f32(top[j]));
+        float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t c = 0; c < kSteps; ++c) {
+            const float sv[4] = {a[c].x, a[c].y, a[c].z, a[c].w};
+            float p[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                p[j] = sv[j] == -INFINITY ? 0.0f : __expf(sv[j] - m[j]);
+                ps[j] += p[j];
+            }
+            if (64 * c + lane < total) sel_p[g][64 * c + lane] = make_float4(p[0], p[1], p[2], p[3]);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) lsum[j] = first_lane(wave_sum_f32(ps[j]));
+    }
+    __builtin_amdgcn_wave_barrier();
+    // ---- o += p * V: lane (row group q16, channel group r16) ----
+    float o[4][8];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j)
+#pragma unroll
+        for (uint32_t c = 0; c < 8; ++c) o[j][c] = 0.0f;
+#pragma unroll
+    for (uint32_t t = 0; t < kTiles; ++t) {
+        if (t < tiles) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) {
+                const uint32_t e = 16 * t + 4 * i + q16;
+                const float4 pp = sel_p[g][min(e, total - 1)];
+                const bool live = e < total;
+                const float p0 = live ? pp.x : 0.0f, p1 = live ? pp.y : 0.0f;
+                const float p2 = live ? pp.z : 0.0f, p3 = live ? pp.w : 0.0f;
+                const uint32_t vwords[4] = {vw[t][i].x, vw[t][i].y, vw[t][i].z, vw[t][i].w};
+#pragma unroll
+                for (uint32_t c2 = 0; c2 < 4; ++c2) {
+                    const float v0 = h2f(vwords[c2] & 0xffffu), v1 = h2f(vwords[c2] >> 16);
+                    o[0][2 * c2] = __builtin_fmaf(p0, v0, o[0][2 * c2]);
+                    o[1][2 * c2] = __builtin_fmaf(p1, v0, o[1][2 * c2]);
+                    o[2][2 * c2] = __builtin_fmaf(p2, v0, o[2][2 * c2]);
+                    o[3][2 * c2] = __builtin_fmaf(p3, v0, o[3][2 * c2]);
+                    o[0][2 * c2 + 1] = __builtin_fmaf(p0, v1, o[0][2 * c2 + 1]);
+                    o[1][2 * c2 + 1] = __builtin_fmaf(p1, v1, o[1][2 * c2 + 1]);
+                    o[2][2 * c2 + 1] = __builtin_fmaf(p2, v1, o[2][2 * c2 + 1]);
+                    o[3][2 * c2 + 1] = __builtin_fmaf(p3, v1, o[3][2 * c2 + 1]);
+                }
+            }
+        }
+    }
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j)
 #pragma unroll
         for (uint32_t c = 0; c < 8; ++c) o[j][c] = rows_sum_f32(o[j][c]);
-    float l[4];
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) l[j] = first_lane(row_sum16(lsum[j]));
-    // ---- this chunk's (m, l, o[128]) record per query head of KV head g -------
     if (lane < 16) {
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
@@ -292,7 +267,7 @@ attn_partial_kernel(const float* __restrict__ q, const uint8_t* __restrict__ poo
             for (uint32_t c = 0; c < 8; ++c) rec[j * kRecord + 2 + r16 * 8 + c] = o[j][c];
             if (lane == 0) {
                 rec[j * kRecord + 0] = m[j];
-                rec[j * kRecord + 1] = l[j];
+                rec[j * kRecord + 1] = lsum[j];
             }
         }
     }
@@ -509,11 +484,11 @@ int launch_attention_partial(const float* q, const uint8_t* k_pool, const uint8_
     const uint32_t chunks = (n + kChunk - 1) / kChunk;
     float* part = static_cast<float*>(workspace);
     if (rows)
-        hipLaunchKernelGGL(attn_partial_kernel<true>, dim3(chunks), dim3(kThreads), 0, stream, q,
+        hipLaunchKernelGGL(attn_kv_kernel<true>, dim3(chunks), dim3(kThreads), 0, stream, q,
                            k_pool, static_cast<uint32_t>(row_bytes), v_delta, rows, pool_rows,
                            member, n, chunks, part);
     else
-        hipLaunchKernelGGL(attn_partial_kernel<false>, dim3(chunks), dim3(kThreads), 0, stream,
+        hipLaunchKernelGGL(attn_kv_kernel<false>, dim3(chunks), dim3(kThreads), 0, stream,
                            q, k_pool, static_cast<uint32_t>(row_bytes), v_delta, rows, 0u, member,
                            n, chunks, part);
     const hipError_t st = hipGetLastError();
