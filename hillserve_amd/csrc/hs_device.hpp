@@ -23,10 +23,11 @@ __device__ __forceinline__ uint32_t f2h(float f) {
 
 // Monotone key of a finite F16 (policy/half_order.hpp:7-10): larger value
 // -> larger key, -0 and +0 share the key of +0.
+// Negative values (bits above 0x8000) flip every bit; the rest, -0 included,
+// keep their magnitude under the top bit: a compare and a select, no branch.
 __device__ __forceinline__ uint32_t order_key(uint32_t bits) {
     bits &= 0xffffu;
-    if ((bits & 0x7fffu) == 0) bits = 0;
-    return (bits & 0x8000u) ? (~bits & 0xffffu) : (bits ^ 0x8000u);
+    return bits > 0x8000u ? (bits ^ 0xffffu) : ((bits & 0x7fffu) | 0x8000u);
 }
 // Inverse of order_key (returns +0 for the zero key).
 __device__ __forceinline__ uint32_t key_bits(uint32_t key) {
@@ -49,6 +50,15 @@ __device__ __forceinline__ uint32_t scale_raw(uint32_t raw) {
     const float q0 = x * kRecip;
     const float e = __builtin_fmaf(-q0, kRoot, x);
     return f2h(__builtin_fmaf(e, kRecip, q0)) | sign;
+}
+// scale_raw of a finite input (no inf / NaN case, so no branch).
+__device__ __forceinline__ uint32_t scale_finite(uint32_t raw) {
+    constexpr float kRoot = 0x1.6a09e6p+3f;
+    constexpr float kRecip = 0x1.6a09e6p-4f;
+    const float x = h2f(raw & 0x7fffu);
+    const float q0 = x * kRecip;
+    const float e = __builtin_fmaf(-q0, kRoot, x);
+    return f2h(__builtin_fmaf(e, kRecip, q0)) | (raw & 0x8000u);
 }
 
 __device__ __forceinline__ bool is_nan_half(uint32_t bits) {

@@ -242,6 +242,16 @@ __device__ __forceinline__ float threshold_from_key(uint32_t key, bool scale, fl
     return h2f(f2h(m - alpha));
 }
 
+// The same threshold as an order key: for every finite F16 b, h2f(b) >= thr
+// exactly when order_key(b) >= this key (0x10000, above every key, when thr
+// is NaN).
+__device__ __forceinline__ uint32_t threshold_key_from_key(uint32_t key, bool scale, float alpha) {
+    uint32_t bits = key_bits(key);
+    if (scale) bits = scale_raw(bits);
+    const uint32_t t = f2h(h2f(bits) - alpha);
+    return is_nan_half(t) ? 0x10000u : order_key(t);
+}
+
 // Block-wide reductions / scan through LDS (tmp: one word per wave).
 template <uint32_t kT = kThreads>
 __device__ uint32_t block_max(uint32_t v, uint32_t* tmp) {
@@ -541,6 +551,24 @@ __device__ __forceinline__ void partial_loads(const SelectArgs& a, uint32_t (&v)
 }
 
 // ---- 1. count ---------------------------------------------------------------
+// One run of kRun finite scores, every id below n: order keys into keyw, each
+// key into the slice histogram, and the number of keys >= kthr (the
+// threshold as a key), with no branch.
+template <bool kScale>
+__device__ __forceinline__ uint32_t count_clean_run(const uint32_t (&packed)[kRun / 2], uint32_t kthr,
+                                                    uint32_t* slice_hist, uint32_t (&keyw)[kRun / 2]) {
+    uint32_t count = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kRun; ++j) {
+        const uint32_t raw = half_at(packed, j);
+        const uint32_t key = order_key(kScale ? scale_finite(raw) : raw);
+        keyw[j >> 1] |= key << ((j & 1u) * 16u);
+        count += key >= kthr ? 1u : 0u;
+        atomicAdd(&slice_hist[key >> 8], 1u);
+    }
+    return count;
+}
+
 // A count group covers kR consecutive slices of one head; it publishes each
 // slice's count, nonfinite flag and high-byte histogram, the same records
 // whatever kR is.  kR = kWideCount serves large batches: one round of fewer,
@@ -631,7 +659,8 @@ __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, ui
         }
     }
     if (g == 0 && tid == 0) a.plan->head_max = best;
-    const float thr = threshold_from_key(best, (a.flags & HS_SELECT_SCALE_RAW) != 0, a.alpha);
+    const float thr = threshold_from_key(best, scale, a.alpha);
+    const uint32_t kthr = threshold_key_from_key(best, scale, a.alpha);
     // the history cover does not reject nonfinite scores (NaN counts as below)
     const bool cover = (a.flags & HS_SELECT_COVER) != 0;
     uint32_t* copy = whist + (tid & (kCountCopies - 1)) * kCountCopyStride;
@@ -641,16 +670,30 @@ __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, ui
         const uint32_t begin = (first + r) * kSlice + tid * kRun;
         uint32_t keyw[kRun / 2] = {};
         counts[r] = 0;
+        // a run of ids below n with no inf or NaN (scaling keeps finiteness)
+        // takes the branch-free loop: the key compared with the threshold's
+        // key, every score into the histogram.  Bit 15 of a half of
+        // (w & 0x7c007c00) + 0x04000400 is set exactly when its exponent is
+        // all ones.
+        uint32_t special = 0;
 #pragma unroll
-        for (uint32_t j = 0; j < kRun; ++j) {
-            const uint32_t b = scale ? scale_raw(half_at(packed[r], j)) : half_at(packed[r], j);
-            keyw[j >> 1] |= order_key(b) << ((j & 1u) * 16u);
-            if (begin + j < a.n) {
-                if (!cover && !finite_half(b)) {
-                    bad |= 1u << r;
-                } else {
-                    counts[r] += h2f(b) >= thr ? 1u : 0u;
-                    atomicAdd(&copy[r * kCountHist + (order_key(b) >> 8)], 1u);
+        for (uint32_t w = 0; w < kRun / 2; ++w) special |= (packed[r][w] & 0x7c007c00u) + 0x04000400u;
+        if ((special & 0x80008000u) == 0 && begin + kRun <= a.n) {
+            uint32_t* slice_hist = copy + r * kCountHist;
+            counts[r] = scale ? count_clean_run<true>(packed[r], kthr, slice_hist, keyw)
+                              : count_clean_run<false>(packed[r], kthr, slice_hist, keyw);
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < kRun; ++j) {
+                const uint32_t b = scale ? scale_raw(half_at(packed[r], j)) : half_at(packed[r], j);
+                keyw[j >> 1] |= order_key(b) << ((j & 1u) * 16u);
+                if (begin + j < a.n) {
+                    if (!cover && !finite_half(b)) {
+                        bad |= 1u << r;
+                    } else {
+                        counts[r] += h2f(b) >= thr ? 1u : 0u;
+                        atomicAdd(&copy[r * kCountHist + (order_key(b) >> 8)], 1u);
+                    }
                 }
             }
         }
