@@ -13,6 +13,9 @@
 namespace hs {
 
 constexpr uint32_t kTileTokens = 64;
+// s_waitcnt immediate (gfx9 encoding) that waits for lgkmcnt = 0 only:
+// vmcnt 63 (bits 3:0 and 15:14), expcnt 7 (bits 6:4), lgkmcnt 0 (bits 11:8).
+constexpr int kWaitLgkm0 = 0xC07F;
 constexpr uint32_t kChunks = 16;  // 16-byte chunks per 128-channel F16 head row
 constexpr uint32_t kHalfTileChunks = kTileTokens * kChunks / 2;  // one wave's LDS region (8 KiB)
 
@@ -163,29 +166,65 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
         const uint32_t q_lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(uint32_t(qa)));
         const uint64_t qu = (static_cast<uint64_t>(q_hi) << 32) | static_cast<uint64_t>(q_lo);
         ConstU32* qh = (ConstU32*)(reinterpret_cast<const uint32_t*>(qu)) + head_kv * 4 * 64 + h * 32;
+        // Two-deep pipeline over the half's 8 chunks of 8 channels: chunk
+        // j + 1's query words (16 SGPRs, four s_load_dwordx4) and K chunk are
+        // requested between chunk j - 1's FMAs and chunk j's.  Scalar loads
+        // return out of order, so the only usable wait for them is
+        // lgkmcnt(0): it comes right before that request, when chunk j's
+        // operands (requested a chunk earlier) are in and nothing newer is
+        // outstanding.  The order is held by data, since the compiler moves
+        // loads and arithmetic freely within a block: an empty asm consumes
+        // the chains after chunk j - 1, and a second one, after the wait,
+        // yields the zero that chunk j + 1's addresses and chunk j's K words
+        // (OR 0, the same bits) depend on.  (The query of a whole half at
+        // once would take 128 SGPRs and spill to VGPR lanes.)
+        uint32_t qb[2][16];
+        uint4 kb[2], qsb[2][2];
+        auto issue = [&](uint32_t j, uint32_t b, uint32_t zero) {
+            ConstU32* qj = qh + j * 4 + zero;
+#pragma unroll
+            for (uint32_t hh = 0; hh < 4; ++hh)
+#pragma unroll
+                for (uint32_t d = 0; d < 4; ++d) qb[b][hh * 4 + d] = qj[hh * 64 + d];
+            kb[b] = region[hslot(lane, j) + zero];
+            if constexpr (kLogits) {
+                const uint32_t qi = (lane & 3u) * 16 + 8 * h + j + zero;  // this lane's head, chunk 8h + j
+                qsb[b][0] = qstage[qi];
+                qsb[b][1] = qstage[64 + qi];
+            }
+        };
+        {
+            uint32_t zero;
+            asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+            issue(0, 0, zero);
+        }
 #pragma unroll
         for (uint32_t j = 0; j < kHalf; ++j) {
-            const uint4 k4 = region[hslot(lane, j)];
-            const uint32_t kw[4] = {k4.x, k4.y, k4.z, k4.w};
+            uint32_t after, zero;
+            asm volatile("s_mov_b32 %0, 0" : "=s"(after) : "v"(a0), "v"(a1), "v"(a2), "v"(a3));
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            asm volatile("s_mov_b32 %0, %1" : "=s"(zero) : "s"(after));
+            if (j + 1 < kHalf) issue(j + 1, (j + 1) & 1u, zero);
+            const uint32_t b = j & 1u;
+            const uint4 k4 = kb[b];
+            const uint32_t kw[4] = {k4.x | zero, k4.y | zero, k4.z | zero, k4.w | zero};
             if constexpr (kLogits) {
                 // channels 8j .. 8j+7 of the half: two 4-channel steps, hi and lo
-                const uint32_t qi = (lane & 3u) * 16 + 8 * h + j;  // this lane's head, chunk 8h + j
-                const uint4 qh = qstage[qi], ql = qstage[64 + qi];
-                const uint2 ka = make_uint2(k4.x, k4.y), kb = make_uint2(k4.z, k4.w);
+                const uint4 qh4 = qsb[b][0], ql4 = qsb[b][1];
+                const uint2 ka = make_uint2(k4.x, k4.y), kc = make_uint2(k4.z, k4.w);
                 dots[0] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, ka),
-                                                             __builtin_bit_cast(half4_t, make_uint2(qh.x, qh.y)), dots[0], 0, 0, 0);
+                                                             __builtin_bit_cast(half4_t, make_uint2(qh4.x, qh4.y)), dots[0], 0, 0, 0);
                 dots[1] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, ka),
-                                                             __builtin_bit_cast(half4_t, make_uint2(ql.x, ql.y)), dots[1], 0, 0, 0);
-                dots[2] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, kb),
-                                                             __builtin_bit_cast(half4_t, make_uint2(qh.z, qh.w)), dots[2], 0, 0, 0);
-                dots[3] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, kb),
-                                                             __builtin_bit_cast(half4_t, make_uint2(ql.z, ql.w)), dots[3], 0, 0, 0);
+                                                             __builtin_bit_cast(half4_t, make_uint2(ql4.x, ql4.y)), dots[1], 0, 0, 0);
+                dots[2] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, kc),
+                                                             __builtin_bit_cast(half4_t, make_uint2(qh4.z, qh4.w)), dots[2], 0, 0, 0);
+                dots[3] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(half4_t, kc),
+                                                             __builtin_bit_cast(half4_t, make_uint2(ql4.z, ql4.w)), dots[3], 0, 0, 0);
             }
 #pragma unroll
             for (uint32_t p = 0; p < 4; ++p) {
-                const uint32_t c2 = j * 4 + p;
                 const float klo = lo_half(kw[p]), khi = hi_half(kw[p]);
-                const uint32_t q0 = qh[c2], q1 = qh[64 + c2], q2 = qh[128 + c2], q3 = qh[192 + c2];
+                const uint32_t q0 = qb[b][p], q1 = qb[b][4 + p], q2 = qb[b][8 + p], q3 = qb[b][12 + p];
                 a0 = __builtin_fmaf(lo_half(q0), klo, a0);
                 a1 = __builtin_fmaf(lo_half(q1), klo, a1);
                 a2 = __builtin_fmaf(lo_half(q2), klo, a2);
