@@ -511,13 +511,16 @@ __device__ __forceinline__ uint32_t sat_sub(uint32_t a, uint32_t b) { return a -
 // in the scorer.  q F16 [32][128], key F16 [8][128] (query head h reads KV
 // head h / 4).  One lane computes it.
 __device__ __noinline__ uint32_t score_current(const uint16_t* q, const uint16_t* key, uint32_t h) {
-    const uint4* qv = reinterpret_cast<const uint4*>(q + h * 128);
-    const uint4* kv = reinterpret_cast<const uint4*>(key + (h >> 2) * 128);
+    // global (not flat) loads: in a call the pointers' address space is
+    // unknown, and flat loads can only be waited for all at once
+    using GlobalU32 = const __attribute__((address_space(1))) uint32_t;
+    GlobalU32* qv = (GlobalU32*)(q + h * 128);
+    GlobalU32* kv = (GlobalU32*)(key + (h >> 2) * 128);
     uint4 qa[16], ka[16];
 #pragma unroll
     for (uint32_t i = 0; i < 16; ++i) {
-        qa[i] = qv[i];
-        ka[i] = kv[i];
+        qa[i] = make_uint4(qv[4 * i], qv[4 * i + 1], qv[4 * i + 2], qv[4 * i + 3]);
+        ka[i] = make_uint4(kv[4 * i], kv[4 * i + 1], kv[4 * i + 2], kv[4 * i + 3]);
     }
     float s = 0.0f;
 #pragma unroll
