@@ -115,6 +115,18 @@ struct MapSource {
     uint32_t prefetched_rows, miss_rows;
 };
 
+// A row every slot may read when it has none of its own (its bytes are
+// discarded): the pool's first row, or the first prefetched or miss record;
+// null when there is no source at all.  For the pool, row 0's K and V
+// segments exist whenever pool_rows > 0.
+__device__ __forceinline__ const uint8_t* fallback_row(const PoolSource& ps, const MapSource& ms,
+                                                       bool pack) {
+    if (pack) return ps.pool_rows > 0 ? ps.pool : nullptr;
+    if (ms.prefetched && ms.prefetched_rows > 0) return reinterpret_cast<const uint8_t*>(ms.prefetched);
+    if (ms.misses && ms.miss_rows > 0) return reinterpret_cast<const uint8_t*>(ms.misses);
+    return nullptr;
+}
+
 // Grid (ceil(count/64), 32 heads), 256 threads.  kPack selects the source.
 template <bool kPack>
 __global__ void __launch_bounds__(256)
@@ -123,7 +135,7 @@ pack_kernel(PoolSource ps, MapSource ms, const uint64_t* __restrict__ positions,
             float* __restrict__ mask, hs_status_t* __restrict__ status) {
     __shared__ uint4 vtile[64][17];  // 64 slots x 256 B V half row (+pad)
     __shared__ const uint8_t* src_row[64];
-    __shared__ uint32_t slot_id[64];
+    __shared__ uint32_t slot_id[64], slot_ok[64];
     const uint32_t h = blockIdx.y, kv = h >> 2, s0 = blockIdx.x * 64, tid = threadIdx.x;
 
     if (tid < 64) {
@@ -167,24 +179,46 @@ pack_kernel(PoolSource ps, MapSource ms, const uint64_t* __restrict__ positions,
                     raise(status, HS_ERR_MISSING);
             }
         }
-        src_row[tid] = src;
+        // a slot with no row reads the fallback row (discarded) so that every
+        // load below can be issued unconditionally
+        src_row[tid] = src ? src : fallback_row(ps, ms, kPack);
+        slot_ok[tid] = src != nullptr;
         slot_id[tid] = id;
     }
     __syncthreads();
     // K rows: 64 slots x 16 x 16 B; V half rows staged for the transpose.
     // (prefetched and miss rows are 4096 B records: V 2048 B after K)
     const int64_t v_delta = kPack ? ps.v_delta : 2048;
-    for (uint32_t i = tid; i < 64 * 16; i += 256) {
-        const uint32_t s = i >> 4, c = i & 15u;
-        const uint8_t* src = src_row[s];
-        uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
-        if (src) {
-            kw = reinterpret_cast<const uint4*>(src + kv * 256)[c];
-            vw = reinterpret_cast<const uint4*>(src + v_delta + kv * 256)[c];
+    // Every K and V chunk of the thread's 4 (slot, chunk) pairs is requested
+    // before any is stored.  The row pointers come back from LDS without
+    // their address space: they are read through global pointers (flat loads
+    // can only be waited for all at once).  With no source at all (every
+    // slot empty) nothing is read.
+    using GlobalU32 = const __attribute__((address_space(1))) uint32_t;
+    constexpr uint32_t kPairs = 64 * 16 / 256;
+    uint4 kw[kPairs], vw[kPairs];
+    if (fallback_row(ps, ms, kPack) != nullptr) {
+#pragma unroll
+        for (uint32_t u = 0; u < kPairs; ++u) {
+            const uint32_t i = tid + 256 * u, s = i >> 4, c = i & 15u;
+            const uint8_t* src = src_row[s];
+            GlobalU32* kp = (GlobalU32*)(src + kv * 256) + 4 * c;
+            GlobalU32* vp = (GlobalU32*)(src + v_delta + kv * 256) + 4 * c;
+            kw[u] = make_uint4(kp[0], kp[1], kp[2], kp[3]);
+            vw[u] = make_uint4(vp[0], vp[1], vp[2], vp[3]);
         }
-        vtile[s][c] = vw;
+    } else {
+#pragma unroll
+        for (uint32_t u = 0; u < kPairs; ++u) kw[u] = vw[u] = make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kPairs; ++u) {
+        const uint32_t i = tid + 256 * u, s = i >> 4, c = i & 15u;
+        const bool ok = slot_ok[s] != 0;
+        vtile[s][c] = ok ? vw[u] : make_uint4(0, 0, 0, 0);
         if (s0 + s < count)
-            reinterpret_cast<uint4*>(k_out + (static_cast<size_t>(s0 + s) * 32 + h) * 128)[c] = kw;
+            reinterpret_cast<uint4*>(k_out + (static_cast<size_t>(s0 + s) * 32 + h) * 128)[c] =
+                ok ? kw[u] : make_uint4(0, 0, 0, 0);
     }
     __syncthreads();
     // V[h][d][s]: 128 channel rows x 64 slots.  A thread gathers 8
