@@ -21,11 +21,11 @@
 //    (XOR-swizzled 16 B chunks: conflict-free writes and reads) so that lane t
 //    then holds token t's 64 channels in order; the 4 chains run on across
 //    the two halves.
-//  * Waves are independent pipelines: both halves of a tile are requested
-//    before the first is used (with the row map and in batched launches: the
-//    second once the first is parked in LDS), the next tile's while the
+//  * Waves are independent pipelines: a tile's second half is requested once
+//    its first is parked in LDS, and the next tile's first half while the
 //    current second half is computed, so loads overlap compute and a half
-//    tile is the most compute left once the last loads land.
+//    tile is the most compute left once the last loads land.  Each 8-channel
+//    chunk's query words are requested one chunk ahead (score_tile.hpp).
 //    16 waves per CU keep the whole key set in flight at N = 32768.
 #include <hip/hip_runtime.h>
 
@@ -45,9 +45,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * 64)
 score_kernel(const ScoreJobs jobs, const int32_t* __restrict__ rows, uint32_t pool_rows) {
     __shared__ uint4 lds[kWavesPerBlock][kHalfTileChunks];
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // both halves ahead for one job without the row map (with the row map
-    // its VGPRs would pass 128; the batched launch gained nothing from it)
-    score_waves<kRows, kBatch, !kRows && !kBatch>(jobs, rows, pool_rows,
+    score_waves<kRows, kBatch>(jobs, rows, pool_rows,
                                __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + w),
                                gridDim.x * kWavesPerBlock, lds[w]);
 }
@@ -61,7 +59,7 @@ score_logits_kernel(const ScoreJobs jobs, const int32_t* __restrict__ rows, uint
     __shared__ uint4 lds[kWavesPerBlock][kHalfTileChunks];
     __shared__ uint4 qstage[kWavesPerBlock][8 * 16];
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    score_waves<kRows, false, false, true>(
+    score_waves<kRows, false, true>(
         jobs, rows, pool_rows, __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + w),
         gridDim.x * kWavesPerBlock, lds[w], lo, qstage[w]);
 }

@@ -48,23 +48,11 @@ struct ScoreJobs {
 // Checks a batch of score jobs and fills the launch table (score.hip).
 int build_score_jobs(const hs_score_job_t* jobs, uint32_t count, ScoreJobs& out);
 
-// The buffer of a tile's second half: its own with kAhead, else the first's.
-template <bool kAhead, size_t kN, size_t kM>
-__device__ __forceinline__ uint4 (&second_half_buffer(uint4 (&first)[kN], uint4 (&own)[kM]))[kN] {
-    if constexpr (kAhead) {
-        static_assert(kM == kN, "a second buffer of the same size");
-        return own;
-    } else {
-        return first;
-    }
-}
-
 // Wave `wave` of `waves` scoring waves takes the (token tile, KV head) ids
 // wave, wave + waves, ... of `jobs`; `region` is its own kHalfTileChunks
-// of LDS.  Waves never wait on one another.  kAhead: both halves of a tile
-// are requested before the first is used (32 more VGPRs), so a tile costs
-// one memory round trip instead of two; otherwise the second half is
-// requested once the first is parked in LDS.
+// of LDS.  Waves never wait on one another.  A tile's second half is
+// requested once its first is parked in LDS, into the same registers.
+// (Both halves requested together cost 32 more VGPRs and measured slower.)
 // kLogits: the same pass also produces the attention's q.k dots of the
 // tile's 64 tokens for the 4 query heads (F32 queries lo.qf), on MFMA from
 // the K values the ordered chains already hold: v_mfma_f32_4x4x4_16b_f16
@@ -76,7 +64,7 @@ __device__ __forceinline__ uint4 (&second_half_buffer(uint4 (&first)[kN], uint4 
 // of LDS per wave), staged when the KV head changes.  Lane 4b + j ends with
 // head j's dots of tokens 4b .. 4b+3, written to lo.out unscaled; the
 // attention then reads V rows only.
-template <bool kRows, bool kBatch, bool kAhead, bool kLogits = false>
+template <bool kRows, bool kBatch, bool kLogits = false>
 __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t* __restrict__ rows,
                                             uint32_t pool_rows, uint32_t wave, uint32_t waves,
                                             uint4* region, const LogitsOut& lo = LogitsOut{},
@@ -273,14 +261,12 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
 
     // Pipeline unit: half a tile.  While one half is computed, the next is
     // in flight; the tile's 4 chains run on across its two halves.
-    uint4 v[kHalf], v2[kAhead ? kHalf : 1];
-    uint4 (&second)[kHalf] = second_half_buffer<kAhead>(v, v2);  // v2, or v itself
+    uint4 v[kHalf];
     uint32_t id = wave;
     if (id >= tiles) return;
     ScoreJob cur = jobs.job[job_of(id)];
     uint32_t row = row_of(cur, id);
     load(cur, id, 0, row, v);
-    if (kAhead) load(cur, id, 1, row, second);
     while (true) {
         if constexpr (kLogits) {
             const uint32_t kv = (id - cur.first_id) & 7u;  // wave-uniform
@@ -291,10 +277,10 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
         }
         stash(v);
         __builtin_amdgcn_wave_barrier();
-        if (!kAhead) load(cur, id, 1, row, second);
+        load(cur, id, 1, row, v);
         compute(cur, id, 0);
         __builtin_amdgcn_wave_barrier();
-        stash(second);
+        stash(v);
         __builtin_amdgcn_wave_barrier();
         const uint32_t next = id + waves;
         ScoreJob nxt = cur;
@@ -303,7 +289,6 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
             nxt = jobs.job[job_of(next)];
             nrow = row_of(nxt, next);
             load(nxt, next, 0, nrow, v);
-            if (kAhead) load(nxt, next, 1, nrow, second);
         }
         compute(cur, id, 1);
         finish(cur, id);

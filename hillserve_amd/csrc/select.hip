@@ -1573,7 +1573,7 @@ select_score_kernel(const SelectJobs js, const ScoreJobs sj) {
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // one half ahead: both halves ahead took more of the memory system from
     // the selection and lengthened the launch
-    score_waves<false, kBatch, false>(sj, nullptr, 0u,
+    score_waves<false, kBatch>(sj, nullptr, 0u,
                                __builtin_amdgcn_readfirstlane((blockIdx.x - selectors) * kHWaves + w),
                                (gridDim.x - selectors) * kHWaves, lds.score[w]);
 }
