@@ -492,9 +492,9 @@ __device__ __forceinline__ uint32_t hist_total(const uint32_t* whist, uint32_t b
 // p[i] for i < n (n >= 1), else 0, with no branch around the load: the
 // index is clamped into range and the value selected afterwards, so all the
 // loads of a phase are in flight together instead of each waiting for the
-// last at a branch join.
+// last at a branch join.  (n >= 1 always: the host rejects n == 0 and
+// heads == 0, so every group, slice and histogram count is positive.)
 __device__ __forceinline__ uint32_t load_or_zero(const uint32_t* p, uint32_t i, uint32_t n) {
-    if (n == 0) return 0u;  // (uniform) nothing to read
     const uint32_t x = p[i < n ? i : n - 1u];
     return i < n ? x : 0u;
 }
