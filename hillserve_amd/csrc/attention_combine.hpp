@@ -68,11 +68,17 @@ __device__ __forceinline__ void combine_records(const float* __restrict__ part, 
     float L = 0.0f;
 #pragma unroll
     for (uint32_t w = 0; w < 8; ++w) L += red[w];
+    // the 16 weights are read before any is used (a read inside the test
+    // below would make each term wait for its own LDS round trip); a zero
+    // weight still skips its term, whose o may be inf or NaN
+    float wv[kFirst];
+#pragma unroll
+    for (uint32_t u = 0; u < kFirst; ++u) wv[u] = weight[r + kCombineRows * u];
     float a = 0.0f;
 #pragma unroll
     for (uint32_t u = 0; u < kFirst; ++u) {
         const uint32_t i = r + kCombineRows * u;
-        if (i < chunks && weight[i] != 0.0f) a = __builtin_fmaf(v[u], weight[i], a);
+        if (i < chunks && wv[u] != 0.0f) a = __builtin_fmaf(v[u], wv[u], a);
     }
     for (uint32_t i = r + kCombineRows * kFirst; i < chunks; i += kCombineRows) {  // n > 32768
         const float x = recs[i * 4 * kAttnRecord + 2 + ch];
