@@ -416,11 +416,15 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
     for (uint32_t j = 0; j < 4; ++j)
 #pragma unroll
         for (uint32_t c = 0; c < 8; ++c) o[j][c] = 0.0f;
+    // each group's p is read one group ahead, under the previous group's
+    // FMAs (a read inside the group's own test waits a full LDS round trip)
+    float4 pnext = sel_p[g][min(q16, total - 1)];
 #pragma unroll
     for (uint32_t i = 0; i < kGroups; ++i) {
         if (i < groups) {
             const uint32_t e = 4 * i + q16;
-            const float4 pp = sel_p[g][min(e, total - 1)];
+            const float4 pp = pnext;
+            if (i + 1 < kGroups) pnext = sel_p[g][min(e + 4, total - 1)];
             const bool live = e < total;
             const float p0 = live ? pp.x : 0.0f, p1 = live ? pp.y : 0.0f;
             const float p2 = live ? pp.z : 0.0f, p3 = live ? pp.w : 0.0f;
