@@ -1,0 +1,138 @@
+"""HIP graph capture of the decode path: the entry points enqueue kernels
+only (no allocation, memset or synchronisation), so a caller can capture a
+layer, or a pipelined run of layers, once and replay it.  Each replay runs on
+new inputs written into the captured buffers by eager kernels between
+replays, and must equal the eager calls on the same inputs bit for bit
+(scores, ids, counts, membership words, status, attention output)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+N, ALPHA, RATIO = 4096, 5.0, 0.2
+KMAX = min(N, math.floor(N * float(np.float32(RATIO))))
+
+
+def fill_layer(hs, k, v, q16, q32, seed):
+    hs.ops.fill_rope_keys(k, N, 1024, 8, seed=seed, theta=500000.0)
+    hs.ops.fill_gaussian(v, seed=seed + 1)
+    hs.ops.fill_gaussian(q16, seed=seed + 2)
+    q32.copy_(torch.randn(q32.shape, generator=torch.Generator(device="cuda").manual_seed(seed),
+                          device="cuda"))
+
+
+def capture(fn, stream):
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def test_decode_layer_graph_replays_equal_eager(hs):
+    dev = "cuda"
+    k = torch.empty(N * 1024, dtype=torch.float16, device=dev)
+    v = torch.empty_like(k)
+    q16 = torch.empty(4096, dtype=torch.float16, device=dev)
+    q32 = torch.empty((32, 128), dtype=torch.float32, device=dev)
+    scores = torch.empty((32, N), dtype=torch.float16, device=dev)
+    ids = torch.empty((32, KMAX), dtype=torch.int32, device=dev)
+    counts = torch.empty(32, dtype=torch.int32, device=dev)
+    out = torch.empty((32, 128), dtype=torch.float32, device=dev)
+    status = hs.ops.new_status(dev)
+    ws = hs.ops.workspace(hs.ops.decode_layer_workspace_bytes(N), dev)
+    outputs = (scores, ids, counts, out, status)
+
+    def layer():
+        hs.ops.decode_layer(q16, q32, k, N, ALPHA, RATIO, scores=scores, ids=ids, ids_stride=KMAX,
+                            counts=counts, out=out, status=status, ws=ws, v_pool=v, row_bytes=2048)
+
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        fill_layer(hs, k, v, q16, q32, 11)
+        layer()
+        torch.cuda.synchronize()
+        graph = capture(layer, side)
+        for seed in (21, 31, 41):
+            fill_layer(hs, k, v, q16, q32, seed)
+            for t in outputs:
+                t.fill_(-1) if t.dtype != torch.float16 else t.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            replayed = [t.clone() for t in outputs]
+            layer()
+            torch.cuda.synchronize()
+            st = hs.ops.read_status(status)
+            assert st["code"] == 0 and st["k"] == KMAX, (seed, st)
+            for name, a, b in zip(("scores", "ids", "counts", "out", "status"), replayed, outputs):
+                assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), (seed, name)
+
+
+def test_pipelined_layers_graph_replays_equal_eager(hs):
+    """Three layers on the realizable schedule: layer 0's history, then each
+    layer's selection (completing its current token) beside the next layer's
+    history scoring, then its attention over K and V rows."""
+    dev, layers = "cuda", 3
+    ks = [torch.empty(N * 1024, dtype=torch.float16, device=dev) for _ in range(layers)]
+    vs = [torch.empty_like(ks[0]) for _ in range(layers)]
+    qs = [torch.empty(4096, dtype=torch.float16, device=dev) for _ in range(layers)]
+    q32s = [torch.empty((32, 128), dtype=torch.float32, device=dev) for _ in range(layers)]
+    raws = [torch.empty((32, N), dtype=torch.float16, device=dev) for _ in range(2)]
+    parts = [torch.empty(N // 64, dtype=torch.int32, device=dev) for _ in range(2)]
+    ids = torch.empty((32, KMAX), dtype=torch.int32, device=dev)
+    counts = torch.empty(32, dtype=torch.int32, device=dev)
+    member = torch.empty((32, N // 32), dtype=torch.int32, device=dev)
+    outs = [torch.empty((32, 128), dtype=torch.float32, device=dev) for _ in range(layers)]
+    statuses = [hs.ops.new_status(dev) for _ in range(layers)]
+    sws = hs.ops.workspace(hs.ops.select_workspace_bytes(32, N), dev)
+    aws = hs.ops.workspace(hs.ops.attention_workspace_bytes(N), dev)
+    outputs = [*raws, ids, counts, member, *outs, *statuses]
+
+    def job(l):
+        return dict(scores=raws[l % 2], n=N, head0_partial=parts[l % 2], ids=ids, ids_stride=KMAX,
+                    counts=counts, member=member, status=statuses[l], ws=sws, current_q=qs[l],
+                    current_key=ks[l][(N - 1) * 1024:])
+
+    def hist(l):
+        return dict(q16=qs[l], keys=ks[l], tokens=N - 1, out=raws[l % 2], score_stride=N,
+                    head0_partial=parts[l % 2])
+
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        flags = dict(scale_raw=True, require_k=True, id_order=True)
+        calls = [hs.ops.prepare_select_then_score([job(l)], [hist(l + 1)], 32, ALPHA, RATIO,
+                                                  **flags) for l in range(layers - 1)]
+        calls.append(hs.ops.prepare_select_batched([job(layers - 1)], 32, ALPHA, RATIO, **flags))
+
+        def run():
+            hs.ops.score(qs[0], ks[0], N - 1, out=raws[0], score_stride=N, head0_partial=parts[0])
+            for l in range(layers):
+                calls[l]()
+                hs.ops.sparse_attention(q32s[l], ks[l], N, member, out=outs[l], ws=aws,
+                                        v_pool=vs[l], row_bytes=2048)
+
+        def fill(seed):
+            for l in range(layers):
+                fill_layer(hs, ks[l], vs[l], qs[l], q32s[l], seed + 10 * l)
+
+        fill(100)
+        run()
+        torch.cuda.synchronize()
+        graph = capture(run, side)
+        for seed in (200, 300):
+            fill(seed)
+            for t in outputs:
+                t.fill_(-1) if t.dtype != torch.float16 else t.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            replayed = [t.clone() for t in outputs]
+            run()
+            torch.cuda.synchronize()
+            for l, st in enumerate(statuses):
+                s = hs.ops.read_status(st)
+                assert s["code"] == 0 and s["k"] == KMAX, (seed, l, s)
+            for i, (a, b) in enumerate(zip(replayed, outputs)):
+                assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), (seed, i)
