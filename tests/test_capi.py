@@ -177,5 +177,6 @@ def test_attention_then_count_rejects_overlap(hs):
     assert call(job(ws=aws)) == hs.HS_ERR_ARGUMENT          # count workspace = attention records
     assert call(job(status=out)) == hs.HS_ERR_ARGUMENT      # status over the attention output
     assert call(job(scores=out)) == hs.HS_ERR_ARGUMENT      # next scores under the output
+    assert call(job(scores=aws)) == hs.HS_ERR_ARGUMENT      # next scores under the records
     assert call(job(), flags=hs.HS_SELECT_SCALE_RAW | hs.HS_SELECT_COUNTED) == hs.HS_ERR_ARGUMENT
     assert call(job(), out_ptr=0) == hs.HS_ERR_ARGUMENT     # attention shape checks still apply
