@@ -174,6 +174,10 @@ struct SelectJobs {
     SelectJob job[kMaxBatch];
     uint32_t count, heads, flags;
     float alpha, ratio;
+    // per-head launches: row r of the grid selects job order[r], the jobs
+    // with the most ids first, so a batch that runs in more than one round
+    // of workgroups starts its longest selections first
+    uint8_t order[kMaxBatch];
 };
 
 // The SelectArgs view of job j: its workspace slices follow plan_select.
@@ -1547,7 +1551,7 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
 template <bool kRankOrder>
 __global__ void __launch_bounds__(kHThreads) head_select_kernel(const SelectJobs js) {
     __shared__ HeadSelectLds<kRankOrder> lds;
-    head_select<kRankOrder>(js, blockIdx.x, blockIdx.y, lds);
+    head_select<kRankOrder>(js, blockIdx.x, js.order[blockIdx.y], lds);
 }
 
 // One layer's per-head selection and the next layer's scoring in one launch
@@ -1567,7 +1571,8 @@ select_score_kernel(const SelectJobs js, const ScoreJobs sj) {
     } lds;
     const uint32_t selectors = js.heads * js.count;
     if (blockIdx.x < selectors) {
-        head_select<kRankOrder>(js, blockIdx.x % js.heads, blockIdx.x / js.heads, lds.select);
+        head_select<kRankOrder>(js, blockIdx.x % js.heads, js.order[blockIdx.x / js.heads],
+                                lds.select);
         return;
     }
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1900,6 +1905,7 @@ int launch_jobs(const SelectJobs& js, hipStream_t stream) {
             SelectJobs one = js;
             one.count = 1;
             one.job[0] = js.job[j];
+            one.order[0] = 0;
             const int rc = launch_jobs(one, stream);
             if (rc != HS_OK) return rc;
         }
@@ -1956,6 +1962,9 @@ int build_select_jobs(const hs_select_job_t* jobs, uint32_t count, uint32_t head
                        q.current_key);
         if (rc != HS_OK) return rc;
     }
+    for (uint32_t j = 0; j < count; ++j) js.order[j] = static_cast<uint8_t>(j);
+    std::stable_sort(js.order, js.order + count,
+                     [&](uint8_t a, uint8_t b) { return js.job[a].n > js.job[b].n; });
     return HS_OK;
 }
 
