@@ -3,7 +3,9 @@ only (no allocation, memset or synchronisation), so a caller can capture a
 layer, or a pipelined run of layers, once and replay it.  Each replay runs on
 new inputs written into the captured buffers by eager kernels between
 replays, and must equal the eager calls on the same inputs bit for bit
-(scores, ids, counts, membership words, status, attention output)."""
+(scores, ids, counts, membership words, status, attention output).  The same
+pipelined run, eager, with a nonfinite key in its middle layer shows that a
+failed layer stays reported and never reuses an earlier layer's selection."""
 import math
 
 import numpy as np
@@ -136,3 +138,50 @@ def test_pipelined_layers_graph_replays_equal_eager(hs):
                 assert s["code"] == 0 and s["k"] == KMAX, (seed, l, s)
             for i, (a, b) in enumerate(zip(replayed, outputs)):
                 assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), (seed, i)
+
+
+def test_failed_middle_layer_is_reported_not_stale(hs):
+    """Three pipelined layers sharing one membership buffer, each with its own
+    status: a NaN key in layer 1's history makes layer 1's selection fail
+    with HS_ERR_NONFINITE, which stays visible after the run; its membership
+    words are cleared, so its attention output is NaN (no selected row), not
+    the previous layer's; layers 0 and 2 select and attend normally."""
+    dev, layers = "cuda", 3
+    ks = [torch.empty(N * 1024, dtype=torch.float16, device=dev) for _ in range(layers)]
+    vs = [torch.empty_like(ks[0]) for _ in range(layers)]
+    qs = [torch.empty(4096, dtype=torch.float16, device=dev) for _ in range(layers)]
+    q32s = [torch.empty((32, 128), dtype=torch.float32, device=dev) for _ in range(layers)]
+    for l in range(layers):
+        fill_layer(hs, ks[l], vs[l], qs[l], q32s[l], 500 + 10 * l)
+    ks[1][100 * 1024 + 5] = float("nan")  # token 100, KV head 0: query heads 0-3
+    raws = [torch.empty((32, N), dtype=torch.float16, device=dev) for _ in range(2)]
+    parts = [torch.empty(N // 64, dtype=torch.int32, device=dev) for _ in range(2)]
+    ids = torch.empty((32, KMAX), dtype=torch.int32, device=dev)
+    member = torch.empty((32, N // 32), dtype=torch.int32, device=dev)
+    outs = [torch.zeros((32, 128), dtype=torch.float32, device=dev) for _ in range(layers)]
+    statuses = [hs.ops.new_status(dev) for _ in range(layers)]
+    sws = hs.ops.workspace(hs.ops.select_workspace_bytes(32, N), dev)
+    aws = hs.ops.workspace(hs.ops.attention_workspace_bytes(N), dev)
+
+    def job(l):
+        return dict(scores=raws[l % 2], n=N, head0_partial=parts[l % 2], ids=ids, ids_stride=KMAX,
+                    member=member, status=statuses[l], ws=sws, current_q=qs[l],
+                    current_key=ks[l][(N - 1) * 1024:])
+
+    flags = dict(scale_raw=True, require_k=True, id_order=True)
+    hs.ops.score(qs[0], ks[0], N - 1, out=raws[0], score_stride=N, head0_partial=parts[0])
+    for l in range(layers):
+        if l + 1 < layers:
+            hs.ops.select_then_score(
+                [job(l)], [dict(q16=qs[l + 1], keys=ks[l + 1], tokens=N - 1, out=raws[(l + 1) % 2],
+                                score_stride=N, head0_partial=parts[(l + 1) % 2])],
+                32, ALPHA, RATIO, **flags)
+        else:
+            hs.ops.prepare_select_batched([job(l)], 32, ALPHA, RATIO, **flags)()
+        hs.ops.sparse_attention(q32s[l], ks[l], N, member, out=outs[l], ws=aws, v_pool=vs[l],
+                                row_bytes=2048)
+    torch.cuda.synchronize()
+    codes = [hs.ops.read_status(st)["code"] for st in statuses]
+    assert codes == [hs.HS_OK, hs.HS_ERR_NONFINITE, hs.HS_OK], codes
+    assert torch.isnan(outs[1]).all()
+    assert torch.isfinite(outs[0]).all() and torch.isfinite(outs[2]).all()
