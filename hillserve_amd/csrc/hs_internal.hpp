@@ -41,6 +41,11 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
                   float alpha, float ratio, uint32_t flags, const uint32_t* head0_partial,
                   uint32_t* ids, size_t ids_stride, uint32_t* counts, uint32_t* member,
                   hs_status_t* status, void* workspace, hipStream_t stream);
+// launch_select's host checks only (nothing enqueued)
+int check_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_t n, float alpha,
+                 float ratio, uint32_t flags, const uint32_t* head0_partial, uint32_t* ids,
+                 size_t ids_stride, uint32_t* counts, uint32_t* member, hs_status_t* status,
+                 void* workspace);
 
 int launch_select_batched(const hs_select_job_t* jobs, uint32_t count, uint32_t heads,
                           float alpha, float ratio, uint32_t flags, hipStream_t stream);

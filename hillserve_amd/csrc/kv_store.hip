@@ -297,11 +297,12 @@ int launch_cold_fetch_runs(const void* image, uint32_t layer, const uint32_t* ru
                            const uint32_t* positions, uint32_t count, uint8_t* k_out,
                            uint8_t* v_out, size_t row_bytes, hs_status_t* status, void* workspace,
                            hipStream_t stream) {
+    if (!raw || !run_first || !run_count || runs == 0) return reject("cold fetch runs: null pointer or no run");
+    if (reinterpret_cast<uintptr_t>(raw) & 15u) return reject("cold fetch runs: raw staging must be 16-byte aligned");
     uint64_t h[8];
     int rc = check_cold_read(image, layer, positions, count, k_out, v_out, row_bytes, status,
                              workspace, h);
     if (rc != HS_OK) return rc;
-    if (!raw || !run_first || !run_count || runs == 0) return reject("cold fetch runs: null pointer or no run");
     uint64_t total = 0;
     for (uint32_t r = 0; r < runs; ++r) {
         if (run_count[r] == 0 || run_first[r] >= h[4] || run_count[r] > h[4] - run_first[r])

@@ -199,17 +199,24 @@ int decode_layer(const uint16_t* q16_dev, const float* q32_dev, const uint8_t* k
     uint32_t* partial = reinterpret_cast<uint32_t*>(ws + p.off_partial);
     uint32_t* member = reinterpret_cast<uint32_t*>(ws + p.off_member);
     float* logits = reinterpret_cast<float*>(ws + p.off_logits);
-    if (reinterpret_cast<uintptr_t>(q32_dev) & 3u) return reject("decode layer: q32 must be 4-byte aligned");
+    // every argument checked before the first launch: an error returns with
+    // scores, ids, counts, status and output untouched
+    if (reinterpret_cast<uintptr_t>(q32_dev) & 15u) return reject("decode layer: q32 must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(k_pool_dev) | reinterpret_cast<uintptr_t>(v_pool_dev)) & 15u)
+        return reject("decode layer: K and V pools must be 16-byte aligned");
+    const uint32_t sel_flags = flags | HS_SELECT_SCALE_RAW | HS_SELECT_REQUIRE_K | HS_SELECT_ID_ORDER;
+    int rc = check_select(scores_dev, 32, n, n, alpha, ratio, sel_flags, partial, ids_dev, ids_stride,
+                          counts_dev, member, status_dev, ws + p.off_select);
+    if (rc != HS_OK) return rc;
     // One pass over the K rows: the ordered raw scores for the selection and,
     // from the same registers, the attention's q32.k dots for every token
     // (both queries are known when a layer is scored at its own step), so the
     // attention reads only the selected V rows.
-    int rc = launch_score(q16_dev, reinterpret_cast<const uint16_t*>(k_pool_dev), row_bytes / 2,
-                          row_of_id_dev, pool_rows, n, scores_dev, n, partial, s, q32_dev, logits, n);
+    rc = launch_score(q16_dev, reinterpret_cast<const uint16_t*>(k_pool_dev), row_bytes / 2,
+                      row_of_id_dev, pool_rows, n, scores_dev, n, partial, s, q32_dev, logits, n);
     if (rc != HS_OK) return rc;
-    rc = launch_select(scores_dev, 32, n, n, alpha, ratio,
-                       flags | HS_SELECT_SCALE_RAW | HS_SELECT_REQUIRE_K | HS_SELECT_ID_ORDER, partial,
-                       ids_dev, ids_stride, counts_dev, member, status_dev, ws + p.off_select, s);
+    rc = launch_select(scores_dev, 32, n, n, alpha, ratio, sel_flags, partial, ids_dev, ids_stride,
+                       counts_dev, member, status_dev, ws + p.off_select, s);
     if (rc != HS_OK) return rc;
     return launch_attention_logits(logits, n, v_pool_dev, row_bytes, row_of_id_dev, pool_rows, member,
                                    n, out_dev, ws + p.off_attn, s);

@@ -81,8 +81,8 @@ int launch_score(const uint16_t* q, const uint16_t* keys, size_t stride_words,
     if ((qf == nullptr) != (logits == nullptr)) return reject("score: logits need the F32 query");
     if (logits && (logit_stride < tokens || logit_stride > 0xffffffffu))
         return reject("score: logit stride must be >= tokens");
-    if (logits && (reinterpret_cast<uintptr_t>(qf) & 3u))
-        return reject("score: F32 query must be 4-byte aligned");
+    if (logits && (reinterpret_cast<uintptr_t>(qf) & 15u))
+        return reject("score: F32 query must be 16-byte aligned");
     if (stride_words != 1024 && stride_words != 2048)
         return reject("score: key stride must be 1024 or 2048 F16 words");
     if (tokens == 0 || tokens > 65536) return reject("score: tokens must be 1..65536");
@@ -97,7 +97,9 @@ int launch_score(const uint16_t* q, const uint16_t* keys, size_t stride_words,
     jobs.job[0] = ScoreJob{reinterpret_cast<const uint32_t*>(q), keys, scores, head0_partial,
                            static_cast<uint32_t>(stride_words), tokens,
                            static_cast<uint32_t>(score_stride), 0u};
-    const LogitsOut lo{qf, logits, static_cast<uint32_t>(logit_stride)};
+    // 16-byte logit stores only where every row start is 16-byte aligned
+    const uint32_t vec = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0 && (logit_stride & 3u) == 0;
+    const LogitsOut lo{qf, logits, static_cast<uint32_t>(logit_stride), vec};
     jobs.total_ids = ((tokens + kTileTokens - 1) / kTileTokens) * 8;  // (token tile, KV head)
     const dim3 grid(score_grid(jobs.total_ids)), block(kWavesPerBlock * 64);
     if (logits && rows)

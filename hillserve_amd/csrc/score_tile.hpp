@@ -38,6 +38,7 @@ struct LogitsOut {
     const float* qf;
     float* out;
     uint32_t stride;
+    uint32_t vec;  // 1: out 16-byte aligned and stride % 4 == 0 (float4 stores)
 };
 constexpr uint32_t kMaxScoreJobs = 16;
 struct ScoreJobs {
@@ -246,7 +247,7 @@ __device__ __forceinline__ void score_waves(const ScoreJobs& jobs, const int32_t
             const uint32_t t0 = (local >> 3) * kTileTokens + 4 * (lane >> 2);
             float* o = lo.out + static_cast<size_t>(head_kv * 4 + (lane & 3u)) * lo.stride + t0;
             const floatx4_t d = (dots[0] + dots[2]) + (dots[1] + dots[3]);
-            if (t0 + 4 <= jb.n && (lo.stride & 3u) == 0) {
+            if (t0 + 4 <= jb.n && lo.vec) {
                 *reinterpret_cast<float4*>(o) = make_float4(d[0], d[1], d[2], d[3]);
             } else {
 #pragma unroll

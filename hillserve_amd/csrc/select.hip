@@ -1942,6 +1942,18 @@ int launch_jobs(const SelectJobs& js, hipStream_t stream) {
 }
 
 // Checked selection jobs of a batch call.
+// Byte ranges [begin, end) of device buffers; empty for null pointers.
+struct Span {
+    uintptr_t begin, end;
+};
+Span span(const void* p, size_t bytes) {
+    const uintptr_t b = reinterpret_cast<uintptr_t>(p);
+    return p ? Span{b, b + bytes} : Span{0, 0};
+}
+bool overlap(const Span& x, const Span& y) {
+    return x.begin < x.end && y.begin < y.end && x.begin < y.end && y.begin < x.end;
+}
+
 int build_select_jobs(const hs_select_job_t* jobs, uint32_t count, uint32_t heads, float alpha,
                       float ratio, uint32_t flags, SelectJobs& js) {
     if (!jobs || count == 0 || count > kMaxBatch) return reject("select batch: 1..16 jobs");
@@ -1962,22 +1974,26 @@ int build_select_jobs(const hs_select_job_t* jobs, uint32_t count, uint32_t head
                        q.current_key);
         if (rc != HS_OK) return rc;
     }
+    // a job that completes its current token writes column n - 1 of its
+    // scores while the other jobs' count groups read theirs: no two jobs may
+    // then share score bytes
+    bool any_current = false;
+    for (uint32_t j = 0; j < count; ++j) any_current |= jobs[j].current_key != nullptr;
+    if (any_current) {
+        for (uint32_t i = 0; i < count; ++i)
+            for (uint32_t j = i + 1; j < count; ++j) {
+                const Span a = span(jobs[i].scores,
+                                    ((size_t(heads) - 1) * jobs[i].stride + jobs[i].n) * sizeof(uint16_t));
+                const Span b = span(jobs[j].scores,
+                                    ((size_t(heads) - 1) * jobs[j].stride + jobs[j].n) * sizeof(uint16_t));
+                if (overlap(a, b))
+                    return reject("select batch: jobs that complete a current token must not share scores");
+            }
+    }
     for (uint32_t j = 0; j < count; ++j) js.order[j] = static_cast<uint8_t>(j);
     std::stable_sort(js.order, js.order + count,
                      [&](uint8_t a, uint8_t b) { return js.job[a].n > js.job[b].n; });
     return HS_OK;
-}
-
-// Byte ranges [begin, end) of device buffers; empty for null pointers.
-struct Span {
-    uintptr_t begin, end;
-};
-Span span(const void* p, size_t bytes) {
-    const uintptr_t b = reinterpret_cast<uintptr_t>(p);
-    return p ? Span{b, b + bytes} : Span{0, 0};
-}
-bool overlap(const Span& x, const Span& y) {
-    return x.begin < x.end && y.begin < y.end && x.begin < y.end && y.begin < x.end;
 }
 
 // The scoring of a combined launch runs while the selection runs: nothing it
@@ -2040,6 +2056,20 @@ int launch_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_
                    workspace, ratio, flags, js.job[0]);
     if (rc != HS_OK) return rc;
     return launch_jobs(js, stream);
+}
+
+// The host checks of launch_select alone, nothing enqueued: a multi-launch
+// entry point runs them before its first launch, so an argument error leaves
+// every output untouched.
+int check_select(const uint16_t* scores, uint32_t heads, size_t stride, uint32_t n, float alpha,
+                 float ratio, uint32_t flags, const uint32_t* head0_partial, uint32_t* ids,
+                 size_t ids_stride, uint32_t* counts, uint32_t* member, hs_status_t* status,
+                 void* workspace) {
+    int rc = check_common(heads, alpha, ratio, flags);
+    if (rc != HS_OK) return rc;
+    SelectJob job{};
+    return check_job(scores, stride, n, head0_partial, ids, ids_stride, counts, member, status,
+                     workspace, ratio, flags, job);
 }
 
 int launch_select_batched(const hs_select_job_t* jobs, uint32_t count, uint32_t heads,

@@ -77,13 +77,24 @@ int hs_gqa_score(const uint16_t *q_dev, const uint16_t *keys_dev,
                  size_t score_stride, uint32_t *head0_partial_dev,
                  void *stream);
 
-/* The scorer (as hs_gqa_score) and, in the same pass over the keys, the
- * decode attention's q.k dots: logits_dev[h*logit_stride + t] = FP32 sum
- * over channels c in order of q32_dev[h][c] * K[t][h/4][c] (q32 F32
- * [32][128], the attention query; FMA per channel), unscaled, for
- * t < tokens.  For a layer scored at its own decode step, when both the
- * rehearsal query and the current query are known, this replaces the K
- * reads of hs_gqa_sparse_attention (see hs_gqa_sparse_attention_logits). */
+/* The scorer (as hs_gqa_score; its scores and tile maxima are bit for bit
+ * those of hs_gqa_score) and, in the same pass over the keys, the decode
+ * attention's unscaled dots logits_dev[h*logit_stride + t] ~ q32[h] .
+ * K[t][h/4] for t < tokens (q32 F32 [32][128], 16-byte aligned, the
+ * attention query).  The dots are NOT an ordered FP32 chain: each query
+ * element is split into F16 hi = f16(q) and lo = f16(q - hi) (about 22
+ * bits of q), both multiplied with the F16 keys on v_mfma_f32_4x4x4f16
+ * (products exact in FP32, sums FP32 in four accumulators of 64 products,
+ * added as (d0 + d2) + (d1 + d3)).  Error: within about 2^-19 of
+ * sum_c |q_c * k_c|, plus 2^-25 * sum_c |k_c| for query elements in the
+ * F16 subnormal range (|q| < 2^-14; below 2^-25 they count as zero).
+ * Valid range: every q32 element finite with |q| < 65504 (a larger one
+ * makes hi infinite and its dots NaN).  Logits are written with 16-byte
+ * stores when logits_dev is 16-byte aligned and logit_stride % 4 == 0,
+ * element by element otherwise.  For a layer scored at its own decode
+ * step, when both the rehearsal query and the current query are known,
+ * this replaces the K reads of hs_gqa_sparse_attention (see
+ * hs_gqa_sparse_attention_logits). */
 int hs_gqa_score_logits(const uint16_t *q_dev, const float *q32_dev, const uint16_t *keys_dev,
                         size_t key_stride_words, const int32_t *rows_dev, uint32_t pool_rows,
                         uint32_t tokens, uint16_t *scores_dev, size_t score_stride,
@@ -185,7 +196,9 @@ typedef struct {
      * head-0 score into the threshold maximum and selects over all n
      * columns.  head0_partial then covers the n - 1 history columns (the
      * scorer's tile maxima of that call).  heads must be 32; not with
-     * HS_SELECT_COVER (history only); 16-byte aligned. */
+     * HS_SELECT_COVER (history only); 16-byte aligned.  When any job of a
+     * batch completes its current token, no two jobs may share score bytes
+     * (HS_ERR_ARGUMENT): that column is written while other jobs read. */
     const uint16_t *current_q;
     const uint16_t *current_key;
 } hs_select_job_t;
@@ -340,7 +353,9 @@ int hs_gqa_gather_rows(const uint16_t *prefetched_dev,
  * Decode attention of patches/llama-b6000-external-attention-device.patch:
  * 49-66 over the selection, read straight from the hot pool (no pack; K
  * and V rows as for hs_gqa_pack, row_bytes 2048..1 MiB):
- * s = (q_h . K_id) / sqrt(128), p = softmax(s), o_h = sum p V_id.  Each
+ * s = (q_h . K_id) / sqrt(128), p = softmax(s), o_h = sum p V_id, with
+ * q_h . K_id formed on MFMA from the split query of hs_gqa_score_logits
+ * (same error bound and q range; q_dev 16-byte aligned).  Each
  * (id, KV head) row is read once for the union of its 4 query heads.
  * q_dev F32 [32][128]; member_dev from hs_gqa_select ([32][ceil(n/32)]);
  * out_dev F32 [32][128].  With row_of_id_dev, rows outside [0, pool_rows)
@@ -384,9 +399,12 @@ int hs_gqa_attention_then_count(const float *q_dev, const uint8_t *k_pool_dev,
 
 /* ---- fused layer step ----------------------------------------------------
  * One sparse decode layer: score (rehearsal q16 over the hot pool's K rows,
- * with the attention's q32.k dots in the same pass) -> select (scaled,
- * alpha, ratio; ids in ascending id order) -> sparse attention (q32) over
- * the selected V rows.  Hot pool as for hs_gqa_pack, with row_bytes 2048 (K
+ * with the attention's q32.k dots in the same pass: the split-query MFMA
+ * dots of hs_gqa_score_logits, with its error bound and its q32 range and
+ * alignment) -> select (scaled, alpha, ratio; ids in ascending id order) ->
+ * sparse attention (q32) over the selected V rows.  Every argument,
+ * including the V pool's alignment and row_bytes, is checked before
+ * anything is enqueued.  Hot pool as for hs_gqa_pack, with row_bytes 2048 (K
  * and V arrays: the scorer streams K contiguously) or 4096 (the reference's
  * KV records).  workspace: hs_decode_layer_workspace_bytes (it holds the
  * [32][n] F32 dots). */
@@ -403,8 +421,11 @@ int hs_decode_layer(const uint16_t *q16_dev, const float *q32_dev,
 /* No counterpart in the reference: hs_decode_layer for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  The same layer, same arguments but no workspace:
- * its scratch is a library-owned device array (18 MiB, one per GPU, held
- * until the process ends), so the call performs no allocation at all.
+ * its scratch is a library-owned device array (18 MiB per GPU), so the
+ * call performs no allocation at all.  The array is a __device__ variable
+ * of the library's code object: every process that loads the library holds
+ * 18 MiB of device memory on each GPU it uses, until the process ends,
+ * whether or not it ever calls this entry point.
  * n <= HS_NOALLOC_MAX_TOKENS (HS_ERR_ARGUMENT beyond it).  Every call on a
  * GPU shares that GPU's array: calls that overlap on one GPU (other streams,
  * other threads) race; order them on one stream.  The first call on a device

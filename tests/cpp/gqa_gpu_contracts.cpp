@@ -177,12 +177,12 @@ void selector_contracts() {
         }
         auto tied = select_gqa_scores(scores, H, P, P, alpha, .2f);
         check(tied.k == 3 && tied.counts[0] == 3 && tied.ids[0] == std::vector<std::uint64_t>({0, 1, 2}),
-              "threshold equality or original-ID tie order changed");
+              "a score equal to the threshold must count, ties kept lowest id first");
         scores[0] = half_bits(120.f);
         auto broadcast = select_gqa_scores(scores, H, P, P, alpha, .2f);
         const float new_threshold = half_value(half_bits(120.f - alpha));
         check(broadcast.counts[1] == std::uint32_t(100.f >= new_threshold),
-              "head0 maximum was silently replaced by per-head maxima");
+              "every head must be counted against head 0's threshold, not its own maximum");
     }
     constexpr std::size_t N = 16384;
     std::vector<std::uint16_t> rounded_scores(H * N, half_bits(-1000.f));
@@ -190,7 +190,7 @@ void selector_contracts() {
     for (float alpha : alphas) {
         auto s = select_gqa_scores(rounded_scores, H, N, N, alpha, .2f);
         check(s.k == 2048 && s.counts[0] == 2049 && s.ids[0].back() == 2047,
-              "alpha variant must retain F16 count rounding and original-ID ties");
+              "2049 hits round to an F16 count of 2048 and keep ids 0..2047, for every alpha");
     }
     // shape and parameter rejections (gqa_policy.cpp:48-49)
     rejects([&] { select_gqa_scores(score, 0, 4, 4, 1, 1); }, "zero heads");

@@ -180,3 +180,54 @@ def test_attention_then_count_rejects_overlap(hs):
     assert call(job(scores=aws)) == hs.HS_ERR_ARGUMENT      # next scores under the records
     assert call(job(), flags=hs.HS_SELECT_SCALE_RAW | hs.HS_SELECT_COUNTED) == hs.HS_ERR_ARGUMENT
     assert call(job(), out_ptr=0) == hs.HS_ERR_ARGUMENT     # attention shape checks still apply
+
+
+def test_layer_and_batch_checks_come_before_any_launch(hs):
+    """Errors found on the host are returned before anything is enqueued, so
+    no output is overwritten: on a machine without a GPU a launch would fail
+    with a HIP error instead of HS_ERR_ARGUMENT."""
+    L = hs.lib()
+    fake = ctypes.c_void_p(0x1000)
+    misaligned = ctypes.c_void_p(0x1008)
+
+    def layer(v_pool=fake, q32=fake, ids_stride=16, row_bytes=2048):
+        return L.hs_decode_layer(fake, q32, fake, v_pool, row_bytes, None, 0, 64, 1.0, 0.2, 0,
+                                 fake, fake, ids_stride, fake, fake, fake, fake, None)
+
+    assert layer(v_pool=misaligned) == hs.HS_ERR_ARGUMENT
+    assert "pools" in hs.last_error()
+    assert layer(q32=misaligned) == hs.HS_ERR_ARGUMENT  # the split query is read as float4
+    assert layer(ids_stride=11) == hs.HS_ERR_ARGUMENT  # floor(64 * 0.2f) = 12 ids per head
+    assert "ids_stride" in hs.last_error()
+    # the dots' F32 query is read 16 bytes at a time
+    assert L.hs_gqa_score_logits(fake, ctypes.c_void_p(0x1004), fake, 1024, None, 0, 64, fake, 64,
+                                 None, fake, 64, None) == hs.HS_ERR_ARGUMENT
+    # the copy-engine staging is read as 16-byte words
+    assert L.hs_kv_cold_fetch_runs(fake, 0, fake, fake, 1, misaligned, fake, 1, fake, fake, 4096,
+                                   fake, fake, None) == hs.HS_ERR_ARGUMENT
+    assert "16-byte" in hs.last_error()
+
+
+def test_batch_with_current_token_rejects_shared_scores(hs):
+    """A job that completes its current token writes column n - 1 of its
+    scores while the batch's other count groups read theirs."""
+    L = hs.lib()
+    MB = 1 << 20
+
+    def job(base, scores_at, current):
+        j = hs.SelectJob()
+        j.scores = base + scores_at
+        j.ids, j.status, j.workspace = base + 8 * MB, base + 9 * MB, base + 10 * MB
+        j.stride, j.n, j.ids_stride = 4096, 4096, 4096
+        if current:
+            j.current_q, j.current_key = base + 20 * MB, base + 21 * MB
+        return j
+
+    # (only rejected calls here: a call that passed would launch kernels on
+    # these fake addresses)
+    for first_current in (True, False):
+        jobs = (hs.SelectJob * 2)(job(0x10000000, 0, first_current),
+                                  job(0x40000000, 0, not first_current))
+        jobs[1].scores = jobs[0].scores + 64 * 1024  # inside job 0's rows
+        assert L.hs_gqa_select_batched(jobs, 2, 32, 1.0, 0.2, 0, None) == hs.HS_ERR_ARGUMENT
+        assert "share scores" in hs.last_error()

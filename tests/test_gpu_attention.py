@@ -126,3 +126,50 @@ def test_empty_head_gives_nan(hs, port):
     keep = [h for h in range(32) if h != 7]
     assert np.isfinite(out[keep]).all()
     assert rel_err(out[keep], ref[keep]) <= TOL
+
+
+def closed_form_pool(n, ln_factor_per_head):
+    """n rows; key 0 of KV head g is e_0 * c_g, key 1 zero; V rows of KV head
+    g are +(g + 1) (id 0) and -(g + 1) (id 1), all other rows zero."""
+    k = np.zeros((n, 8, 128), dtype=np.uint16)
+    v = np.zeros((n, 8, 128), dtype=np.uint16)
+    for g, c in enumerate(ln_factor_per_head):
+        k[0, g, 0] = f16_bits(float(c))
+        v[0, g, :] = f16_bits(float(g + 1))
+        v[1, g, :] = f16_bits(-float(g + 1))
+    return k, v
+
+
+@pytest.mark.parametrize("form", ["kv", "logits"])
+@pytest.mark.parametrize("case", ["ln3", "kv_head_marker"])
+def test_closed_forms(hs, port, form, case):
+    """The device attention's scale and GQA mapping pinned by closed forms,
+    not through the oracle: q.k1 - q.k2 = sqrt(128) ln 3 gives weights 3/4
+    and 1/4 (every KV head alike); with KV head g's key 0 at g sqrt(128) ln 2
+    above key 1, query head h weighs its two rows 2^(h/4) : 1 and reads the
+    values +-(h/4 + 1) of KV head h / 4 only."""
+    n = 64
+    if case == "ln3":
+        c, base = [1.0] * 8, np.log(3.0)
+    else:
+        c, base = [float(g) for g in range(8)], np.log(2.0)
+    k, v = closed_form_pool(n, c)
+    q = np.zeros((32, 128), dtype=np.float32)
+    q[:, 0] = np.float32(np.sqrt(128.0) * base)
+    ids = [np.array([0, 1])] * 32
+    member = to_dev(member_words(ids, n).reshape(-1))
+    qd = torch.from_numpy(q).cuda()
+    if form == "kv":
+        out = hs.ops.sparse_attention(qd, to_dev(pool_rows(k, v).reshape(-1)), n, member)
+    else:
+        q16 = to_dev(np.zeros(4096, dtype=np.uint16))
+        _, dots = hs.ops.score_logits(q16, qd, to_dev(k.reshape(-1)), n)
+        out = hs.ops.sparse_attention_logits(dots, to_dev(v.reshape(-1)), n, member)
+    got = out.cpu().numpy().astype(np.float64)
+    for h in range(32):
+        g = h // 4
+        w = (3.0 / 4.0) if case == "ln3" else 2.0**g / (2.0**g + 1.0)
+        expect = (g + 1) * (2.0 * w - 1.0)
+        assert np.allclose(got[h], expect, rtol=0, atol=2e-3 * (g + 1)), (h, got[h][0], expect)
+    ref = port.attention(q, pool_rows(k, v).view(np.uint8), [list(r) for r in ids])
+    assert rel_err(got, ref) <= TOL

@@ -118,3 +118,37 @@ def test_gather_rows(hs, port):
     _, _, status = hs.ops.gather_rows(torch.from_numpy(pre).cuda(), torch.from_numpy(mis).cuda(),
                                       to_dev(row_map), slots)
     assert hs.ops.read_status(status)["code"] == hs.HS_ERR_MISSING
+
+
+@pytest.mark.parametrize("queries", [1, 64])
+def test_pack_and_gather_at_layer_size(hs, port, queries):
+    """configs[2] size: N = 32768 hot rows, k = 6553 ids per head (the cap at
+    ratio 0.2), sparse_slots = 6560, with 1 and 64 query positions.  K, V and
+    the F32 mask equal the oracle byte for byte; the row-map gather over the
+    same selection (half the rows prefetched, half misses) too."""
+    n, k, slots = 32768, 6553, 6560
+    g = rng(6553 + queries)
+    payload = g.integers(0, 256, size=n * 4096, dtype=np.uint8)
+    selected = [np.sort(g.choice(n, size=k, replace=False)) for _ in range(32)]
+    qpos = sorted(g.choice(n, size=queries, replace=False).tolist())
+    qpos[-1] = n - 1
+    rows = np.arange(n, dtype=np.uint32)
+    st, kd, vd, mask = gpu_pack(hs, selected, qpos, rows, payload, slots, split=queries == 64)
+    rc, pk, pv, pmask = port.pack(selected, qpos, rows, payload, slots)
+    assert st["code"] == 0 and rc == 0
+    assert np.array_equal(kd, pk) and np.array_equal(vd, pv)
+    assert np.array_equal(mask.view(np.uint32), pmask.view(np.uint32))
+    del kd, vd, mask, pk, pv, pmask
+    # gather: even ids prefetched (row id / 2), odd ids misses (row id // 2)
+    rec = payload.reshape(n, 4096)
+    pre, mis = np.ascontiguousarray(rec[0::2]), np.ascontiguousarray(rec[1::2])
+    row_map = np.full((32, slots), -1, dtype=np.int32)
+    for h in range(32):
+        s = selected[h].astype(np.int64)
+        row_map[h, : len(s)] = np.where(s % 2 == 0, s // 2, -2 - s // 2)
+    kd, vd, status = hs.ops.gather_rows(torch.from_numpy(pre.reshape(-1)).cuda(),
+                                        torch.from_numpy(mis.reshape(-1)).cuda(),
+                                        to_dev(row_map.reshape(-1)), slots)
+    gk, gv = port.gather_rows(pre.view(np.uint16), mis.view(np.uint16), row_map.reshape(-1), slots)
+    assert hs.ops.read_status(status)["code"] == 0
+    assert np.array_equal(from_dev(kd), gk) and np.array_equal(from_dev(vd), gv)

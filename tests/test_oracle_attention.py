@@ -1,5 +1,7 @@
-"""Closed-form checks of the FP64 attention oracle (parity unpinned against
-the reference, whose attention is third-party ggml CUDA)."""
+"""Checks of the FP64 attention oracle: closed forms (one key, equal keys,
+the ln 3 two-key weights that fix the scale, a KV-head marker) and torch's
+own GQA attention in FP64.  Parity against the reference's attention
+(third-party ggml CUDA) stays unpinned."""
 import numpy as np
 
 from hs_data import f16_bits, pool_rows, rng
@@ -56,3 +58,67 @@ def test_row_map_and_numpy_softmax(port):
         p = np.exp(s - s.max())
         p /= p.sum()
         assert np.allclose(a[h], p @ vf[ids[h], h // 4], rtol=1e-10, atol=1e-12)
+
+
+def test_two_keys_ln3_gives_three_to_one(port):
+    """Closed form that fixes the scale: with q.k1 - q.k2 = sqrt(128) ln 3 the
+    softmax weights are exactly 3/4 and 1/4.  A missing or wrong 1/sqrt(128)
+    (1/128, 1/sqrt(64), none) moves them far from that."""
+    k = np.zeros((2, 8, 128), dtype=np.uint16)
+    v = np.zeros((2, 8, 128), dtype=np.uint16)
+    k[0, :, 0] = f16_bits(1.0)  # key 0 of every KV head: e_0; key 1: zero
+    v[0, :, :] = f16_bits(4.0)
+    v[1, :, :] = f16_bits(-4.0)
+    pool = pool_rows(k, v).view(np.uint8)
+    q = np.zeros((32, 128), dtype=np.float32)
+    q[:, 0] = np.float32(np.sqrt(128.0) * np.log(3.0))
+    out = port.attention(q, pool, [[0, 1]] * 32)
+    # 3/4 * 4 + 1/4 * (-4) = 2, up to the F32 rounding of q (relative 6e-8)
+    assert np.allclose(out, 2.0, rtol=0, atol=1e-6)
+
+
+def test_kv_head_marker(port):
+    """Query head h reads KV head h // 4 for both K and V: KV head g's key 0
+    scores g ln 2 above its key 1 (so weights 2^g : 1), and its V rows carry g.
+    A mapping h % 8 or h // 8 gives other weights and values."""
+    k = np.zeros((2, 8, 128), dtype=np.uint16)
+    v = np.zeros((2, 8, 128), dtype=np.uint16)
+    for g in range(8):
+        k[0, g, 0] = f16_bits(float(g))
+        v[0, g, :] = f16_bits(float(g + 1))
+        v[1, g, :] = f16_bits(-float(g + 1))
+    pool = pool_rows(k, v).view(np.uint8)
+    q = np.zeros((32, 128), dtype=np.float32)
+    q[:, 0] = np.float32(np.sqrt(128.0) * np.log(2.0))
+    out = port.attention(q, pool, [[0, 1]] * 32)
+    for h in range(32):
+        g = h // 4
+        w = 2.0**g / (2.0**g + 1.0)
+        expect = (g + 1) * (2.0 * w - 1.0)
+        assert np.allclose(out[h], expect, rtol=0, atol=1e-6), (h, out[h][0], expect)
+
+
+def test_matches_torch_gqa_attention(port):
+    """FP64 against torch's scaled_dot_product_attention on the CPU, which
+    states the scale (1/sqrt(E)) and the GQA head mapping (enable_gqa: query
+    head h uses KV head h // (32 / 8)) independently of the oracle.  Each
+    query head's selection is a boolean mask over the union of ids."""
+    import torch
+
+    g = rng(11)
+    n = 400
+    k, v, pool = make_pool(g, n)
+    q = (3.0 * g.standard_normal((32, 128))).astype(np.float32)
+    ids = [sorted(g.choice(n, size=int(g.integers(1, 120)), replace=False).tolist())
+           for _ in range(32)]
+    got = port.attention(q, pool, ids)
+    kf = torch.from_numpy(k.view(np.float16).astype(np.float64)).permute(1, 0, 2)[None]
+    vf = torch.from_numpy(v.view(np.float16).astype(np.float64)).permute(1, 0, 2)[None]
+    qf = torch.from_numpy(q.astype(np.float64))[None, :, None, :]
+    mask = torch.zeros((1, 32, 1, n), dtype=torch.bool)
+    for h in range(32):
+        mask[0, h, 0, ids[h]] = True
+    ref = torch.nn.functional.scaled_dot_product_attention(qf, kf, vf, attn_mask=mask,
+                                                           enable_gqa=True)
+    ref = ref[0, :, 0, :].numpy()
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)

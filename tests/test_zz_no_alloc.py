@@ -74,3 +74,56 @@ def test_noalloc_refuses_beyond_its_array(hs):
     o = _outputs(n, int(np.floor(n * np.float32(RATIO))))
     assert _call(hs, d, o, True) == hs.HS_ERR_ARGUMENT
     assert "HS_NOALLOC_MAX_TOKENS" in hs.last_error()
+
+
+def test_noalloc_allocates_nothing(hs):
+    """The contract itself: after the first call on the device (which only
+    looks up the array's address), calls change no device memory in use."""
+    n = 4096
+    d = _layer(n, 903)
+    kmax = int(np.floor(n * np.float32(RATIO)))
+    o = _outputs(n, kmax)
+    assert _call(hs, d, o, True) == 0
+    torch.cuda.synchronize()
+    free_before = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        assert _call(hs, d, o, True) == 0
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free_before
+    assert hs.ops.read_status(o["status"])["code"] == 0
+
+
+def test_noalloc_graph_replays_equal_eager(hs):
+    """hs_decode_layer_noalloc captured in a HIP graph (torch.cuda.graph) and
+    replayed on new inputs copied into the captured buffers by eager work
+    between replays: every replay equals an eager hs_decode_layer (caller
+    workspace) on the same inputs, bit for bit."""
+    n = 4096
+    kmax = int(np.floor(n * np.float32(RATIO)))
+    d = _layer(n, 910)
+    got = _outputs(n, kmax)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert _call(hs, d, got, True) == 0  # first call on the device: address lookup
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            rc = _call(hs, d, got, True)
+        assert rc == 0
+        torch.cuda.synchronize()
+    for seed in (911, 912, 913):
+        fresh = _layer(n, seed)
+        for key in ("q16", "q32", "kpool", "vpool"):
+            d[key].copy_(fresh[key])
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _outputs(n, kmax)
+        assert _call(hs, fresh, want, False) == 0
+        torch.cuda.synchronize()
+        assert hs.ops.read_status(got["status"])["code"] == 0
+        for name in ("scores", "ids", "counts", "out", "status"):
+            a, b = got[name], want[name]
+            if name == "out":
+                a, b = a.view(torch.int32), b.view(torch.int32)
+            assert torch.equal(a, b), (seed, name)
