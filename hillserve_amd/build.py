@@ -52,7 +52,7 @@ DEVICE = [
 
 HIP_SOURCES = ["score.hip", "select.hip", "attention.hip", "pack.hip", "rehearsal.hip",
                "kv_store.hip", "runtime.hip"]
-HOST_SOURCES = ["gqa_gpu.cpp"]
+HOST_SOURCES = ["gqa_gpu.cpp", "host_common.cpp", "kv_image.cpp"]
 
 
 def _run(cmd: list[str]) -> None:

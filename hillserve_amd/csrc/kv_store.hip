@@ -36,14 +36,11 @@
 
 #include "hs_device.hpp"
 #include "hs_internal.hpp"
+#include "kv_format.hpp"
 
 namespace hs {
 namespace {
 
-constexpr uint64_t kMagic = 0x48534b5653454731ull;
-constexpr uint64_t kFnvSeed = 14695981039346656037ull, kFnvPrime = 1099511628211ull;
-constexpr uint32_t kRow = 4096, kHeader = 32, kStride = kRow + kHeader;
-constexpr uint32_t kMaxLayers = 128, kMaxPositions = 66048;  // segmented_store.cpp:31
 constexpr uint32_t kPad = 0xffffffffu;  // a position list's padding entry: no record
 constexpr uint32_t kPadFlag = 4u;
 // Workgroups (4 waves each) of a copy over the host link: 96 records of
@@ -51,24 +48,6 @@ constexpr uint32_t kPadFlag = 4u;
 // while the CUs left free run the main stream's attention within 2x of its
 // speed alone (one wave per record over the whole chip: 7x).
 constexpr uint32_t kLinkBlocks = 24;
-
-uint64_t extent_of(uint32_t layers, uint32_t capacity) {
-    return (4096ull + uint64_t(layers) * capacity * kStride + 4095) / 4096 * 4096;
-}
-uint64_t record_offset(uint32_t layer, uint32_t capacity, uint32_t position) {
-    return 4096ull + (uint64_t(layer) * capacity + position) * kStride;
-}
-uint64_t fnv1a(const uint8_t* p, size_t n) {
-    uint64_t h = kFnvSeed;
-    for (size_t i = 0; i < n; ++i) h = (h ^ p[i]) * kFnvPrime;
-    return h;
-}
-
-struct RecordHeader {
-    uint64_t digest, position, request;
-    uint32_t layer, version;
-};
-static_assert(sizeof(RecordHeader) == kHeader, "32-byte record header");
 
 // Record i (position positions[i]) into its staging row: copy, header identity.
 template <bool kStaged>
@@ -351,43 +330,6 @@ int hs_gqa_cold_plan(const uint32_t* member_dev, uint32_t heads, uint32_t n,
     hs::clear_error();
     return hs::launch_cold_plan(member_dev, heads, n, slot_dev, staging_base, list_size,
                                 positions_dev, rows_dev, count_dev, hs::as_stream(stream));
-}
-
-uint64_t hs_kv_store_bytes(uint32_t layers, uint32_t capacity) {
-    if (layers == 0 || layers > hs::kMaxLayers || capacity == 0 || capacity > hs::kMaxPositions)
-        return 0;
-    return hs::extent_of(layers, capacity);
-}
-
-int hs_kv_store_init(void* image, uint64_t request, uint32_t layers, uint32_t capacity) {
-    hs::clear_error();
-    if (!image) return hs::reject("kv store: null image");
-    const uint64_t extent = hs_kv_store_bytes(layers, capacity);
-    if (!extent) return hs::reject("bounded segmented geometry/quota");
-    std::memset(image, 0, extent);
-    uint64_t h[8] = {hs::kMagic, 1, request, layers, capacity, hs::kRow, hs::kStride, extent};
-    std::memcpy(image, h, sizeof h);
-    return HS_OK;
-}
-
-int hs_kv_store_append(void* image, uint32_t layer, uint32_t first, const uint8_t* rows,
-                       uint32_t count) {
-    hs::clear_error();
-    if (!image || !rows || count == 0) return hs::reject("kv store: null image/rows or count 0");
-    uint64_t h[8];
-    std::memcpy(h, image, sizeof h);
-    if (h[0] != hs::kMagic || h[1] != 1) return hs::reject("kv store: not a v1 image");
-    if (layer >= h[3] || first > h[4] || count > h[4] - first)
-        return hs::reject("append capacity");
-    auto* base = static_cast<uint8_t*>(image);
-    for (uint32_t i = 0; i < count; ++i) {
-        const uint8_t* row = rows + uint64_t(i) * hs::kRow;
-        hs::RecordHeader hdr{hs::fnv1a(row, hs::kRow), uint64_t(first) + i, h[2], layer, 1};
-        uint8_t* rec = base + hs::record_offset(layer, static_cast<uint32_t>(h[4]), first + i);
-        std::memcpy(rec, &hdr, sizeof hdr);
-        std::memcpy(rec + hs::kHeader, row, hs::kRow);
-    }
-    return HS_OK;
 }
 
 size_t hs_kv_cold_fetch_workspace_bytes(uint32_t count) {

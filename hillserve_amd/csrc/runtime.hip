@@ -16,37 +16,6 @@
 namespace hs {
 
 namespace {
-thread_local std::string g_last_error;
-std::array<std::atomic<int>, 64> g_cu_count{};
-}  // namespace
-
-void set_error(const std::string& message) { g_last_error = message; }
-void clear_error() { g_last_error.clear(); }
-
-int reject(const char* message) {
-    g_last_error = message;
-    return HS_ERR_ARGUMENT;
-}
-
-int hip_fail(hipError_t status, const char* what) {
-    g_last_error = std::string(what) + ": " + hipGetErrorString(status);
-    return HS_ERR_HIP;
-}
-
-int device_cu_count() {
-    int device = 0;
-    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
-    int cached = g_cu_count[device].load(std::memory_order_relaxed);
-    if (cached > 0) return cached;
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
-        cus <= 0)
-        cus = 256;
-    g_cu_count[device].store(cus, std::memory_order_relaxed);
-    return cus;
-}
-
-namespace {
 
 // ---- fused decode layer ------------------------------------------------------
 
@@ -226,8 +195,6 @@ int decode_layer(const uint16_t* q16_dev, const float* q32_dev, const uint8_t* k
 
 extern "C" {
 
-const char* hs_version(void) { return "hillserve_amd 0.1 gfx950"; }
-const char* hs_last_error(void) { return hs::g_last_error.c_str(); }
 
 size_t hs_decode_layer_workspace_bytes(uint32_t n) { return hs::plan_layer(n ? n : 1).total; }
 

@@ -12,6 +12,7 @@ CPU baseline).  The product package ``hillserve_amd`` never imports it.
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from pathlib import Path
 
@@ -345,9 +346,12 @@ _ref = None
 
 
 def port() -> Port:
+    """The restatement; HS_ORACLE_LIB names another build of hs_oracle.c (the
+    sanitizer test runs the oracle tests against an ASan + UBSan build)."""
     global _port
     if _port is None:
-        _port = Port()
+        alt = os.environ.get("HS_ORACLE_LIB")
+        _port = Port(alt) if alt else Port()
     return _port
 
 

@@ -5,7 +5,8 @@
 //   scorer    tests/full_gqa_cpu_tests.cpp:19-121
 //   kernel    tests/full_gqa_kernel_check.cpp:31-37,70-139 (V2/V3 ABI)
 //   pack      tests/gqa_pack_tests.cpp:6-38
-// Exit status: 0 passed, 1 failed, 77 no GPU visible (nothing run).
+// Exit status: 0 passed, 1 failed, 77 no GPU visible (only the host-only
+// contracts ran: the stream planner and the KV image writer).
 #include <hip/hip_runtime_api.h>
 
 #include <fcntl.h>
@@ -796,9 +797,63 @@ void pipeline_contracts() {
     check(from_dev<std::uint32_t>(counts1, H) == from_dev<std::uint32_t>(counts2, H), "counts equal");
 }
 
+// The SegmentedKVStore v1 image writer (hs_kv_store_*; host only): header
+// page, record placement and headers, FNV-1a 64 digests (the test's own
+// byte loop, pinned by the published vectors of the empty string and "a"),
+// and the bounds rejections of storage/segmented_store.cpp:31.
+std::uint64_t fnv1a64(const std::uint8_t* p, std::size_t n) {
+    std::uint64_t h = 0xcbf29ce484222325ull;
+    for (std::size_t i = 0; i < n; ++i) h = (h ^ p[i]) * 0x100000001b3ull;
+    return h;
+}
+void kv_image_contracts() {
+    const std::uint8_t a = 'a';
+    check(fnv1a64(nullptr, 0) == 0xcbf29ce484222325ull && fnv1a64(&a, 1) == 0xaf63dc4c8601ec8cull,
+          "FNV-1a 64 published vectors");
+    check(hs_kv_store_bytes(0, 64) == 0 && hs_kv_store_bytes(129, 64) == 0 &&
+              hs_kv_store_bytes(2, 0) == 0 && hs_kv_store_bytes(2, 66049) == 0,
+          "image geometry bounds");
+    const std::uint32_t layers = 3, capacity = 70;
+    const std::uint64_t bytes = hs_kv_store_bytes(layers, capacity);
+    check(bytes == (4096ull + std::uint64_t(layers) * capacity * 4128 + 4095) / 4096 * 4096,
+          "image extent: header page plus records, rounded to pages");
+    std::vector<std::uint8_t> image(bytes, 0xee);
+    check(hs_kv_store_init(image.data(), 77, layers, capacity) == HS_OK, "image init");
+    std::uint64_t h[8];
+    std::memcpy(h, image.data(), sizeof h);
+    check(h[0] == 0x48534b5653454731ull && h[1] == 1 && h[2] == 77 && h[3] == layers &&
+              h[4] == capacity && h[5] == 4096 && h[6] == 4128 && h[7] == bytes,
+          "header page words");
+    check(std::all_of(image.begin() + 64, image.end(), [](std::uint8_t b) { return b == 0; }),
+          "the rest of the image starts zeroed");
+    std::mt19937 gen(4128);
+    const std::uint32_t first = 60, count = 10;
+    std::vector<std::uint8_t> rows(std::size_t(count) * 4096);
+    for (auto& b : rows) b = static_cast<std::uint8_t>(gen());
+    check(hs_kv_store_append(image.data(), 2, first, rows.data(), count) == HS_OK, "append");
+    for (std::uint32_t i = 0; i < count; ++i) {
+        const std::uint8_t* rec = image.data() + 4096 + (std::uint64_t(2) * capacity + first + i) * 4128;
+        std::uint64_t w[3];
+        std::uint32_t lv[2];
+        std::memcpy(w, rec, sizeof w);
+        std::memcpy(lv, rec + 24, sizeof lv);
+        const std::uint8_t* row = rows.data() + std::size_t(i) * 4096;
+        check(w[0] == fnv1a64(row, 4096) && w[1] == first + i && w[2] == 77 && lv[0] == 2 && lv[1] == 1,
+              "record header {digest, position, request, layer, version}");
+        check(std::memcmp(rec + 32, row, 4096) == 0, "record payload");
+    }
+    check(hs_kv_store_append(image.data(), 3, 0, rows.data(), 1) == HS_ERR_ARGUMENT, "layer bound");
+    check(hs_kv_store_append(image.data(), 0, 61, rows.data(), 10) == HS_ERR_ARGUMENT,
+          "append past the capacity");
+    check(hs_kv_store_append(image.data(), 0, 0, nullptr, 1) == HS_ERR_ARGUMENT, "null rows");
+    check(hs_kv_store_init(nullptr, 0, 1, 1) == HS_ERR_ARGUMENT, "null image");
+}
+
 int main() {
     try {
-        stream_layout_contracts();  // host-only contracts run with or without a GPU
+        // host-only contracts run with or without a GPU
+        stream_layout_contracts();
+        kv_image_contracts();
     } catch (const std::exception& e) {
         std::cerr << e.what() << std::endl;
         return 1;

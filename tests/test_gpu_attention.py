@@ -171,5 +171,6 @@ def test_closed_forms(hs, port, form, case):
         w = (3.0 / 4.0) if case == "ln3" else 2.0**g / (2.0**g + 1.0)
         expect = (g + 1) * (2.0 * w - 1.0)
         assert np.allclose(got[h], expect, rtol=0, atol=2e-3 * (g + 1)), (h, got[h][0], expect)
+    # (KV head 0's marker output is exactly zero: compare element-wise)
     ref = port.attention(q, pool_rows(k, v).view(np.uint8), [list(r) for r in ids])
-    assert rel_err(got, ref) <= TOL
+    assert np.allclose(got, ref, rtol=TOL, atol=1e-5)
