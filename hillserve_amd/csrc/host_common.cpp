@@ -41,6 +41,11 @@ int device_cu_count() {
     return cus;
 }
 
+uint32_t next_stamp() {
+    static std::atomic<uint32_t> calls{0};
+    return (calls.fetch_add(1, std::memory_order_relaxed) & 0x7fffffffu) | 0x80000000u;
+}
+
 }  // namespace hs
 
 extern "C" {

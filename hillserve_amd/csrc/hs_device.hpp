@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "hs_gpu.h"
+
 namespace hs {
 
 // binary16 <-> binary32 through the hardware converters.  v_cvt_f32_f16 is
@@ -156,6 +158,36 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
     const uint32_t lane = __lane_id();
     const uint64_t below = lane ? (mask & ((~0ull) >> (64 - lane))) : 0ull;
     return static_cast<uint32_t>(__popcll(below));
+}
+
+// Status of a launch that no earlier kernel cleared (pack, gather, the
+// rehearsal query).  The host gives every call a distinct stamp with the
+// top bit set (next_stamp; a selection's k never has it).  The 8-byte word
+// (k << 32) | code of a status is claimed for the call by the first
+// workgroup that writes it: a word carrying another stamp is stale and is
+// replaced.  Within the call a code is only raised in rank (HS_OK, then any
+// error, HS_ERR_NONFINITE above the others), so the first error of the
+// highest rank wins; an anchor workgroup stamps HS_OK when no error came.
+// Only the anchor and the workgroups holding an error touch the word, each
+// retrying only when another changed it, so no workgroup waits on another.
+// The status must be 8-byte aligned (checked by the host).
+__device__ __forceinline__ uint32_t status_rank(int code) {
+    return code == HS_OK ? 0u : (code == HS_ERR_NONFINITE ? 2u : 1u);
+}
+__device__ inline void publish_stamped(hs_status_t* status, uint32_t stamp, int err, bool anchor) {
+    if (err == HS_OK && !anchor) return;
+    auto* word = reinterpret_cast<unsigned long long*>(status);
+    unsigned long long old = 0;
+    for (;;) {
+        const bool ours = static_cast<uint32_t>(old >> 32) == stamp;
+        const int code = static_cast<int>(static_cast<uint32_t>(old));
+        if (ours && status_rank(err) <= status_rank(code)) return;
+        const unsigned long long want =
+            (static_cast<unsigned long long>(stamp) << 32) | static_cast<uint32_t>(err);
+        const unsigned long long seen = atomicCAS(word, old, want);
+        if (seen == old) return;
+        old = seen;
+    }
 }
 
 }  // namespace hs

@@ -21,6 +21,9 @@ int hip_fail(hipError_t status, const char* what);
 
 // Compute units of the current device (cached per device ordinal).
 int device_cu_count();
+// A fresh status stamp per call (publish_stamped): distinct for 2^31 calls,
+// top bit set.
+uint32_t next_stamp();
 
 inline hipStream_t as_stream(void* stream) { return static_cast<hipStream_t>(stream); }
 

@@ -118,26 +118,56 @@ cold_digest_kernel(const uint8_t* k_rows, uint32_t row_bytes, int64_t v_delta,
     if (i >= count || (flags[i] & kPadFlag)) return;
     const uint8_t* k = k_rows + uint64_t(i) * row_bytes;
     uint64_t h = kFnvSeed;
-    for (uint32_t c = 0; c < kRow / 16; ++c) {
-        const uint4 w = *reinterpret_cast<const uint4*>(k + (c < 128 ? 0 : v_delta - 2048) + c * 16);
-        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    // 128 B per step, the next step's loads requested before this step's
+    // bytes are hashed (the hash chain is sequential; the loads need not be)
+    constexpr uint32_t kStep = 8;  // 16 B words per step
+    auto chunk = [&](uint32_t c) {
+        return reinterpret_cast<const uint4*>(k + (c < 128 ? 0 : v_delta - 2048) + c * 16);
+    };
+    uint4 cur[kStep], nxt[kStep];
 #pragma unroll
-        for (uint32_t k = 0; k < 4; ++k)
+    for (uint32_t u = 0; u < kStep; ++u) cur[u] = *chunk(u);
+    for (uint32_t c0 = 0; c0 < kRow / 16; c0 += kStep) {
+        const uint32_t c1 = c0 + kStep < kRow / 16 ? c0 + kStep : c0;  // last step re-reads its own
 #pragma unroll
-            for (uint32_t b = 0; b < 4; ++b) h = (h ^ ((words[k] >> (8 * b)) & 0xffu)) * kFnvPrime;
+        for (uint32_t u = 0; u < kStep; ++u) nxt[u] = *chunk(c1 + u);
+#pragma unroll
+        for (uint32_t u = 0; u < kStep; ++u) {
+            const uint32_t words[4] = {cur[u].x, cur[u].y, cur[u].z, cur[u].w};
+#pragma unroll
+            for (uint32_t w = 0; w < 4; ++w)
+#pragma unroll
+                for (uint32_t b = 0; b < 4; ++b) h = (h ^ ((words[w] >> (8 * b)) & 0xffu)) * kFnvPrime;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kStep; ++u) cur[u] = nxt[u];
     }
     if (h != digests[i]) flags[i] |= 2u;
 }
 
 // Status: code HS_ERR_CORRUPT when any record failed, k = failed records.
-__global__ void __launch_bounds__(256)
+// Each thread's flags are read 16 at a time, all requested before any is
+// tested (a loop of single loads waits one round trip per flag).
+constexpr uint32_t kStatusThreads = 1024, kStatusBatch = 16;
+__global__ void __launch_bounds__(kStatusThreads)
 cold_status_kernel(const uint32_t* __restrict__ flags, uint32_t count, hs_status_t* status) {
     __shared__ uint32_t bad;
     if (threadIdx.x == 0) bad = 0;
     __syncthreads();
     uint32_t mine = 0;
-    for (uint32_t i = threadIdx.x; i < count; i += 256) mine += (flags[i] & 3u) ? 1u : 0u;
-    if (mine) atomicAdd(&bad, mine);
+    for (uint32_t base = 0; base < count; base += kStatusThreads * kStatusBatch) {
+        uint32_t f[kStatusBatch];
+#pragma unroll
+        for (uint32_t u = 0; u < kStatusBatch; ++u) {
+            const uint32_t i = base + threadIdx.x + u * kStatusThreads;
+            f[u] = flags[i < count ? i : count - 1u];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kStatusBatch; ++u)
+            mine += base + threadIdx.x + u * kStatusThreads < count && (f[u] & 3u) ? 1u : 0u;
+    }
+    mine = wave_sum_u32(mine);
+    if ((threadIdx.x & 63u) == 0 && mine) atomicAdd(&bad, mine);
     __syncthreads();
     if (threadIdx.x == 0) {
         hs_status_t s{};
@@ -147,64 +177,94 @@ cold_status_kernel(const uint32_t* __restrict__ flags, uint32_t count, hs_status
     }
 }
 
-// Cold plan of one sequence (n <= 32768, one 1024-thread workgroup, one
-// membership word per thread): the tokens selected by any head whose row is
-// cold, ascending, padded with kPad to `list_size`; the row map of every
-// token (its hot-pool slot, staging_base + its cold-list index, or -1 for a
-// cold token nobody selected); and the cold count.
-__global__ void __launch_bounds__(1024)
+// Cold plan of one sequence (n <= 32768, one 1024-thread workgroup): the
+// tokens selected by any head whose row is cold, ascending, padded with kPad
+// to `list_size`; the row map of every token (its hot-pool slot,
+// staging_base + its cold-list index, or -1 for a cold token nobody
+// selected); and the cold count.
+// Every load is issued before any is used: thread t ORs the heads'
+// membership words t (32 heads per batch of loads) and reads the slots of
+// tokens t + 1024 j, j < 32 (each instruction one contiguous 256 B run);
+// ballots over `slot < 0` turn those into cold words in LDS.  One block scan
+// of the per-word counts of selected cold tokens gives each word's first
+// list index; the row map and the list are then written in the same
+// coalesced token order.
+constexpr uint32_t kPlanThreads = 1024, kPlanRuns = 32768 / kPlanThreads;
+__global__ void __launch_bounds__(kPlanThreads)
 cold_plan_kernel(const uint32_t* __restrict__ member, uint32_t heads, uint32_t n,
                  const int32_t* __restrict__ slot, uint32_t staging_base, uint32_t list_size,
                  uint32_t* __restrict__ positions, int32_t* __restrict__ rows,
                  uint32_t* __restrict__ count_out) {
-    __shared__ uint32_t wsum[16];
+    __shared__ uint32_t cold_word[1024], take_word[1024], first_at[1024];
+    __shared__ uint32_t wsum[kPlanThreads / 64];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t words = (n + 31) / 32;
-    uint32_t any = 0, cold = 0;
-    if (tid < words) {
-        for (uint32_t h = 0; h < heads; ++h) any |= member[static_cast<size_t>(h) * words + tid];
-#pragma unroll 4
-        for (uint32_t j = 0; j < 32; ++j) {
-            const uint32_t p = tid * 32 + j;
-            if (p < n && slot[p] < 0) cold |= 1u << j;
+    const uint32_t wi = tid < words ? tid : words - 1u;
+    int32_t sv[kPlanRuns];
+#pragma unroll
+    for (uint32_t j = 0; j < kPlanRuns; ++j) {
+        const uint32_t p = tid + kPlanThreads * j;
+        sv[j] = slot[p < n ? p : n - 1u];
+    }
+    uint32_t any = 0;
+    for (uint32_t h0 = 0; h0 < heads; h0 += 32) {  // 32 heads' loads in flight at a time
+        uint32_t mw[32];
+#pragma unroll
+        for (uint32_t u = 0; u < 32; ++u) {
+            const uint32_t h = h0 + u < heads ? h0 + u : heads - 1u;
+            mw[u] = member[static_cast<size_t>(h) * words + wi];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 32; ++u) any |= mw[u];
+    }
+    if (tid >= words) any = 0;
+    // cold bits of tokens 1024 j + 64 wave + lane: words 32 j + 2 wave (+1)
+#pragma unroll
+    for (uint32_t j = 0; j < kPlanRuns; ++j) {
+        const uint32_t p = tid + kPlanThreads * j;
+        const uint64_t cold = __ballot(p < n && sv[j] < 0);
+        if (lane == 0) {
+            cold_word[32 * j + 2 * wave] = static_cast<uint32_t>(cold);
+            cold_word[32 * j + 2 * wave + 1] = static_cast<uint32_t>(cold >> 32);
         }
     }
-    const uint32_t take = any & cold;
-    // exclusive scan of the per-thread counts
+    __syncthreads();
+    const uint32_t take = any & cold_word[tid];
     const uint32_t c = static_cast<uint32_t>(__popc(take));
-    uint32_t x = c;
-#pragma unroll
-    for (uint32_t off = 1; off < 64; off <<= 1) {
-        const uint32_t y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
-    }
+    const uint32_t x = wave_inclusive_sum_u32(c);
     if (lane == 63) wsum[wave] = x;
+    take_word[tid] = take;
     __syncthreads();
     uint32_t before = 0, total = 0;
 #pragma unroll
-    for (uint32_t w = 0; w < 16; ++w) {
+    for (uint32_t w = 0; w < kPlanThreads / 64; ++w) {
         before += w < wave ? wsum[w] : 0u;
         total += wsum[w];
     }
-    uint32_t at = before + x - c;
-    if (tid < words) {
-        for (uint32_t j = 0; j < 32; ++j) {
-            const uint32_t p = tid * 32 + j;
-            if (p >= n) break;
-            if (!((cold >> j) & 1u)) {
-                rows[p] = slot[p];
-            } else if ((take >> j) & 1u) {
+    first_at[tid] = before + x - c;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t j = 0; j < kPlanRuns; ++j) {
+        const uint32_t p = tid + kPlanThreads * j;
+        if (p >= n) break;
+        const uint32_t w = p >> 5, b = p & 31u;
+        const uint32_t tw = take_word[w];
+        int32_t r = sv[j];
+        if (r < 0) {
+            r = -1;
+            if ((tw >> b) & 1u) {
                 // a list shorter than the cold count drops the excess (the
                 // count tells the caller); no write goes past list_size
-                if (at < list_size) positions[at] = p;
-                rows[p] = at < list_size ? static_cast<int32_t>(staging_base + at) : -1;
-                ++at;
-            } else {
-                rows[p] = -1;
+                const uint32_t at = first_at[w] + static_cast<uint32_t>(__popc(tw & ((1u << b) - 1u)));
+                if (at < list_size) {
+                    positions[at] = p;
+                    r = static_cast<int32_t>(staging_base + at);
+                }
             }
         }
+        rows[p] = r;
     }
-    for (uint32_t i = total + tid; i < list_size; i += 1024) positions[i] = kPad;
+    for (uint32_t i = total + tid; i < list_size; i += kPlanThreads) positions[i] = kPad;
     if (tid == 0) *count_out = total;
 }
 
@@ -255,7 +315,7 @@ int launch_cold_checks(const uint8_t* records, uint32_t layer, const uint64_t (&
                        static_cast<uint32_t>(row_bytes), v_delta, digests, flags);
     hipLaunchKernelGGL(cold_digest_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, k_out,
                        static_cast<uint32_t>(row_bytes), v_delta, digests, count, flags);
-    hipLaunchKernelGGL(cold_status_kernel, dim3(1), dim3(256), 0, stream, flags, count, status);
+    hipLaunchKernelGGL(cold_status_kernel, dim3(1), dim3(kStatusThreads), 0, stream, flags, count, status);
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "cold fetch launch");
 }

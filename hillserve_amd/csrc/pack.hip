@@ -132,35 +132,37 @@ template <bool kPack>
 __global__ void __launch_bounds__(256)
 pack_kernel(PoolSource ps, MapSource ms, const uint64_t* __restrict__ positions, uint32_t nq,
             uint32_t count, uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out,
-            float* __restrict__ mask, hs_status_t* __restrict__ status) {
+            float* __restrict__ mask, hs_status_t* __restrict__ status, uint32_t stamp) {
     __shared__ uint4 vtile[64][17];  // 64 slots x 256 B V half row (+pad)
     __shared__ const uint8_t* src_row[64];
     __shared__ uint32_t slot_id[64], slot_ok[64];
     const uint32_t h = blockIdx.y, kv = h >> 2, s0 = blockIdx.x * 64, tid = threadIdx.x;
 
-    if (tid < 64) {
+    if (tid < 64) {  // wave 0
         const uint32_t s = s0 + tid;
         const uint8_t* src = nullptr;
         uint32_t id = 0xffffffffu;
+        int err = HS_OK;  // this lane's first error
+        auto fail = [&](int code) { err = err != HS_OK ? err : code; };
         // gqa_pack.hpp:29: positions.back() < 66048; ids beyond it are future.
         uint64_t extent = 0;
         if (kPack) {
             const uint64_t last = positions[nq - 1];
-            if (last >= kMaxVisible) raise(status, HS_ERR_ARGUMENT);
+            if (last >= kMaxVisible) fail(HS_ERR_ARGUMENT);
             else extent = last + 1;
         }
         if (s < count) {
             if (kPack) {
                 const uint32_t len = ps.lens[h];
                 if (len == 0 || len > count) {
-                    raise(status, HS_ERR_ARGUMENT);
+                    fail(HS_ERR_ARGUMENT);
                 } else if (s < len) {
                     id = ps.ids[static_cast<size_t>(h) * ps.ids_stride + s];
                     int32_t row = -1;
                     if (id < extent && id < ps.max_id)
                         row = ps.row_of_id ? ps.row_of_id[id] : static_cast<int32_t>(id);
                     if (row < 0 || static_cast<uint32_t>(row) >= ps.pool_rows) {
-                        raise(status, HS_ERR_MISSING);
+                        fail(HS_ERR_MISSING);
                         id = 0xffffffffu;
                     } else {
                         src = ps.pool + static_cast<size_t>(row) * ps.row_bytes;
@@ -176,7 +178,7 @@ pack_kernel(PoolSource ps, MapSource ms, const uint64_t* __restrict__ positions,
                     src = reinterpret_cast<const uint8_t*>(ms.misses) +
                           static_cast<size_t>(miss) * 4096;
                 else if (row != -1)  // gqa_prefetch_cuda.cu:69 refuses rows beyond the payload
-                    raise(status, HS_ERR_MISSING);
+                    fail(HS_ERR_MISSING);
             }
         }
         // a slot with no row reads the fallback row (discarded) so that every
@@ -184,6 +186,10 @@ pack_kernel(PoolSource ps, MapSource ms, const uint64_t* __restrict__ positions,
         src_row[tid] = src ? src : fallback_row(ps, ms, kPack);
         slot_ok[tid] = src != nullptr;
         slot_id[tid] = id;
+        // the workgroup's first error (lowest slot), published by lane 0
+        const uint64_t failing = __ballot(err != HS_OK);
+        const int first = failing ? __shfl(err, __ffsll(static_cast<long long>(failing)) - 1) : HS_OK;
+        if (tid == 0) publish_stamped(status, stamp, first, blockIdx.x == 0 && blockIdx.y == 0);
     }
     __syncthreads();
     // K rows: 64 slots x 16 x 16 B; V half rows staged for the transpose.
@@ -316,6 +322,8 @@ int hs_gqa_pack(const uint8_t* k_pool_dev, const uint8_t* v_pool_dev, size_t row
     if (!k_pool_dev || !v_pool_dev || !ids_dev || !lens_dev || !positions_dev || !k_dev ||
         !v_dev || !mask_dev || !status_dev)
         return hs::reject("GQA packing: null pointer");
+    if (reinterpret_cast<uintptr_t>(status_dev) & 7u)
+        return hs::reject("GQA packing: status must be 8-byte aligned");
     if (nq == 0 || nq > 256 || count == 0 || count > hs::kMaxVisible)
         return hs::reject("GQA packing shape");
     if (ids_stride > 0xffffffffu) return hs::reject("GQA packing: ids_stride too large");
@@ -329,11 +337,10 @@ int hs_gqa_pack(const uint8_t* k_pool_dev, const uint8_t* v_pool_dev, size_t row
         reinterpret_cast<intptr_t>(v_pool_dev) - reinterpret_cast<intptr_t>(k_pool_dev);
     hs::PoolSource ps{k_pool_dev, pool_rows, static_cast<uint32_t>(row_bytes), v_delta,
                       row_of_id_dev, max_id, ids_dev, lens_dev, static_cast<uint32_t>(ids_stride)};
-    hipLaunchKernelGGL(hs::fill_u32_kernel, dim3(1), dim3(256), 0, s,
-                       reinterpret_cast<uint32_t*>(status_dev), 4u, 0u);
     hs::MapSource ms{nullptr, nullptr, nullptr};
     hipLaunchKernelGGL(hs::pack_kernel<true>, dim3((count + 63) / 64, 32), dim3(256), 0, s, ps, ms,
-                       positions_dev, nq, count, k_dev, v_dev, mask_dev, status_dev);
+                       positions_dev, nq, count, k_dev, v_dev, mask_dev, status_dev,
+                       hs::next_stamp());
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hs::hip_fail(st, "pack launch");
 }
@@ -344,14 +351,14 @@ int hs_gqa_gather_rows(const uint16_t* prefetched_dev, uint32_t prefetched_rows,
                        void* stream) {
     hs::clear_error();
     if (!map_dev || !k_dev || !v_dev || !status_dev) return hs::reject("gather: null pointer");
+    if (reinterpret_cast<uintptr_t>(status_dev) & 7u)
+        return hs::reject("gather: status must be 8-byte aligned");
     if (count == 0 || count > hs::kMaxVisible) return hs::reject("gather: count out of range");
     hs::PoolSource ps{};
     hs::MapSource ms{prefetched_dev, misses_dev, map_dev, prefetched_rows, miss_rows};
     hipStream_t s = hs::as_stream(stream);
-    hipLaunchKernelGGL(hs::fill_u32_kernel, dim3(1), dim3(256), 0, s,
-                       reinterpret_cast<uint32_t*>(status_dev), 4u, 0u);
     hipLaunchKernelGGL(hs::pack_kernel<false>, dim3((count + 63) / 64, 32), dim3(256), 0, s, ps,
-                       ms, nullptr, 0u, count, k_dev, v_dev, nullptr, status_dev);
+                       ms, nullptr, 0u, count, k_dev, v_dev, nullptr, status_dev, hs::next_stamp());
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hs::hip_fail(st, "gather launch");
 }

@@ -23,8 +23,10 @@
 // partial tiles are added in LDS in a fixed order (deterministic), the RMS
 // scale (sums of squares taken from the same A fragments, so hidden is never
 // rounded again) and RoPE (FP64 angle and rotation) run in the epilogue, and
-// each workgroup records per-sequence nonfinite / overflow flags that
-// rehearsal_status_kernel folds into the status words.
+// each workgroup publishes its per-sequence nonfinite / overflow findings
+// straight into the sequences' status words (publish_stamped: workgroup 0
+// stamps HS_OK, a workgroup with a finding raises it, NONFINITE above
+// OVERFLOW), so no second launch folds them.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -51,7 +53,8 @@ struct RehearsalArgs {
     const uint16_t* hidden;  // BF16 [batch][4096]
     const uint16_t* wq;      // BF16 [4096][4096]
     uint16_t* q;             // F16 [batch][4096]
-    uint32_t* flags;         // [batch][kTiles] or null
+    hs_status_t* status;     // [batch] or null
+    uint32_t stamp;          // this call's status stamp
     uint32_t batch;
     float eps;
     uint32_t pos[kMaxBatch];
@@ -150,22 +153,10 @@ __global__ void __launch_bounds__(kSplits * 64) rehearsal_kernel(const Rehearsal
         if (flag) atomicOr(&bad[b], flag);
     }
     __syncthreads();
-    if (a.flags && tid < a.batch) a.flags[tid * kTiles + blockIdx.x] = bad[tid];
-}
-
-// Status of each sequence from its tiles' flags.
-__global__ void __launch_bounds__(kTiles) rehearsal_status_kernel(const uint32_t* __restrict__ flags,
-                                                                  hs_status_t* __restrict__ status) {
-    __shared__ uint32_t any;
-    if (threadIdx.x == 0) any = 0;
-    __syncthreads();
-    const uint32_t f = flags[blockIdx.x * kTiles + threadIdx.x];
-    if (f) atomicOr(&any, f);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        hs_status_t s{};
-        s.code = (any & 1u) ? HS_ERR_NONFINITE : ((any & 2u) ? HS_ERR_OVERFLOW : HS_OK);
-        status[blockIdx.x] = s;
+    if (a.status && tid < a.batch) {
+        const uint32_t f = bad[tid];
+        const int code = (f & 1u) ? HS_ERR_NONFINITE : ((f & 2u) ? HS_ERR_OVERFLOW : HS_OK);
+        publish_stamped(a.status + tid, a.stamp, code, blockIdx.x == 0);
     }
 }
 
@@ -184,21 +175,20 @@ int launch_rehearsal(const uint16_t* hidden, const uint16_t* wq, const uint32_t*
         return reject("rehearsal: eps > 0 and theta > 1 required");
     if ((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(wq)) & 15u)
         return reject("rehearsal: hidden and Wq must be 16-byte aligned");
-    if (status && !workspace) return reject("rehearsal: a status needs the workspace");
+    if (reinterpret_cast<uintptr_t>(status) & 7u) return reject("rehearsal: status must be 8-byte aligned");
+    (void)workspace;  // no longer used: the GEMM publishes the status itself
     RehearsalArgs args{};
     args.hidden = hidden;
     args.wq = wq;
     args.q = q;
-    args.flags = status ? static_cast<uint32_t*>(workspace) : nullptr;
+    args.status = status;
+    args.stamp = next_stamp();
     args.batch = batch;
     args.eps = eps;
     for (uint32_t b = 0; b < batch; ++b) args.pos[b] = positions[b];
     for (uint32_t i = 0; i < 64; ++i)
         args.inv_freq[i] = std::pow(static_cast<double>(theta), -2.0 * static_cast<double>(i) / 128.0);
     hipLaunchKernelGGL(rehearsal_kernel, dim3(kTiles), dim3(kSplits * 64), 0, stream, args);
-    if (status)
-        hipLaunchKernelGGL(rehearsal_status_kernel, dim3(batch), dim3(kTiles), 0, stream,
-                           args.flags, status);
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "rehearsal launch");
 }

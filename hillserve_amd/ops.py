@@ -353,14 +353,11 @@ def rehearsal_query(hidden, wq, positions, eps=1e-5, theta=500000.0, out=None, s
     pos = (ctypes.c_uint32 * max(1, batch))(*[int(p) for p in positions])
     if out is None:
         out = torch.empty((batch, 32, 128), dtype=torch.float16, device=hidden.device)
-    st = ws = None
-    if status:
+    st = None
+    if status:  # written by the launch itself: no clearing
         st = torch.empty((batch, 4), dtype=torch.int32, device=hidden.device)
-        with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
-            st.zero_()
-        ws = _scratch(lib().hs_rehearsal_workspace_bytes(batch), hidden.device, stream)
     check(lib().hs_rehearsal_query(_p(hidden), _p(wq), ctypes.cast(pos, ctypes.c_void_p), batch,
-                                   eps, theta, _p(out), _p(st), _p(ws), _s(stream)))
+                                   eps, theta, _p(out), _p(st), None, _s(stream)))
     return out, st
 
 
@@ -392,16 +389,18 @@ def _kv_pool(pool, v_pool, row_bytes):
 
 
 def pack(pool, ids, lens, ids_stride, positions, count, row_of_id=None, max_id=None,
-         v_pool=None, row_bytes=4096, stream=None):
+         v_pool=None, row_bytes=4096, status=None, stream=None):
     """pack_gqa_workspace from the device hot pool -> (K, V, mask, status).
-    pool: 4096 B KV records, or with v_pool the K and V row arrays."""
+    pool: 4096 B KV records, or with v_pool the K and V row arrays.  status:
+    any 8-byte aligned int32[4] (no clearing needed: the call stamps it)."""
     dev = pool.device
     nq = positions.numel()
     qpad = (nq + 63) // 64 * 64
     k = torch.empty(count * H * D, dtype=torch.float16, device=dev)
     v = torch.empty(count * H * D, dtype=torch.float16, device=dev)
     mask = torch.empty(H * qpad * count, dtype=torch.float32, device=dev)
-    status = new_status(dev, stream)
+    if status is None:
+        status = torch.empty(4, dtype=torch.int32, device=dev)
     kp, vp, row_bytes, pool_rows = _kv_pool(pool, v_pool, row_bytes)
     if max_id is None:
         max_id = row_of_id.numel() if row_of_id is not None else pool_rows
@@ -412,11 +411,14 @@ def pack(pool, ids, lens, ids_stride, positions, count, row_of_id=None, max_id=N
     return k, v, mask, status
 
 
-def gather_rows(prefetched, misses, row_map, count, stream=None):
+def gather_rows(prefetched, misses, row_map, count, status=None, stream=None):
+    """GQAPrefetchCuda's gather_gqa on device rows -> (K, V, status); status
+    as for pack (no clearing needed)."""
     dev = row_map.device
     k = torch.empty(count * H * D, dtype=torch.float16, device=dev)
     v = torch.empty(count * H * D, dtype=torch.float16, device=dev)
-    status = new_status(dev, stream)
+    if status is None:
+        status = torch.empty(4, dtype=torch.int32, device=dev)
     rows_of = lambda t: 0 if t is None else t.numel() * t.element_size() // 4096
     check(lib().hs_gqa_gather_rows(_p(prefetched), rows_of(prefetched), _p(misses), rows_of(misses),
                                    _p(row_map), count, _p(k), _p(v), _p(status), _s(stream)))

@@ -230,9 +230,12 @@ int hs_gqa_select_then_score(const hs_select_job_t *select_jobs, uint32_t select
  * angle pos_b * theta^(-2i/128) (ggml NORM rope); positions: HOST array of
  * batch entries; q_dev F16 [batch][32][128], the scorer's query layout.  The
  * product runs on MFMA (BF16 operands, FP32 accumulation).  status_dev
- * (nullable, [batch]) gets HS_ERR_NONFINITE for a nonfinite value and
- * HS_ERR_OVERFLOW for one beyond F16, as query_f16 rejects them; it needs
- * workspace_dev of hs_rehearsal_workspace_bytes(batch) bytes. */
+ * (nullable, [batch], 8-byte aligned, no clearing needed) gets per sequence
+ * HS_ERR_NONFINITE for a nonfinite value and HS_ERR_OVERFLOW for one beyond
+ * F16, as query_f16 rejects them, else HS_OK; the launch writes it itself
+ * (its k field holds a stamp of the call, the other fields are unchanged).
+ * workspace_dev is not used (nullable); hs_rehearsal_workspace_bytes is kept
+ * for callers that size one. */
 size_t hs_rehearsal_workspace_bytes(uint32_t batch);
 int hs_rehearsal_query(const uint16_t *hidden_dev, const uint16_t *wq_dev,
                        const uint32_t *positions, uint32_t batch, float eps, float theta,
@@ -328,7 +331,10 @@ int hs_gqa_physical_union(const uint32_t *ids_dev, const uint32_t *lens_dev,
  * ids_dev/lens_dev as above (lens <= count, nonzero), positions_dev [nq]
  * ascending query positions (1 <= nq <= 256).  Writes K F16[count][32][128],
  * V F16[32][128][count], mask F32[32][qpad][count], qpad = ceil(nq/64)*64;
- * byte-identical to the reference, zero/-inf padding included. */
+ * byte-identical to the reference, zero/-inf padding included.
+ * Status: status_dev (8-byte aligned) needs no clearing before the call;
+ * the call reports through status->code (HS_OK or its first error) and
+ * leaves a stamp of its own in status->k (the other fields unchanged). */
 int hs_gqa_pack(const uint8_t *k_pool_dev, const uint8_t *v_pool_dev, size_t row_bytes,
                 uint32_t pool_rows, const int32_t *row_of_id_dev, uint32_t max_id,
                 const uint32_t *ids_dev,
@@ -342,7 +348,8 @@ int hs_gqa_pack(const uint8_t *k_pool_dev, const uint8_t *v_pool_dev, size_t row
  * Rows are 2048 F16 words (K[8][128] then V[8][128]).  Map entries beyond
  * prefetched_rows / miss_rows are refused on the device (zeros written,
  * HS_ERR_MISSING in the status), as GQAPrefetchCuda::deliver refuses them on
- * the host (runtime/gqa_prefetch_cuda.cu:69). */
+ * the host (runtime/gqa_prefetch_cuda.cu:69).  Status as for hs_gqa_pack:
+ * no clearing needed, status->code is the result, status->k a stamp. */
 int hs_gqa_gather_rows(const uint16_t *prefetched_dev,
                        uint32_t prefetched_rows, const uint16_t *misses_dev,
                        uint32_t miss_rows, const int32_t *map_dev,

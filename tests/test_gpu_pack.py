@@ -152,3 +152,36 @@ def test_pack_and_gather_at_layer_size(hs, port, queries):
     gk, gv = port.gather_rows(pre.view(np.uint16), mis.view(np.uint16), row_map.reshape(-1), slots)
     assert hs.ops.read_status(status)["code"] == 0
     assert np.array_equal(from_dev(kd), gk) and np.array_equal(from_dev(vd), gv)
+
+
+def test_status_needs_no_clearing(hs, port):
+    """Pack and gather stamp their status themselves: a status holding a stale
+    error (or another call's stamp) reads HS_OK after a clean call, an error
+    after a failing one, and HS_OK again after the next clean call."""
+    ids = [[8, 12] for _ in range(32)]
+    bad = [list(r) for r in ids]
+    bad[0] = [13]
+    stale = np.array([hs.HS_ERR_MISSING, np.int32(-2147483643), 5, 6], dtype=np.int32)
+    status = torch.from_numpy(stale.copy()).cuda()
+
+    def run(sel):
+        dids, lens, stride = dev_ids(sel)
+        row_of_id = np.full(13, -1, dtype=np.int32)
+        row_of_id[[8, 12]] = [0, 1]
+        pos = torch.tensor([12], dtype=torch.int64, device="cuda")
+        pool = torch.from_numpy(kat_payload().reshape(-1, 4096)).cuda()
+        hs.ops.pack(pool, dids, lens, stride, pos, 32, row_of_id=to_dev(row_of_id), status=status)
+        return hs.ops.read_status(status)["code"]
+
+    assert run(ids) == 0
+    assert run(bad) == hs.HS_ERR_MISSING
+    assert run(ids) == 0
+    status.copy_(torch.from_numpy(stale))
+    pre = torch.from_numpy(kat_payload()).cuda()
+    row_map = np.full(32 * 32, -1, dtype=np.int32)
+    row_map[::32] = 0
+    _, _, st = hs.ops.gather_rows(pre, None, to_dev(row_map), 32, status=status)
+    assert hs.ops.read_status(st)["code"] == 0
+    row_map[5] = 3  # beyond the two prefetched rows
+    _, _, st = hs.ops.gather_rows(pre, None, to_dev(row_map), 32, status=status)
+    assert hs.ops.read_status(st)["code"] == hs.HS_ERR_MISSING

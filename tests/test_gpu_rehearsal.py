@@ -6,6 +6,8 @@ sequence and, for every element of at least 1/64 of that largest |q|, within
 2 F16 ulps of the F16-rounded FP64 value (the only roundings are FP32
 accumulation and the final F16 conversion; on smaller values FP32
 cancellation can exceed 2 ulps of their own size)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -65,3 +67,26 @@ def test_status_flags(hs):
     codes = status.cpu().numpy()[:, 0]
     assert codes[1] == hs.HS_ERR_NONFINITE
     assert codes[0] == hs.HS_ERR_OVERFLOW and codes[2] == hs.HS_ERR_OVERFLOW
+
+
+def test_status_precedence_across_tiles_and_stale_status(hs):
+    """One launch publishes every sequence's status itself (no clearing, no
+    second launch): a NONFINITE found by one tile of a sequence outranks an
+    OVERFLOW found by another tile, and a stale status word is replaced."""
+    hidden = np.full((2, 4096), bf16(1.0), dtype=np.uint16)
+    hidden[1, :2] = 0  # sequence 1 does not see Wq's huge columns 0 and 1
+    wq = np.full((4096, 4096), bf16(0.01), dtype=np.uint16)
+    wq[7, :] = bf16(32.0)          # feature 7 (tile 0): beyond F16 for both sequences
+    wq[20, :2] = bf16(3.0e38)      # feature 20 (tile 1): 6e38 -> inf in FP32 for sequence 0
+    hd, wd = to_bf16_dev(hidden), to_bf16_dev(wq)  # held until the launches are done
+    for stale in (hs.HS_OK, hs.HS_ERR_NONFINITE):
+        out = torch.empty((2, 32, 128), dtype=torch.float16, device="cuda")
+        status = torch.full((2, 4), stale, dtype=torch.int32, device="cuda")
+        status[:, 1] = -5  # a stamp-like k from an earlier call
+        L = hs.lib()
+        pos = (ctypes.c_uint32 * 2)(0, 0)
+        hs.check(L.hs_rehearsal_query(hd.data_ptr(), wd.data_ptr(),
+                                      ctypes.cast(pos, ctypes.c_void_p), 2, EPS, THETA,
+                                      out.data_ptr(), status.data_ptr(), None, None))
+        codes = status.cpu().numpy()[:, 0]
+        assert codes[0] == hs.HS_ERR_NONFINITE and codes[1] == hs.HS_ERR_OVERFLOW, (stale, codes)
