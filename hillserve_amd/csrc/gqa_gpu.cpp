@@ -687,3 +687,193 @@ DeviceScores GpuScoreBackend::score(const std::vector<std::uint16_t>&,
 }
 
 }  // namespace hillserve::gpu
+
+// ---- payload prefetch (runtime/gqa_prefetch_cuda.hpp:8-25, .cu:44-87) -------------
+
+namespace hillserve::gpu {
+namespace {
+constexpr std::size_t kRowBytes = 4096;  // one physical row: K[8][128] then V[8][128] F16
+std::uint64_t now_ns() {
+    return static_cast<std::uint64_t>(
+        std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now().time_since_epoch()).count());
+}
+}  // namespace
+
+struct GQAPrefetchGpu::Impl {
+    int device = 0;
+    std::size_t rows = 0, bytes = 0;
+    struct Slot {
+        PinnedBuffer host;
+        DeviceBuffer gpu;
+        hipStream_t stream = nullptr;
+        hipEvent_t start = nullptr, ready = nullptr;
+        std::size_t valid = 0;  // rows staged
+    };
+    Slot slots[2];
+    DeviceBuffer misses, map, status;
+    PinnedBuffer misses_host, map_host, mask_host, status_host;
+    hipEvent_t delivery = nullptr;
+    // the consumer stream of a delivery that may still read the slots
+    hipStream_t consumer = nullptr;
+    ~Impl() {
+        (void)hipSetDevice(device);
+        if (consumer) (void)hipStreamSynchronize(consumer);
+        if (delivery) (void)hipEventSynchronize(delivery);
+        for (auto& s : slots)
+            if (s.stream) (void)hipStreamSynchronize(s.stream);
+        for (auto& s : slots) {
+            if (s.start) (void)hipEventDestroy(s.start);
+            if (s.ready) (void)hipEventDestroy(s.ready);
+            if (s.stream) (void)hipStreamDestroy(s.stream);
+        }
+        if (delivery) (void)hipEventDestroy(delivery);
+    }
+};
+
+GQAPrefetchGpu::GQAPrefetchGpu(void* device_pointer, std::size_t max_rows)
+    : impl_(std::make_unique<Impl>()) {
+    auto& p = *impl_;
+    if (max_rows == 0 || max_rows > 66048)
+        throw std::runtime_error("prefetch GPU: max_rows must be 1..66048");
+    hipPointerAttribute_t attributes{};
+    if (hipPointerGetAttributes(&attributes, device_pointer) != hipSuccess) {
+        (void)hipGetLastError();  // leave no error behind for the next launch check
+        throw std::runtime_error("prefetch GPU: the target pointer must be device memory");
+    }
+    if (attributes.type != hipMemoryTypeDevice)
+        throw std::runtime_error("prefetch GPU: the target pointer must be device memory");
+    p.device = attributes.device;
+    p.rows = max_rows;
+    p.bytes = max_rows * kRowBytes;
+    hip_check(hipSetDevice(p.device), "prefetch set device");
+    for (auto& s : p.slots) {
+        s.gpu.ensure(p.bytes);
+        s.host.ensure(p.bytes);
+        hip_check(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking), "prefetch private stream");
+        hip_check(hipEventCreate(&s.start), "prefetch start event");
+        hip_check(hipEventCreate(&s.ready), "prefetch ready event");
+    }
+    p.misses.ensure(p.bytes);
+    p.map.ensure(max_rows * 32 * sizeof(std::int32_t));
+    p.status.ensure(sizeof(hs_status_t));
+    p.misses_host.ensure(p.bytes);
+    p.map_host.ensure(max_rows * 32 * sizeof(std::int32_t));
+    p.status_host.ensure(sizeof(hs_status_t));
+    hip_check(hipEventCreateWithFlags(&p.delivery, hipEventDisableTiming), "prefetch delivery event");
+}
+
+GQAPrefetchGpu::~GQAPrefetchGpu() = default;
+
+std::size_t GQAPrefetchGpu::gpu_bytes() const {
+    return impl_->bytes * 3 + impl_->rows * 32 * sizeof(std::int32_t) + sizeof(hs_status_t);
+}
+
+std::size_t GQAPrefetchGpu::host_bytes() const {
+    return impl_->bytes * 3 + impl_->rows * 32 * sizeof(std::int32_t) + impl_->mask_host.size();
+}
+
+GQAPrefetchGpu::Upload GQAPrefetchGpu::stage(unsigned slot, const std::vector<std::uint8_t>& payload) {
+    auto& p = *impl_;
+    if (slot >= 2 || payload.size() > p.bytes || payload.size() % kRowBytes)
+        throw std::runtime_error("prefetch GPU slot geometry");
+    auto& s = p.slots[slot];
+    hip_check(hipSetDevice(p.device), "prefetch worker device");
+    Upload out;
+    // the pinned buffer is reused: an earlier upload from it has completed
+    // (stage waits for its own upload before returning)
+    if (!payload.empty()) std::memcpy(s.host.ensure(p.bytes), payload.data(), payload.size());
+    out.started_ns = now_ns();
+    out.bytes = payload.size();
+    s.valid = payload.size() / kRowBytes;
+    try {
+        hip_check(hipEventRecord(s.start, s.stream), "prefetch upload start");
+        if (!payload.empty())
+            hip_check(hipMemcpyAsync(s.gpu.ensure(p.bytes), s.host.ensure(p.bytes), payload.size(),
+                                     hipMemcpyHostToDevice, s.stream),
+                      "prefetch upload");
+        hip_check(hipEventRecord(s.ready, s.stream), "prefetch ready record");
+        hip_check(hipEventSynchronize(s.ready), "prefetch upload completion");
+        out.ready_observed_ns = now_ns();
+        hip_check(hipEventElapsedTime(&out.device_ms, s.start, s.ready), "prefetch upload interval");
+        return out;
+    } catch (...) {
+        // an earlier upload on this private stream may still read the pinned source
+        (void)hipStreamSynchronize(s.stream);
+        throw;
+    }
+}
+
+GQAPrefetchGpu::Delivery GQAPrefetchGpu::deliver(unsigned slot, const std::vector<std::int32_t>& map,
+                                                 const std::vector<std::uint8_t>& misses,
+                                                 const float* mask, std::size_t mask_elements,
+                                                 std::size_t count, void* k, void* v,
+                                                 void* gpu_mask, void* stream) {
+    auto& p = *impl_;
+    if (slot >= 2 || !stream || count == 0 || count > p.rows || map.size() != count * 32 ||
+        misses.size() > p.bytes || misses.size() % kRowBytes || !k || !v ||
+        (mask_elements && (!mask || !gpu_mask)))
+        throw std::runtime_error("prefetch GPU delivery geometry/stream");
+    auto& s = p.slots[slot];
+    const std::size_t miss_rows = misses.size() / kRowBytes;
+    std::size_t valid_pairs = 0;
+    for (const std::int32_t row : map) {
+        if (row >= 0 && static_cast<std::size_t>(row) >= s.valid)
+            throw std::runtime_error("prefetch GPU: a map row lies outside the staged payload");
+        if (row <= -2 && static_cast<std::size_t>(-2 - static_cast<std::int64_t>(row)) >= miss_rows)
+            throw std::runtime_error("prefetch GPU: a miss row lies outside the miss payload");
+        if (row != -1) ++valid_pairs;
+    }
+    hip_check(hipSetDevice(p.device), "prefetch consumer device");
+    const auto consumer = as_stream(stream);
+    Delivery out;
+    out.started_ns = now_ns();
+    // the pinned staging of the previous delivery is free: deliver waits for
+    // its own completion before returning
+    const std::size_t map_bytes = map.size() * sizeof(std::int32_t), mask_bytes = mask_elements * sizeof(float);
+    std::memcpy(p.map_host.ensure(map_bytes), map.data(), map_bytes);
+    if (!misses.empty()) std::memcpy(p.misses_host.ensure(p.bytes), misses.data(), misses.size());
+    if (mask_bytes) std::memcpy(p.mask_host.ensure(mask_bytes), mask, mask_bytes);
+    p.consumer = consumer;
+    try {
+        hip_check(hipStreamWaitEvent(consumer, s.ready, 0), "attention stream waits for the staged payload");
+        if (!misses.empty())
+            hip_check(hipMemcpyAsync(p.misses.ensure(p.bytes), p.misses_host.ensure(p.bytes),
+                                     misses.size(), hipMemcpyHostToDevice, consumer),
+                      "prefetch miss upload");
+        hip_check(hipMemcpyAsync(p.map.ensure(map_bytes), p.map_host.ensure(map_bytes), map_bytes,
+                                 hipMemcpyHostToDevice, consumer),
+                  "prefetch map upload");
+        if (mask_bytes)
+            hip_check(hipMemcpyAsync(gpu_mask, p.mask_host.ensure(mask_bytes), mask_bytes,
+                                     hipMemcpyHostToDevice, consumer),
+                      "prefetch mask upload");
+        auto* st = static_cast<hs_status_t*>(p.status.ensure(sizeof(hs_status_t)));
+        api_check(hs_gqa_gather_rows(static_cast<const std::uint16_t*>(s.gpu.ensure(p.bytes)),
+                                     static_cast<std::uint32_t>(s.valid),
+                                     static_cast<const std::uint16_t*>(p.misses.ensure(p.bytes)),
+                                     static_cast<std::uint32_t>(miss_rows),
+                                     static_cast<const std::int32_t*>(p.map.ensure(map_bytes)),
+                                     static_cast<std::uint32_t>(count), static_cast<std::uint16_t*>(k),
+                                     static_cast<std::uint16_t*>(v), st, stream));
+        auto* result = static_cast<hs_status_t*>(p.status_host.ensure(sizeof(hs_status_t)));
+        hip_check(hipMemcpyAsync(result, st, sizeof(hs_status_t), hipMemcpyDeviceToHost, consumer),
+                  "prefetch status readback");
+        hip_check(hipEventRecord(p.delivery, consumer), "prefetch delivery record");
+        const auto wait = Clock::now();
+        hip_check(hipEventSynchronize(p.delivery), "prefetch delivery completion");
+        out.wait_ms = ms_since(wait);
+        out.ready_observed_ns = now_ns();
+        p.consumer = nullptr;
+        if (result->code != HS_OK)
+            throw DeviceError(result->code, "prefetch GPU: the device gather refused the map");
+        out.h2d_bytes = misses.size() + map_bytes + mask_bytes;
+        out.d2d_bytes = valid_pairs * 128 * 4;  // a K and a V half row of one KV head
+        return out;
+    } catch (...) {
+        // the map, misses and mask staging must outlive every enqueued copy
+        if (hipStreamSynchronize(consumer) == hipSuccess) p.consumer = nullptr;
+        throw;
+    }
+}
+
+}  // namespace hillserve::gpu

@@ -527,6 +527,25 @@ def kv_cold_fetch(image, layer, positions, k_out, *, v_out=None, row_bytes=4096,
     return status
 
 
+def cold_plan(member, heads, n, slot, staging_base, list_size, positions=None, rows=None,
+              count=None, stream=None):
+    """hs_gqa_cold_plan of one sequence -> (positions, rows, count): the
+    selected tokens whose slot is negative, ascending (padded with
+    0xffffffff to list_size), the row map (slot, staging_base + list index,
+    or -1) and their count."""
+    _need_cuda(member, slot)
+    dev = member.device
+    if positions is None:
+        positions = torch.empty(list_size, dtype=torch.int32, device=dev)
+    if rows is None:
+        rows = torch.empty(n, dtype=torch.int32, device=dev)
+    if count is None:
+        count = torch.empty(1, dtype=torch.int32, device=dev)
+    check(lib().hs_gqa_cold_plan(_p(member), heads, n, _p(slot), staging_base, list_size,
+                                 _p(positions), _p(rows), _p(count), _s(stream)))
+    return positions, rows, count
+
+
 def cold_runs(positions):
     """(run_first, run_count) ctypes arrays of the consecutive runs of an
     ascending host list of positions."""

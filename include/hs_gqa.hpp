@@ -212,4 +212,54 @@ private:
     std::unique_ptr<Impl> impl_;
 };
 
+// ---- payload prefetch: staging and delivery (runtime/gqa_prefetch_cuda.hpp:8-25) ----
+// The executor's payload prefetch (runtime/gqa_executor.cpp:67-71,202-221):
+// a background thread stages a prefetched payload (physical rows of 4096 B,
+// K[8][128] then V[8][128] F16) into one of two slots; the executor thread
+// later delivers the layer's packed K / V workspace from that slot plus the
+// rows the prefetch missed, on the attention stream.
+//   stage(slot, payload):   copies the payload into the slot's pinned host
+//       buffer, uploads it on the slot's private stream (default priority)
+//       and waits for it; slot < 2, payload a whole number of rows, at most
+//       max_rows.
+//   deliver(slot, map, misses, mask, mask_elements, count, k, v, gpu_mask,
+//           stream):  map[h*count + s] >= 0 a staged row, <= -2 miss row
+//       -2-map, -1 padding (checked on the host against the staged rows and
+//       the misses before any work); the attention stream waits for the
+//       slot's upload, then the misses, map and mask go up (through pinned
+//       staging, so the copies are asynchronous) and the gather
+//       (hs_gqa_gather_rows) writes K [count][32][128] and V [32][128][count];
+//       the call waits for the delivery and returns its timings.
+// Geometry and stream errors throw std::runtime_error, as the reference's;
+// device failures throw DeviceError.  stage and deliver may run on different
+// threads for different slots; calls on one slot must be serialized.
+class GQAPrefetchGpu {
+public:
+    struct Upload {
+        std::uint64_t started_ns = 0, ready_observed_ns = 0, bytes = 0;
+        float device_ms = 0;
+    };
+    struct Delivery {
+        std::uint64_t started_ns = 0, ready_observed_ns = 0, h2d_bytes = 0, d2d_bytes = 0;
+        double wait_ms = 0;
+    };
+    // device_pointer: any allocation on the GPU the prefetch serves (it picks
+    // the device); max_rows: payload rows per slot, and the largest count.
+    GQAPrefetchGpu(void* device_pointer, std::size_t max_rows);
+    ~GQAPrefetchGpu();
+    GQAPrefetchGpu(const GQAPrefetchGpu&) = delete;
+    GQAPrefetchGpu& operator=(const GQAPrefetchGpu&) = delete;
+    std::size_t gpu_bytes() const;
+    std::size_t host_bytes() const;
+    Upload stage(unsigned slot, const std::vector<std::uint8_t>& payload);
+    Delivery deliver(unsigned slot, const std::vector<std::int32_t>& map,
+                     const std::vector<std::uint8_t>& misses, const float* mask,
+                     std::size_t mask_elements, std::size_t count, void* k, void* v,
+                     void* gpu_mask, void* stream);
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
 }  // namespace hillserve::gpu

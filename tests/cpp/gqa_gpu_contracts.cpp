@@ -22,6 +22,7 @@
 #include <random>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "hs_gqa.hpp"
@@ -797,6 +798,110 @@ void pipeline_contracts() {
     check(from_dev<std::uint32_t>(counts1, H) == from_dev<std::uint32_t>(counts2, H), "counts equal");
 }
 
+// GQAPrefetchGpu: the stage / deliver contract of GQAPrefetchCuda
+// (runtime/gqa_prefetch_cuda.cu:44-87), against a host restatement of
+// gather_gqa (:12-22): two slots staged (one from a second thread while the
+// other is delivered), K / V of the delivered workspace byte for byte, the
+// mask copied verbatim, the map bound checks made on the host before any
+// work, and the reported byte counts.
+void prefetch_contracts() {
+    constexpr std::size_t kRows = 300, kPre = 200;
+    std::mt19937 gen(87);
+    std::vector<std::uint8_t> payload(kRows * 4096), other(kRows * 4096);
+    for (auto& b : payload) b = static_cast<std::uint8_t>(gen());
+    for (auto& b : other) b = static_cast<std::uint8_t>(gen());
+    const std::size_t count = 96;
+    Dev k(count * 32 * 128 * 2), v(count * 32 * 128 * 2), gmask(32 * 64 * count * 4), anchor(256);
+    GQAPrefetchGpu prefetch(anchor.p, kRows);
+    check(prefetch.gpu_bytes() >= 3 * kRows * 4096 && prefetch.host_bytes() >= 2 * kRows * 4096,
+          "prefetch byte accounting covers both slots and the misses");
+    hipStream_t stream = nullptr;
+    check(hipStreamCreate(&stream) == hipSuccess, "consumer stream");
+    // slot 0: the first kPre rows prefetched, the rest are misses; slot 1 another payload
+    const std::vector<std::uint8_t> staged0(payload.begin(), payload.begin() + kPre * 4096);
+    const std::vector<std::uint8_t> misses(payload.begin() + kPre * 4096, payload.end());
+    prefetch.stage(0, staged0);
+    std::exception_ptr worker_error;
+    std::thread worker([&] {
+        try {
+            prefetch.stage(1, other);
+        } catch (...) {
+            worker_error = std::current_exception();
+        }
+    });
+    std::vector<std::int32_t> map(32 * count, -1);
+    std::size_t pairs = 0;
+    for (std::size_t h = 0; h < 32; ++h)
+        for (std::size_t s = 0; s < count - 5 * (h % 3); ++s) {  // ragged heads, -1 padding
+            const std::size_t row = (h * 37 + s * 11) % kRows;
+            map[h * count + s] = row < kPre ? std::int32_t(row) : std::int32_t(-2 - std::int64_t(row - kPre));
+            ++pairs;
+        }
+    std::vector<float> mask(32 * 64 * count);
+    for (std::size_t i = 0; i < mask.size(); ++i)
+        mask[i] = (i % 7) ? 0.0f : -std::numeric_limits<float>::infinity();
+    auto expect = [&](const std::vector<std::uint8_t>& pre, const std::vector<std::uint8_t>& mis,
+                      std::vector<std::uint16_t>& ek, std::vector<std::uint16_t>& ev) {
+        ek.assign(count * 32 * 128, 0);
+        ev.assign(count * 32 * 128, 0);
+        for (std::size_t s = 0; s < count; ++s)
+            for (std::size_t h = 0; h < 32; ++h) {
+                const std::int32_t row = map[h * count + s];
+                if (row == -1) continue;
+                const std::uint8_t* src = row >= 0 ? pre.data() + std::size_t(row) * 4096
+                                                   : mis.data() + std::size_t(-2 - std::int64_t(row)) * 4096;
+                for (std::size_t d = 0; d < 128; ++d) {
+                    std::uint16_t kk, vv;
+                    std::memcpy(&kk, src + ((h / 4) * 128 + d) * 2, 2);
+                    std::memcpy(&vv, src + 2048 + ((h / 4) * 128 + d) * 2, 2);
+                    ek[(s * 32 + h) * 128 + d] = kk;
+                    ev[(h * 128 + d) * count + s] = vv;
+                }
+            }
+    };
+    auto got = [&](const Dev& d) {
+        std::vector<std::uint16_t> h(count * 32 * 128);
+        check(hipMemcpy(h.data(), d.p, h.size() * 2, hipMemcpyDeviceToHost) == hipSuccess, "readback");
+        return h;
+    };
+    std::vector<std::uint16_t> ek, ev;
+    auto delivered = prefetch.deliver(0, map, misses, mask.data(), mask.size(), count, k.p, v.p,
+                                      gmask.p, stream);
+    expect(staged0, misses, ek, ev);
+    check(got(k) == ek && got(v) == ev, "slot 0: delivered K / V equal gather_gqa's");
+    std::vector<float> mback(mask.size());
+    check(hipMemcpy(mback.data(), gmask.p, mask.size() * 4, hipMemcpyDeviceToHost) == hipSuccess &&
+              std::memcmp(mback.data(), mask.data(), mask.size() * 4) == 0,
+          "the mask arrives verbatim");
+    check(delivered.d2d_bytes == pairs * 512 &&
+              delivered.h2d_bytes == misses.size() + map.size() * 4 + mask.size() * 4,
+          "delivery byte accounting");
+    worker.join();
+    if (worker_error) std::rethrow_exception(worker_error);
+    // slot 1 (staged by the worker) with the same map: prefetched rows from `other`
+    prefetch.deliver(1, map, misses, nullptr, 0, count, k.p, v.p, nullptr, stream);
+    expect(other, misses, ek, ev);
+    check(got(k) == ek && got(v) == ev, "slot 1: delivered from the second thread's staging");
+    // host-side refusals, before any device work
+    auto bad = map;
+    bad[7] = std::int32_t(kPre);  // one past the staged rows
+    rejects([&] { prefetch.deliver(0, bad, misses, nullptr, 0, count, k.p, v.p, nullptr, stream); },
+            "a map row past the staged payload");
+    bad = map;
+    bad[9] = -2 - std::int32_t(kRows - kPre);  // one past the misses
+    rejects([&] { prefetch.deliver(0, bad, misses, nullptr, 0, count, k.p, v.p, nullptr, stream); },
+            "a miss row past the misses");
+    rejects([&] { prefetch.deliver(2, map, misses, nullptr, 0, count, k.p, v.p, nullptr, stream); }, "slot 2");
+    rejects([&] { prefetch.deliver(0, map, misses, nullptr, 0, count, k.p, v.p, nullptr, nullptr); },
+            "no consumer stream");
+    rejects([&] { prefetch.deliver(0, map, misses, nullptr, 0, count + 1, k.p, v.p, nullptr, stream); },
+            "map size against count");
+    rejects([&] { prefetch.stage(0, std::vector<std::uint8_t>(4095)); }, "a partial row");
+    rejects([&] { prefetch.stage(0, std::vector<std::uint8_t>((kRows + 1) * 4096)); }, "beyond max_rows");
+    rejects([&] { GQAPrefetchGpu host_target(payload.data(), 4); }, "a host pointer as the target");
+    (void)hipStreamDestroy(stream);
+}
+
 // The SegmentedKVStore v1 image writer (hs_kv_store_*; host only): header
 // page, record placement and headers, FNV-1a 64 digests (the test's own
 // byte loop, pinned by the published vectors of the empty string and "a"),
@@ -871,6 +976,7 @@ int main() {
         cover_contracts();
         stream_score_contracts();
         pipeline_contracts();
+        prefetch_contracts();
         std::cout << "{\"status\":\"passed\",\"cases\":" << cases
                   << ",\"bitwise_scores_compared\":" << comparisons << "}" << std::endl;
         return 0;

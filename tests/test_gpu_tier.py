@@ -174,3 +174,113 @@ def test_corrupt_cold_record_surfaces(hs):
     status = hs.ops.kv_cold_fetch(image, 0, pos, staging)
     st = hs.ops.read_status(status)
     assert st["code"] == hs.HS_ERR_CORRUPT and st["k"] == 1
+
+
+@pytest.mark.parametrize("current_cold", [False, True])
+def test_cover_prefetch_then_misses(hs, port, current_cold):
+    """The payload prefetch of the reference's executor on the device
+    (prefetch_payload, policy/full_gqa_runtime.cpp:299-344, consumed at
+    runtime/gqa_executor.cpp:202-221): before the current token exists, the
+    history cover's cold rows are fetched on a side stream; after the final
+    selection (which completes the current token), only the selected cold
+    rows outside the cover are fetched, on the main stream.  Attention then
+    reads hot rows, cover rows and miss rows through one row map.
+
+    The current token's K row copies the history's best head-0 key, so it is
+    selected; when its row is cold it is the one miss (the cover holds
+    history only), else there is none.  Checks: the final ids equal the
+    oracle's one-shot selection over all n columns; the cover fetched exactly
+    its cold union; the misses are exactly the selected cold rows outside it;
+    the attention equals the all-hot attention bit for bit and is within
+    2e-3 of the FP64 oracle."""
+    n = 4096
+    g = rng(8100 + current_cold)
+    k, rows, slot, hot = _sequence(g, n, 8200 + current_cold)
+    q16 = f16_bits(g.standard_normal((32, 128)))
+    hist_raw = port.score(q16, rows[: n - 1].reshape(-1), n - 1, 2048)
+    best = int(np.argmax(hist_raw[0].view(np.float16).astype(np.float32)))
+    k = k.copy()
+    k[n - 1] = k[best]
+    rows = pool_rows(k, rows.reshape(n, 2, 8, 128)[:, 1].reshape(n, 8, 128))
+    if current_cold != (slot[n - 1] < 0):  # place the current token's row as asked
+        b = (n - 1) // 64
+        if current_cold:
+            slot[b * 64:] = -1
+        else:
+            slot[b * 64:] = np.arange(hot.size, hot.size + n - b * 64, dtype=np.int32)
+        hot = np.nonzero(slot >= 0)[0]
+        order = np.argsort(slot[hot])
+        hot = hot[order]
+    hot_rows, cold_tokens = hot.size, n - hot.size
+    q32 = g.standard_normal((32, 128)).astype(np.float32)
+    image = _image(hs, rows, 71)
+    pool = torch.zeros((hot_rows + 2 * cold_tokens, 2048), dtype=torch.float16, device="cuda")
+    pool[:hot_rows] = to_dev(rows[hot])
+    keys = to_dev(k.reshape(-1))
+    slot_d = to_dev(slot)
+    side = torch.cuda.Stream()
+    main = torch.cuda.current_stream()
+    # one layer early: the history (n - 1 columns), its cover, the cover's cold plan and fetch
+    scores = torch.empty((32, n), dtype=torch.float16, device="cuda")
+    part = torch.empty((n - 1 + 63) // 64, dtype=torch.int32, device="cuda")
+    hs.ops.score(to_dev(q16.reshape(-1)), keys, n - 1, out=scores, score_stride=n,
+                 head0_partial=part)
+    words_h = (n - 1 + 31) // 32
+    cover_member = torch.zeros((32, words_h), dtype=torch.int32, device="cuda")
+    _, _, _, cst = hs.ops.select(scores, 32, n, n - 1, ALPHA, RATIO, scale_raw=True, cover=True,
+                                 head0_partial=part, member=cover_member)
+    cover_rows = torch.empty(n, dtype=torch.int32, device="cuda")
+    cover_pos, _, cover_count = hs.ops.cold_plan(cover_member, 32, n - 1, slot_d, hot_rows,
+                                                 cold_tokens, rows=cover_rows)
+    cover_rows[n - 1:] = slot_d[n - 1:]  # the current token's own slot (hot or -1)
+    fetched = torch.cuda.Event()
+    fetched_from = main.record_event()
+    with torch.cuda.stream(side):
+        side.wait_event(fetched_from)
+        cover_status = hs.ops.kv_cold_fetch(image, 0, cover_pos,
+                                            pool[hot_rows: hot_rows + cold_tokens], stream=side)
+        fetched.record(side)
+    # the final selection: the current token completed, every column
+    words = (n + 31) // 32
+    member = torch.zeros((32, words), dtype=torch.int32, device="cuda")
+    sel = hs.ops.select_batched(
+        [dict(scores=scores, n=n, head0_partial=part, member=member,
+              current_q=to_dev(q16.reshape(-1)), current_key=keys[(n - 1) * 1024:])],
+        32, ALPHA, RATIO, scale_raw=True, id_order=True, require_k=True)
+    ids, _, _, status = sel[0]
+    miss_pos, final_rows, miss_count = hs.ops.cold_plan(member, 32, n, cover_rows,
+                                                        hot_rows + cold_tokens, cold_tokens)
+    miss_status = hs.ops.kv_cold_fetch(image, 0, miss_pos, pool[hot_rows + cold_tokens:])
+    main.wait_event(fetched)
+    q = torch.from_numpy(q32).cuda()
+    out = hs.ops.sparse_attention(q, pool.reshape(-1), n, member, rows=final_rows)
+    torch.cuda.synchronize()
+    st = hs.ops.read_status(status)
+    assert hs.ops.read_status(cst)["code"] == 0 and st["code"] == 0
+    assert hs.ops.read_status(cover_status)["code"] == 0
+    assert hs.ops.read_status(miss_status)["code"] == 0
+    # final selection = the oracle's one-shot selection over all n columns
+    raw = port.score(q16, rows.reshape(-1), n, 2048)
+    assert np.array_equal(from_dev(scores), raw)
+    rc, kk, pids, _, _ = port.select(port.scale(raw), 32, n, n, ALPHA, RATIO)
+    assert rc == 0 and st["k"] == kk
+    assert np.array_equal(from_dev(ids)[:, :kk], np.sort(pids, axis=1))
+    # the cover fetched its cold union; the misses are the selected cold rows outside it
+    cbits = from_dev(cover_member).view(np.uint32)
+    cover_union = np.nonzero(np.unpackbits(np.bitwise_or.reduce(cbits, axis=0).view(np.uint8),
+                                           bitorder="little")[: n - 1])[0]
+    cover_cold = cover_union[slot[cover_union] < 0]
+    assert int(cover_count.item()) == cover_cold.size
+    assert np.array_equal(from_dev(cover_pos)[: cover_cold.size], cover_cold)
+    selected = np.unique(np.concatenate([np.asarray(p) for p in pids]))
+    misses = np.setdiff1d(selected[slot[selected] < 0], cover_cold)
+    assert int(miss_count.item()) == misses.size
+    assert np.array_equal(from_dev(miss_pos)[: misses.size], misses)
+    assert misses.size == (1 if current_cold else 0) and (not current_cold or misses[0] == n - 1)
+    # attention through hot + cover + miss rows = the all-hot attention, bit for bit
+    ref_dev = hs.ops.sparse_attention(q, to_dev(rows.reshape(-1)), n, member)
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref_dev.cpu().numpy().view(np.uint32))
+    ref = port.attention(q32, rows.view(np.uint8).reshape(-1), list(pids))
+    err = np.max(np.linalg.norm(got.astype(np.float64) - ref, axis=1) / np.linalg.norm(ref, axis=1))
+    assert err <= TOL, err
