@@ -730,6 +730,10 @@ def batch_leg(g, args):
 
 
 TIER_SEQS, TIER_N, TIER_PHYS = 8, 32768, 2
+# staging rows per sequence for cold rows selected outside the history cover
+# (the reference guarantees the final selection's history lies inside it, so
+# only the current token can miss; the bench asserts the count fits)
+TIER_MISSES = 64
 
 
 def tier_leg(g, args):
@@ -778,7 +782,9 @@ def tier_leg(g, args):
             rows[:, 1024:] = v
             keys = rows[:, :1024].contiguous()  # every token's K, for scoring
             slot_dev = torch.from_numpy(slot).to(dev)
-            pool = torch.empty((hot_rows + cold_rows, 2048), dtype=torch.float16, device=dev)
+            # hot rows, then staging for the cold rows, then for the cover's misses
+            pool = torch.empty((hot_rows + cold_rows + TIER_MISSES, 2048), dtype=torch.float16,
+                               device=dev)
             hot_ids = torch.from_numpy(np.nonzero(slot >= 0)[0]).to(dev)
             pool[:hot_rows] = rows[hot_ids]
             host_rows = rows.view(torch.uint8).cpu().numpy()
@@ -805,7 +811,24 @@ def tier_leg(g, args):
                 cstatus=ops.new_status(dev),
                 cws=ops.workspace(L.hs_kv_cold_fetch_workspace_bytes(cold_rows), dev),
                 out=torch.empty((32, 128), dtype=torch.float32, device=dev),
-                aws=ops.workspace(ops.attention_workspace_bytes(TIER_N), dev)))
+                aws=ops.workspace(ops.attention_workspace_bytes(TIER_N), dev),
+                # the cover schedule: history partials, cover selection and plan,
+                # miss plan and fetch (the current token's row-map entry is its
+                # slot: the cover plans write entries 0 .. N-2 only)
+                hpartial=torch.empty((TIER_N - 1 + 63) // 64, dtype=torch.int32, device=dev),
+                cmember=torch.empty((32, (TIER_N - 1 + 31) // 32), dtype=torch.int32, device=dev),
+                cids=torch.empty((32, kmax), dtype=torch.int32, device=dev),
+                ccounts=torch.empty(32, dtype=torch.int32, device=dev),
+                cselstatus=ops.new_status(dev),
+                cselws=ops.workspace(ops.select_workspace_bytes(32, TIER_N - 1), dev),
+                cpos=torch.empty(cold_rows, dtype=torch.int32, device=dev),
+                crows=slot_dev.clone(),
+                ccount=torch.empty(1, dtype=torch.int32, device=dev),
+                mpos=torch.empty(TIER_MISSES, dtype=torch.int32, device=dev),
+                mrows=torch.empty(TIER_N, dtype=torch.int32, device=dev),
+                mcount=torch.empty(1, dtype=torch.int32, device=dev),
+                mstatus=ops.new_status(dev),
+                mws=ops.workspace(L.hs_kv_cold_fetch_workspace_bytes(TIER_MISSES), dev)))
             del rows, v, host_rows
         # the copy-engine variant stages every cold row of a layer: its runs of
         # consecutive cold positions, their expected positions on the device,
@@ -838,6 +861,31 @@ def tier_leg(g, args):
         sel_tabs.append(lt_)
     score_ptr = [score_tabs[2 * l] for l in range(TIER_PHYS)]
     sel_ptr = [sel_tabs[2 * l] for l in range(TIER_PHYS)]
+    # the cover schedule's batched calls: history scoring (N - 1 tokens into
+    # the layer's scores, stride N), the history cover, and the final
+    # selection that completes each sequence's current token (column N - 1)
+    hist_tabs, cover_tabs, final_tabs = [], [], []
+    for l in range(TIER_PHYS):
+        ht = (hs.ScoreJob * TIER_SEQS)()
+        ct = (hs.SelectJob * TIER_SEQS)()
+        ft = (hs.SelectJob * TIER_SEQS)()
+        for s_i, sq in enumerate(seqs):
+            d = sq["layers"][l]
+            ht[s_i] = hs.ScoreJob(d["q"].data_ptr(), d["keys"].data_ptr(), d["scores"].data_ptr(),
+                                  d["hpartial"].data_ptr(), 1024, TIER_N - 1, TIER_N, 0)
+            ct[s_i] = hs.SelectJob(d["scores"].data_ptr(), d["hpartial"].data_ptr(),
+                                   d["cids"].data_ptr(), d["ccounts"].data_ptr(),
+                                   d["cmember"].data_ptr(), d["cselstatus"].data_ptr(),
+                                   d["cselws"].data_ptr(), TIER_N, TIER_N - 1, d["kmax"], 0)
+            ft[s_i] = hs.SelectJob(d["scores"].data_ptr(), d["hpartial"].data_ptr(), d["ids"].data_ptr(),
+                                   d["counts"].data_ptr(), d["member"].data_ptr(),
+                                   d["status"].data_ptr(), d["ws"].data_ptr(), TIER_N, TIER_N,
+                                   d["kmax"], 0, d["q"].data_ptr(),
+                                   d["keys"].data_ptr() + (TIER_N - 1) * 2048)
+        hist_tabs.append(ht)
+        cover_tabs.append(ct)
+        final_tabs.append(ft)
+    cast = lambda t: ctypes.cast(t, ctypes.c_void_p)
 
     def front(l, plan=True):  # main stream: score, select (and cold plan) of layer l
         p = l % TIER_PHYS
@@ -910,6 +958,88 @@ def tier_leg(g, args):
             stream.wait_event(pending[1])
         attend(pending[0], engines, marks)
 
+    def cover_prep(l):  # main stream, one layer early: history, cover, cover plans
+        p = l % TIER_PHYS
+        hs.check(L.hs_gqa_score_batched(cast(hist_tabs[p]), TIER_SEQS, sp))
+        hs.check(L.hs_gqa_select_batched(cast(cover_tabs[p]), TIER_SEQS, 32, ALPHA, RATIO,
+                                         hs.HS_SELECT_SCALE_RAW | hs.HS_SELECT_COVER, sp))
+        for sq in seqs:
+            d = sq["layers"][p]
+            hs.check(L.hs_gqa_cold_plan(vp(d["cmember"]), 32, TIER_N - 1, vp(d["slot"]), hot_rows,
+                                        cold_rows, vp(d["cpos"]), vp(d["crows"]), vp(d["ccount"]),
+                                        sp))
+
+    def cover_fetch(l, strm):  # the cover's cold rows into the cold staging rows
+        p = l % TIER_PHYS
+        for sq in seqs:
+            d = sq["layers"][p]
+            staging = d["pool"][hot_rows:hot_rows + cold_rows]
+            hs.check(L.hs_kv_cold_fetch(vp(sq["image"]), p, vp(d["cpos"]), cold_rows, vp(staging),
+                                        ctypes.c_void_p(staging.data_ptr() + 2048), 4096,
+                                        vp(d["cstatus"]), vp(d["cws"]), strm))
+
+    def cover_final(l, fetch_misses=True):  # main stream: final selection, miss plans, miss fetch
+        p = l % TIER_PHYS
+        hs.check(L.hs_gqa_select_batched(cast(final_tabs[p]), TIER_SEQS, 32, ALPHA, RATIO,
+                                         hs.HS_SELECT_SCALE_RAW | hs.HS_SELECT_ID_ORDER
+                                         | hs.HS_SELECT_REQUIRE_K, sp))
+        for sq in seqs:
+            d = sq["layers"][p]
+            hs.check(L.hs_gqa_cold_plan(vp(d["member"]), 32, TIER_N, vp(d["crows"]),
+                                        hot_rows + cold_rows, TIER_MISSES, vp(d["mpos"]),
+                                        vp(d["mrows"]), vp(d["mcount"]), sp))
+            if fetch_misses:
+                staging = d["pool"][hot_rows + cold_rows:]
+                hs.check(L.hs_kv_cold_fetch(vp(sq["image"]), p, vp(d["mpos"]), TIER_MISSES,
+                                            vp(staging), ctypes.c_void_p(staging.data_ptr() + 2048),
+                                            4096, vp(d["mstatus"]), vp(d["mws"]), sp))
+
+    def cover_attend(l, marks=None):
+        p = l % TIER_PHYS
+        if marks is not None:
+            b = torch.cuda.Event(enable_timing=True)
+            b.record(stream)
+        for sq in seqs:
+            d = sq["layers"][p]
+            hs.check(L.hs_gqa_sparse_attention(vp(d["q32"]), vp(d["pool"]),
+                                               ctypes.c_void_p(d["pool"].data_ptr() + 2048), 4096,
+                                               vp(d["mrows"]), hot_rows + cold_rows + TIER_MISSES,
+                                               vp(d["member"]), TIER_N, vp(d["out"]), vp(d["aws"]),
+                                               sp))
+        if marks is not None:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record(stream)
+            marks.append((b, e))
+
+    def cover_step(with_cold=True, marks=None):
+        """Layer l + 1's history, cover and cover fetch start before layer l's
+        final selection (the early history preparation of the reference's
+        executor); layer l's attention waits for its cover rows."""
+        done = [None] * LAYERS
+
+        def prep(l):
+            cover_prep(l)
+            if with_cold:
+                ev = torch.cuda.Event()
+                ev.record(stream)
+                side.wait_event(ev)
+                cover_fetch(l, sside)
+                done[l] = torch.cuda.Event()
+                done[l].record(side)
+
+        prep(0)
+        for l in range(LAYERS):
+            if l + 1 < LAYERS:
+                prep(l + 1)
+            cover_final(l, fetch_misses=with_cold)
+            if with_cold:
+                stream.wait_event(done[l])
+            cover_attend(l, marks)
+
+    def cover_cold_only():
+        for l in range(LAYERS):
+            cover_fetch(l, sp)
+
     def cold_only(engines=False):
         for l in range(LAYERS):
             (cold_engines if engines else cold)(l, sp)
@@ -968,6 +1098,15 @@ def tier_leg(g, args):
     step(engines=True)
     torch.cuda.synchronize()
     check_outputs("copy engines")
+    cover_step()
+    torch.cuda.synchronize()
+    check_outputs("cover prefetch")
+    misses = [int(d["mcount"].item()) for sq in seqs for d in sq["layers"]]
+    assert max(misses) <= TIER_MISSES, f"configs[4] cover: {max(misses)} misses overflow the staging"
+    for sq in seqs:
+        for d in sq["layers"]:
+            assert ops.read_status(d["cselstatus"])["code"] == 0
+            assert ops.read_status(d["mstatus"])["code"] == 0
     del full, fws
     reps = 2
     step_ms = timed(step, reps)
@@ -976,10 +1115,17 @@ def tier_leg(g, args):
     ce_step_ms = timed(lambda: step(engines=True), reps)
     ce_main_ms = timed(lambda: step(False, engines=True), reps)
     ce_cold_ms = timed(lambda: cold_only(True), reps)
+    cv_step_ms = timed(cover_step, reps)
+    cv_main_ms = timed(lambda: cover_step(False), reps)
+    cv_cold_ms = timed(cover_cold_only, reps)
+    cover_counts = [int(d["ccount"].item()) for sq in seqs for d in sq["layers"]]
     attn_alone_us = 1e3 * timed(lambda: [attend(l, True) for l in range(LAYERS)], reps) / (
         LAYERS * TIER_SEQS)
     attn_kernel_us = attention_us(lambda m: step(marks=m))
     attn_engines_us = attention_us(lambda m: step(engines=True, marks=m))
+    attn_cover_us = attention_us(lambda m: cover_step(marks=m))
+    cv_overlap = max(0.0, min(1.0, (cv_main_ms + cv_cold_ms - cv_step_ms) / cv_cold_ms))
+    cv_bytes = sum(cover_counts) / len(cover_counts) * TIER_SEQS * LAYERS * 4128
     cold_bytes = sum(counts) / len(counts) * TIER_SEQS * LAYERS * 4128
     overlap = max(0.0, min(1.0, (main_ms + cold_ms - step_ms) / cold_ms))
     ce_bytes = cold_rows * TIER_SEQS * LAYERS * 4128
@@ -1008,6 +1154,20 @@ def tier_leg(g, args):
             "attention_us_in_step": attn_engines_us,
             "runs_per_seq": sum(sq["runs"][2] for sq in seqs) / len(seqs),
         },
+        "cover_prefetch": {
+            "what": "the payload prefetch of the reference's executor on the device: layer l+1's "
+                    "history scored, its history cover selected (HS_SELECT_COVER) and the cover's "
+                    "cold rows fetched on the side stream before layer l's final selection; after "
+                    "the final selection (current token completed) only the selected cold rows "
+                    "outside the cover are fetched, on the main stream",
+            "ms_per_step": cv_step_ms, "main_stream_ms": cv_main_ms, "cold_fetch_ms": cv_cold_ms,
+            "cold_link_gbps": cv_bytes / (cv_cold_ms * 1e-3) / 1e9,
+            "overlap_fraction": cv_overlap,
+            "overlap_ceiling": min(1.0, cv_main_ms / cv_cold_ms),
+            "cover_cold_rows_per_seq_layer": sum(cover_counts) / len(cover_counts),
+            "misses_per_seq_layer": sum(misses) / len(misses),
+            "attention_us_in_step": attn_cover_us,
+        },
     }
     log(f"configs[4]: {step_ms:.1f} ms/step (main stream alone {main_ms:.1f} ms, cold fetch alone "
         f"{cold_ms:.1f} ms = {out['cold_link_gbps']:.1f} GB/s over the host link, "
@@ -1018,6 +1178,12 @@ def tier_leg(g, args):
         f"{ce_cold_ms:.1f} ms = {out['copy_engines']['cold_link_gbps']:.1f} GB/s, "
         f"{out['copy_engines']['runs_per_seq']:.0f} runs per sequence-layer); overlap "
         f"{ce_overlap:.3f}; attention {attn_engines_us:.1f} us per call in the step")
+    cv = out["cover_prefetch"]
+    log(f"configs[4] cover prefetch: {cv_step_ms:.1f} ms/step (main {cv_main_ms:.1f} ms, cover "
+        f"fetch {cv_cold_ms:.1f} ms = {cv['cold_link_gbps']:.1f} GB/s, "
+        f"{cv['cover_cold_rows_per_seq_layer']:.0f} cover rows and "
+        f"{cv['misses_per_seq_layer']:.2f} misses per sequence-layer); overlap {cv_overlap:.3f}; "
+        f"attention {attn_cover_us:.1f} us per call in the step")
     del seqs
     return out
 
