@@ -543,10 +543,11 @@ def layer_leg(g, args):
     for stt in b.statuses:
         assert ops.read_status(stt)["code"] == 0
     assert torch.equal(b.ids, serial_ids), "pipelined and one-layer-at-a-time ids differ"
-    # the pipelined attention forms its dots itself (MFMA, split F32 query):
-    # the same output to about 1e-6 relative
+    # the pipelined attention forms its dots itself (MFMA, split F32 query)
+    # and rounds its softmax weights to F16 once, as the fused layer does:
+    # a weight may round to the other neighbour (2^-11 relative)
     rel = float(((b.out - serial_out).norm(dim=1) / serial_out.norm(dim=1)).max())
-    assert rel <= 1e-4, f"pipelined and fused-layer attention differ: {rel:.3g}"
+    assert rel <= 1e-3, f"pipelined and fused-layer attention differ: {rel:.3g}"
     pipe_us = g.timed_us(b.pipelined_pass, args.layer_steps, LAYERS)
 
     b.select_last()

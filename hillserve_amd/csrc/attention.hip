@@ -50,7 +50,41 @@ __device__ __forceinline__ float first_lane(float v) {
 }
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// o += p * V on v_dot2_f32_f16, two rows per instruction.  Each softmax
+// weight p is rounded once to F16 (RNE) and l sums the same rounded weights,
+// so the weights o / l applies stay consistent (a relative change of at most
+// 2^-11 per weight); the products of two F16 are exact in FP32 and the sums
+// are FP32.
+__device__ __forceinline__ float weight_f16(float p) { return h2f(f2h(p)); }
+// weights of rows a and b (values already F16, so the packing conversion's
+// rounding toward zero is exact) as one dot2 operand
+__device__ __forceinline__ half2v weight_pair(float a, float b) {
+    return __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+// channel 2w (lo) or 2w+1 (hi) of rows a and b, from their word w
+__device__ __forceinline__ half2v rows_lo(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(b, a, 0x05040100u));
+}
+__device__ __forceinline__ half2v rows_hi(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(b, a, 0x07060302u));
+}
+// 8 channels of rows a and b (16 B each) into o[4 heads][8 channels]
+__device__ __forceinline__ void accumulate_pair(float (&o)[4][8], const half2v (&w)[4], const uint4& va,
+                                                const uint4& vb) {
+    const uint32_t wa[4] = {va.x, va.y, va.z, va.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+    for (uint32_t c2 = 0; c2 < 4; ++c2) {
+        const half2v lo = rows_lo(wa[c2], wb[c2]), hi = rows_hi(wa[c2], wb[c2]);
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            o[j][2 * c2] = __builtin_amdgcn_fdot2(w[j], lo, o[j][2 * c2], false);
+            o[j][2 * c2 + 1] = __builtin_amdgcn_fdot2(w[j], hi, o[j][2 * c2 + 1], false);
+        }
+    }
+}
 
 // ---- K and V rows in two waves of loads -------------------------------------
 // One workgroup per kChunk ids, one wave per KV head g; the union's loads
@@ -215,7 +249,7 @@ attn_kv_kernel(const float* __restrict__ q, const uint8_t* __restrict__ pool, ui
             float p[4];
 #pragma unroll
             for (uint32_t j = 0; j < 4; ++j) {
-                p[j] = sv[j] == -INFINITY ? 0.0f : __expf(sv[j] - m[j]);
+                p[j] = sv[j] == -INFINITY ? 0.0f : weight_f16(__expf(sv[j] - m[j]));
                 ps[j] += p[j];
             }
             if (64 * c + lane < total) sel_p[g][64 * c + lane] = make_float4(p[0], p[1], p[2], p[3]);
@@ -234,25 +268,15 @@ attn_kv_kernel(const float* __restrict__ q, const uint8_t* __restrict__ pool, ui
     for (uint32_t t = 0; t < kTiles; ++t) {
         if (t < tiles) {
 #pragma unroll
-            for (uint32_t i = 0; i < 4; ++i) {
+            for (uint32_t i = 0; i < 4; i += 2) {  // rows 16t + 4i + q16 and 4 after it
                 const uint32_t e = 16 * t + 4 * i + q16;
-                const float4 pp = sel_p[g][min(e, total - 1)];
-                const bool live = e < total;
-                const float p0 = live ? pp.x : 0.0f, p1 = live ? pp.y : 0.0f;
-                const float p2 = live ? pp.z : 0.0f, p3 = live ? pp.w : 0.0f;
-                const uint32_t vwords[4] = {vw[t][i].x, vw[t][i].y, vw[t][i].z, vw[t][i].w};
-#pragma unroll
-                for (uint32_t c2 = 0; c2 < 4; ++c2) {
-                    const float v0 = h2f(vwords[c2] & 0xffffu), v1 = h2f(vwords[c2] >> 16);
-                    o[0][2 * c2] = __builtin_fmaf(p0, v0, o[0][2 * c2]);
-                    o[1][2 * c2] = __builtin_fmaf(p1, v0, o[1][2 * c2]);
-                    o[2][2 * c2] = __builtin_fmaf(p2, v0, o[2][2 * c2]);
-                    o[3][2 * c2] = __builtin_fmaf(p3, v0, o[3][2 * c2]);
-                    o[0][2 * c2 + 1] = __builtin_fmaf(p0, v1, o[0][2 * c2 + 1]);
-                    o[1][2 * c2 + 1] = __builtin_fmaf(p1, v1, o[1][2 * c2 + 1]);
-                    o[2][2 * c2 + 1] = __builtin_fmaf(p2, v1, o[2][2 * c2 + 1]);
-                    o[3][2 * c2 + 1] = __builtin_fmaf(p3, v1, o[3][2 * c2 + 1]);
-                }
+                const float4 pa = sel_p[g][min(e, total - 1)], pb = sel_p[g][min(e + 4, total - 1)];
+                const bool la = e < total, lb = e + 4 < total;
+                const half2v w[4] = {weight_pair(la ? pa.x : 0.0f, lb ? pb.x : 0.0f),
+                                     weight_pair(la ? pa.y : 0.0f, lb ? pb.y : 0.0f),
+                                     weight_pair(la ? pa.z : 0.0f, lb ? pb.z : 0.0f),
+                                     weight_pair(la ? pa.w : 0.0f, lb ? pb.w : 0.0f)};
+                accumulate_pair(o, w, vw[t][i], vw[t][i + 1]);
             }
         }
     }
@@ -401,7 +425,7 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
             float p[4];
 #pragma unroll
             for (uint32_t j = 0; j < 4; ++j) {
-                p[j] = sv[j] == -INFINITY ? 0.0f : __expf(sv[j] - m[j]);
+                p[j] = sv[j] == -INFINITY ? 0.0f : weight_f16(__expf(sv[j] - m[j]));
                 ps[j] += p[j];
             }
             if (64 * c + lane < total) sel_p[g][64 * c + lane] = make_float4(p[0], p[1], p[2], p[3]);
@@ -416,31 +440,20 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
     for (uint32_t j = 0; j < 4; ++j)
 #pragma unroll
         for (uint32_t c = 0; c < 8; ++c) o[j][c] = 0.0f;
-    // each group's p is read one group ahead, under the previous group's
-    // FMAs (a read inside the group's own test waits a full LDS round trip)
-    float4 pnext = sel_p[g][min(q16, total - 1)];
+    // groups i and i + 1 (rows 4i + q16 and 4 after it) per step; a group
+    // past the union's last holds zero weights and zero rows
 #pragma unroll
-    for (uint32_t i = 0; i < kGroups; ++i) {
+    for (uint32_t i = 0; i < kGroups; i += 2) {
         if (i < groups) {
             const uint32_t e = 4 * i + q16;
-            const float4 pp = pnext;
-            if (i + 1 < kGroups) pnext = sel_p[g][min(e + 4, total - 1)];
-            const bool live = e < total;
-            const float p0 = live ? pp.x : 0.0f, p1 = live ? pp.y : 0.0f;
-            const float p2 = live ? pp.z : 0.0f, p3 = live ? pp.w : 0.0f;
-            const uint32_t vwords[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
-#pragma unroll
-            for (uint32_t c2 = 0; c2 < 4; ++c2) {
-                const float v0 = h2f(vwords[c2] & 0xffffu), v1 = h2f(vwords[c2] >> 16);
-                o[0][2 * c2] = __builtin_fmaf(p0, v0, o[0][2 * c2]);
-                o[1][2 * c2] = __builtin_fmaf(p1, v0, o[1][2 * c2]);
-                o[2][2 * c2] = __builtin_fmaf(p2, v0, o[2][2 * c2]);
-                o[3][2 * c2] = __builtin_fmaf(p3, v0, o[3][2 * c2]);
-                o[0][2 * c2 + 1] = __builtin_fmaf(p0, v1, o[0][2 * c2 + 1]);
-                o[1][2 * c2 + 1] = __builtin_fmaf(p1, v1, o[1][2 * c2 + 1]);
-                o[2][2 * c2 + 1] = __builtin_fmaf(p2, v1, o[2][2 * c2 + 1]);
-                o[3][2 * c2 + 1] = __builtin_fmaf(p3, v1, o[3][2 * c2 + 1]);
-            }
+            const float4 pa = sel_p[g][min(e, total - 1)], pb = sel_p[g][min(e + 4, total - 1)];
+            const bool la = e < total, lb = e + 4 < total;
+            const half2v w[4] = {weight_pair(la ? pa.x : 0.0f, lb ? pb.x : 0.0f),
+                                 weight_pair(la ? pa.y : 0.0f, lb ? pb.y : 0.0f),
+                                 weight_pair(la ? pa.z : 0.0f, lb ? pb.z : 0.0f),
+                                 weight_pair(la ? pa.w : 0.0f, lb ? pb.w : 0.0f)};
+            const uint4 vb = i + 1 < groups ? vw[i + 1] : make_uint4(0u, 0u, 0u, 0u);
+            accumulate_pair(o, w, vw[i], vb);
         }
     }
 #pragma unroll

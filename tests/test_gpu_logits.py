@@ -5,7 +5,8 @@ Bars: the raw scores and tile maxima equal the plain scorer's bit for bit;
 the dots are within 1e-5 relative of an FP64 dot of the same F32 query and
 F16 keys; the attention is within 2e-3 of the FP64 oracle on the same
 selection, with and without a row map, and agrees
-closely with the attention that reads K itself."""
+with the attention that reads K itself within 1e-3 (both round their
+softmax weights to F16 once)."""
 import numpy as np
 import pytest
 import torch
@@ -68,7 +69,10 @@ def test_attention_from_dots(hs, port, n, frac, mapped):
     ref = port.attention(q32, records.view(np.uint8).reshape(-1), ids, rows=perm)
     got = out.cpu().numpy().astype(np.float64)
     assert rel_err(got, ref) <= TOL
-    # against the attention that reads K itself (MFMA dots of a split query)
+    # against the attention that reads K itself (MFMA dots of a split query):
+    # each form rounds its softmax weights to F16 once, and the two forms'
+    # dots differ in their last bits, so a weight may round to the other
+    # neighbour (2^-11 relative); over few rows that does not average out
     via_k = hs.ops.sparse_attention(qd, k_rows, n, member, rows=rows, v_pool=v_rows,
                                     row_bytes=2048).cpu().numpy().astype(np.float64)
-    assert rel_err(got, via_k) <= 1e-4
+    assert rel_err(got, via_k) <= 1e-3
