@@ -178,6 +178,9 @@ struct SelectJobs {
     // with the most ids first, so a batch that runs in more than one round
     // of workgroups starts its longest selections first
     uint8_t order[kMaxBatch];
+    // select-then-score: scoring waves per workgroup (the rest of a
+    // workgroup's waves leave at once) and scoring waves in all
+    uint32_t score_wpb, score_waves;
 };
 
 // The SelectArgs view of job j: its workspace slices follow plan_select.
@@ -1576,11 +1579,14 @@ select_score_kernel(const SelectJobs js, const ScoreJobs sj) {
         return;
     }
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // js.score_wpb waves of each scoring workgroup score (the same number of
+    // waves as a full workgroup per CU would give, spread over more CUs);
     // one half ahead: both halves ahead took more of the memory system from
     // the selection and lengthened the launch
-    score_waves<false, kBatch>(sj, nullptr, 0u,
-                               __builtin_amdgcn_readfirstlane((blockIdx.x - selectors) * kHWaves + w),
-                               (gridDim.x - selectors) * kHWaves, lds.score[w]);
+    const uint32_t id = (blockIdx.x - selectors) * js.score_wpb + w;
+    if (w >= js.score_wpb || id >= js.score_waves) return;
+    score_waves<false, kBatch>(sj, nullptr, 0u, __builtin_amdgcn_readfirstlane(id), js.score_waves,
+                               lds.score[w]);
 }
 
 // ---- 4. rank ----------------------------------------------------------------
@@ -1941,7 +1947,6 @@ int launch_jobs(const SelectJobs& js, hipStream_t stream) {
     return st == hipSuccess ? HS_OK : hip_fail(st, "select launch");
 }
 
-// Checked selection jobs of a batch call.
 // Byte ranges [begin, end) of device buffers; empty for null pointers.
 struct Span {
     uintptr_t begin, end;
@@ -1954,6 +1959,7 @@ bool overlap(const Span& x, const Span& y) {
     return x.begin < x.end && y.begin < y.end && x.begin < y.end && y.begin < x.end;
 }
 
+// Checked selection jobs of a batch call.
 int build_select_jobs(const hs_select_job_t* jobs, uint32_t count, uint32_t heads, float alpha,
                       float ratio, uint32_t flags, SelectJobs& js) {
     if (!jobs || count == 0 || count > kMaxBatch) return reject("select batch: 1..16 jobs");
@@ -2107,7 +2113,10 @@ int launch_select_then_score(const hs_select_job_t* select_jobs, uint32_t select
     const uint32_t cus = static_cast<uint32_t>(device_cu_count());
     const uint32_t free_cus = selectors < cus ? cus - selectors : cus;
     const uint32_t rounds = (sj.total_ids + free_cus * kHWaves - 1) / (free_cus * kHWaves);
-    const uint32_t scorers = std::max(1u, (sj.total_ids + rounds * kHWaves - 1) / (rounds * kHWaves));
+    // the scoring waves those rounds need, spread over every free CU
+    js.score_waves = std::max(1u, (sj.total_ids + rounds - 1) / rounds);
+    js.score_wpb = std::min(kHWaves, (js.score_waves + free_cus - 1) / free_cus);
+    const uint32_t scorers = (js.score_waves + js.score_wpb - 1) / js.score_wpb;
     const dim3 grid(selectors + scorers), block(kHThreads);
     const bool id_order = (js.flags & HS_SELECT_ID_ORDER) != 0, batch = sj.count > 1;
     if (id_order && batch)
