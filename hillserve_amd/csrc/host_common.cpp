@@ -41,6 +41,21 @@ int device_cu_count() {
     return cus;
 }
 
+bool stream_capturing(hipStream_t stream) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
+        (void)hipGetLastError();  // not the caller's launch error
+        return true;
+    }
+    return capture != hipStreamCaptureStatusNone;
+}
+
+void clear_status_if_captured(hs_status_t* status, uint32_t count, hipStream_t stream) {
+    if (status && count && stream_capturing(stream))
+        launch_fill_u32(reinterpret_cast<uint32_t*>(status),
+                        count * static_cast<uint32_t>(sizeof(hs_status_t) / sizeof(uint32_t)), 0u, stream);
+}
+
 uint32_t next_stamp() {
     static std::atomic<uint32_t> calls{0};
     return (calls.fetch_add(1, std::memory_order_relaxed) & 0x7fffffffu) | 0x80000000u;

@@ -24,6 +24,16 @@ int device_cu_count();
 // A fresh status stamp per call (publish_stamped): distinct for 2^31 calls,
 // top bit set.
 uint32_t next_stamp();
+// Whether `stream` is being captured into a graph (true also when the query
+// fails: the caller then takes its capture-safe path).
+bool stream_capturing(hipStream_t stream);
+// `count` words of `dst` set to `value` by a small kernel on `stream` (no
+// hipMemsetAsync: it is captured into graphs as a memset node).
+void launch_fill_u32(uint32_t* dst, uint32_t count, uint32_t value, hipStream_t stream);
+// A self-stamping call (pack, gather, the rehearsal query) captured into a
+// graph replays one stamp, so a replay would read an earlier replay's error
+// as its own: under capture its status words are cleared first.
+void clear_status_if_captured(hs_status_t* status, uint32_t count, hipStream_t stream);
 
 inline hipStream_t as_stream(void* stream) { return static_cast<hipStream_t>(stream); }
 

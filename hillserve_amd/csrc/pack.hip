@@ -33,6 +33,15 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t count, uint
     if (i < count) dst[i] = value;
 }
 
+}  // namespace
+
+void launch_fill_u32(uint32_t* dst, uint32_t count, uint32_t value, hipStream_t stream) {
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((count + 255) / 256), dim3(256), 0, stream, dst, count,
+                       value);
+}
+
+namespace {
+
 __device__ __forceinline__ void raise(hs_status_t* status, int code) {
     atomicCAS(reinterpret_cast<int*>(&status->code), HS_OK, code);
 }
@@ -338,6 +347,7 @@ int hs_gqa_pack(const uint8_t* k_pool_dev, const uint8_t* v_pool_dev, size_t row
     hs::PoolSource ps{k_pool_dev, pool_rows, static_cast<uint32_t>(row_bytes), v_delta,
                       row_of_id_dev, max_id, ids_dev, lens_dev, static_cast<uint32_t>(ids_stride)};
     hs::MapSource ms{nullptr, nullptr, nullptr};
+    hs::clear_status_if_captured(status_dev, 1, s);
     hipLaunchKernelGGL(hs::pack_kernel<true>, dim3((count + 63) / 64, 32), dim3(256), 0, s, ps, ms,
                        positions_dev, nq, count, k_dev, v_dev, mask_dev, status_dev,
                        hs::next_stamp());
@@ -357,6 +367,7 @@ int hs_gqa_gather_rows(const uint16_t* prefetched_dev, uint32_t prefetched_rows,
     hs::PoolSource ps{};
     hs::MapSource ms{prefetched_dev, misses_dev, map_dev, prefetched_rows, miss_rows};
     hipStream_t s = hs::as_stream(stream);
+    hs::clear_status_if_captured(status_dev, 1, s);
     hipLaunchKernelGGL(hs::pack_kernel<false>, dim3((count + 63) / 64, 32), dim3(256), 0, s, ps,
                        ms, nullptr, 0u, count, k_dev, v_dev, nullptr, status_dev, hs::next_stamp());
     const hipError_t st = hipGetLastError();

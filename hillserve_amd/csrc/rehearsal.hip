@@ -188,6 +188,7 @@ int launch_rehearsal(const uint16_t* hidden, const uint16_t* wq, const uint32_t*
     for (uint32_t b = 0; b < batch; ++b) args.pos[b] = positions[b];
     for (uint32_t i = 0; i < 64; ++i)
         args.inv_freq[i] = std::pow(static_cast<double>(theta), -2.0 * static_cast<double>(i) / 128.0);
+    clear_status_if_captured(status, batch, stream);
     hipLaunchKernelGGL(rehearsal_kernel, dim3(kTiles), dim3(kSplits * 64), 0, stream, args);
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hip_fail(st, "rehearsal launch");

@@ -233,7 +233,9 @@ int hs_gqa_select_then_score(const hs_select_job_t *select_jobs, uint32_t select
  * (nullable, [batch], 8-byte aligned, no clearing needed) gets per sequence
  * HS_ERR_NONFINITE for a nonfinite value and HS_ERR_OVERFLOW for one beyond
  * F16, as query_f16 rejects them, else HS_OK; the launch writes it itself
- * (its k field holds a stamp of the call, the other fields are unchanged).
+ * (its k field holds a stamp of the call, the other fields are unchanged;
+ * under graph capture the call first clears the status words with a small
+ * kernel, since every replay carries the captured stamp).
  * workspace_dev is not used (nullable); hs_rehearsal_workspace_bytes is kept
  * for callers that size one. */
 size_t hs_rehearsal_workspace_bytes(uint32_t batch);
@@ -334,7 +336,10 @@ int hs_gqa_physical_union(const uint32_t *ids_dev, const uint32_t *lens_dev,
  * byte-identical to the reference, zero/-inf padding included.
  * Status: status_dev (8-byte aligned) needs no clearing before the call;
  * the call reports through status->code (HS_OK or its first error) and
- * leaves a stamp of its own in status->k (the other fields unchanged). */
+ * leaves a stamp of its own in status->k (the other fields unchanged).
+ * Under graph capture the call enqueues a one-workgroup clear of the status
+ * before its kernel: every replay carries the captured stamp, so without it a
+ * replay would read an earlier replay's error as its own. */
 int hs_gqa_pack(const uint8_t *k_pool_dev, const uint8_t *v_pool_dev, size_t row_bytes,
                 uint32_t pool_rows, const int32_t *row_of_id_dev, uint32_t max_id,
                 const uint32_t *ids_dev,

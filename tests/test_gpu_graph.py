@@ -185,3 +185,62 @@ def test_failed_middle_layer_is_reported_not_stale(hs):
     assert codes == [hs.HS_OK, hs.HS_ERR_NONFINITE, hs.HS_OK], codes
     assert torch.isnan(outs[1]).all()
     assert torch.isfinite(outs[0]).all() and torch.isfinite(outs[2]).all()
+
+
+def test_self_stamped_status_under_graph_replays(hs):
+    """Gather and the rehearsal query stamp their own status with a per-call
+    stamp; a captured call replays the captured stamp, so under capture the
+    library clears the status first.  Replays alternate failing and clean
+    inputs (written in place between replays, eagerly): every replay reports
+    its own outcome, a clean one after a failing one reads HS_OK, and the
+    rows equal the eager call's."""
+    dev = "cuda"
+    slots = 32
+    g = torch.Generator(device="cpu").manual_seed(5)
+    pre = torch.randint(0, 256, (3 * 4096,), dtype=torch.uint8, generator=g).to(dev)
+    row_map = torch.full((32 * slots,), -1, dtype=torch.int32, device=dev)
+    good = row_map.clone()
+    good[::slots] = 0
+    good[1::slots] = 2
+    bad = good.clone()
+    bad[5] = 3  # beyond the three prefetched rows
+    hidden = torch.randn((4, 4096), generator=g).to(torch.bfloat16).to(dev)
+    wq = (torch.randn((4096, 4096), generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    hidden_bad = hidden.clone()
+    hidden_bad[2, 7] = float("nan")
+    h_in = hidden.clone()
+    q_out = torch.empty((4, 32, 128), dtype=torch.float16, device=dev)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        row_map.copy_(good)
+        eager_k, eager_v, _ = hs.ops.gather_rows(pre, None, row_map, slots)
+        eager_q, _ = hs.ops.rehearsal_query(h_in, wq, [100, 200, 300, 400])
+        torch.cuda.synchronize()
+        captured = {}
+
+        def step():
+            captured["gather"] = hs.ops.gather_rows(pre, None, row_map, slots)
+            captured["rehearsal"] = hs.ops.rehearsal_query(h_in, wq, [100, 200, 300, 400],
+                                                           out=q_out)
+
+        graph = capture(step, side)
+        for rnd, failing in enumerate([True, False, False, True, False]):
+            row_map.copy_(bad if failing else good)
+            h_in.copy_(hidden_bad if failing else hidden)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            k, v, st = captured["gather"]
+            q, qst = captured["rehearsal"]
+            code = hs.ops.read_status(st)["code"]
+            codes = [int(c) for c in qst[:, 0].cpu().tolist()]
+            if failing:
+                assert code == hs.HS_ERR_MISSING, (rnd, code)
+                assert codes == [0, 0, hs.HS_ERR_NONFINITE, 0], (rnd, codes)
+            else:
+                assert code == 0, (rnd, code)
+                assert codes == [0, 0, 0, 0], (rnd, codes)
+                # bit patterns (random bytes hold NaN encodings, which == refuses)
+                bits = lambda t: t.view(torch.int16)
+                assert torch.equal(bits(k), bits(eager_k)) and torch.equal(bits(v), bits(eager_v))
+                assert torch.equal(bits(q), bits(eager_q))
