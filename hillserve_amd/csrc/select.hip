@@ -516,29 +516,22 @@ __device__ __forceinline__ uint32_t sat_sub(uint32_t a, uint32_t b) { return a -
 // s = fl(s + fl(q[c] * k[c])) over channels 0..127 in order, rounded to F16
 // once.  F16 x F16 products are exact in FP32, so each step is one FMA, as
 // in the scorer.  q F16 [32][128], key F16 [8][128] (query head h reads KV
-// head h / 4).  One lane computes it.
-__device__ __noinline__ uint32_t score_current(const uint16_t* q, const uint16_t* key, uint32_t h) {
-    // global (not flat) loads: in a call the pointers' address space is
-    // unknown, and flat loads can only be waited for all at once
-    using GlobalU32 = const __attribute__((address_space(1))) uint32_t;
-    GlobalU32* qv = (GlobalU32*)(q + h * 128);
-    GlobalU32* kv = (GlobalU32*)(key + (h >> 2) * 128);
-    uint4 qa[16], ka[16];
-#pragma unroll
-    for (uint32_t i = 0; i < 16; ++i) {
-        qa[i] = make_uint4(qv[4 * i], qv[4 * i + 1], qv[4 * i + 2], qv[4 * i + 3]);
-        ka[i] = make_uint4(kv[4 * i], kv[4 * i + 1], kv[4 * i + 2], kv[4 * i + 3]);
-    }
+// head h / 4).  A whole wave computes it (every lane active; every lane
+// returns it): lane l loads channels 2l and 2l + 1 of the query row and of
+// the K row, one 4-byte word each, so the wave's loads are two 256-byte rows
+// in one round trip and hold two registers, and every lane runs the
+// 128-step chain over the words read back from the lanes in channel order.
+__device__ __forceinline__ uint32_t score_current(const uint16_t* q, const uint16_t* key, uint32_t h) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t qw = reinterpret_cast<const uint32_t*>(q + h * 128)[lane];
+    const uint32_t kw = reinterpret_cast<const uint32_t*>(key + (h >> 2) * 128)[lane];
     float s = 0.0f;
 #pragma unroll
-    for (uint32_t i = 0; i < 16; ++i) {
-        const uint32_t qw[4] = {qa[i].x, qa[i].y, qa[i].z, qa[i].w};
-        const uint32_t kw[4] = {ka[i].x, ka[i].y, ka[i].z, ka[i].w};
-#pragma unroll
-        for (uint32_t p = 0; p < 4; ++p) {
-            s = __builtin_fmaf(h2f(qw[p] & 0xffffu), h2f(kw[p] & 0xffffu), s);
-            s = __builtin_fmaf(h2f(qw[p] >> 16), h2f(kw[p] >> 16), s);
-        }
+    for (uint32_t c = 0; c < 64; ++c) {
+        const uint32_t qc = __builtin_amdgcn_readlane(qw, c);
+        const uint32_t kc = __builtin_amdgcn_readlane(kw, c);
+        s = __builtin_fmaf(h2f(qc & 0xffffu), h2f(kc & 0xffffu), s);
+        s = __builtin_fmaf(h2f(qc >> 16), h2f(kc >> 16), s);
     }
     return f2h(s);
 }
@@ -603,10 +596,9 @@ struct CountLds {
 // kR * t + kR - 1 of head h (g = h * ceil(S / kR) + t), each thread kRun
 // consecutive ids of every slice, so every load and key store of a wave
 // covers whole consecutive lines.  kR > 1 only for batches whose score rows
-// are all 16-byte aligned with n >= 8 (checked by the host).  kCurrent: some job of the batch completes
-// its current token (the scoring call it makes takes more registers than the
-// rest of the count: batches without one run the leaner instance, four
-// workgroups per CU).
+// are all 16-byte aligned with n >= 8 (checked by the host).  kCurrent: some
+// job of the batch completes its current token (waves 0 and 1 of a group
+// score its column; batches without one compile that part out).
 template <bool kCurrent, uint32_t kR>
 __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, uint32_t job,
                                             CountLds& lds) {
@@ -634,23 +626,26 @@ __device__ __forceinline__ void count_group(const SelectJobs& js, uint32_t g, ui
     for (uint32_t i = tid; i < kR * kCountHist; i += kThreads) whist[i] = 0;
     if (tid == 0) lds.bad = 0;
     // Current-token completion: column n - 1 is scored here from the query
-    // and the appended K row.  Every group folds its head-0 score into the
-    // threshold maximum (wave 0); the group holding the column scores it for
-    // its head (wave 1, on another SIMD), writes it into the scores and
+    // and the appended K row, each score by a whole wave.  Every group folds
+    // its head-0 score into the threshold maximum (wave 0); the group holding
+    // the column scores it for its head (wave 1, on another SIMD), writes it
+    // into the scores and
     // counts it in place of what the column held.
     const uint32_t last = a.n - 1u;
     const bool holds_last =
         kCurrent && a.cur_key && last >= first * kSlice && last < (first + kR) * kSlice;
     if (kCurrent && a.cur_key) {
-        if (tid == 0) {
+        const uint32_t wave = tid >> 6;  // (the branches below are wave-uniform)
+        if (wave == 0) {
             const uint32_t c0 = score_current(a.cur_q, a.cur_key, 0);
-            if (!is_nan_half(c0)) best = max(best, order_key(c0));
-        }
-        if (tid == 64 && holds_last) {
+            if (tid == 0 && !is_nan_half(c0)) best = max(best, order_key(c0));
+        } else if (wave == 1 && holds_last) {
             const uint32_t ch = score_current(a.cur_q, a.cur_key, h);
-            lds.current = ch;
-            const_cast<uint16_t*>(a.scores)[static_cast<size_t>(h) * a.stride + last] =
-                static_cast<uint16_t>(ch);
+            if (tid == 64) {
+                lds.current = ch;
+                const_cast<uint16_t*>(a.scores)[static_cast<size_t>(h) * a.stride + last] =
+                    static_cast<uint16_t>(ch);
+            }
         }
     }
     best = block_max(best, tmp);  // its barrier also orders the histogram clear
