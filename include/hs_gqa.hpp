@@ -232,7 +232,9 @@ private:
 //       the call waits for the delivery and returns its timings.
 // Geometry and stream errors throw std::runtime_error, as the reference's;
 // device failures throw DeviceError.  stage and deliver may run on different
-// threads for different slots; calls on one slot must be serialized.
+// threads for different slots; calls on one slot must be serialized, and
+// deliver calls must not overlap one another (they share the staging of the
+// misses, map and mask), as the executor delivers from one thread.
 class GQAPrefetchGpu {
 public:
     struct Upload {
