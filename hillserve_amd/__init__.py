@@ -147,6 +147,7 @@ SIGNATURES = {
     "hs_decode_layer_noalloc": (_I, [_P, _P, _P, _P, _SZ, _P, _U32, _U32, _F, _F, _U32, _P, _P, _SZ, _P, _P, _P, _P]),
     "hs_selftest_f16_checksums": (_I, [_P, _P]),
     "hs_selftest_scale_table": (_I, [_P, _P]),
+    "hs_selftest_key_table": (_I, [_P, _P]),
     "hs_fill_gaussian_f16": (_I, [_P, _SZ, _U64, _F, _P]),
     "hs_fill_rope_keys_f16": (_I, [_P, _U32, _SZ, _U32, _U64, _F, _P]),
 }

@@ -63,6 +63,32 @@ __device__ __forceinline__ uint32_t scale_finite(uint32_t raw) {
     return f2h(__builtin_fmaf(e, kRecip, q0)) | (raw & 0x8000u);
 }
 
+// Order keys of the two finite F16 values of x (low half first), scaled
+// first when kScale: order_key(scale_finite(b)) per half.  The quotient is
+// that of scale_finite computed on the signed value (the steps are symmetric
+// in the sign, so only a zero's sign can differ, and -0 and +0 share a key).
+// The key of both halves at once: an F16 add of +0 turns -0 into +0, then
+// negative halves flip every bit and the others the top bit.
+__device__ __forceinline__ uint32_t pair_keys_from_bits(uint32_t p) {
+    asm("v_pk_add_f16 %0, %1, 0" : "=v"(p) : "v"(p));
+    uint32_t s;
+    // (op_sel_hi:[0,1]: the high half shifts by the constant's low half too)
+    asm("v_pk_ashrrev_i16 %0, 15, %1 op_sel_hi:[0,1]" : "=v"(s) : "v"(p));
+    return p ^ (s | 0x80008000u);
+}
+template <bool kScale>
+__device__ __forceinline__ uint32_t pair_keys(uint32_t x) {
+    if constexpr (kScale) {
+        constexpr float kRoot = 0x1.6a09e6p+3f;
+        constexpr float kRecip = 0x1.6a09e6p-4f;
+        const float xl = h2f(x & 0xffffu), xh = h2f(x >> 16);
+        const float ql = xl * kRecip, qh = xh * kRecip;
+        const float el = __builtin_fmaf(-ql, kRoot, xl), eh = __builtin_fmaf(-qh, kRoot, xh);
+        x = f2h(__builtin_fmaf(el, kRecip, ql)) | (f2h(__builtin_fmaf(eh, kRecip, qh)) << 16);
+    }
+    return pair_keys_from_bits(x);
+}
+
 __device__ __forceinline__ bool is_nan_half(uint32_t bits) {
     return (bits & 0x7c00u) == 0x7c00u && (bits & 0x03ffu) != 0;
 }

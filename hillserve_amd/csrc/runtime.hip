@@ -64,6 +64,18 @@ __global__ void scale_table_kernel(uint16_t* __restrict__ out) {
     if (i < 65536) out[i] = static_cast<uint16_t>(scale_raw(i));
 }
 
+// out[0][b] = pair_keys<true> of b, out[1][b] = pair_keys<false> of b, for
+// all 65536 patterns, two per thread (values of inf / NaN inputs are unused
+// by the kernels).
+__global__ void key_table_kernel(uint32_t* __restrict__ out) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;  // pair index
+    if (i < 32768) {
+        const uint32_t x = (2 * i) | ((2 * i + 1) << 16);
+        out[i] = pair_keys<true>(x);
+        out[32768 + i] = pair_keys<false>(x);
+    }
+}
+
 // ---- synthetic inputs --------------------------------------------------------
 
 __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
@@ -245,6 +257,15 @@ int hs_selftest_scale_table(uint16_t* table_dev, void* stream) {
     if (!table_dev) return hs::reject("selftest: null pointer");
     hipLaunchKernelGGL(hs::scale_table_kernel, dim3(256), dim3(256), 0, hs::as_stream(stream),
                        table_dev);
+    const hipError_t st = hipGetLastError();
+    return st == hipSuccess ? HS_OK : hs::hip_fail(st, "selftest launch");
+}
+
+int hs_selftest_key_table(uint16_t* keys_dev, void* stream) {
+    hs::clear_error();
+    if (!keys_dev || (reinterpret_cast<uintptr_t>(keys_dev) & 3u)) return hs::reject("selftest: null or unaligned pointer");
+    hipLaunchKernelGGL(hs::key_table_kernel, dim3(128), dim3(256), 0, hs::as_stream(stream),
+                       reinterpret_cast<uint32_t*>(keys_dev));
     const hipError_t st = hipGetLastError();
     return st == hipSuccess ? HS_OK : hs::hip_fail(st, "selftest launch");
 }

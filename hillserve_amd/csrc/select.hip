@@ -354,6 +354,11 @@ __device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {
     asm("v_pk_sub_u16 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
     return d;
 }
+__device__ __forceinline__ uint32_t pk_add_u16(uint32_t a, uint32_t b) {
+    uint32_t d;
+    asm("v_pk_add_u16 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
 __device__ __forceinline__ uint32_t pk_min1_u16(uint32_t a) {  // min(half, 1) per half
     uint32_t d;
     asm("v_pk_min_u16 %0, %1, 1 op_sel_hi:[1,0]" : "=v"(d) : "v"(a));
@@ -554,22 +559,24 @@ __device__ __forceinline__ void partial_loads(const SelectArgs& a, uint32_t (&v)
 }
 
 // ---- 1. count ---------------------------------------------------------------
-// One run of kRun finite scores, every id below n: order keys into keyw, each
-// key into the slice histogram, and the number of keys >= kthr (the
-// threshold as a key), with no branch.
+// One run of kRun finite scores, every id below n: order keys into keyw (two
+// to a word, pair_keys), each key into the slice histogram, and the number of
+// keys >= kthr (the threshold as a key), with no branch.
 template <bool kScale>
 __device__ __forceinline__ uint32_t count_clean_run(const uint32_t (&packed)[kRun / 2], uint32_t kthr,
                                                     uint32_t* slice_hist, uint32_t (&keyw)[kRun / 2]) {
-    uint32_t count = 0;
+    // finite keys are <= 0xfbff: a threshold key above 0xffff counts none of them
+    const uint32_t kt2 = min(kthr, 0xffffu) * 0x10001u;
+    uint32_t below = 0;  // per half: keys < kthr
 #pragma unroll
-    for (uint32_t j = 0; j < kRun; ++j) {
-        const uint32_t raw = half_at(packed, j);
-        const uint32_t key = order_key(kScale ? scale_finite(raw) : raw);
-        keyw[j >> 1] |= key << ((j & 1u) * 16u);
-        count += key >= kthr ? 1u : 0u;
-        atomicAdd(&slice_hist[key >> 8], 1u);
+    for (uint32_t w = 0; w < kRun / 2; ++w) {
+        const uint32_t kw = pair_keys<kScale>(packed[w]);
+        keyw[w] = kw;
+        below = pk_add_u16(below, pk_min1_u16(pk_sub_sat_u16(kt2, kw)));
+        atomicAdd(&slice_hist[(kw >> 8) & 0xffu], 1u);
+        atomicAdd(&slice_hist[kw >> 24], 1u);
     }
-    return count;
+    return kRun - (below & 0xffffu) - (below >> 16);
 }
 
 // A count group covers kR consecutive slices of one head; it publishes each

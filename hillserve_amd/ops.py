@@ -604,6 +604,14 @@ def selftest_scale_table(stream=None):
     return out
 
 
+def selftest_key_table(stream=None):
+    """[2, 65536] order keys the selection computes two at a time: row 0 of
+    the scaled values, row 1 of the raw ones (finite inputs only meaningful)."""
+    out = torch.empty((2, 65536), dtype=torch.int16, device="cuda")
+    check(lib().hs_selftest_key_table(_p(out), _s(stream)))
+    return out
+
+
 def fill_gaussian(t, seed, scale=1.0, stream=None):
     check(lib().hs_fill_gaussian_f16(_p(t), t.numel(), seed, scale, _s(stream)))
     return t

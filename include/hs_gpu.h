@@ -457,6 +457,10 @@ int hs_decode_layer_noalloc(const uint16_t *q16_dev, const float *q32_dev,
 int hs_selftest_f16_checksums(uint64_t *checksums_dev, void *stream);
 /* scaled value table for all 65536 raw F16 patterns */
 int hs_selftest_scale_table(uint16_t *table_dev, void *stream);
+/* order keys the selection computes two at a time, for all 65536 patterns:
+ * keys_dev [2][65536] (4-byte aligned), row 0 of the scaled values, row 1 of
+ * the raw ones (entries of inf / NaN inputs are not meaningful) */
+int hs_selftest_key_table(uint16_t *keys_dev, void *stream);
 
 /* ---- synthetic inputs (bench and tests; generated on device) -------------
  * Deterministic counter-based generator: value i of stream `seed` is a
