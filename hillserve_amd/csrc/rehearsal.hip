@@ -16,10 +16,11 @@
 // K = 4096 and HBM-bound (Wq is 32 MiB, read once); each workgroup owns 16
 // output features and its 8 waves split K eight ways, each issuing
 // v_mfma_f32_16x16x32_bf16 over a 512-wide K slice (A = the batch's hidden
-// rows, B = 16 rows of Wq).  A wave reads its Wq slice one row per
-// instruction (64 lanes x 16 B = 1 KiB contiguous) into a padded LDS tile
-// and takes the MFMA B operands from there: read straight into the MFMA
-// layout, an instruction would cover only 64 B of each of 16 rows.  The 8
+// rows, B = 16 rows of Wq), in two halves of 256 columns.  A wave reads each
+// half of its Wq rows and of the hidden rows two rows per instruction (512
+// contiguous bytes of each) into padded LDS tiles and takes both MFMA
+// operands from there: read straight into the MFMA layout, an instruction
+// would cover only 64 B of each of 16 rows.  The 8
 // partial tiles are added in LDS in a fixed order (deterministic), the RMS
 // scale (sums of squares taken from the same A fragments, so hidden is never
 // rounded again) and RoPE (FP64 angle and rotation) run in the epilogue, and
@@ -45,7 +46,6 @@ constexpr uint32_t kTileN = 16;                 // output features per workgroup
 constexpr uint32_t kSplits = 8;                 // waves per workgroup, one K slice each
 constexpr uint32_t kSliceK = kModel / kSplits;  // 512
 constexpr uint32_t kMfmaK = 32;
-constexpr uint32_t kSteps = kSliceK / kMfmaK;   // 16 MFMAs per wave
 constexpr uint32_t kTiles = kModel / kTileN;    // 256 workgroups
 constexpr uint32_t kMaxBatch = 16;
 
@@ -64,12 +64,42 @@ struct RehearsalArgs {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// A wave's Wq slice in LDS: 16 rows of 1 KiB (64 x 16 B), padded by 16 B so
-// the 16 rows of an MFMA operand read fall in different banks.
-constexpr uint32_t kRowChunks = kSliceK * 2 / 16;  // 64
+// A wave's K slice runs in two halves of 256 columns.  Per half, its 16 Wq
+// rows and the batch's 16 hidden rows (512 B each) sit in LDS, padded by
+// 16 B per row so the 16 rows of an MFMA operand read fall in different
+// banks, and both MFMA operands come from there.
+constexpr uint32_t kHalves = 2;
+constexpr uint32_t kHalfK = kSliceK / kHalves;      // 256 columns
+constexpr uint32_t kHalfChunks = kHalfK * 2 / 16;   // 32 chunks of 16 B per row
+constexpr uint32_t kHalfSteps = kHalfK / kMfmaK;    // 8 MFMAs per half
+constexpr uint32_t kRowLoads = kTileN / 2;          // load instructions per 16 rows, 2 rows each
+typedef uint4 HalfTile[kTileN][kHalfChunks + 1];
+
+// The 8 products of one half from its LDS tiles (lane (r, grp): A = hidden
+// row r, B = Wq row o0 + r, columns 32 s + 8 grp .. +7 of the half), and the
+// sums of squares of the same A fragments (bf16 squares are exact in FP32).
+__device__ __forceinline__ void half_products(const HalfTile& wt, const HalfTile& ht, uint32_t r,
+                                              uint32_t grp, bool live, floatx4& acc, float& ss) {
+#pragma unroll
+    for (uint32_t s = 0; s < kHalfSteps; ++s) {
+        uint4 hb = ht[r][4 * s + grp];
+        if (!live) hb = make_uint4(0u, 0u, 0u, 0u);
+        const uint4 wb = wt[r][4 * s + grp];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hb),
+                                                      __builtin_bit_cast(bf16x8, wb), acc, 0, 0, 0);
+        const uint32_t hw[4] = {hb.x, hb.y, hb.z, hb.w};
+#pragma unroll
+        for (uint32_t c = 0; c < 4; ++c) {
+            const float lo = bf16_lo(hw[c]), hi = bf16_hi(hw[c]);
+            ss = __builtin_fmaf(lo, lo, ss);
+            ss = __builtin_fmaf(hi, hi, ss);
+        }
+    }
+}
 
 __global__ void __launch_bounds__(kSplits * 64) rehearsal_kernel(const RehearsalArgs a) {
-    __shared__ uint4 wtile[kSplits][kTileN][kRowChunks + 1];
+    __shared__ HalfTile wtile[kSplits];
+    __shared__ HalfTile htile[kSplits];
     __shared__ float part[kSplits][16][kTileN + 1];
     __shared__ float sq[kSplits][16];
     __shared__ float yv[16][kTileN];
@@ -79,45 +109,51 @@ __global__ void __launch_bounds__(kSplits * 64) rehearsal_kernel(const Rehearsal
     const uint32_t o0 = blockIdx.x * kTileN;
     const uint32_t r = lane & 15u, grp = lane >> 4;  // A row (sequence) / B column (feature)
     const bool live = r < a.batch;
-    const uint32_t k0 = w * kSliceK + 8 * grp;
-    const uint16_t* hrow = a.hidden + static_cast<size_t>(live ? r : 0u) * kModel + k0;
     if (tid < 16) bad[tid] = 0;
 
-    // every load of the K slice is issued before the first product: with 8
-    // waves per CU the whole of Wq is in flight at once.  Wq: row i of the
-    // tile per instruction; hidden (small, cached): straight into the MFMA
-    // layout.
-    const uint16_t* wslice = a.wq + static_cast<size_t>(o0) * kModel + w * kSliceK + lane * 8;
-    uint4 wv[kTileN], hb[kSteps];
+    // Every load of the K slice is requested before the first product: with
+    // 8 waves per CU the whole of Wq is in flight at once, half 0's rows
+    // first, so half 0 is staged and multiplied while half 1 is still on its
+    // way.  Instruction i of a half reads rows 2i and 2i + 1 (lanes 0-31 and
+    // 32-63), 512 contiguous bytes of each, of Wq and of hidden.  (Read
+    // straight into the MFMA layout, a hidden load covers 64 B of each of 16
+    // rows 8 KiB apart; every workgroup reads all of hidden, and that read
+    // alone took ~10 us per call.)
+    const uint32_t pair_row = lane >> 5, chunk = lane & 31u;
+    const uint16_t* wslice = a.wq + static_cast<size_t>(o0 + pair_row) * kModel + w * kSliceK + chunk * 8;
+    const uint16_t* hslice = a.hidden + w * kSliceK + chunk * 8;
+    uint4 wv0[kRowLoads], hv0[kRowLoads], wv1[kRowLoads], hv1[kRowLoads];
+    auto hidden_row = [&](uint32_t i) {  // rows past the batch read row 0 (their A operands are zeroed)
+        const uint32_t row = 2 * i + pair_row;
+        return hslice + static_cast<size_t>(row < a.batch ? row : 0u) * kModel;
+    };
 #pragma unroll
-    for (uint32_t i = 0; i < kTileN; ++i)
-        wv[i] = *reinterpret_cast<const uint4*>(wslice + static_cast<size_t>(i) * kModel);
+    for (uint32_t i = 0; i < kRowLoads; ++i)
+        wv0[i] = *reinterpret_cast<const uint4*>(wslice + static_cast<size_t>(2 * i) * kModel);
 #pragma unroll
-    for (uint32_t s = 0; s < kSteps; ++s)
-        hb[s] = live ? *reinterpret_cast<const uint4*>(hrow + s * kMfmaK)
-                     : make_uint4(0u, 0u, 0u, 0u);
+    for (uint32_t i = 0; i < kRowLoads; ++i) hv0[i] = *reinterpret_cast<const uint4*>(hidden_row(i));
 #pragma unroll
-    for (uint32_t i = 0; i < kTileN; ++i) wtile[w][i][lane] = wv[i];
-    // the tile is this wave's alone: its LDS writes precede its reads in
-    // issue order, and the barrier keeps the compiler from moving them
-    __builtin_amdgcn_wave_barrier();
+    for (uint32_t i = 0; i < kRowLoads; ++i)
+        wv1[i] = *reinterpret_cast<const uint4*>(wslice + static_cast<size_t>(2 * i) * kModel + kHalfK);
+#pragma unroll
+    for (uint32_t i = 0; i < kRowLoads; ++i) hv1[i] = *reinterpret_cast<const uint4*>(hidden_row(i) + kHalfK);
+    // The tiles are this wave's alone: a wave's LDS accesses run in issue
+    // order, and the compiler keeps these writes and reads of one array in
+    // program order, so half 1's writes follow half 0's reads.
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     float ss = 0.0f;
 #pragma unroll
-    for (uint32_t s = 0; s < kSteps; ++s) {
-        // B: Wq[o0 + r][w * kSliceK + 32 s + 8 grp .. +7] = 16 B chunk 4 s + grp of row r
-        const uint4 wb = wtile[w][r][4 * s + grp];
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hb[s]),
-                                                      __builtin_bit_cast(bf16x8, wb), acc, 0,
-                                                      0, 0);
-        const uint32_t hw[4] = {hb[s].x, hb[s].y, hb[s].z, hb[s].w};
-#pragma unroll
-        for (uint32_t c = 0; c < 4; ++c) {
-            const float lo = bf16_lo(hw[c]), hi = bf16_hi(hw[c]);
-            ss = __builtin_fmaf(lo, lo, ss);  // bf16 squares are exact in FP32
-            ss = __builtin_fmaf(hi, hi, ss);
-        }
+    for (uint32_t i = 0; i < kRowLoads; ++i) {
+        wtile[w][2 * i + pair_row][chunk] = wv0[i];
+        htile[w][2 * i + pair_row][chunk] = hv0[i];
     }
+    half_products(wtile[w], htile[w], r, grp, live, acc, ss);
+#pragma unroll
+    for (uint32_t i = 0; i < kRowLoads; ++i) {
+        wtile[w][2 * i + pair_row][chunk] = wv1[i];
+        htile[w][2 * i + pair_row][chunk] = hv1[i];
+    }
+    half_products(wtile[w], htile[w], r, grp, live, acc, ss);
     // lane holds D[4*grp + i][r] of this K slice; squares of row r over 4 groups
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) part[w][4 * grp + i][r] = acc[i];
