@@ -294,6 +294,26 @@ __device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* tmp) {
     __syncthreads();
     return before + x - v;
 }
+// Two exclusive scans with one exchange between the waves: (scan of v0,
+// scan of v1); tmp0 and tmp1 hold kT / 64 words each.
+template <uint32_t kT = kThreads>
+__device__ uint2 block_exclusive_scan2(uint32_t v0, uint32_t v1, uint32_t* tmp0, uint32_t* tmp1) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t x0 = wave_inclusive_sum_u32(v0), x1 = wave_inclusive_sum_u32(v1);
+    if (lane == 63) {
+        tmp0[wave] = x0;
+        tmp1[wave] = x1;
+    }
+    __syncthreads();
+    uint32_t b0 = 0, b1 = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < kT / 64; ++w) {
+        b0 += w < wave ? tmp0[w] : 0u;
+        b1 += w < wave ? tmp1[w] : 0u;
+    }
+    __syncthreads();
+    return make_uint2(b0 + x0 - v0, b1 + x1 - v1);
+}
 
 // Bucket b (scanning 255 -> 0) where the running count from the top first
 // reaches `need` (1 <= need <= total).  Wave 0 only; results through LDS.
@@ -1278,7 +1298,7 @@ struct HeadSelectLds {
     uint32_t head_count[kMaxHeads], head_bad[kMaxHeads];
     uint32_t tmp[kHWaves];
     uint32_t sh[8];
-    uint32_t sort_lds[kRankOrder ? 2 * kHeadMaxK : 1];
+    uint32_t sort_lds[kRankOrder ? 2 * kHeadMaxK + 8 : 1];
     alignas(16) uint32_t tables[kRankOrder ? 2 * kSortRange : 1];
     uint32_t whist[kRankOrder ? kHWaves : 1][256];
     uint32_t stage[kRankOrder ? 1 : kHeadMaxK];  // id order: the ids before their store
@@ -1420,8 +1440,38 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
     // one scan of both counts (each total <= 32768 fits its 16 bits): the ties
     // taken before this thread are min(ties before it, t_need)
     const uint32_t my_ties = static_cast<uint32_t>(__popc(tie_mask));
-    const uint32_t both = block_exclusive_scan<kHThreads>(
-        (static_cast<uint32_t>(__popc(above_mask)) << 16) | my_ties, tmp);
+    const uint32_t my_counts = (static_cast<uint32_t>(__popc(above_mask)) << 16) | my_ties;
+    // Rank order: the counting sort's bins (below) are scanned in the same
+    // exchange.  Bins above K*'s hold every key, K*'s bin the t_need ties
+    // taken, lower bins nothing.  Thread t owns kPer consecutive bins, thread
+    // 0 the top ones.
+    constexpr uint32_t kPer = kSortRange / kHThreads;
+    const uint32_t first = (kHThreads - 1 - tid) * kPer;
+    uint32_t c[kRankOrder ? kPer : 1], sum = 0, higher = 0, both;
+    if constexpr (kRankOrder) {
+        const uint32_t tie_bin = kstar - base;
+        // a thread's bins move as 16-byte LDS accesses: word accesses at the
+        // 8-word stride between lanes would conflict 16 ways
+        static_assert(kPer == 8, "two 16-byte accesses per thread");
+        uint32_t big = 0;
+        const uint4 b0 = *reinterpret_cast<const uint4*>(table + first);
+        const uint4 b1 = *reinterpret_cast<const uint4*>(table + first + 4);
+        const uint32_t in[kPer] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (uint32_t i = 0; i < kPer; ++i) {
+            const uint32_t bin = first + i;
+            c[i] = bin > tie_bin ? in[i] : (bin == tie_bin ? t_need : 0u);
+            sum += c[i];
+            big = max(big, c[i]);
+        }
+        if (big > kGroupCap) sh[kFlag] = 1u;  // read after the scan's barriers
+        // (hist[1], the id-order table, is free in rank order)
+        const uint2 sc = block_exclusive_scan2<kHThreads>(my_counts, sum, tmp, hist[1]);
+        both = sc.x;
+        higher = sc.y;
+    } else {
+        both = block_exclusive_scan<kHThreads>(my_counts, tmp);
+    }
     const uint32_t tie_start = both & 0xffffu;
     const uint32_t my_taken = std::min(my_ties, sat_sub(t_need, tie_start));
     uint32_t pos = (both >> 16) + std::min(tie_start, t_need);
@@ -1462,32 +1512,9 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
         }
     } else {
         // Rank order (k <= kHeadMaxK here): a counting sort by key over the
-        // table's bins, larger keys first.  Bins above K*'s hold every key,
-        // K*'s bin the t_need ties taken, lower bins nothing.  Thread t owns
-        // kPer consecutive bins, thread 0 the top ones.
+        // table's bins (counted and scanned above), larger keys first.
         const uint32_t m = k;
-        const uint32_t tie_bin = kstar - base;
         uint32_t* cursor = tables + kSortRange;
-        constexpr uint32_t kPer = kSortRange / kHThreads;
-        const uint32_t first = (kHThreads - 1 - tid) * kPer;
-        // a thread's bins move as 16-byte LDS accesses: word accesses at the
-        // 8-word stride between lanes would conflict 16 ways
-        static_assert(kPer == 8, "two 16-byte accesses per thread");
-        uint32_t c[kPer], sum = 0, big = 0;
-        {
-            const uint4 b0 = *reinterpret_cast<const uint4*>(table + first);
-            const uint4 b1 = *reinterpret_cast<const uint4*>(table + first + 4);
-            const uint32_t in[kPer] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-            for (uint32_t i = 0; i < kPer; ++i) {
-                const uint32_t bin = first + i;
-                c[i] = bin > tie_bin ? in[i] : (bin == tie_bin ? t_need : 0u);
-                sum += c[i];
-                big = max(big, c[i]);
-            }
-        }
-        if (big > kGroupCap) sh[kFlag] = 1u;  // read after the scan's barriers
-        const uint32_t higher = block_exclusive_scan<kHThreads>(sum, tmp);
         uint32_t* B = sort_lds;
         if (sh[kFlag] == 0) {
             uint32_t run = higher + sum, at[kPer];
@@ -1503,13 +1530,33 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
             *reinterpret_cast<uint4*>(cursor + first) = a0;
             *reinterpret_cast<uint4*>(cursor + first + 4) = a1;
             if (tid < 8) B[m + tid] = 0xffffffffu;  // past every composite
-            __syncthreads();
-            // each selected composite ((0xffff - key) << 16 | id) into its key's group
+            // the selected composites ((0xffff - key) << 16 | id) in id order into
+            // C (past B and its padding), then each into its key's group from
+            // there, one per lane: a pass over the ids would spend an LDS atomic
+            // and an exec-mask change per id on the 20 % selected.  The
+            // compaction has no branch either: an id not selected writes its
+            // composite to the thread's own spare word (in the radix sort's
+            // histograms, unused on this path).
+            uint32_t* C = sort_lds + kHeadMaxK + 8;
+            static_assert(sizeof(whist) >= kHThreads * sizeof(uint32_t), "a spare word per thread");
+            {
+                uint32_t* spare = &whist[0][0] + tid;
+                uint32_t at = pos;
 #pragma unroll
-            for (uint32_t j = 0; j < kHRun; ++j) {
-                if ((bits32 >> j) & 1u) {
-                    const uint32_t key = half_at(keys, j);
-                    B[atomicAdd(&cursor[key - base], 1u)] = ((0xffffu - key) << 16) | (begin + j);
+                for (uint32_t j = 0; j < kHRun; ++j) {
+                    const uint32_t sel = (bits32 >> j) & 1u;
+                    *(sel ? C + at : spare) = ((0xffffu - half_at(keys, j)) << 16) | (begin + j);
+                    at += sel;
+                }
+            }
+            __syncthreads();
+            constexpr uint32_t kDense = kHeadMaxK / kHThreads;
+#pragma unroll
+            for (uint32_t u = 0; u < kDense; ++u) {
+                const uint32_t q = tid + u * kHThreads;
+                if (q < m) {
+                    const uint32_t e = C[q];
+                    B[atomicAdd(&cursor[0xffffu - (e >> 16) - base], 1u)] = e;
                 }
             }
             __syncthreads();
