@@ -125,15 +125,16 @@ def order_keys(bits):
     return np.where(b & 0x8000, (~b) & 0xFFFF, b | 0x8000)
 
 
-@pytest.mark.parametrize("case", ["counting", "full_k", "wide_range", "long_run"])
+@pytest.mark.parametrize("case", ["counting", "full_k", "wide_range", "long_run", "full_k_long_run"])
 def test_rank_order_placement_paths(hs, port, case):
     # The per-head rank order places the selection by a counting sort over
     # the 8192 keys from K*'s 256-key bucket upward, and falls back to a radix
     # sort when a selected key lies past them or more than 64 selected keys
     # are equal.  Each case is checked (on the oracle's selection) to take
     # the path it names.  full_k selects the most a per-head workgroup holds
-    # (k = 8192): the counting sort's lists then fill its LDS buffers.
-    g = rng({"counting": 21, "full_k": 24, "wide_range": 22, "long_run": 23}[case])
+    # (k = 8192): the counting sort's lists, or the radix sort's two
+    # buffers (full_k_long_run), then fill its LDS.
+    g = rng({"counting": 21, "full_k": 24, "wide_range": 22, "long_run": 23, "full_k_long_run": 25}[case])
     heads, n = 4, 32768
     if case == "wide_range":
         # 30 % of the tokens spread over every positive normal key, the rest
@@ -144,13 +145,13 @@ def test_rank_order_placement_paths(hs, port, case):
         alpha, ratio = 70000.0, 0.25
     else:
         s = f16_bits(g.standard_normal((heads, n)) * 2.0)
-        if case == "long_run":
+        if case in ("long_run", "full_k_long_run"):
             s[:, 1000:1100] = hb(9.5)  # 100 equal keys at the top of every head
         # full_k: every key within alpha of the maximum, so k = the cap n / 4
-        alpha, ratio = (100.0, 0.25) if case == "full_k" else (5.0, 0.2)
+        alpha, ratio = (100.0, 0.25) if case.startswith("full_k") else (5.0, 0.2)
     rc, k, ids, _, _ = port.select(s, heads, n, n, alpha, ratio)
     assert rc == 0 and k <= 8192
-    if case == "full_k":
+    if case.startswith("full_k"):
         assert k == 8192
     keys = order_keys(s[np.arange(heads)[:, None], ids])
     kstar = keys.min(axis=1)
@@ -160,7 +161,7 @@ def test_rank_order_placement_paths(hs, port, case):
         assert (span < 8192).all() and run <= 64
     elif case == "wide_range":
         assert (span >= 8192).any()
-    else:
+    else:  # long_run, full_k_long_run
         assert (span < 8192).all() and run > 64
     check_against_port(hs, port, s, heads, n, n, alpha, ratio)
 
