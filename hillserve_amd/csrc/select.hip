@@ -40,6 +40,15 @@
 //  4. rank:   (rank order only) each id lands at (#head keys above its key)
 //             + (#equal keys in earlier slices) + (its rank among equal keys
 //             of its slice), from histograms over the selected key range.
+// For n <= 32768 steps 2-4 are one launch of a 1024-thread workgroup per
+// head (section 2' below).  Its rank order is a counting sort over the 8192
+// keys from K*'s 256-key bucket upward: the selected (key, id) composites
+// compacted in id order, scattered one per lane into their key's group, and
+// each placed by its rank among its group's ids; a radix sort takes over
+// when the selected keys span more than that table or more than 64 are
+// equal.  Its phases are bound by instruction issue (16 waves on one CU's 4
+// SIMDs), so the placement avoids per-id branches.  The count launch runs
+// over every (head, slice) pair before it, as in step 1.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
