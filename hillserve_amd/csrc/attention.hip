@@ -252,7 +252,7 @@ attn_kv_kernel(const float* __restrict__ q, const uint8_t* __restrict__ pool, ui
                 p[j] = sv[j] == -INFINITY ? 0.0f : weight_f16(__expf(sv[j] - m[j]));
                 ps[j] += p[j];
             }
-            if (64 * c + lane < total) sel_p[g][64 * c + lane] = make_float4(p[0], p[1], p[2], p[3]);
+            sel_p[g][64 * c + lane] = make_float4(p[0], p[1], p[2], p[3]);  // 0 past the union
         }
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) lsum[j] = first_lane(wave_sum_f32(ps[j]));
@@ -269,13 +269,11 @@ attn_kv_kernel(const float* __restrict__ q, const uint8_t* __restrict__ pool, ui
         if (t < tiles) {
 #pragma unroll
             for (uint32_t i = 0; i < 4; i += 2) {  // rows 16t + 4i + q16 and 4 after it
+                // (a row past the union has weight 0 and a finite V row)
                 const uint32_t e = 16 * t + 4 * i + q16;
-                const float4 pa = sel_p[g][min(e, total - 1)], pb = sel_p[g][min(e + 4, total - 1)];
-                const bool la = e < total, lb = e + 4 < total;
-                const half2v w[4] = {weight_pair(la ? pa.x : 0.0f, lb ? pb.x : 0.0f),
-                                     weight_pair(la ? pa.y : 0.0f, lb ? pb.y : 0.0f),
-                                     weight_pair(la ? pa.z : 0.0f, lb ? pb.z : 0.0f),
-                                     weight_pair(la ? pa.w : 0.0f, lb ? pb.w : 0.0f)};
+                const float4 pa = sel_p[g][e], pb = sel_p[g][e + 4];
+                const half2v w[4] = {weight_pair(pa.x, pb.x), weight_pair(pa.y, pb.y),
+                                     weight_pair(pa.z, pb.z), weight_pair(pa.w, pb.w)};
                 accumulate_pair(o, w, vw[t][i], vw[t][i + 1]);
             }
         }
@@ -382,7 +380,8 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
     // the lane's rows 4i + q16 first (4 per LDS read), then the loads back to
     // back; a row past the union reads the union's last row again
     constexpr uint32_t kGroups = kChunk / 4;
-    const uint32_t groups = (total + 3) / 4;  // wave-uniform
+    // groups in pairs: an odd count loads one more group, of the last row
+    const uint32_t groups = ((total + 3) / 4 + 1) & ~1u;  // wave-uniform
     const uint32_t last_row = reinterpret_cast<const uint32_t*>(&sel_row[g][(total - 1) & 3u][0])[(total - 1) >> 2];
     uint32_t my_row[kGroups];
 #pragma unroll
@@ -428,7 +427,7 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
                 p[j] = sv[j] == -INFINITY ? 0.0f : weight_f16(__expf(sv[j] - m[j]));
                 ps[j] += p[j];
             }
-            if (64 * c + lane < total) sel_p[g][64 * c + lane] = make_float4(p[0], p[1], p[2], p[3]);
+            sel_p[g][64 * c + lane] = make_float4(p[0], p[1], p[2], p[3]);  // 0 past the union
         }
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) lsum[j] = first_lane(wave_sum_f32(ps[j]));
@@ -440,20 +439,17 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
     for (uint32_t j = 0; j < 4; ++j)
 #pragma unroll
         for (uint32_t c = 0; c < 8; ++c) o[j][c] = 0.0f;
-    // groups i and i + 1 (rows 4i + q16 and 4 after it) per step; a group
-    // past the union's last holds zero weights and zero rows
+    // groups i and i + 1 (rows 4i + q16 and 4 after it) per step; a row
+    // past the union holds weight 0 and the union's last (finite) V row, so
+    // it adds exactly nothing
 #pragma unroll
     for (uint32_t i = 0; i < kGroups; i += 2) {
         if (i < groups) {
             const uint32_t e = 4 * i + q16;
-            const float4 pa = sel_p[g][min(e, total - 1)], pb = sel_p[g][min(e + 4, total - 1)];
-            const bool la = e < total, lb = e + 4 < total;
-            const half2v w[4] = {weight_pair(la ? pa.x : 0.0f, lb ? pb.x : 0.0f),
-                                 weight_pair(la ? pa.y : 0.0f, lb ? pb.y : 0.0f),
-                                 weight_pair(la ? pa.z : 0.0f, lb ? pb.z : 0.0f),
-                                 weight_pair(la ? pa.w : 0.0f, lb ? pb.w : 0.0f)};
-            const uint4 vb = i + 1 < groups ? vw[i + 1] : make_uint4(0u, 0u, 0u, 0u);
-            accumulate_pair(o, w, vw[i], vb);
+            const float4 pa = sel_p[g][e], pb = sel_p[g][e + 4];
+            const half2v w[4] = {weight_pair(pa.x, pb.x), weight_pair(pa.y, pb.y),
+                                 weight_pair(pa.z, pb.z), weight_pair(pa.w, pb.w)};
+            accumulate_pair(o, w, vw[i], vw[i + 1]);
         }
     }
 #pragma unroll
