@@ -310,12 +310,18 @@ attn_kv_kernel(const float* __restrict__ q, const uint8_t* __restrict__ pool, ui
 //  4. o += p * V as the rows land; the 4 row groups' o are added and the
 //     wave writes the chunk's (m, l, o[128]) record per query head, merged by
 //     attn_combine_kernel as before.
-template <bool kRows>
+// kBuffer: the V rows are read through a raw buffer over the pool
+// (pool_bytes < kBufferLimit), where a load at kPastEnd returns zeros with
+// no memory access (the buffer's range check).
+constexpr uint32_t kBufferLimit = 0xffff0000u, kPastEnd = 0xfffffff0u;
+constexpr int kBufferWord3 = 0x00020000;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <bool kRows, bool kBuffer>
 __global__ void __launch_bounds__(kThreads)
 attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* __restrict__ v_pool,
               uint32_t row_bytes, const int32_t* __restrict__ rows, uint32_t pool_rows,
-              const uint32_t* __restrict__ member, uint32_t n, uint32_t chunks,
-              float* __restrict__ part) {
+              uint32_t pool_bytes, const uint32_t* __restrict__ member, uint32_t n,
+              uint32_t chunks, float* __restrict__ part) {
     // union row e's pool row at sel_row[g][e % 4][e / 4]: the row group a
     // lane reads (e % 4 = l / 16) is contiguous, so its rows come in 4 at a time
     __shared__ uint4 sel_row[8][4][kChunk / 16];
@@ -351,7 +357,9 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
         const uint64_t any = __ballot(mk != 0);
         if (mk) {
             const uint32_t at = total + lanes_below(any);
-            reinterpret_cast<uint32_t*>(&sel_row[g][at & 3u][0])[at >> 2] = r;
+            // (buffer: the byte offset of the row's KV-head segment)
+            reinterpret_cast<uint32_t*>(&sel_row[g][at & 3u][0])[at >> 2] =
+                kBuffer ? r * row_bytes + g * 256 : r;
             float sv[4];
 #pragma unroll
             for (uint32_t j = 0; j < 4; ++j) sv[j] = ((mk >> j) & 1u) ? sd[c][j] * kScale : -INFINITY;
@@ -378,11 +386,10 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
     }
     // ---- every V segment of the union in flight (groups of 4 rows) ----
     // the lane's rows 4i + q16 first (4 per LDS read), then the loads back to
-    // back; a row past the union reads the union's last row again
+    // back; a row past the union reads zeros (buffer) or the union's last row
     constexpr uint32_t kGroups = kChunk / 4;
-    // groups in pairs: an odd count loads one more group, of the last row
+    // groups in pairs: an odd count loads one more group
     const uint32_t groups = ((total + 3) / 4 + 1) & ~1u;  // wave-uniform
-    const uint32_t last_row = reinterpret_cast<const uint32_t*>(&sel_row[g][(total - 1) & 3u][0])[(total - 1) >> 2];
     uint32_t my_row[kGroups];
 #pragma unroll
     for (uint32_t i4 = 0; i4 < kGroups / 4; ++i4) {
@@ -393,12 +400,35 @@ attn_v_kernel(const float* __restrict__ dots, uint32_t dstride, const uint8_t* _
         my_row[4 * i4 + 3] = r4.w;
     }
     uint4 vw[kGroups];
-    const uint8_t* vbase = v_pool + g * 256 + 16 * r16;
+    if constexpr (kBuffer) {
+        // whole batches of 8 groups, a batch's loads unconditional (rows past
+        // the union at kPastEnd): the compiler then knows how many loads follow
+        // each group within its batch, and a pair of groups waits for its own
+        // rows rather than for every load the wave has in flight
+        const __amdgpu_buffer_rsrc_t vbuf = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(v_pool), static_cast<short>(0), static_cast<int>(pool_bytes), kBufferWord3);
 #pragma unroll
-    for (uint32_t i = 0; i < kGroups; ++i) {
-        if (i < groups) {
-            const uint32_t r = 4 * i + q16 < total ? my_row[i] : last_row;
-            vw[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(r) * row_bytes);
+        for (uint32_t b = 0; b < kGroups / 8; ++b) {
+            if (8 * b < groups) {
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j) {
+                    const uint32_t i = 8 * b + j;
+                    const uint32_t off = 4 * i + q16 < total ? my_row[i] + 16 * r16 : kPastEnd;
+                    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(vbuf, off, 0, 0);
+                    vw[i] = make_uint4(x.x, x.y, x.z, x.w);
+                }
+            }
+        }
+    } else {
+        const uint32_t last_row =
+            reinterpret_cast<const uint32_t*>(&sel_row[g][(total - 1) & 3u][0])[(total - 1) >> 2];
+        const uint8_t* vbase = v_pool + g * 256 + 16 * r16;
+#pragma unroll
+        for (uint32_t i = 0; i < kGroups; ++i) {
+            if (i < groups) {
+                const uint32_t r = 4 * i + q16 < total ? my_row[i] : last_row;
+                vw[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(r) * row_bytes);
+            }
         }
     }
     // ---- the chunk's exact maximum per head, then p and l ----
@@ -524,12 +554,24 @@ int launch_attention_logits(const float* logits, size_t logit_stride, const uint
     float* part = static_cast<float*>(workspace);
     const auto ls = static_cast<uint32_t>(logit_stride);
     const auto rb = static_cast<uint32_t>(row_bytes);
-    if (rows)
-        hipLaunchKernelGGL(attn_v_kernel<true>, dim3(chunks), dim3(kThreads), 0, stream, logits, ls,
-                           v_pool, rb, rows, pool_rows, member, n, chunks, part);
-    else
-        hipLaunchKernelGGL(attn_v_kernel<false>, dim3(chunks), dim3(kThreads), 0, stream, logits, ls,
-                           v_pool, rb, rows, 0u, member, n, chunks, part);
+    // the rows a V read can reach: the pool's rows, or ids below n
+    const uint64_t pool_bytes = static_cast<uint64_t>(rows ? pool_rows : n) * row_bytes;
+    const auto pb = static_cast<uint32_t>(pool_bytes);
+    if (pool_bytes < kBufferLimit) {
+        if (rows)
+            hipLaunchKernelGGL((attn_v_kernel<true, true>), dim3(chunks), dim3(kThreads), 0, stream, logits,
+                               ls, v_pool, rb, rows, pool_rows, pb, member, n, chunks, part);
+        else
+            hipLaunchKernelGGL((attn_v_kernel<false, true>), dim3(chunks), dim3(kThreads), 0, stream, logits,
+                               ls, v_pool, rb, rows, 0u, pb, member, n, chunks, part);
+    } else {
+        if (rows)
+            hipLaunchKernelGGL((attn_v_kernel<true, false>), dim3(chunks), dim3(kThreads), 0, stream, logits,
+                               ls, v_pool, rb, rows, pool_rows, 0u, member, n, chunks, part);
+        else
+            hipLaunchKernelGGL((attn_v_kernel<false, false>), dim3(chunks), dim3(kThreads), 0, stream, logits,
+                               ls, v_pool, rb, rows, 0u, 0u, member, n, chunks, part);
+    }
     hipLaunchKernelGGL(attn_combine_kernel, dim3(32, 4), dim3(kCombineThreads), 0, stream,
                        static_cast<const float*>(workspace), chunks, out);
     const hipError_t st = hipGetLastError();

@@ -66,6 +66,12 @@ def test_attention_from_dots(hs, port, n, frac, mapped):
     q16 = to_dev(f16_bits(g.standard_normal((32, 128))).reshape(-1))
     _, dots = hs.ops.score_logits(q16, qd, k_rows, n, rows=rows)
     out = hs.ops.sparse_attention_logits(dots, v_rows, n, member, rows=rows)
+    if mapped:
+        # a pool declared at 4 GiB (2^21 rows of 2048 B) takes the kernel's
+        # 64-bit row addressing instead of its buffer reads; the rows the map
+        # names are the same, and so are the output's bits
+        wide = hs.ops.sparse_attention_logits(dots, v_rows, n, member, rows=rows, pool_rows=1 << 21)
+        assert torch.equal(wide, out)
     ref = port.attention(q32, records.view(np.uint8).reshape(-1), ids, rows=perm)
     got = out.cpu().numpy().astype(np.float64)
     assert rel_err(got, ref) <= TOL
