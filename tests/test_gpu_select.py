@@ -347,6 +347,27 @@ def test_random_sweep_against_oracle(hs, port):
         check_against_port(hs, port, s, heads, stride, n, alpha, ratio, fp32)
 
 
+def test_per_head_sweep_against_oracle(hs, port):
+    # the per-head launch (32 heads, n <= 32768) at every cap up to the
+    # largest rank-order selection it holds (k <= 8192): tie-heavy, Gaussian,
+    # narrow (long runs of equal F16 keys, the radix fallback) and wide (key
+    # ranges past the counting table) scores, FP32 counts on and off
+    g = rng(424242)
+    for case in range(64):
+        heads, n = 32, int(g.integers(500, 32769))
+        stride = n + int(g.integers(0, 16))
+        alpha = float(g.choice([0.0, 0.5, 2.0, 5.0, 8.0, 100.0]))
+        ratio = float(np.float32(g.choice([0.05, 0.1, 0.2, 0.25])))
+        s = np.full((heads, stride), hb(-60000), dtype=np.uint16)
+        kind = case % 4
+        if kind == 0:
+            vals = (g.integers(0, 64, size=(heads, n)) - 32) / 4.0
+        else:
+            vals = g.standard_normal((heads, n)) * (3.0, 0.05, 30.0)[kind - 1]
+        s[:, :n] = f16_bits(vals)
+        check_against_port(hs, port, s, heads, stride, n, alpha, ratio, bool(case % 2))
+
+
 def test_random_batch_sweep_against_oracle(hs, port):
     # a batch of 16 raw-score jobs with 16-byte aligned rows (four slices per
     # count group) and one with a ragged stride, each against the oracle over
