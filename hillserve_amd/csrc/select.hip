@@ -1545,17 +1545,25 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
             // and an exec-mask change per id on the 20 % selected.  The
             // compaction has no branch either: an id not selected writes its
             // composite to the thread's own spare word (in the radix sort's
-            // histograms, unused on this path).
+            // histograms, unused on this path).  The store's address is
+            // spare + sel * gap, gap the bytes from the spare word to the next
+            // place in C: one 24-bit multiply-add per id instead of a compare
+            // and a select, and one shift-add to move the place on.
             uint32_t* C = sort_lds + kHeadMaxK + 8;
             static_assert(sizeof(whist) >= kHThreads * sizeof(uint32_t), "a spare word per thread");
+            static_assert(sizeof(HeadSelectLds<kRankOrder>) < (1u << 23), "gap fits 24 signed bits");
             {
-                uint32_t* spare = &whist[0][0] + tid;
-                uint32_t at = pos;
+                char* const spare = reinterpret_cast<char*>(&whist[0][0] + tid);
+                int gap = static_cast<int>(reinterpret_cast<char*>(C + pos) - spare);  // < 0
 #pragma unroll
                 for (uint32_t j = 0; j < kHRun; ++j) {
                     const uint32_t sel = (bits32 >> j) & 1u;
-                    *(sel ? C + at : spare) = ((0xffffu - half_at(keys, j)) << 16) | (begin + j);
-                    at += sel;
+                    *reinterpret_cast<uint32_t*>(spare + __mul24(static_cast<int>(sel), gap)) =
+                        ((0xffffu - half_at(keys, j)) << 16) | (begin + j);
+                    gap += static_cast<int>(sel << 2);
+                    // opaque, so the place stays in bytes: folded back into
+                    // a count of words it costs a shift per id
+                    asm("" : "+v"(gap));
                 }
             }
             __syncthreads();
