@@ -1405,7 +1405,24 @@ __device__ __forceinline__ void head_select(const SelectJobs& js, uint32_t h, ui
     constexpr uint32_t kSpan = kRankOrder ? kSortRange : 256u;
     uint32_t* table = kRankOrder ? tables : hist[1];
     uint32_t top = 0;  // the largest key counted from the base (rank order)
-    if (begin + kHRun <= n) {  // every thread but a row's last, partial one
+    if (kRankOrder && begin + kHRun <= n) {
+        // no branch per key (three VALU instructions and an LDS add, where a
+        // branch costs six and two exec-mask changes): a key outside the
+        // table counts into this lane's own word past it, a cursor word
+        // that the placement writes before it reads any; the largest key
+        // comes from packed 16-bit maxima of the key words
+        const uint32_t lim = kSpan + lane;
+        typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+        u16x2 pm = __builtin_bit_cast(u16x2, keys[0]);
+#pragma unroll
+        for (uint32_t j = 0; j < kHRun; ++j) {
+            const uint32_t d = half_at(keys, j) - base;  // wraps below the bucket
+            atomicAdd(&table[min(d, lim)], 1u);
+            if (j % 2 == 1 && j > 1)
+                pm = __builtin_elementwise_max(pm, __builtin_bit_cast(u16x2, keys[j / 2]));
+        }
+        top = max(static_cast<uint32_t>(pm.x), static_cast<uint32_t>(pm.y));
+    } else if (begin + kHRun <= n) {  // every thread but a row's last, partial one
 #pragma unroll
         for (uint32_t j = 0; j < kHRun; ++j) {
             const uint32_t key = half_at(keys, j);
